@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""Decode-step benchmark on one MI355X (Llama-3-8B shape).
+
+Workload (synthetic, seeded): 64 sequences, 32 query / 8 KV heads, head_dim
+128, block_size 16, context ~ U[512, 4096] plus one token appended per
+sequence before attention, bf16 K/V scattered over a shuffled page pool.  The
+pool holds several layers and consecutive steps cycle through them, so each
+step reads KV that is not resident in the 256 MB Infinity Cache -- as the 32
+layers of a real decode step do.
+
+A timed step = one transformer layer of a decode step through libkcmm.so:
+QKV GEMM -> KV append (device slots) -> paged attention -> O GEMM -> gate+up
+GEMM -> down GEMM.  HIP events on the launch stream time every call.
+
+Printed JSON: `value` is decode-attention KV GB/s (algorithmic K+V bytes of
+one layer-step / attention call time); decode tokens/s = 64 / (32 * t_layer)
+with t_layer the sum of the six calls (lm_head, sampling, norms, RoPE and
+SwiGLU glue are not in this path and are excluded).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, vendor figure
+
+B, HQ, HKV, D, BS = 64, 32, 8, 128, 16
+CTX_LO, CTX_HI = 512, 4096
+MODEL_LAYERS = 32
+HIDDEN, INTER = 4096, 14336
+GEMMS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--layers", type=int, default=4, help="KV/weight sets cycled through")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--attn-only", action="store_true", help="time attention (+append) only")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(case, seconds, threads):
+    """The reference kernel's loop (oracle restatement) on host cores, on a
+    bounded sample: layer 0 of the same workload, the first sequences that
+    fit the time budget."""
+    import oracle as O
+    from lattice_amd.bindings import memcpy_dtoh
+    g = case.geometry
+    kreg = memcpy_dtoh(case.pool.va_k(0), g["mapped_bytes"])
+    vreg = memcpy_dtoh(case.pool.va_v(0), g["mapped_bytes"])
+    scale = 1 / math.sqrt(D)
+    # estimate with 4 sequences, then size the sample to ~`seconds`
+    def run(nseq, reps=1):
+        bt = case.block_tables[:nseq]
+        sl = case.seq_lens[:nseq]
+        q = case.q_bits[:nseq]
+        out = np.zeros((nseq, HQ, D), np.float32)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            O.attn_decode_ref_f32(1, q, kreg, vreg, bt, sl, case.offsets_f16, HQ, HKV, D, BS,
+                                  g["row_bytes"], scale, threads=threads, out=out)
+        return (time.perf_counter() - t0) / reps
+    t4 = run(4)
+    per_seq = t4 / 4
+    nseq = B
+    reps = max(1, int(seconds / max(per_seq * B, 1e-6)))
+    if per_seq * B > seconds:
+        nseq = max(4, int(seconds / per_seq))
+        reps = 1
+    t = run(nseq, reps)
+    kv = int(case.seq_lens[:nseq].astype(np.int64).sum()) * 2 * HKV * D * 2
+    return dict(value=round(kv / t / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                sample=(f"oracle restatement of ref kcmm_vllm_paged_attn.cu loop (fp32, bf16 KV), "
+                        f"layer 0, {nseq} of {B} seqs ({kv / 1e6:.1f} MB KV) x {reps} reps, "
+                        f"{t * 1e3:.1f} ms per pass"))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                          "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+        sys.exit(2)
+    import torch
+    from lattice_amd.bindings import KV_BF16, KcmmLibrary, make_config
+    from lattice_amd.workload import build_decode_case
+
+    assert torch.cuda.is_available(), "bench needs a GPU"
+    lib = KcmmLibrary()
+    rng = np.random.default_rng(args.seed)
+    ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B)          # context before the appended token
+    L = ctx + 1
+    t0 = time.perf_counter()
+    case = build_decode_case(lib, batch=B, num_q_heads=HQ, kv_heads=HKV, head_dim=D,
+                             block_size=BS, ctx_lens=L, dtype=KV_BF16, num_layers=args.layers,
+                             seed=args.seed + 1, host_mirror=False)
+    log(f"workload built in {time.perf_counter() - t0:.1f}s: {case.pool.stats()['superblock_count']} "
+        f"superblocks/region, backing={'vmm' if case.pool.backing_kind() == 0 else 'flat'}")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 2)
+
+    # appended token: device slot ids of position ctx_b in each sequence
+    slots = np.array([case.block_tables[b, int(ctx[b]) // BS] * BS + int(ctx[b]) % BS
+                      for b in range(B)], dtype=np.int64)
+    slots_t = torch.from_numpy(slots).to(dev)
+    offs_t = case.dev["offs"]
+    k_new = torch.randn((B, HKV * D), generator=g, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((B, HKV * D), generator=g, device=dev).to(torch.bfloat16)
+
+    # projection weights (two sets, alternating by layer) and activations
+    nw = 2
+    weights = [{name: (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+                for name, n, k in GEMMS} for _ in range(nw)]
+    x_in = torch.randn((B, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
+    x_act = torch.randn((B, INTER), generator=g, device=dev).to(torch.bfloat16)
+    outs = {name: torch.empty((B, n), dtype=torch.bfloat16, device=dev) for name, n, _ in GEMMS}
+    kv_bytes = case.kv_bytes()                     # identical for every layer
+    scale = 1 / math.sqrt(D)
+
+    def append(layer):
+        case.pool.append_kv_device_slots_on_stream(
+            layer_idx=layer, slot_mapping_ptr=slots_t.data_ptr(),
+            block_offsets_f16_ptr=offs_t.data_ptr(), valid_blocks_ptr=0,
+            block_offsets_f16_len=offs_t.numel(), batch=B, k_src_ptr=k_new.data_ptr(),
+            v_src_ptr=v_new.data_ptr(), status_ptr=0, stream_ptr=sp)
+
+    def gemm(name, layer):
+        w = weights[layer % nw][name]
+        x = x_act if name == "down" else x_in       # [64][14336] or [64][4096] activations
+        n, k = w.shape
+        lib.gemm_bf16(x.data_ptr(), w.data_ptr(), outs[name].data_ptr(), B, n, k, sp)
+
+    names = ["qkv", "append", "attn", "o", "gate_up", "down"]
+    if args.attn_only:
+        names = ["append", "attn"]
+    calls = {
+        "qkv": lambda l: gemm("qkv", l),
+        "append": append,
+        "attn": lambda l: case.run_attention(layer=l, stream_ptr=sp, scale=scale),
+        "o": lambda l: gemm("o", l),
+        "gate_up": lambda l: gemm("gate_up", l),
+        "down": lambda l: gemm("down", l),
+    }
+
+    for i in range(args.warmup):
+        for n in names:
+            calls[n](i % args.layers)
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} steps)")
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(args.steps):
+        layer = i % args.layers
+        ev[i][0].record(stream)
+        for j, n in enumerate(names):
+            calls[n](layer)
+            ev[i][j + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    per = {n: np.mean([ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(args.steps)])
+           for j, n in enumerate(names)}
+    step_ms = float(np.mean([ev[i][0].elapsed_time(ev[i][-1]) for i in range(args.steps)]))
+    log("per-call ms: " + ", ".join(f"{k}={v:.4f}" for k, v in per.items()))
+
+    attn_s = per["attn"] / 1e3
+    kv_gbs = kv_bytes / attn_s / 1e9
+    result = {
+        "metric": "decode attn KV GB/s (% HBM peak) + decode tokens/s, 8B-shape bs=64, 1 GPU",
+        "value": round(kv_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V, N(0,0.02) weights; no checkpoint)",
+        "config": {"workload": "llama3-8b-shape decode layer-step: paged attention + KV append "
+                               "+ QKV/O/gate_up/down GEMMs",
+                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "block_size": BS,
+                   "ctx": f"U[{CTX_LO},{CTX_HI}]+1", "mean_len": float(L.mean()),
+                   "kv_sets_cycled": args.layers, "kv_dtype": "bf16"},
+        "kv_frac_of_hbm_peak": round(kv_gbs / HBM_PEAK_GBS, 4),
+        "attn_us_per_layer_step": round(per["attn"] * 1e3, 2),
+        "kv_bytes_per_layer_step": kv_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(kv_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "paged decode attention call (attn_decode_mfma + split merge)"},
+        "append_us": round(per["append"] * 1e3, 2),
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.attn_only:
+        t_layer_s = sum(per[n] for n in names) / 1e3
+        result["decode_tokens_per_s"] = round(B / (MODEL_LAYERS * t_layer_s), 1)
+        result["t_layer_us"] = round(t_layer_s * 1e6, 2)
+        gem = {}
+        for name, n, k in GEMMS:
+            s = per[name] / 1e3
+            flops = 2.0 * B * n * k
+            byts = 2.0 * (n * k + B * k + B * n)
+            ceiling = min(BF16_PEAK_TFLOPS * 1e12, HBM_PEAK_GBS * 1e9 * flops / byts)
+            gem[name] = {"us": round(per[name] * 1e3, 2), "tflops": round(flops / s / 1e12, 1),
+                         "gbs": round(byts / s / 1e9, 1),
+                         "frac_of_min_roofline": round(flops / s / ceiling, 4),
+                         "frac_of_mfma_peak": round(flops / s / (BF16_PEAK_TFLOPS * 1e12), 4)}
+        result["gemm_m64"] = gem
+    if not args.no_cpu_baseline:
+        threads = len(os.sched_getaffinity(0))
+        log(f"cpu baseline on {threads} threads ...")
+        result["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds, threads)
+    else:
+        result["cpu_baseline"] = None
+    case.pool.destroy()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

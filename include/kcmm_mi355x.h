@@ -1,0 +1,132 @@
+/*
+ * kcmm_mi355x.h -- MI355X additions to the KCMM C ABI.
+ *
+ * The reference ships an f16-only cache (ref pool.rs:203-204), a placeholder
+ * prefix-sharing manager (ref sharing.rs:24-65) and runs its projections
+ * through cuBLAS (ref runtime.rs:17-41).  The entry points below add what the
+ * decode-step data path needs on MI355X, next to the reference ABI in
+ * kcmm.h and with the same conventions (0 / -1, per-pool error text,
+ * device addresses as uint64_t, stream_ptr = hipStream_t).
+ */
+#ifndef KCMM_MI355X_H
+#define KCMM_MI355X_H
+
+#include "kcmm.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/** Element type of a pool's K/V pages. */
+typedef enum {
+    KCMM_KV_F16 = 0,       /* IEEE half (the reference's only type) */
+    KCMM_KV_BF16 = 1,      /* bfloat16 */
+    KCMM_KV_FP8_E4M3 = 2,  /* OCP e4m3fn + one fp32 scale per (page, kv head) */
+} kcmm_kv_dtype_t;
+
+/**
+ * Create a pool whose pages hold `kv_dtype` elements.  Page layout in every
+ * layer's K and V region: [block_size][kv_heads][head_dim] elements, token
+ * major, exactly as the reference (ref pool.rs:1036-1098).  fp8 pages add a
+ * footer of kv_heads fp32 scales at byte bs*kv_heads*head_dim and are padded
+ * to a multiple of 256 bytes, so a page copy moves its scales with it.
+ * Extends kcmm_pool_create (ref kcmm.h:193), which is the KCMM_KV_F16 case.
+ */
+kcmm_pool_t *kcmm_pool_create_typed(const kcmm_config_t *config, int32_t kv_dtype);
+
+/** Pool element type (kcmm_kv_dtype_t), or -1 for NULL. */
+int32_t kcmm_get_kv_dtype(kcmm_pool_t *pool);
+
+/** 0 = pages backed by HIP VMM 2 MiB superblocks mapped on demand (the
+ *  reference design, ref cuda_vmm.rs), 1 = one hipMalloc per region (used
+ *  when VMM is unavailable or KCMM_BACKING=flat), -1 for NULL. */
+int32_t kcmm_get_backing_kind(kcmm_pool_t *pool);
+
+/** Why the last kcmm_pool_create* on this thread returned NULL (the reference
+ *  has no channel for this, ref ffi.rs:500-531). */
+size_t kcmm_last_create_error(char *buf, size_t max_len);
+
+/* ---- decode attention for bf16 / fp8 pools ------------------------------ */
+
+/** Same tensor contract as kcmm_paged_attn_decode_f16 (ref kcmm.h:505) with
+ *  bf16 q/out and a bf16 pool.  Synchronizes before returning. */
+int kcmm_paged_attn_decode_bf16(kcmm_pool_t *pool, uint32_t layer_idx,
+                                uint64_t query_ptr, uint64_t out_ptr,
+                                uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+                                uint64_t block_offsets_f16_ptr,
+                                uint32_t batch, uint32_t num_q_heads,
+                                uint32_t kv_heads, uint32_t head_dim,
+                                uint32_t block_size, uint32_t max_blocks_per_seq,
+                                float scale);
+
+/** As kcmm_paged_attn_decode_f16_on_stream (ref kcmm.h:525) for bf16. */
+int kcmm_paged_attn_decode_bf16_on_stream(
+    kcmm_pool_t *pool, uint32_t layer_idx, uint64_t query_ptr, uint64_t out_ptr,
+    uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+    uint64_t block_offsets_f16_ptr, uint32_t batch, uint32_t num_q_heads,
+    uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
+    uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
+
+/** fp8-e4m3 pool: bf16 q/out; K/V are dequantized in registers with the
+ *  page-footer scale of their (page, kv head).  Enqueue only. */
+int kcmm_paged_attn_decode_fp8_on_stream(
+    kcmm_pool_t *pool, uint32_t layer_idx, uint64_t query_ptr, uint64_t out_ptr,
+    uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+    uint64_t block_offsets_f16_ptr, uint32_t batch, uint32_t num_q_heads,
+    uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
+    uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
+
+/* ---- copy-on-write fork ------------------------------------------------- */
+
+/** Fork `src_seq` (beam search): a new sequence holding the same block ids
+ *  and seq_len; every shared block's reference count is incremented.  The
+ *  reference has only a placeholder (ref sharing.rs:24-65); semantics follow
+ *  the vLLM fork it mirrors (ref patch_vllm.py:1092-1101,
+ *  shadow_allocator.py:63-73). */
+int kcmm_fork_sequence(kcmm_pool_t *pool, uint32_t src_seq, uint32_t *out_seq);
+
+/** Reference count of a block (0 if not in use). */
+uint32_t kcmm_get_block_refcount(kcmm_pool_t *pool, uint32_t block_idx);
+
+/**
+ * Make logical block `logical_block` of `seq_idx` private before an append
+ * (ref patch_vllm.py:1083-1090, shadow_allocator.py:94-118).  Returns 1 when
+ * the block was shared: a fresh block is allocated, the sequence's table is
+ * repointed to it, the old block's count drops by one and (*out_src,
+ * *out_dst) name the page copy the caller must enqueue with
+ * kcmm_copy_blocks_on_stream.  Returns 0 when the block is already private
+ * (nothing to copy), -1 on error.
+ */
+int kcmm_cow_block_for_append(kcmm_pool_t *pool, uint32_t seq_idx,
+                              uint32_t logical_block, uint32_t *out_src,
+                              uint32_t *out_dst);
+
+/** Copy whole pages src->dst for every layer's K and V region (and fp8
+ *  scale footers), one HIP kernel per call.  `src_dst` is a host array of
+ *  num_pairs (src, dst) block ids; both ids must be in use.  Enqueue only. */
+int kcmm_copy_blocks_on_stream(kcmm_pool_t *pool, const uint32_t *src_dst,
+                               uint32_t num_pairs, uint64_t stream_ptr);
+
+/** Device-side variant (vLLM copy_blocks contract): `pairs_ptr` is a device
+ *  int64 [num_pairs][2] array of block ids, translated through the device
+ *  f16-unit offset table.  Enqueue only; no host state is read. */
+int kcmm_copy_blocks_device_on_stream(kcmm_pool_t *pool, uint64_t pairs_ptr,
+                                      uint64_t block_offsets_f16_ptr,
+                                      uint32_t num_pairs, uint64_t stream_ptr);
+
+/* ---- projection GEMM ---------------------------------------------------- */
+
+/** Y[m][n] = X[m][k] * W[n][k]^T (row major, the HF Linear layout used by
+ *  ref llama_transformer.rs:115-120), bf16 inputs and output, fp32
+ *  accumulation on MFMA.  Replaces the cuBLAS call of ref runtime.rs:17-41
+ *  (whose column-major arguments equal this product only at m == 1).
+ *  Enqueue only; requires k % 64 == 0 and n % 64 == 0. */
+int kcmm_gemm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
+                             uint32_t m, uint32_t n, uint32_t k,
+                             uint64_t stream_ptr);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KCMM_MI355X_H */

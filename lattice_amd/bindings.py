@@ -1,0 +1,447 @@
+"""ctypes bindings of libkcmm.so -- the host-side mirror of the reference's
+Python seam (ref scripts/kcmm/bindings.py: KcmmConfig, KcmmLibrary, KcmmPool,
+KcmmError), over this build's C ABI (include/kcmm.h, include/kcmm_mi355x.h).
+
+The HIP runtime: libkcmm.so and PyTorch-ROCm both need libamdhip64.so.7; the
+loader resolves that soname to whichever copy is loaded first, so this module
+imports torch (when installed) before opening libkcmm.so to keep one runtime
+per process.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+try:  # load torch's HIP runtime first (see module docstring)
+    import torch  # noqa: F401
+except Exception:  # pragma: no cover - torch is optional for the host-check tier
+    torch = None
+
+PKG = Path(__file__).resolve().parent
+DEFAULT_LIB = PKG / "libkcmm.so"
+
+KV_F16, KV_BF16, KV_FP8 = 0, 1, 2
+
+
+class KcmmError(RuntimeError):
+    """A libkcmm call returned failure (message from kcmm_get_last_error)."""
+
+
+class KcmmConfig(C.Structure):
+    """kcmm_config_t (ref kcmm.h:81-144); 376 bytes on LP64."""
+
+    _fields_ = [
+        ("block_size", C.c_size_t),
+        ("max_blocks", C.c_size_t),
+        ("cpu_cache_path", C.c_char * 256),
+        ("tiering", C.c_int32),
+        ("eviction_policy", C.c_int32),
+        ("prefetch_window", C.c_size_t),
+        ("max_batch_blocks", C.c_size_t),
+        ("device_ordinal", C.c_size_t),
+        ("num_layers", C.c_size_t),
+        ("kv_heads", C.c_size_t),
+        ("head_dim", C.c_size_t),
+        ("max_batch", C.c_size_t),
+        ("max_seq_len", C.c_size_t),
+        ("low_watermark_threshold", C.c_float),
+        ("background_evict_interval_ms", C.c_uint64),
+        ("attention_sink_blocks", C.c_size_t),
+        ("recent_window_blocks", C.c_size_t),
+    ]
+
+
+class KcmmMetrics(C.Structure):
+    _fields_ = [("ifr", C.c_double), ("pme", C.c_double), ("bu", C.c_double),
+                ("rfi", C.c_double), ("gpu_blocks", C.c_uint64), ("cpu_blocks", C.c_uint64),
+                ("nvme_blocks", C.c_uint64), ("eviction_count", C.c_uint64),
+                ("restoration_count", C.c_uint64)]
+
+
+class KcmmPoolStats(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "blocks_in_use", "total_blocks", "total_physical_blocks", "free_physical_blocks",
+        "active_sequences", "num_layers", "blocks_per_superblock", "superblock_count",
+        "block_size", "max_blocks_per_seq", "block_bytes")] + [
+        ("tiering_enabled", C.c_int32), ("sharing_enabled", C.c_int32),
+        ("physical_idle_ratio", C.c_float)]
+
+
+def make_config(*, num_layers, kv_heads, head_dim, max_batch, max_seq_len, block_size=16,
+                max_blocks=0, device_ordinal=0) -> KcmmConfig:
+    cfg = KcmmConfig()
+    cfg.block_size = block_size
+    cfg.max_blocks = max_blocks
+    cfg.num_layers = num_layers
+    cfg.kv_heads = kv_heads
+    cfg.head_dim = head_dim
+    cfg.max_batch = max_batch
+    cfg.max_seq_len = max_seq_len
+    cfg.device_ordinal = device_ordinal
+    return cfg
+
+
+_P, _U32, _U64, _I32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int32
+_ATTN = [_P, _U32, _U64, _U64, _U64, _U64, _U64] + [_U32] * 6 + [C.c_float]
+
+SIGNATURES = {
+    "kcmm_pool_create": ([C.POINTER(KcmmConfig)], _P),
+    "kcmm_pool_create_typed": ([C.POINTER(KcmmConfig), _I32], _P),
+    "kcmm_pool_destroy": ([_P], None),
+    "kcmm_last_create_error": ([C.c_char_p, C.c_size_t], C.c_size_t),
+    "kcmm_get_kv_dtype": ([_P], _I32),
+    "kcmm_get_backing_kind": ([_P], _I32),
+    "kcmm_get_last_error": ([_P, C.c_char_p, C.c_size_t], C.c_size_t),
+    "kcmm_clear_error": ([_P], None),
+    "kcmm_alloc_blocks": ([_P, _U32, _P], C.c_int),
+    "kcmm_free_blocks": ([_P, _P, _U32], C.c_int),
+    "kcmm_register_sequence": ([_P, _P, _U32, _P], C.c_int),
+    "kcmm_unregister_sequence": ([_P, _U32], C.c_int),
+    "kcmm_touch": ([_P, _U32], None),
+    "kcmm_cool": ([_P, _U32], None),
+    "kcmm_update_seq_len": ([_P, _U32, _U32], None),
+    "kcmm_get_seq_len": ([_P, _U32], _U32),
+    "kcmm_append_block_to_sequence": ([_P, _U32, _U32], C.c_int),
+    "kcmm_get_block_table": ([_P, _U32, _P, _U32, _P], C.c_int),
+    "kcmm_get_block_va_offset": ([_P, _U32], _U64),
+    "kcmm_get_all_block_offsets_f16": ([_P, _P, _U32, _P], C.c_int),
+    "kcmm_get_all_block_valid": ([_P, _P, _U32, _P], C.c_int),
+    "kcmm_get_block_location": ([_P, _U32, _P], C.c_int),
+    "kcmm_get_block_table_va_offsets": ([_P, _U32, _P, _U32, _P], C.c_int),
+    "kcmm_get_va_k": ([_P, _U32], _U64),
+    "kcmm_get_va_v": ([_P, _U32], _U64),
+    "kcmm_append_kv_step": ([_P, _U32, _P, _P, _U32, _U64, _U64], C.c_int),
+    "kcmm_append_kv_slots": ([_P, _U32, _P, _U32, _U64, _U64], C.c_int),
+    "kcmm_append_kv_slots_on_stream": ([_P, _U32, _P, _U32, _U64, _U64, _U64], C.c_int),
+    "kcmm_append_kv_device_slots_on_stream": ([_P, _U32, _U64, _U64, _U64, _U32, _U32, _U64,
+                                               _U64, _U64, _U64], C.c_int),
+    "kcmm_precompile_vllm_kv_write_f16": ([_P], C.c_int),
+    "kcmm_paged_attn_decode_f16": (_ATTN, C.c_int),
+    "kcmm_paged_attn_decode_f16_on_stream": (_ATTN + [_U64], C.c_int),
+    "kcmm_paged_attn_decode_f16_on_current_context_stream": (_ATTN + [_U64], C.c_int),
+    "kcmm_paged_attn_decode_bf16": (_ATTN, C.c_int),
+    "kcmm_paged_attn_decode_bf16_on_stream": (_ATTN + [_U64], C.c_int),
+    "kcmm_paged_attn_decode_fp8_on_stream": (_ATTN + [_U64], C.c_int),
+    "kcmm_precompile_paged_attn_decode_f16": ([_P], C.c_int),
+    "kcmm_evict_blocks": ([_P, _U32], _U32),
+    "kcmm_restore_evicted_block": ([_P, _U32], _U64),
+    "kcmm_restore_evicted_blocks": ([_P, _P, _U32], C.c_int),
+    "kcmm_is_gpu_resident": ([_P, _U32], C.c_int),
+    "kcmm_get_metrics": ([_P, C.POINTER(KcmmMetrics)], C.c_int),
+    "kcmm_get_pool_stats": ([_P, C.POINTER(KcmmPoolStats)], C.c_int),
+    "kcmm_blocks_in_use": ([_P], _U32),
+    "kcmm_total_blocks": ([_P], _U32),
+    "kcmm_block_state_epoch": ([_P], _U64),
+    "kcmm_free_physical_blocks": ([_P], _U32),
+    "kcmm_has_free_blocks": ([_P], C.c_int),
+    "kcmm_active_sequences": ([_P], _U32),
+    "kcmm_set_eviction_policy": ([_P, C.c_char_p], C.c_int),
+    "kcmm_get_eviction_policy": ([_P, C.c_char_p, _U32], _U32),
+    "kcmm_is_tiering_enabled": ([_P], C.c_int),
+    "kcmm_hint": ([_P, _U32, C.c_int], C.c_int),
+    "kcmm_protect": ([_P, _U32, _P, _U32, C.c_int], C.c_int),
+    "kcmm_share_prefix": ([_P, _U32, _U32, _U32, _P], C.c_int),
+    "kcmm_fork_sequence": ([_P, _U32, _P], C.c_int),
+    "kcmm_get_block_refcount": ([_P, _U32], _U32),
+    "kcmm_cow_block_for_append": ([_P, _U32, _U32, _P, _P], C.c_int),
+    "kcmm_copy_blocks_on_stream": ([_P, _P, _U32, _U64], C.c_int),
+    "kcmm_copy_blocks_device_on_stream": ([_P, _U64, _U64, _U32, _U64], C.c_int),
+    "kcmm_gemm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
+    "kcmm_below_low_watermark": ([_P, C.c_float], C.c_int),
+    "kcmm_synchronize": ([_P], C.c_int),
+    "kcmm_get_block_size": ([_P], _U32),
+    "kcmm_get_max_blocks_per_seq": ([_P], _U32),
+    "kcmm_get_block_bytes": ([_P], _U32),
+    "kcmm_get_num_layers": ([_P], _U32),
+    "kcmm_get_max_batch": ([_P], _U32),
+    "kcmm_get_max_seq_len": ([_P], _U32),
+}
+
+
+def _arr(ctype, values):
+    values = list(values)
+    return (ctype * max(1, len(values)))(*values)
+
+
+class KcmmLibrary:
+    """Loads libkcmm.so (or the host-check build) and declares every entry point."""
+
+    def __init__(self, path: str | os.PathLike | None = None):
+        path = Path(path) if path else Path(os.environ.get("KCMM_LIB_PATH", DEFAULT_LIB))
+        if not path.exists():
+            raise KcmmError(f"{path} not built: run `python -m lattice_amd.build`")
+        self.path = path
+        self.lib = C.CDLL(str(path))
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(self.lib, name)
+            fn.argtypes = args
+            fn.restype = res
+
+    def create_pool(self, config: KcmmConfig, kv_dtype: int = KV_F16) -> "KcmmPool":
+        h = self.lib.kcmm_pool_create_typed(C.byref(config), kv_dtype)
+        if not h:
+            buf = C.create_string_buffer(512)
+            self.lib.kcmm_last_create_error(buf, 512)
+            raise KcmmError(f"kcmm_pool_create failed: {buf.value.decode()}")
+        return KcmmPool(self, h)
+
+    def gemm_bf16(self, x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr=0) -> None:
+        if self.lib.kcmm_gemm_bf16_on_stream(x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr) != 0:
+            raise KcmmError("kcmm_gemm_bf16_on_stream failed")
+
+
+class KcmmPool:
+    """One KCMM pool handle (ref scripts/kcmm/bindings.py KcmmPool)."""
+
+    def __init__(self, library: KcmmLibrary, handle):
+        self.library = library
+        self.lib = library.lib
+        self.handle = C.c_void_p(handle)
+
+    # -- lifecycle / errors --
+    def destroy(self) -> None:
+        if self.handle:
+            self.lib.kcmm_pool_destroy(self.handle)
+            self.handle = C.c_void_p(0)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()
+
+    def last_error(self) -> str:
+        buf = C.create_string_buffer(1024)
+        self.lib.kcmm_get_last_error(self.handle, buf, 1024)
+        return buf.value.decode()
+
+    def _check(self, rc: int, op: str) -> None:
+        if rc != 0:
+            raise KcmmError(f"{op} failed: {self.last_error()}")
+
+    # -- allocation / sequences --
+    def alloc_blocks(self, n: int) -> list[int]:
+        out = (C.c_uint32 * max(1, n))()
+        self._check(self.lib.kcmm_alloc_blocks(self.handle, n, out), "kcmm_alloc_blocks")
+        return list(out[:n])
+
+    def free_blocks(self, blocks) -> None:
+        a = _arr(C.c_uint32, blocks)
+        self._check(self.lib.kcmm_free_blocks(self.handle, a, len(list(blocks))), "kcmm_free_blocks")
+
+    def register_sequence(self, table) -> int:
+        table = list(table)
+        out = C.c_uint32(0)
+        self._check(self.lib.kcmm_register_sequence(self.handle, _arr(C.c_uint32, table),
+                                                    len(table), C.byref(out)),
+                    "kcmm_register_sequence")
+        return out.value
+
+    def unregister_sequence(self, seq: int) -> None:
+        self._check(self.lib.kcmm_unregister_sequence(self.handle, seq), "kcmm_unregister_sequence")
+
+    def append_block_to_sequence(self, seq: int, blk: int) -> None:
+        self._check(self.lib.kcmm_append_block_to_sequence(self.handle, seq, blk),
+                    "kcmm_append_block_to_sequence")
+
+    def update_seq_len(self, seq: int, n: int) -> None:
+        self.lib.kcmm_update_seq_len(self.handle, seq, n)
+
+    def seq_len(self, seq: int) -> int:
+        return self.lib.kcmm_get_seq_len(self.handle, seq)
+
+    def block_table(self, seq: int, max_blocks: int = 1 << 16) -> list[int]:
+        out = (C.c_uint32 * max_blocks)()
+        cnt = C.c_uint32(0)
+        self._check(self.lib.kcmm_get_block_table(self.handle, seq, out, max_blocks, C.byref(cnt)),
+                    "kcmm_get_block_table")
+        return list(out[: cnt.value])
+
+    def block_table_va_offsets(self, seq: int, max_blocks: int = 1 << 16) -> list[int]:
+        out = (C.c_uint64 * max_blocks)()
+        cnt = C.c_uint32(0)
+        self._check(self.lib.kcmm_get_block_table_va_offsets(self.handle, seq, out, max_blocks,
+                                                             C.byref(cnt)),
+                    "kcmm_get_block_table_va_offsets")
+        return list(out[: cnt.value])
+
+    def block_va_offset(self, blk: int) -> int:
+        return self.lib.kcmm_get_block_va_offset(self.handle, blk)
+
+    def all_block_offsets_f16(self, max_blocks: int | None = None) -> list[int]:
+        n = max_blocks if max_blocks is not None else max(1, self.total_blocks())
+        out = (C.c_uint64 * n)()
+        cnt = C.c_uint32(0)
+        self._check(self.lib.kcmm_get_all_block_offsets_f16(self.handle, out, n, C.byref(cnt)),
+                    "kcmm_get_all_block_offsets_f16")
+        return list(out[: cnt.value])
+
+    def all_block_valid_flags(self, max_blocks: int | None = None) -> list[int]:
+        n = max_blocks if max_blocks is not None else max(1, self.total_blocks())
+        out = (C.c_uint8 * n)()
+        cnt = C.c_uint32(0)
+        self._check(self.lib.kcmm_get_all_block_valid(self.handle, out, n, C.byref(cnt)),
+                    "kcmm_get_all_block_valid")
+        return list(out[: cnt.value])
+
+    def va_k(self, layer: int) -> int:
+        return self.lib.kcmm_get_va_k(self.handle, layer)
+
+    def va_v(self, layer: int) -> int:
+        return self.lib.kcmm_get_va_v(self.handle, layer)
+
+    def total_blocks(self) -> int:
+        return self.lib.kcmm_total_blocks(self.handle)
+
+    def blocks_in_use(self) -> int:
+        return self.lib.kcmm_blocks_in_use(self.handle)
+
+    def epoch(self) -> int:
+        return self.lib.kcmm_block_state_epoch(self.handle)
+
+    def kv_dtype(self) -> int:
+        return self.lib.kcmm_get_kv_dtype(self.handle)
+
+    def backing_kind(self) -> int:
+        return self.lib.kcmm_get_backing_kind(self.handle)
+
+    def stats(self) -> dict:
+        s = KcmmPoolStats()
+        self._check(self.lib.kcmm_get_pool_stats(self.handle, C.byref(s)), "kcmm_get_pool_stats")
+        return {name: getattr(s, name) for name, _ in s._fields_}
+
+    def metrics(self) -> dict:
+        m = KcmmMetrics()
+        self._check(self.lib.kcmm_get_metrics(self.handle, C.byref(m)), "kcmm_get_metrics")
+        return {name: getattr(m, name) for name, _ in m._fields_}
+
+    def synchronize(self) -> None:
+        self._check(self.lib.kcmm_synchronize(self.handle), "kcmm_synchronize")
+
+    # -- KV write --
+    def append_kv_step(self, layer_idx, seq_indices, positions, k_src_ptr, v_src_ptr) -> None:
+        seq_indices, positions = list(seq_indices), list(positions)
+        self._check(self.lib.kcmm_append_kv_step(self.handle, layer_idx, _arr(C.c_uint32, seq_indices),
+                                                 _arr(C.c_uint32, positions), len(seq_indices),
+                                                 k_src_ptr, v_src_ptr), "kcmm_append_kv_step")
+
+    def append_kv_slots(self, layer_idx, slot_mapping, k_src_ptr, v_src_ptr, stream_ptr=None):
+        slot_mapping = list(slot_mapping)
+        a = _arr(C.c_int64, slot_mapping)
+        if stream_ptr is None:
+            rc = self.lib.kcmm_append_kv_slots(self.handle, layer_idx, a, len(slot_mapping),
+                                               k_src_ptr, v_src_ptr)
+        else:
+            rc = self.lib.kcmm_append_kv_slots_on_stream(self.handle, layer_idx, a,
+                                                         len(slot_mapping), k_src_ptr, v_src_ptr,
+                                                         stream_ptr)
+        self._check(rc, "kcmm_append_kv_slots")
+
+    def append_kv_device_slots_on_stream(self, *, layer_idx, slot_mapping_ptr,
+                                         block_offsets_f16_ptr, valid_blocks_ptr,
+                                         block_offsets_f16_len, batch, k_src_ptr, v_src_ptr,
+                                         status_ptr, stream_ptr) -> None:
+        self._check(self.lib.kcmm_append_kv_device_slots_on_stream(
+            self.handle, layer_idx, slot_mapping_ptr, block_offsets_f16_ptr, valid_blocks_ptr,
+            block_offsets_f16_len, batch, k_src_ptr, v_src_ptr, status_ptr, stream_ptr),
+            "kcmm_append_kv_device_slots_on_stream")
+
+    # -- attention --
+    def paged_attn_decode(self, *, layer_idx, query_ptr, out_ptr, block_tables_ptr, seq_lens_ptr,
+                          block_offsets_f16_ptr, batch, num_q_heads, kv_heads, head_dim,
+                          block_size, max_blocks_per_seq, scale, stream_ptr=None,
+                          variant="auto") -> None:
+        """Dispatch to the entry point matching the pool dtype (f16/bf16/fp8)."""
+        dt = self.kv_dtype()
+        args = (self.handle, layer_idx, query_ptr, out_ptr, block_tables_ptr, seq_lens_ptr,
+                block_offsets_f16_ptr, batch, num_q_heads, kv_heads, head_dim, block_size,
+                max_blocks_per_seq, C.c_float(scale))
+        if dt == KV_F16:
+            if stream_ptr is None:
+                rc = self.lib.kcmm_paged_attn_decode_f16(*args)
+            elif variant == "current_context":
+                rc = self.lib.kcmm_paged_attn_decode_f16_on_current_context_stream(*args, stream_ptr)
+            else:
+                rc = self.lib.kcmm_paged_attn_decode_f16_on_stream(*args, stream_ptr)
+        elif dt == KV_BF16:
+            if stream_ptr is None:
+                rc = self.lib.kcmm_paged_attn_decode_bf16(*args)
+            else:
+                rc = self.lib.kcmm_paged_attn_decode_bf16_on_stream(*args, stream_ptr)
+        else:
+            rc = self.lib.kcmm_paged_attn_decode_fp8_on_stream(*args, stream_ptr or 0)
+        self._check(rc, "paged_attn_decode")
+
+    # -- copy-on-write --
+    def fork_sequence(self, src: int) -> int:
+        out = C.c_uint32(0)
+        self._check(self.lib.kcmm_fork_sequence(self.handle, src, C.byref(out)), "kcmm_fork_sequence")
+        return out.value
+
+    def share_prefix(self, src: int, dst: int, n: int) -> list[int]:
+        out = (C.c_uint32 * max(1, n))()
+        self._check(self.lib.kcmm_share_prefix(self.handle, src, dst, n, out), "kcmm_share_prefix")
+        return list(out[:n])
+
+    def refcount(self, blk: int) -> int:
+        return self.lib.kcmm_get_block_refcount(self.handle, blk)
+
+    def cow_block_for_append(self, seq: int, logical: int):
+        s, d = C.c_uint32(0), C.c_uint32(0)
+        rc = self.lib.kcmm_cow_block_for_append(self.handle, seq, logical, C.byref(s), C.byref(d))
+        if rc < 0:
+            raise KcmmError(f"kcmm_cow_block_for_append failed: {self.last_error()}")
+        return (s.value, d.value) if rc == 1 else None
+
+    def copy_blocks(self, pairs, stream_ptr=0) -> None:
+        flat = [v for p in pairs for v in p]
+        self._check(self.lib.kcmm_copy_blocks_on_stream(self.handle, _arr(C.c_uint32, flat),
+                                                        len(flat) // 2, stream_ptr),
+                    "kcmm_copy_blocks_on_stream")
+
+    def copy_blocks_device(self, pairs_ptr, offsets_ptr, n, stream_ptr=0) -> None:
+        self._check(self.lib.kcmm_copy_blocks_device_on_stream(self.handle, pairs_ptr, offsets_ptr,
+                                                               n, stream_ptr),
+                    "kcmm_copy_blocks_device_on_stream")
+
+
+# ---- raw HIP helpers (test/bench plumbing for pool-owned device memory) ----
+
+_hip = None
+
+
+def hip() -> C.CDLL:
+    """The process's HIP runtime (torch's copy when torch is loaded)."""
+    global _hip
+    if _hip is None:
+        _hip = C.CDLL("libamdhip64.so.7")
+        _hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        _hip.hipMemcpy.restype = C.c_int
+        _hip.hipDeviceSynchronize.restype = C.c_int
+        _hip.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+        _hip.hipMemset.restype = C.c_int
+    return _hip
+
+
+def memset_d8(ptr: int, value: int, nbytes: int) -> None:
+    rc = hip().hipMemset(C.c_void_p(ptr), value, nbytes)
+    if rc != 0:
+        raise KcmmError(f"hipMemset failed ({rc})")
+
+
+def memcpy_htod(dst_ptr: int, src) -> None:
+    import numpy as np
+    src = np.ascontiguousarray(src)
+    rc = hip().hipMemcpy(C.c_void_p(dst_ptr), src.ctypes.data_as(C.c_void_p), src.nbytes, 1)
+    if rc != 0:
+        raise KcmmError(f"hipMemcpy H2D failed ({rc})")
+
+
+def memcpy_dtoh(src_ptr: int, nbytes: int):
+    import numpy as np
+    out = np.empty(nbytes, dtype=np.uint8)
+    rc = hip().hipMemcpy(out.ctypes.data_as(C.c_void_p), C.c_void_p(src_ptr), nbytes, 2)
+    if rc != 0:
+        raise KcmmError(f"hipMemcpy D2H failed ({rc})")
+    return out

@@ -1,0 +1,78 @@
+// Device-side entry points used by the C ABI layer (ffi.cpp).  Plain C++
+// types only: the HIP implementation lives in device_hip.cpp and kernels/*.hip,
+// so ffi.cpp and pool_core.cpp compile without HIP headers.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "pool_core.hpp"
+
+namespace kcmm {
+namespace dev {
+
+// Page backing for `device`: HIP VMM superblocks, or one hipMalloc per
+// region when VMM is unavailable or KCMM_BACKING=flat.
+std::unique_ptr<PageBacking> make_backing(int device, std::string* err);
+
+bool set_device(int device, std::string* err);
+
+// Per-(device, stream, slot) device scratch for split-K partials; grown on
+// demand (slot 0: decode attention, slot 1: GEMM).
+bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, std::string* err);
+bool synchronize_device(int device, std::string* err);
+
+// Paged decode attention over one layer's K/V regions.
+struct AttnDecodeArgs {
+    int32_t dtype;          // pool dtype (kF16: f16 q/out; kBF16, kFP8: bf16 q/out)
+    uint64_t q, out;        // [batch][num_q_heads][head_dim]
+    uint64_t k_base, v_base;
+    uint64_t block_tables;  // int32 [batch][mbps]
+    uint64_t seq_lens;      // int32 [batch]
+    uint64_t offsets_f16;   // u64 [ids], page byte offset / 2
+    uint32_t batch, num_q_heads, kv_heads, head_dim, block_size, mbps;
+    uint32_t row_bytes;     // token stride inside a page
+    uint32_t data_bytes;    // bytes of page data before the fp8 scale footer
+    float scale;
+    uint64_t stream;
+};
+bool attn_decode(const AttnDecodeArgs& a, std::string* err);
+
+// KV append of host-resolved rows: source row r (elements of the pool dtype;
+// bf16 for fp8 pools) lands at page_offset + slot*row_bytes in both regions.
+struct KvRowsArgs {
+    int32_t dtype;
+    uint64_t k_base, v_base, k_src, v_src;
+    uint32_t kv_heads, head_dim, row_bytes, data_bytes;
+    const RowDst* rows;
+    size_t num_rows;
+    uint64_t stream;
+};
+bool kv_write_rows(const KvRowsArgs& a, std::string* err);
+
+// KV append from device-resident int64 slot ids (ref kcmm_vllm_kv_write.cu).
+struct KvDeviceSlotsArgs {
+    int32_t dtype;
+    uint64_t k_base, v_base, k_src, v_src;
+    uint64_t slot_mapping, offsets_f16, valid_blocks, status;
+    uint32_t offsets_len, batch, block_size;
+    uint32_t kv_heads, head_dim, row_bytes, data_bytes;
+    uint64_t stream;
+};
+bool kv_write_device_slots(const KvDeviceSlotsArgs& a, std::string* err);
+
+// Page copies: every (src, dst) byte-offset pair is copied in every region.
+bool copy_pages(const std::vector<uint64_t>& region_bases, const uint64_t* pair_offsets,
+                size_t num_pairs, uint32_t block_bytes, uint64_t stream, std::string* err);
+bool copy_pages_device(const std::vector<uint64_t>& region_bases, uint64_t pairs_ptr,
+                       uint64_t offsets_f16, size_t num_pairs, uint32_t block_bytes,
+                       uint64_t stream, std::string* err);
+
+// Y = X W^T, bf16, fp32 accumulate.
+bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
+               uint64_t stream, std::string* err);
+
+}  // namespace dev
+}  // namespace kcmm

@@ -1,0 +1,799 @@
+// The KCMM C ABI (include/kcmm.h, include/kcmm_mi355x.h).  Argument checks,
+// error channel and return conventions follow the reference's Rust FFI
+// (ref src/kcmm/ffi.rs); bookkeeping is PoolCore, device work goes through
+// device_api.hpp.  This file has no HIP dependency.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/kcmm.h"
+#include "../../include/kcmm_mi355x.h"
+#include "device_api.hpp"
+#include "pool_core.hpp"
+
+struct kcmm_pool_t {
+    std::unique_ptr<kcmm::PoolCore> core;
+    int device = 0;
+    std::mutex err_mu;
+    std::string last_error;
+
+    void set_error(const std::string& s) {
+        std::lock_guard<std::mutex> lk(err_mu);
+        last_error = s;
+    }
+};
+
+namespace {
+
+thread_local std::string g_create_error;
+
+size_t write_c_str(char* buf, size_t max_len, const std::string& s) {
+    // ref ffi.rs:412-422: copy at most max_len-1 bytes and terminate.
+    if (buf == nullptr || max_len == 0) return 0;
+    const size_t n = s.size() < max_len - 1 ? s.size() : max_len - 1;
+    std::memcpy(buf, s.data(), n);
+    buf[n] = '\0';
+    return n;
+}
+
+std::string fmtu(const char* f, unsigned long long a = 0, unsigned long long b = 0) {
+    char buf[256];
+    std::snprintf(buf, sizeof(buf), f, a, b);
+    return buf;
+}
+
+bool layer_ok(kcmm_pool_t* p, uint32_t layer, const char* fn) {
+    if (layer < p->core->geo().num_layers) return true;
+    p->set_error(std::string(fn) + fmtu(": layer_idx %llu out of bounds", layer));
+    return false;
+}
+
+// Shared body of every decode-attention entry point (ref ffi.rs:1710-1895).
+int attn_impl(kcmm_pool_t* pool, int32_t want_dtype, const char* fn, uint32_t layer_idx,
+              uint64_t q, uint64_t out, uint64_t bt, uint64_t sl, uint64_t offs, uint32_t batch,
+              uint32_t hq, uint32_t hkv, uint32_t d, uint32_t bs, uint32_t mbps, float scale,
+              uint64_t stream, bool sync_after, bool bind_device) {
+    if (pool == nullptr || q == 0 || out == 0 || bt == 0 || sl == 0 || offs == 0) {
+        if (pool) pool->set_error(std::string(fn) + ": null pointer argument");
+        return -1;
+    }
+    if (batch == 0 || hq == 0 || hkv == 0 || d == 0 || bs == 0 || mbps == 0) {
+        pool->set_error(std::string(fn) + ": shape arguments must be positive");
+        return -1;
+    }
+    if (d > 256) {
+        pool->set_error(std::string(fn) + fmtu(": head_dim %llu exceeds kernel limit 256", d));
+        return -1;
+    }
+    if (hq > 0xFFFF || hkv > 0xFFFF || bs > 0xFFFF || mbps > 0xFFFF) {
+        pool->set_error(std::string(fn) + ": packed shape argument exceeds 65535");
+        return -1;
+    }
+    if (!layer_ok(pool, layer_idx, fn)) return -1;
+    const kcmm::PoolGeometry& g = pool->core->geo();
+    if (g.dtype != want_dtype) {
+        pool->set_error(std::string(fn) + fmtu(": pool holds kv dtype %llu, this entry point "
+                                               "reads dtype %llu",
+                                               (unsigned long long)g.dtype,
+                                               (unsigned long long)want_dtype));
+        return -1;
+    }
+    // The kernels address pages with the pool's own geometry; a mismatching
+    // shape would read past the mapped pages.
+    if (hkv != g.kv_heads || d != g.head_dim || bs != g.block_size) {
+        pool->set_error(std::string(fn) +
+                        ": kv_heads/head_dim/block_size differ from the pool's geometry");
+        return -1;
+    }
+    std::string err;
+    if (bind_device && !kcmm::dev::set_device(pool->device, &err)) {
+        pool->set_error(std::string(fn) + ": bind device failed: " + err);
+        return -1;
+    }
+    kcmm::dev::AttnDecodeArgs a{};
+    a.dtype = g.dtype;
+    a.q = q;
+    a.out = out;
+    a.k_base = pool->core->va_k(layer_idx);
+    a.v_base = pool->core->va_v(layer_idx);
+    a.block_tables = bt;
+    a.seq_lens = sl;
+    a.offsets_f16 = offs;
+    a.batch = batch;
+    a.num_q_heads = hq;
+    a.kv_heads = hkv;
+    a.head_dim = d;
+    a.block_size = bs;
+    a.mbps = mbps;
+    a.row_bytes = static_cast<uint32_t>(g.row_bytes);
+    a.data_bytes = static_cast<uint32_t>(g.data_bytes);
+    a.scale = scale;
+    a.stream = stream;
+    if (!kcmm::dev::attn_decode(a, &err)) {
+        pool->set_error(std::string(fn) + ": launch failed: " + err);
+        return -1;
+    }
+    if (sync_after && !kcmm::dev::synchronize_device(pool->device, &err)) {
+        pool->set_error(std::string(fn) + ": synchronize failed: " + err);
+        return -1;
+    }
+    return 0;
+}
+
+int write_rows(kcmm_pool_t* pool, const char* fn, uint32_t layer_idx,
+               const std::vector<kcmm::RowDst>& rows, uint64_t k_src, uint64_t v_src,
+               uint64_t stream) {
+    if (rows.empty()) return 0;
+    if (k_src == 0 || v_src == 0) {
+        pool->set_error(std::string(fn) + ": null source pointer");
+        return -1;
+    }
+    const kcmm::PoolGeometry& g = pool->core->geo();
+    std::string err;
+    if (!kcmm::dev::set_device(pool->device, &err)) {
+        pool->set_error(std::string(fn) + ": bind device failed: " + err);
+        return -1;
+    }
+    kcmm::dev::KvRowsArgs a{};
+    a.dtype = g.dtype;
+    a.k_base = pool->core->va_k(layer_idx);
+    a.v_base = pool->core->va_v(layer_idx);
+    a.k_src = k_src;
+    a.v_src = v_src;
+    a.kv_heads = static_cast<uint32_t>(g.kv_heads);
+    a.head_dim = static_cast<uint32_t>(g.head_dim);
+    a.row_bytes = static_cast<uint32_t>(g.row_bytes);
+    a.data_bytes = static_cast<uint32_t>(g.data_bytes);
+    a.rows = rows.data();
+    a.num_rows = rows.size();
+    a.stream = stream;
+    if (!kcmm::dev::kv_write_rows(a, &err)) {
+        pool->set_error(std::string(fn) + ": " + err);
+        return -1;
+    }
+    return 0;
+}
+
+int slots_impl(kcmm_pool_t* pool, uint32_t layer_idx, const int64_t* slots, uint32_t batch,
+               uint64_t k, uint64_t v, uint64_t stream) {
+    // ref ffi.rs:1258-1383
+    if (pool == nullptr || slots == nullptr) {
+        if (pool) pool->set_error("kcmm_append_kv_slots: null arguments");
+        return -1;
+    }
+    if (!layer_ok(pool, layer_idx, "kcmm_append_kv_slots")) return -1;
+    std::vector<kcmm::RowDst> rows;
+    std::string err;
+    if (!pool->core->resolve_slots(slots, batch, &rows, &err)) {
+        pool->set_error(err);
+        return -1;
+    }
+    return write_rows(pool, "kcmm_append_kv_slots", layer_idx, rows, k, v, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---- lifecycle -----------------------------------------------------------
+
+kcmm_pool_t* kcmm_pool_create_typed(const kcmm_config_t* cfg, int32_t kv_dtype) {
+    g_create_error.clear();
+    if (cfg == nullptr) {
+        g_create_error = "kcmm_pool_create: null config";
+        return nullptr;
+    }
+    kcmm::PoolGeometry g;
+    g.block_size = cfg->block_size ? cfg->block_size : 16;  // ref ffi.rs:477
+    g.num_layers = cfg->num_layers;
+    g.kv_heads = cfg->kv_heads;
+    g.head_dim = cfg->head_dim;
+    g.max_batch = cfg->max_batch;
+    g.max_seq_len = cfg->max_seq_len;
+    g.dtype = kv_dtype;
+    std::string err;
+    if (!g.compute(&err)) {
+        g_create_error = "kcmm_pool_create: " + err;
+        return nullptr;
+    }
+    const int device = static_cast<int>(cfg->device_ordinal);
+    if (!kcmm::dev::set_device(device, &err)) {
+        g_create_error = "kcmm_pool_create: " + err;
+        return nullptr;
+    }
+    std::unique_ptr<kcmm::PageBacking> backing = kcmm::dev::make_backing(device, &err);
+    if (!backing) {
+        g_create_error = "kcmm_pool_create: " + err;
+        return nullptr;
+    }
+    if (!backing->reserve(2 * g.num_layers, g.region_bytes, &err)) {
+        g_create_error = "kcmm_pool_create: " + err;
+        return nullptr;
+    }
+    auto* p = new kcmm_pool_t;
+    p->core.reset(new kcmm::PoolCore(g, std::move(backing)));
+    p->device = device;
+    return p;
+}
+
+kcmm_pool_t* kcmm_pool_create(const kcmm_config_t* cfg) {
+    return kcmm_pool_create_typed(cfg, kcmm::kF16);
+}
+
+void kcmm_pool_destroy(kcmm_pool_t* pool) {
+    if (pool == nullptr) return;
+    std::string err;
+    kcmm::dev::synchronize_device(pool->device, &err);  // ref ffi.rs:552-553
+    delete pool;
+}
+
+size_t kcmm_last_create_error(char* buf, size_t max_len) {
+    if (g_create_error.empty()) return 0;
+    return write_c_str(buf, max_len, g_create_error);
+}
+
+int32_t kcmm_get_kv_dtype(kcmm_pool_t* pool) { return pool ? pool->core->geo().dtype : -1; }
+
+int32_t kcmm_get_backing_kind(kcmm_pool_t* pool) {
+    return pool ? pool->core->backing_kind() : -1;
+}
+
+// ---- errors ----------------------------------------------------------------
+
+size_t kcmm_get_last_error(kcmm_pool_t* pool, char* buf, size_t max_len) {
+    if (pool == nullptr || buf == nullptr || max_len == 0) return 0;
+    std::lock_guard<std::mutex> lk(pool->err_mu);
+    if (pool->last_error.empty()) return 0;
+    return write_c_str(buf, max_len, pool->last_error);
+}
+
+void kcmm_clear_error(kcmm_pool_t* pool) {
+    if (pool == nullptr) return;
+    std::lock_guard<std::mutex> lk(pool->err_mu);
+    pool->last_error.clear();
+}
+
+// ---- allocation -------------------------------------------------------------
+
+int kcmm_alloc_blocks(kcmm_pool_t* pool, uint32_t n, uint32_t* out) {
+    if (pool == nullptr || out == nullptr || n == 0) {
+        if (pool) pool->set_error("kcmm_alloc_blocks: null output buffer or zero count");
+        return -1;
+    }
+    std::vector<uint32_t> tmp(n);
+    std::string err;
+    if (!pool->core->alloc_blocks(n, tmp.data(), &err)) {
+        pool->set_error("kcmm_alloc_blocks: " + err);
+        return -1;
+    }
+    std::memcpy(out, tmp.data(), n * sizeof(uint32_t));
+    return 0;
+}
+
+int kcmm_free_blocks(kcmm_pool_t* pool, const uint32_t* blocks, uint32_t num) {
+    if (pool == nullptr || blocks == nullptr || num == 0) return 0;
+    pool->core->free_blocks(blocks, num);
+    return 0;
+}
+
+// ---- sequences ------------------------------------------------------------------
+
+int kcmm_register_sequence(kcmm_pool_t* pool, const uint32_t* table, uint32_t n,
+                           uint32_t* out_seq) {
+    if (pool == nullptr || table == nullptr || out_seq == nullptr) {
+        if (pool) pool->set_error("kcmm_register_sequence: null arguments");
+        return -1;
+    }
+    *out_seq = pool->core->register_sequence(table, n);
+    return 0;
+}
+
+int kcmm_unregister_sequence(kcmm_pool_t* pool, uint32_t seq) {
+    if (pool == nullptr) return -1;
+    pool->core->unregister_sequence(seq);
+    return 0;
+}
+
+void kcmm_touch(kcmm_pool_t* pool, uint32_t seq) {
+    if (pool) pool->core->touch(seq);
+}
+
+void kcmm_cool(kcmm_pool_t* pool, uint32_t seq) {
+    if (pool) pool->core->cool(seq);
+}
+
+void kcmm_update_seq_len(kcmm_pool_t* pool, uint32_t seq, uint32_t len) {
+    if (pool) pool->core->update_seq_len(seq, len);
+}
+
+uint32_t kcmm_get_seq_len(kcmm_pool_t* pool, uint32_t seq) {
+    return pool ? pool->core->get_seq_len(seq) : 0;
+}
+
+int kcmm_append_block_to_sequence(kcmm_pool_t* pool, uint32_t seq, uint32_t blk) {
+    if (pool == nullptr) return -1;
+    if (!pool->core->append_block_to_sequence(seq, blk)) {
+        pool->set_error(fmtu("kcmm_append_block_to_sequence: seq_idx %llu out of bounds", seq));
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_get_block_table(kcmm_pool_t* pool, uint32_t seq, uint32_t* out, uint32_t max_blocks,
+                         uint32_t* count) {
+    if (pool == nullptr || out == nullptr || count == nullptr) {
+        if (pool) pool->set_error("kcmm_get_block_table: null arguments");
+        return -1;
+    }
+    std::vector<uint32_t> t;
+    if (!pool->core->get_block_table(seq, &t)) {
+        pool->set_error(fmtu("kcmm_get_block_table: seq_idx %llu not found", seq));
+        *count = 0;
+        return -1;
+    }
+    const size_t n = t.size() < max_blocks ? t.size() : max_blocks;
+    if (n) std::memcpy(out, t.data(), n * sizeof(uint32_t));
+    *count = static_cast<uint32_t>(n);
+    return 0;
+}
+
+// ---- block queries -------------------------------------------------------------
+
+uint64_t kcmm_get_block_va_offset(kcmm_pool_t* pool, uint32_t blk) {
+    if (pool == nullptr) return 0;
+    uint64_t v = 0;
+    return pool->core->block_va_offset(blk, &v) ? v : 0;
+}
+
+int kcmm_get_all_block_offsets_f16(kcmm_pool_t* pool, uint64_t* out, uint32_t max_blocks,
+                                   uint32_t* count) {
+    if (pool == nullptr || out == nullptr || count == nullptr) {
+        if (pool) pool->set_error("kcmm_get_all_block_offsets_f16: null arguments");
+        return -1;
+    }
+    const std::vector<uint64_t> v = pool->core->all_offsets_f16();
+    const size_t n = v.size() < max_blocks ? v.size() : max_blocks;
+    if (n) std::memcpy(out, v.data(), n * sizeof(uint64_t));
+    *count = static_cast<uint32_t>(n);
+    return 0;
+}
+
+int kcmm_get_all_block_valid(kcmm_pool_t* pool, uint8_t* out, uint32_t max_blocks,
+                             uint32_t* count) {
+    if (pool == nullptr || out == nullptr || count == nullptr) {
+        if (pool) pool->set_error("kcmm_get_all_block_valid: null arguments");
+        return -1;
+    }
+    const std::vector<uint8_t> v = pool->core->all_valid_flags();
+    const size_t n = v.size() < max_blocks ? v.size() : max_blocks;
+    if (n) std::memcpy(out, v.data(), n);
+    *count = static_cast<uint32_t>(n);
+    return 0;
+}
+
+int kcmm_get_block_location(kcmm_pool_t* pool, uint32_t blk, kcmm_block_location_t* loc) {
+    if (pool == nullptr || loc == nullptr) return -1;
+    uint64_t v;
+    if (!pool->core->block_va_offset(blk, &v)) {
+        pool->set_error(fmtu("kcmm_get_block_location: block_idx %llu not found", blk));
+        return -1;
+    }
+    *loc = KCMM_LOC_GPU_RESIDENT;
+    return 0;
+}
+
+int kcmm_get_block_table_va_offsets(kcmm_pool_t* pool, uint32_t seq, uint64_t* out,
+                                    uint32_t max_blocks, uint32_t* count) {
+    if (pool == nullptr || out == nullptr || count == nullptr) {
+        if (pool) pool->set_error("kcmm_get_block_table_va_offsets: null arguments");
+        return -1;
+    }
+    std::vector<uint64_t> v;
+    if (!pool->core->table_va_offsets(seq, &v)) {
+        pool->set_error(fmtu("kcmm_get_block_table_va_offsets: seq_idx %llu not found", seq));
+        *count = 0;
+        return -1;
+    }
+    const size_t n = v.size() < max_blocks ? v.size() : max_blocks;
+    if (n) std::memcpy(out, v.data(), n * sizeof(uint64_t));
+    *count = static_cast<uint32_t>(n);
+    return 0;
+}
+
+uint64_t kcmm_get_va_k(kcmm_pool_t* pool, uint32_t layer) {
+    if (pool == nullptr || layer >= pool->core->geo().num_layers) return 0;
+    return pool->core->va_k(layer);
+}
+
+uint64_t kcmm_get_va_v(kcmm_pool_t* pool, uint32_t layer) {
+    if (pool == nullptr || layer >= pool->core->geo().num_layers) return 0;
+    return pool->core->va_v(layer);
+}
+
+// ---- KV write ---------------------------------------------------------------------
+
+int kcmm_append_kv_step(kcmm_pool_t* pool, uint32_t layer_idx, const uint32_t* seqs,
+                        const uint32_t* positions, uint32_t batch, uint64_t k_src,
+                        uint64_t v_src) {
+    // ref ffi.rs:1088-1200
+    if (pool == nullptr || seqs == nullptr || positions == nullptr) {
+        if (pool) pool->set_error("kcmm_append_kv_step: null arguments");
+        return -1;
+    }
+    if (!layer_ok(pool, layer_idx, "kcmm_append_kv_step")) return -1;
+    std::vector<kcmm::RowDst> rows;
+    std::string err;
+    if (!pool->core->resolve_positions(seqs, positions, batch, &rows, &err)) {
+        pool->set_error(err);
+        return -1;
+    }
+    return write_rows(pool, "kcmm_append_kv_step", layer_idx, rows, k_src, v_src, 0);
+}
+
+int kcmm_append_kv_slots(kcmm_pool_t* pool, uint32_t layer_idx, const int64_t* slots,
+                         uint32_t batch, uint64_t k, uint64_t v) {
+    return slots_impl(pool, layer_idx, slots, batch, k, v, 0);
+}
+
+int kcmm_append_kv_slots_on_stream(kcmm_pool_t* pool, uint32_t layer_idx, const int64_t* slots,
+                                   uint32_t batch, uint64_t k, uint64_t v, uint64_t stream) {
+    return slots_impl(pool, layer_idx, slots, batch, k, v, stream);
+}
+
+int kcmm_append_kv_device_slots_on_stream(kcmm_pool_t* pool, uint32_t layer_idx,
+                                          uint64_t slot_ptr, uint64_t offs_ptr,
+                                          uint64_t valid_ptr, uint32_t offs_len,
+                                          uint32_t batch, uint64_t k, uint64_t v,
+                                          uint64_t status_ptr, uint64_t stream) {
+    // ref ffi.rs:1399-1551
+    const char* fn = "kcmm_append_kv_device_slots_on_stream";
+    if (pool == nullptr || slot_ptr == 0 || offs_ptr == 0 || k == 0 || v == 0) {
+        if (pool) pool->set_error(std::string(fn) + ": null pointer argument");
+        return -1;
+    }
+    if (batch == 0 || offs_len == 0) {
+        pool->set_error(std::string(fn) +
+                        ": batch and offset table length must be positive");
+        return -1;
+    }
+    if (!layer_ok(pool, layer_idx, fn)) return -1;
+    const kcmm::PoolGeometry& g = pool->core->geo();
+    std::string err;
+    if (!kcmm::dev::set_device(pool->device, &err)) {
+        pool->set_error(std::string(fn) + ": bind device failed: " + err);
+        return -1;
+    }
+    kcmm::dev::KvDeviceSlotsArgs a{};
+    a.dtype = g.dtype;
+    a.k_base = pool->core->va_k(layer_idx);
+    a.v_base = pool->core->va_v(layer_idx);
+    a.k_src = k;
+    a.v_src = v;
+    a.slot_mapping = slot_ptr;
+    a.offsets_f16 = offs_ptr;
+    a.valid_blocks = valid_ptr;
+    a.status = status_ptr;
+    a.offsets_len = offs_len;
+    a.batch = batch;
+    a.block_size = static_cast<uint32_t>(g.block_size);
+    a.kv_heads = static_cast<uint32_t>(g.kv_heads);
+    a.head_dim = static_cast<uint32_t>(g.head_dim);
+    a.row_bytes = static_cast<uint32_t>(g.row_bytes);
+    a.data_bytes = static_cast<uint32_t>(g.data_bytes);
+    a.stream = stream;
+    if (!kcmm::dev::kv_write_device_slots(a, &err)) {
+        pool->set_error(std::string(fn) + ": launch failed: " + err);
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_precompile_vllm_kv_write_f16(kcmm_pool_t* pool) { return pool ? 0 : -1; }
+
+// ---- decode attention -------------------------------------------------------------
+
+#define KCMM_ATTN_ARGS                                                                     \
+    kcmm_pool_t *pool, uint32_t layer_idx, uint64_t q, uint64_t out, uint64_t bt,          \
+        uint64_t sl, uint64_t offs, uint32_t batch, uint32_t hq, uint32_t hkv, uint32_t d, \
+        uint32_t bs, uint32_t mbps, float scale
+#define KCMM_ATTN_PASS layer_idx, q, out, bt, sl, offs, batch, hq, hkv, d, bs, mbps, scale
+
+int kcmm_paged_attn_decode_f16(KCMM_ATTN_ARGS) {
+    return attn_impl(pool, kcmm::kF16, "kcmm_paged_attn_decode_f16", KCMM_ATTN_PASS, 0, true,
+                     true);
+}
+
+int kcmm_paged_attn_decode_f16_on_stream(KCMM_ATTN_ARGS, uint64_t stream) {
+    return attn_impl(pool, kcmm::kF16, "kcmm_paged_attn_decode_f16", KCMM_ATTN_PASS, stream,
+                     false, true);
+}
+
+int kcmm_paged_attn_decode_f16_on_current_context_stream(KCMM_ATTN_ARGS, uint64_t stream) {
+    return attn_impl(pool, kcmm::kF16, "kcmm_paged_attn_decode_f16", KCMM_ATTN_PASS, stream,
+                     false, false);
+}
+
+int kcmm_paged_attn_decode_bf16(KCMM_ATTN_ARGS) {
+    return attn_impl(pool, kcmm::kBF16, "kcmm_paged_attn_decode_bf16", KCMM_ATTN_PASS, 0, true,
+                     true);
+}
+
+int kcmm_paged_attn_decode_bf16_on_stream(KCMM_ATTN_ARGS, uint64_t stream) {
+    return attn_impl(pool, kcmm::kBF16, "kcmm_paged_attn_decode_bf16", KCMM_ATTN_PASS, stream,
+                     false, true);
+}
+
+int kcmm_paged_attn_decode_fp8_on_stream(KCMM_ATTN_ARGS, uint64_t stream) {
+    return attn_impl(pool, kcmm::kFP8, "kcmm_paged_attn_decode_fp8", KCMM_ATTN_PASS, stream,
+                     false, true);
+}
+
+int kcmm_precompile_paged_attn_decode_f16(kcmm_pool_t* pool) { return pool ? 0 : -1; }
+
+// ---- tiering: not built (every block stays resident in HBM) ----------------------
+
+uint32_t kcmm_evict_blocks(kcmm_pool_t*, uint32_t) { return 0; }
+
+uint64_t kcmm_restore_evicted_block(kcmm_pool_t* pool, uint32_t blk) {
+    if (pool == nullptr) return 0;
+    uint64_t v = 0;
+    if (!pool->core->block_va_offset(blk, &v)) {
+        pool->set_error(fmtu("kcmm_restore_evicted_block: block_idx %llu not found", blk));
+        return 0;
+    }
+    return v;
+}
+
+int kcmm_restore_evicted_blocks(kcmm_pool_t*, const uint32_t*, uint32_t) { return 0; }
+
+int kcmm_is_gpu_resident(kcmm_pool_t* pool, uint32_t blk) {
+    if (pool == nullptr) return 0;
+    uint64_t v;
+    return pool->core->block_va_offset(blk, &v) ? 1 : 0;
+}
+
+// ---- metrics ---------------------------------------------------------------------
+
+int kcmm_get_metrics(kcmm_pool_t* pool, kcmm_metrics_t* out) {
+    if (pool == nullptr || out == nullptr) return -1;
+    const kcmm::Metrics m = pool->core->metrics();
+    out->ifr = m.ifr;
+    out->pme = m.pme;
+    out->bu = m.bu;
+    out->rfi = m.rfi;
+    out->gpu_blocks = m.gpu_blocks;
+    out->cpu_blocks = 0;
+    out->nvme_blocks = 0;
+    out->eviction_count = 0;
+    out->restoration_count = 0;
+    return 0;
+}
+
+int kcmm_get_pool_stats(kcmm_pool_t* pool, kcmm_pool_stats_t* out) {
+    if (pool == nullptr || out == nullptr) return -1;
+    const kcmm::Stats s = pool->core->stats();
+    out->blocks_in_use = s.blocks_in_use;
+    out->total_blocks = s.total_blocks;
+    out->total_physical_blocks = s.total_physical_blocks;
+    out->free_physical_blocks = s.free_physical_blocks;
+    out->active_sequences = s.active_sequences;
+    out->num_layers = s.num_layers;
+    out->blocks_per_superblock = s.blocks_per_superblock;
+    out->superblock_count = s.superblock_count;
+    out->block_size = s.block_size;
+    out->max_blocks_per_seq = s.max_blocks_per_seq;
+    out->block_bytes = s.block_bytes;
+    out->tiering_enabled = 0;
+    out->sharing_enabled = 1;
+    out->physical_idle_ratio = s.physical_idle_ratio;
+    return 0;
+}
+
+uint32_t kcmm_blocks_in_use(kcmm_pool_t* pool) { return pool ? pool->core->blocks_in_use() : 0; }
+uint32_t kcmm_total_blocks(kcmm_pool_t* pool) { return pool ? pool->core->total_blocks() : 0; }
+uint64_t kcmm_block_state_epoch(kcmm_pool_t* pool) { return pool ? pool->core->epoch() : 0; }
+uint32_t kcmm_free_physical_blocks(kcmm_pool_t* pool) {
+    return pool ? pool->core->free_physical_blocks() : 0;
+}
+int kcmm_has_free_blocks(kcmm_pool_t* pool) {
+    return pool && pool->core->has_free_blocks() ? 1 : 0;
+}
+uint32_t kcmm_active_sequences(kcmm_pool_t* pool) {
+    return pool ? pool->core->active_sequences() : 0;
+}
+
+// ---- policy / hints -------------------------------------------------------------------
+
+int kcmm_set_eviction_policy(kcmm_pool_t* pool, const char* policy) {
+    if (pool == nullptr || policy == nullptr) return -1;
+    pool->set_error("kcmm_set_eviction_policy: tiering is disabled");
+    return -1;
+}
+
+uint32_t kcmm_get_eviction_policy(kcmm_pool_t*, char*, uint32_t) { return 0; }
+
+int kcmm_is_tiering_enabled(kcmm_pool_t*) { return 0; }
+
+int kcmm_hint(kcmm_pool_t* pool, uint32_t seq, kcmm_hint_t hint) {
+    // ref ffi.rs:2296-2379 with tiering off: touch/cool and priority class.
+    if (pool == nullptr) return -1;
+    if (!pool->core->has_sequence(seq)) {
+        pool->set_error(fmtu("kcmm_hint: seq_idx %llu out of bounds", seq));
+        return -1;
+    }
+    switch (hint) {
+        case KCMM_HINT_MULTI_TURN:
+        case KCMM_HINT_SYSTEM_PROMPT:
+        case KCMM_HINT_ATTENTION_SINK:
+        case KCMM_HINT_HEAVY_HITTER: pool->core->touch(seq); break;
+        case KCMM_HINT_HIGH_PRIORITY:
+            pool->core->touch(seq);
+            pool->core->set_priority(seq, 3);
+            break;
+        case KCMM_HINT_NEAR_END: pool->core->cool(seq); break;
+        case KCMM_HINT_LOW_PRIORITY:
+            pool->core->cool(seq);
+            pool->core->set_priority(seq, 1);
+            break;
+        case KCMM_HINT_EVICTABLE:
+            pool->core->cool(seq);
+            pool->core->set_priority(seq, 0);
+            break;
+        default: break;
+    }
+    return 0;
+}
+
+int kcmm_protect(kcmm_pool_t* pool, uint32_t, const uint32_t* ids, uint32_t n,
+                 kcmm_protection_t) {
+    // ref ffi.rs:2388-2442: with tiering off only the argument check remains.
+    if (pool == nullptr || ids == nullptr || n == 0) return -1;
+    return 0;
+}
+
+// ---- prefix sharing / copy-on-write ---------------------------------------------------
+
+int kcmm_share_prefix(kcmm_pool_t* pool, uint32_t src, uint32_t dst, uint32_t n,
+                      uint32_t* out) {
+    if (pool == nullptr || out == nullptr || n == 0) return -1;  // ref ffi.rs:2458-2460
+    std::string err;
+    if (!pool->core->share_prefix(src, dst, n, out, &err)) {
+        pool->set_error(err);
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_fork_sequence(kcmm_pool_t* pool, uint32_t src, uint32_t* out_seq) {
+    if (pool == nullptr || out_seq == nullptr) {
+        if (pool) pool->set_error("kcmm_fork_sequence: null arguments");
+        return -1;
+    }
+    std::string err;
+    if (!pool->core->fork_sequence(src, out_seq, &err)) {
+        pool->set_error(err);
+        return -1;
+    }
+    return 0;
+}
+
+uint32_t kcmm_get_block_refcount(kcmm_pool_t* pool, uint32_t blk) {
+    return pool ? pool->core->refcount(blk) : 0;
+}
+
+int kcmm_cow_block_for_append(kcmm_pool_t* pool, uint32_t seq, uint32_t logical,
+                              uint32_t* out_src, uint32_t* out_dst) {
+    if (pool == nullptr || out_src == nullptr || out_dst == nullptr) {
+        if (pool) pool->set_error("kcmm_cow_block_for_append: null arguments");
+        return -1;
+    }
+    std::string err;
+    const int rc = pool->core->cow_block_for_append(seq, logical, out_src, out_dst, &err);
+    if (rc < 0) pool->set_error(err);
+    return rc;
+}
+
+static std::vector<uint64_t> region_bases(kcmm_pool_t* pool) {
+    std::vector<uint64_t> r;
+    const size_t L = pool->core->geo().num_layers;
+    for (size_t l = 0; l < L; ++l) {
+        r.push_back(pool->core->va_k(l));
+        r.push_back(pool->core->va_v(l));
+    }
+    return r;
+}
+
+int kcmm_copy_blocks_on_stream(kcmm_pool_t* pool, const uint32_t* pairs, uint32_t n,
+                               uint64_t stream) {
+    if (pool == nullptr || (pairs == nullptr && n > 0)) {
+        if (pool) pool->set_error("kcmm_copy_blocks_on_stream: null arguments");
+        return -1;
+    }
+    if (n == 0) return 0;
+    std::vector<uint64_t> offs;
+    std::string err;
+    if (!pool->core->resolve_pairs(pairs, n, &offs, &err)) {
+        pool->set_error(err);
+        return -1;
+    }
+    if (!kcmm::dev::set_device(pool->device, &err) ||
+        !kcmm::dev::copy_pages(region_bases(pool), offs.data(), n,
+                               static_cast<uint32_t>(pool->core->geo().block_bytes), stream,
+                               &err)) {
+        pool->set_error("kcmm_copy_blocks_on_stream: " + err);
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_copy_blocks_device_on_stream(kcmm_pool_t* pool, uint64_t pairs_ptr, uint64_t offs_ptr,
+                                      uint32_t n, uint64_t stream) {
+    if (pool == nullptr || pairs_ptr == 0 || offs_ptr == 0) {
+        if (pool) pool->set_error("kcmm_copy_blocks_device_on_stream: null pointer argument");
+        return -1;
+    }
+    if (n == 0) return 0;
+    std::string err;
+    if (!kcmm::dev::set_device(pool->device, &err) ||
+        !kcmm::dev::copy_pages_device(region_bases(pool), pairs_ptr, offs_ptr, n,
+                                      static_cast<uint32_t>(pool->core->geo().block_bytes),
+                                      stream, &err)) {
+        pool->set_error("kcmm_copy_blocks_device_on_stream: " + err);
+        return -1;
+    }
+    return 0;
+}
+
+// ---- GEMM ---------------------------------------------------------------------------------
+
+int kcmm_gemm_bf16_on_stream(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n,
+                             uint32_t k, uint64_t stream) {
+    if (x == 0 || w == 0 || y == 0 || m == 0 || n == 0 || k == 0) return -1;
+    std::string err;
+    if (!kcmm::dev::gemm_bf16(x, w, y, m, n, k, stream, &err)) {
+        std::fprintf(stderr, "kcmm_gemm_bf16_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+// ---- utilities ---------------------------------------------------------------------------------
+
+int kcmm_below_low_watermark(kcmm_pool_t* pool, float threshold) {
+    return pool && pool->core->below_low_watermark(threshold) ? 1 : 0;
+}
+
+int kcmm_synchronize(kcmm_pool_t* pool) {
+    if (pool == nullptr) return -1;
+    std::string err;
+    if (!kcmm::dev::synchronize_device(pool->device, &err)) {
+        pool->set_error("kcmm_synchronize: " + err);
+        return -1;
+    }
+    return 0;
+}
+
+uint32_t kcmm_get_block_size(kcmm_pool_t* p) {
+    return p ? static_cast<uint32_t>(p->core->geo().block_size) : 0;
+}
+uint32_t kcmm_get_max_blocks_per_seq(kcmm_pool_t* p) {
+    return p ? static_cast<uint32_t>(p->core->geo().max_blocks_per_seq) : 0;
+}
+uint32_t kcmm_get_block_bytes(kcmm_pool_t* p) {
+    return p ? static_cast<uint32_t>(p->core->geo().block_bytes) : 0;
+}
+uint32_t kcmm_get_num_layers(kcmm_pool_t* p) {
+    return p ? static_cast<uint32_t>(p->core->geo().num_layers) : 0;
+}
+uint32_t kcmm_get_max_batch(kcmm_pool_t* p) {
+    return p ? static_cast<uint32_t>(p->core->geo().max_batch) : 0;
+}
+uint32_t kcmm_get_max_seq_len(kcmm_pool_t* p) {
+    return p ? static_cast<uint32_t>(p->core->geo().max_seq_len) : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,188 @@
+// Device page backing for a KCMM pool on MI355X.
+//
+// HipVmmBacking restates the reference's CUDA-VMM design (ref
+// src/cache/cuda_vmm.rs:6-234, pool.rs:211-221,287-322) with HIP VMM: each of
+// the 2*L regions is one virtual-address reservation, and a 2 MiB physical
+// superblock is created and mapped at byte sb*2MiB of every region when the
+// allocator grows.  HipFlatBacking backs each region with one hipMalloc of
+// the full capacity; it is used when the device reports no VMM support or
+// KCMM_BACKING=flat, and yields the same block ids and offsets.
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "../device_api.hpp"
+#include "common.hpp"
+
+namespace kcmm {
+namespace {
+
+class HipVmmBacking final : public PageBacking {
+public:
+    explicit HipVmmBacking(int device) : device_(device) {
+        std::memset(&prop_, 0, sizeof(prop_));
+        prop_.type = hipMemAllocationTypePinned;
+        prop_.location.type = hipMemLocationTypeDevice;
+        prop_.location.id = device;
+    }
+    ~HipVmmBacking() override { release(); }
+
+    bool reserve(size_t num_regions, size_t region_bytes, std::string* err) override {
+        size_t gran = 0;
+        KCMM_HIP_CHECK(hipMemGetAllocationGranularity(&gran, &prop_,
+                                                      hipMemAllocationGranularityMinimum),
+                       err);
+        if (gran == 0 || kSuperblockBytes % gran != 0) {
+            *err = "HIP VMM granularity does not divide the 2 MiB superblock";
+            return false;
+        }
+        region_bytes_ = region_bytes;
+        for (size_t r = 0; r < num_regions; ++r) {
+            void* p = nullptr;
+            KCMM_HIP_CHECK(hipMemAddressReserve(&p, region_bytes, kSuperblockBytes, nullptr, 0),
+                           err);
+            bases_.push_back(p);
+        }
+        return true;
+    }
+
+    uint64_t region_base(size_t r) const override {
+        return reinterpret_cast<uint64_t>(bases_[r]);
+    }
+
+    bool map_superblock(size_t sb, std::string* err) override {
+        if ((sb + 1) * kSuperblockBytes > region_bytes_) {
+            *err = "superblock beyond the reserved region";
+            return false;
+        }
+        hipMemAccessDesc desc;
+        std::memset(&desc, 0, sizeof(desc));
+        desc.location = prop_.location;
+        desc.flags = hipMemAccessFlagsProtReadWrite;
+        for (void* base : bases_) {
+            char* at = static_cast<char*>(base) + sb * kSuperblockBytes;
+            hipMemGenericAllocationHandle_t h;
+            KCMM_HIP_CHECK(hipMemCreate(&h, kSuperblockBytes, &prop_, 0), err);
+            hipError_t e = hipMemMap(at, kSuperblockBytes, 0, h, 0);
+            if (e != hipSuccess) {
+                (void)hipMemRelease(h);
+                *err = std::string("hipMemMap: ") + hipGetErrorString(e);
+                return false;
+            }
+            mapped_.push_back({at, h});
+            KCMM_HIP_CHECK(hipMemSetAccess(at, kSuperblockBytes, &desc, 1), err);
+        }
+        return true;
+    }
+
+    void release() override {
+        for (auto& m : mapped_) {
+            (void)hipMemUnmap(m.first, kSuperblockBytes);
+            (void)hipMemRelease(m.second);
+        }
+        mapped_.clear();
+        for (void* b : bases_) (void)hipMemAddressFree(b, region_bytes_);
+        bases_.clear();
+    }
+
+    int kind() const override { return 0; }
+
+private:
+    int device_;
+    hipMemAllocationProp prop_;
+    size_t region_bytes_ = 0;
+    std::vector<void*> bases_;
+    std::vector<std::pair<void*, hipMemGenericAllocationHandle_t>> mapped_;
+};
+
+class HipFlatBacking final : public PageBacking {
+public:
+    ~HipFlatBacking() override { release(); }
+
+    bool reserve(size_t num_regions, size_t region_bytes, std::string* err) override {
+        for (size_t r = 0; r < num_regions; ++r) {
+            void* p = nullptr;
+            KCMM_HIP_CHECK(hipMalloc(&p, region_bytes), err);
+            bases_.push_back(p);
+        }
+        return true;
+    }
+    uint64_t region_base(size_t r) const override {
+        return reinterpret_cast<uint64_t>(bases_[r]);
+    }
+    bool map_superblock(size_t, std::string*) override { return true; }
+    void release() override {
+        for (void* b : bases_) (void)hipFree(b);
+        bases_.clear();
+    }
+    int kind() const override { return 1; }
+
+private:
+    std::vector<void*> bases_;
+};
+
+}  // namespace
+
+namespace dev {
+
+std::unique_ptr<PageBacking> make_backing(int device, std::string* err) {
+    const char* env = std::getenv("KCMM_BACKING");
+    if (env != nullptr && std::strcmp(env, "flat") == 0)
+        return std::unique_ptr<PageBacking>(new HipFlatBacking());
+    int vmm = 0;
+    if (hipDeviceGetAttribute(&vmm, hipDeviceAttributeVirtualMemoryManagementSupported,
+                              device) != hipSuccess)
+        vmm = 0;
+    if (vmm) return std::unique_ptr<PageBacking>(new HipVmmBacking(device));
+    (void)err;
+    return std::unique_ptr<PageBacking>(new HipFlatBacking());
+}
+
+bool set_device(int device, std::string* err) {
+    KCMM_HIP_CHECK(hipSetDevice(device), err);
+    return true;
+}
+
+// Device scratch for split-K partials, one buffer per (device, stream, user
+// slot) so launches on different streams never share one.  Grows on demand;
+// the old buffer is released only after its stream has drained.
+bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, std::string* err) {
+    struct Ws {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+    };
+    static std::mutex mu;
+    static std::map<std::tuple<int, uint64_t, int>, Ws> table;
+    int dev = 0;
+    KCMM_HIP_CHECK(hipGetDevice(&dev), err);
+    std::lock_guard<std::mutex> lk(mu);
+    Ws& w = table[std::make_tuple(dev, stream, slot)];
+    if (w.bytes < bytes) {
+        if (w.ptr) {
+            KCMM_HIP_CHECK(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)), err);
+            KCMM_HIP_CHECK(hipFree(w.ptr), err);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        const size_t want = bytes + bytes / 4;
+        KCMM_HIP_CHECK(hipMalloc(&w.ptr, want), err);
+        w.bytes = want;
+    }
+    *out = w.ptr;
+    return true;
+}
+
+bool synchronize_device(int device, std::string* err) {
+    int cur = 0;
+    KCMM_HIP_CHECK(hipGetDevice(&cur), err);
+    if (cur != device) KCMM_HIP_CHECK(hipSetDevice(device), err);
+    KCMM_HIP_CHECK(hipDeviceSynchronize(), err);
+    if (cur != device) KCMM_HIP_CHECK(hipSetDevice(cur), err);
+    return true;
+}
+
+}  // namespace dev
+}  // namespace kcmm

@@ -1,0 +1,79 @@
+// Shared device helpers for the gfx950 kernels: vector types, element
+// conversions, HIP error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace kcmm {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Element codes shared with PoolGeometry::dtype.
+constexpr int kDtF16 = 0;
+constexpr int kDtBF16 = 1;
+constexpr int kDtFP8 = 2;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+    return __uint_as_float(h << 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// fp32 -> IEEE half, round to nearest even (hardware conversion).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <int DT>
+__device__ __forceinline__ float elem_to_f32(uint32_t bits) {
+    if constexpr (DT == kDtF16) return f16_bits_to_f32(bits);
+    else return bf16_bits_to_f32(bits);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t f32_to_elem(float f) {
+    if constexpr (DT == kDtF16) return f32_to_f16_bits(f);
+    else return f32_to_bf16_bits(f);
+}
+
+// OCP e4m3fn decode: 1 sign, 4 exponent (bias 7), 3 mantissa bits; the only
+// NaN codes are S.1111.111; no infinities.
+__device__ __forceinline__ float fp8e4m3_to_f32(uint32_t b) {
+    const uint32_t s = (b & 0x80u) << 24;
+    const uint32_t e = (b >> 3) & 0xFu;
+    const uint32_t m = b & 0x7u;
+    if (e == 0xFu && m == 0x7u) return __uint_as_float(s | 0x7fc00000u);
+    if (e == 0) {
+        // subnormal: m * 2^-9
+        return __uint_as_float(s) + (s ? -1.0f : 1.0f) * static_cast<float>(m) * 0.001953125f;
+    }
+    return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+}  // namespace kcmm
+
+#define KCMM_HIP_CHECK(expr, errp)                                              \
+    do {                                                                        \
+        hipError_t e_ = (expr);                                                 \
+        if (e_ != hipSuccess) {                                                 \
+            if (errp) *(errp) = std::string(#expr) + ": " + hipGetErrorString(e_); \
+            return false;                                                       \
+        }                                                                       \
+    } while (0)

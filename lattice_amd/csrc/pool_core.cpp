@@ -1,0 +1,521 @@
+// Host bookkeeping of a KCMM pool.  The allocation rules this file must keep
+// bit-exact are listed in pool_core.hpp with their reference lines.
+#include "pool_core.hpp"
+
+#include <algorithm>
+#include <cstdio>
+
+namespace kcmm {
+
+namespace {
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+std::string fmt(const char* f, unsigned long long a = 0, unsigned long long b = 0,
+                unsigned long long c = 0, unsigned long long d = 0) {
+    char buf[512];
+    std::snprintf(buf, sizeof(buf), f, a, b, c, d);
+    return buf;
+}
+
+}  // namespace
+
+bool PoolGeometry::compute(std::string* err) {
+    if (num_layers == 0 || kv_heads == 0 || head_dim == 0 || block_size == 0) {
+        *err = "pool geometry: num_layers, kv_heads, head_dim and block_size must be positive";
+        return false;
+    }
+    switch (dtype) {
+        case kF16:
+        case kBF16: elem_bytes = 2; break;
+        case kFP8: elem_bytes = 1; break;
+        default: *err = "pool geometry: unknown kv dtype"; return false;
+    }
+    row_bytes = kv_heads * head_dim * elem_bytes;
+    data_bytes = block_size * row_bytes;
+    // fp8 pages carry their per-kv-head fp32 scales in a footer; the page is
+    // padded to 256 B so every page starts on a 256-B boundary.
+    block_bytes = dtype == kFP8 ? align_up(data_bytes + kv_heads * 4, 256) : data_bytes;
+    blocks_per_superblock = kSuperblockBytes / block_bytes;
+    if (blocks_per_superblock == 0) {
+        *err = fmt("pool geometry: block_bytes (%llu) too large for a 2 MiB superblock",
+                   (unsigned long long)block_bytes);
+        return false;
+    }
+    // ref pool.rs:206-207
+    max_blocks_per_seq = (max_seq_len + block_size - 1) / block_size;
+    max_blocks_total = max_batch * max_blocks_per_seq;
+    if (max_blocks_total == 0) {
+        *err = "pool geometry: max_batch and max_seq_len must be positive";
+        return false;
+    }
+    // ref pool.rs:1145-1152
+    const size_t sbs = (max_blocks_total + blocks_per_superblock - 1) / blocks_per_superblock;
+    max_physical_blocks = sbs * blocks_per_superblock;
+    // The reference reserves align_up(max_blocks_total*block_bytes, 2 MiB)
+    // (ref pool.rs:211-212), which can be one superblock short of its own
+    // capacity limit when block_bytes does not divide 2 MiB; reserve enough
+    // for every superblock the capacity rule admits.
+    region_bytes = std::max(align_up(max_blocks_total * block_bytes, kSuperblockBytes),
+                            sbs * kSuperblockBytes);
+    return true;
+}
+
+PoolCore::PoolCore(const PoolGeometry& g, std::unique_ptr<PageBacking> backing)
+    : geo_(g), backing_(std::move(backing)) {}
+
+PoolCore::~PoolCore() {
+    if (backing_) backing_->release();
+}
+
+bool PoolCore::ensure_capacity_locked(std::string* err) {
+    if (!free_handles_.empty()) return true;
+    const size_t bps = geo_.blocks_per_superblock;
+    const size_t total = superblock_count_ * bps;
+    if (total >= geo_.max_physical_blocks) {
+        // ref pool.rs:328-337 (same wording)
+        *err = fmt("KCMM physical block capacity exhausted: total_physical_blocks=%llu "
+                   "max_physical_blocks_per_layer=%llu max_blocks_total=%llu "
+                   "blocks_per_superblock=%llu",
+                   total, geo_.max_physical_blocks, geo_.max_blocks_total, bps);
+        return false;
+    }
+    if (!backing_->map_superblock(superblock_count_, err)) return false;
+    const uint32_t sb = static_cast<uint32_t>(superblock_count_);
+    for (size_t i = 0; i < bps; ++i) free_handles_.emplace_back(sb, static_cast<uint32_t>(i));
+    ++superblock_count_;
+    ++epoch_;
+    return true;
+}
+
+bool PoolCore::alloc_one_locked(uint32_t* id_out, std::string* err) {
+    if (!ensure_capacity_locked(err)) return false;
+    const auto h = free_handles_.back();
+    free_handles_.pop_back();
+    BlockInfo bi;
+    bi.va_offset = static_cast<uint64_t>(h.first) * kSuperblockBytes +
+                   static_cast<uint64_t>(h.second) * geo_.block_bytes;
+    bi.superblock_idx = h.first;
+    bi.block_index = h.second;
+    bi.refcount = 1;
+    bi.in_use = true;
+    uint32_t id;
+    if (!free_ids_.empty()) {
+        id = free_ids_.back();
+        free_ids_.pop_back();
+        blocks_[id] = bi;
+    } else {
+        id = static_cast<uint32_t>(blocks_.size());
+        blocks_.push_back(bi);
+    }
+    ++epoch_;
+    *id_out = id;
+    return true;
+}
+
+bool PoolCore::alloc_blocks(uint32_t n, uint32_t* out, std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    const size_t ids_before = blocks_.size();
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!alloc_one_locked(&out[i], err)) {
+            // Undo this call's allocations in reverse so the free lists are
+            // exactly as before (superblocks mapped meanwhile stay mapped).
+            for (uint32_t j = i; j-- > 0;) {
+                BlockInfo& bi = blocks_[out[j]];
+                free_handles_.emplace_back(bi.superblock_idx, bi.block_index);
+                if (out[j] >= ids_before) {
+                    blocks_.pop_back();
+                } else {
+                    bi = BlockInfo{};
+                    free_ids_.push_back(out[j]);
+                }
+            }
+            ++epoch_;
+            return false;
+        }
+    }
+    return true;
+}
+
+void PoolCore::release_locked(const uint32_t* ids, size_t n) {
+    std::vector<uint32_t> recycled;
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t id = ids[i];
+        if (id >= blocks_.size()) continue;
+        BlockInfo& bi = blocks_[id];
+        if (!bi.in_use) continue;
+        if (bi.refcount > 1) {
+            --bi.refcount;
+            continue;
+        }
+        bi.in_use = false;
+        bi.refcount = 0;
+        free_handles_.emplace_back(bi.superblock_idx, bi.block_index);
+        recycled.push_back(id);
+    }
+    if (!recycled.empty()) {
+        ++epoch_;
+        free_ids_.insert(free_ids_.end(), recycled.begin(), recycled.end());
+    }
+}
+
+void PoolCore::free_blocks(const uint32_t* ids, size_t n) {
+    std::lock_guard<std::mutex> lk(mu_);
+    release_locked(ids, n);
+}
+
+uint32_t PoolCore::register_sequence(const uint32_t* table, size_t n) {
+    std::lock_guard<std::mutex> lk(mu_);
+    SequenceState s;
+    s.table.assign(table, table + n);
+    seqs_.push_back(std::move(s));
+    return static_cast<uint32_t>(seqs_.size() - 1);
+}
+
+void PoolCore::unregister_sequence(uint32_t seq) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq >= seqs_.size()) return;
+    std::vector<uint32_t> table;
+    table.swap(seqs_[seq].table);
+    seqs_[seq].seq_len = 0;
+    if (!table.empty()) release_locked(table.data(), table.size());
+}
+
+void PoolCore::touch(uint32_t seq) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq < seqs_.size()) seqs_[seq].active = true;
+}
+
+void PoolCore::cool(uint32_t seq) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq < seqs_.size()) seqs_[seq].active = false;
+}
+
+void PoolCore::set_priority(uint32_t seq, int prio) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq < seqs_.size()) seqs_[seq].priority = prio;
+}
+
+bool PoolCore::has_sequence(uint32_t seq) {
+    std::lock_guard<std::mutex> lk(mu_);
+    return seq < seqs_.size();
+}
+
+void PoolCore::update_seq_len(uint32_t seq, uint32_t len) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq < seqs_.size()) seqs_[seq].seq_len = len;
+}
+
+uint32_t PoolCore::get_seq_len(uint32_t seq) {
+    std::lock_guard<std::mutex> lk(mu_);
+    return seq < seqs_.size() ? seqs_[seq].seq_len : 0;
+}
+
+bool PoolCore::append_block_to_sequence(uint32_t seq, uint32_t block) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq >= seqs_.size()) return false;
+    seqs_[seq].table.push_back(block);
+    return true;
+}
+
+bool PoolCore::get_block_table(uint32_t seq, std::vector<uint32_t>* out) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq >= seqs_.size()) return false;
+    *out = seqs_[seq].table;
+    return true;
+}
+
+bool PoolCore::block_va_offset(uint32_t block, uint64_t* out) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (block >= blocks_.size() || !blocks_[block].in_use) return false;
+    *out = blocks_[block].va_offset;
+    return true;
+}
+
+std::vector<uint64_t> PoolCore::all_offsets_f16() {
+    std::lock_guard<std::mutex> lk(mu_);
+    std::vector<uint64_t> v(blocks_.size());
+    for (size_t i = 0; i < blocks_.size(); ++i)
+        v[i] = blocks_[i].in_use ? blocks_[i].va_offset / 2 : 0;
+    return v;
+}
+
+std::vector<uint8_t> PoolCore::all_valid_flags() {
+    std::lock_guard<std::mutex> lk(mu_);
+    std::vector<uint8_t> v(blocks_.size());
+    for (size_t i = 0; i < blocks_.size(); ++i) v[i] = blocks_[i].in_use ? 1 : 0;
+    return v;
+}
+
+bool PoolCore::table_va_offsets(uint32_t seq, std::vector<uint64_t>* out) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq >= seqs_.size()) return false;
+    out->clear();
+    for (uint32_t id : seqs_[seq].table) {
+        if (id >= blocks_.size() || !blocks_[id].in_use) return false;
+        out->push_back(blocks_[id].va_offset);
+    }
+    return true;
+}
+
+uint32_t PoolCore::refcount(uint32_t block) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (block >= blocks_.size() || !blocks_[block].in_use) return 0;
+    return blocks_[block].refcount;
+}
+
+bool PoolCore::fork_sequence(uint32_t src, uint32_t* out_seq, std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (src >= seqs_.size()) {
+        *err = fmt("kcmm_fork_sequence: seq_idx %llu out of bounds", src);
+        return false;
+    }
+    SequenceState s;
+    s.table = seqs_[src].table;
+    s.seq_len = seqs_[src].seq_len;
+    for (uint32_t id : s.table)
+        if (id < blocks_.size() && blocks_[id].in_use) ++blocks_[id].refcount;
+    seqs_.push_back(std::move(s));
+    *out_seq = static_cast<uint32_t>(seqs_.size() - 1);
+    return true;
+}
+
+bool PoolCore::share_prefix(uint32_t src, uint32_t dst, uint32_t n, uint32_t* out,
+                            std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (src >= seqs_.size() || dst >= seqs_.size()) {
+        *err = fmt("kcmm_share_prefix: sequence index out of bounds (src %llu, dst %llu)", src,
+                   dst);
+        return false;
+    }
+    const auto& st = seqs_[src].table;
+    if (st.size() < n) {
+        *err = fmt("kcmm_share_prefix: src seq %llu holds %llu blocks, %llu requested", src,
+                   st.size(), n);
+        return false;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        if (st[i] >= blocks_.size() || !blocks_[st[i]].in_use) {
+            *err = fmt("kcmm_share_prefix: block %llu not in use", st[i]);
+            return false;
+        }
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t id = seqs_[src].table[i];
+        ++blocks_[id].refcount;
+        seqs_[dst].table.push_back(id);
+        out[i] = id;
+    }
+    return true;
+}
+
+int PoolCore::cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src,
+                                   uint32_t* dst, std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (seq >= seqs_.size()) {
+        *err = fmt("kcmm_cow_block_for_append: seq_idx %llu out of bounds", seq);
+        return -1;
+    }
+    if (logical >= seqs_[seq].table.size()) {
+        *err = fmt("kcmm_cow_block_for_append: logical block %llu >= allocated %llu", logical,
+                   seqs_[seq].table.size());
+        return -1;
+    }
+    const uint32_t old_id = seqs_[seq].table[logical];
+    if (old_id >= blocks_.size() || !blocks_[old_id].in_use) {
+        *err = fmt("kcmm_cow_block_for_append: block %llu not in use", old_id);
+        return -1;
+    }
+    if (blocks_[old_id].refcount <= 1) return 0;
+    uint32_t new_id;
+    if (!alloc_one_locked(&new_id, err)) return -1;
+    seqs_[seq].table[logical] = new_id;
+    --blocks_[old_id].refcount;
+    *src = old_id;
+    *dst = new_id;
+    return 1;
+}
+
+bool PoolCore::resolve_pairs(const uint32_t* pairs, size_t n, std::vector<uint64_t>* out,
+                             std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    out->resize(2 * n);
+    for (size_t i = 0; i < 2 * n; ++i) {
+        const uint32_t id = pairs[i];
+        if (id >= blocks_.size() || !blocks_[id].in_use) {
+            *err = fmt("kcmm_copy_blocks: block %llu not in use", id);
+            return false;
+        }
+        (*out)[i] = blocks_[id].va_offset;
+    }
+    return true;
+}
+
+bool PoolCore::resolve_positions(const uint32_t* seqs, const uint32_t* pos, uint32_t batch,
+                                 std::vector<RowDst>* out, std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    out->clear();
+    out->reserve(batch);
+    for (uint32_t b = 0; b < batch; ++b) {
+        if (seqs[b] >= seqs_.size()) {
+            *err = fmt("kcmm_append_kv_step: seq_idx %llu out of bounds", seqs[b]);
+            return false;
+        }
+        const auto& table = seqs_[seqs[b]].table;
+        const size_t lb = pos[b] / geo_.block_size;
+        const size_t off = pos[b] % geo_.block_size;
+        if (lb >= table.size()) {
+            *err = fmt("kcmm_append_kv_step: logical_block %llu >= allocated %llu for seq %llu",
+                       lb, table.size(), seqs[b]);
+            return false;
+        }
+        const uint32_t id = table[lb];
+        if (id >= blocks_.size() || !blocks_[id].in_use) {
+            *err = fmt("kcmm_append_kv_step: block_idx %llu not in use", id);
+            return false;
+        }
+        if (blocks_[id].refcount > 1) {
+            *err = fmt("kcmm_append_kv_step: block_idx %llu is shared (refcount %llu); "
+                       "make it private with kcmm_cow_block_for_append first",
+                       id, blocks_[id].refcount);
+            return false;
+        }
+        out->push_back(RowDst{b, blocks_[id].va_offset, static_cast<uint32_t>(off)});
+    }
+    return true;
+}
+
+bool PoolCore::resolve_slots(const int64_t* slots, uint32_t batch, std::vector<RowDst>* out,
+                             std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    out->clear();
+    out->reserve(batch);
+    for (uint32_t b = 0; b < batch; ++b) {
+        if (slots[b] < 0) continue;  // padding row (ref ffi.rs:1327)
+        const uint64_t s = static_cast<uint64_t>(slots[b]);
+        const uint64_t id = s / geo_.block_size;
+        const uint32_t off = static_cast<uint32_t>(s % geo_.block_size);
+        if (id >= blocks_.size() || !blocks_[id].in_use) {
+            *err = fmt("kcmm_append_kv_slots: block_idx %llu from slot %llu not in use", id,
+                       s);
+            return false;
+        }
+        if (blocks_[id].refcount > 1) {
+            *err = fmt("kcmm_append_kv_slots: block_idx %llu is shared (refcount %llu)", id,
+                       blocks_[id].refcount);
+            return false;
+        }
+        out->push_back(RowDst{b, blocks_[id].va_offset, off});
+    }
+    return true;
+}
+
+uint32_t PoolCore::blocks_in_use_locked() const {
+    uint32_t n = 0;
+    for (const auto& b : blocks_) n += b.in_use ? 1 : 0;
+    return n;
+}
+
+Stats PoolCore::stats() {
+    std::lock_guard<std::mutex> lk(mu_);
+    Stats s{};
+    s.blocks_in_use = blocks_in_use_locked();
+    s.total_blocks = static_cast<uint32_t>(blocks_.size());
+    s.total_physical_blocks = static_cast<uint32_t>(superblock_count_ * geo_.blocks_per_superblock);
+    s.free_physical_blocks = static_cast<uint32_t>(free_handles_.size());
+    s.active_sequences = static_cast<uint32_t>(seqs_.size());
+    s.num_layers = static_cast<uint32_t>(geo_.num_layers);
+    s.blocks_per_superblock = static_cast<uint32_t>(geo_.blocks_per_superblock);
+    s.superblock_count = static_cast<uint32_t>(superblock_count_);
+    s.block_size = static_cast<uint32_t>(geo_.block_size);
+    s.max_blocks_per_seq = static_cast<uint32_t>(geo_.max_blocks_per_seq);
+    s.block_bytes = static_cast<uint32_t>(geo_.block_bytes);
+    // ref pool.rs:1160-1172
+    s.physical_idle_ratio = 0.0f;
+    if (superblock_count_ > 0) {
+        const uint64_t total = static_cast<uint64_t>(superblock_count_) * kSuperblockBytes *
+                               geo_.num_layers * 2;
+        const uint64_t used = static_cast<uint64_t>(s.blocks_in_use) * geo_.block_bytes *
+                              geo_.num_layers * 2;
+        if (used < total)
+            s.physical_idle_ratio = static_cast<float>(total - used) / static_cast<float>(total);
+    }
+    return s;
+}
+
+Metrics PoolCore::metrics() {
+    // ref pool.rs:1179-1240 (collect_metrics) and metrics.rs:142-162, computed
+    // in f32 exactly as the reference does.
+    std::lock_guard<std::mutex> lk(mu_);
+    Metrics m{};
+    const uint64_t total_physical = superblock_count_ * geo_.blocks_per_superblock;
+    const uint64_t in_use = blocks_in_use_locked();
+    uint64_t blocks_used = 0, tokens = 0;
+    for (const auto& s : seqs_) {
+        blocks_used += s.table.size();
+        tokens += s.seq_len;
+    }
+    const uint64_t layers2 = geo_.num_layers * 2;
+    const uint64_t actual_physical = superblock_count_ * kSuperblockBytes * layers2;
+    const uint64_t slots = blocks_used * geo_.block_size;
+    m.ifr = slots > 0 ? static_cast<float>(static_cast<int64_t>(slots) -
+                                           static_cast<int64_t>(tokens)) /
+                            static_cast<float>(slots)
+                      : 0.0f;
+    m.bu = total_physical > 0
+               ? static_cast<float>(in_use) / static_cast<float>(total_physical)
+               : 0.0f;
+    // The reference multiplies tokens by elements (not bytes) per token here.
+    const uint64_t bpt_all = geo_.kv_heads * geo_.head_dim * layers2;
+    const uint64_t ideal = tokens * bpt_all;
+    m.pme = actual_physical > 0
+                ? static_cast<float>(ideal) / static_cast<float>(actual_physical)
+                : 1.0f;
+    const uint64_t bps = geo_.blocks_per_superblock;
+    const uint64_t active_sb = (in_use + bps - 1) / bps;
+    const uint64_t actual_active = active_sb * kSuperblockBytes * layers2;
+    m.rfi = actual_active > 0
+                ? 1.0f - static_cast<float>(ideal) / static_cast<float>(actual_active)
+                : 0.0f;
+    m.gpu_blocks = in_use;
+    return m;
+}
+
+bool PoolCore::below_low_watermark(float threshold) {
+    std::lock_guard<std::mutex> lk(mu_);
+    const size_t total = superblock_count_ * geo_.blocks_per_superblock;
+    if (total == 0) return false;
+    return static_cast<float>(free_handles_.size()) / static_cast<float>(total) < threshold;
+}
+
+bool PoolCore::has_free_blocks() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return !free_handles_.empty();
+}
+
+uint32_t PoolCore::blocks_in_use() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return blocks_in_use_locked();
+}
+
+uint32_t PoolCore::total_blocks() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return static_cast<uint32_t>(blocks_.size());
+}
+
+uint32_t PoolCore::free_physical_blocks() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return static_cast<uint32_t>(free_handles_.size());
+}
+
+uint32_t PoolCore::active_sequences() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return static_cast<uint32_t>(seqs_.size());
+}
+
+uint64_t PoolCore::epoch() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return epoch_;
+}
+
+}  // namespace kcmm

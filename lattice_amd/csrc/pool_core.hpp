@@ -1,0 +1,186 @@
+// Host bookkeeping of a KCMM pool: the 2 MiB superblock page allocator, the
+// logical block-id table, sequences and their block tables, reference counts
+// for copy-on-write sharing.  Pure C++17 -- no HIP types -- so the exact same
+// code is linked into libkcmm.so and into the host-only check library the CPU
+// tests load.  Device memory is reached only through PageBacking.
+//
+// Allocation rules restated from the reference (all must hold bit-exactly):
+//   block_bytes        = kv_heads*block_size*head_dim*elem  (ref pool.rs:203-204)
+//   blocks/superblock  = floor(2 MiB / block_bytes), tail is padding
+//                                                        (ref superblock.rs:55-70,139-141)
+//   new superblock     pushes handles 0..bps-1, allocation pops (LIFO)
+//                                                        (ref superblock.rs:95-116)
+//   growth             only when the free list is empty; capacity
+//                      ceil(max_blocks_total/bps)*bps    (ref pool.rs:323-337,1145-1152)
+//   superblock s       mapped at byte s*2MiB of every layer's K and V region
+//                                                        (ref pool.rs:287-322)
+//   block id           LIFO pop of recycled ids, else len(block_info)
+//                                                        (ref pool.rs:412-454)
+//   va offset          s*2MiB + index*block_bytes        (ref pool.rs:404-407)
+//   free order         handles and ids returned in table order
+//                                                        (ref pool.rs:478-549)
+//   sequence ids       len(sequences), never reused      (ref pool.rs:551-572)
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace kcmm {
+
+constexpr size_t kSuperblockBytes = 2u * 1024u * 1024u;
+
+enum KvDtype : int32_t { kF16 = 0, kBF16 = 1, kFP8 = 2 };
+
+// Maps 2 MiB superblocks into 2*num_layers device VA regions (layer l: K at
+// region 2l, V at region 2l+1).  Implemented over HIP VMM / hipMalloc in the
+// product library and over host memory in the CPU check library.
+class PageBacking {
+public:
+    virtual ~PageBacking() = default;
+    virtual bool reserve(size_t num_regions, size_t region_bytes, std::string* err) = 0;
+    virtual uint64_t region_base(size_t region) const = 0;
+    virtual bool map_superblock(size_t sb_idx, std::string* err) = 0;
+    virtual void release() = 0;
+    virtual int kind() const = 0;
+};
+
+struct PoolGeometry {
+    size_t block_size = 16;
+    size_t num_layers = 0;
+    size_t kv_heads = 0;
+    size_t head_dim = 0;
+    size_t max_batch = 0;
+    size_t max_seq_len = 0;
+    int32_t dtype = kF16;
+
+    size_t elem_bytes = 2;          // bytes per K/V element
+    size_t row_bytes = 0;           // one token row of a page: kv_heads*head_dim*elem
+    size_t data_bytes = 0;          // block_size*row_bytes
+    size_t block_bytes = 0;         // data_bytes (+ fp8 scale footer, 256-B padded)
+    size_t blocks_per_superblock = 0;
+    size_t max_blocks_per_seq = 0;
+    size_t max_blocks_total = 0;
+    size_t max_physical_blocks = 0; // ceil(max_blocks_total/bps)*bps
+    size_t region_bytes = 0;        // VA reserved per region
+
+    // Returns false with a message when the shape cannot form a pool.
+    bool compute(std::string* err);
+};
+
+struct BlockInfo {
+    uint64_t va_offset = 0;
+    uint32_t superblock_idx = 0;
+    uint32_t block_index = 0;
+    uint32_t refcount = 0;
+    bool in_use = false;
+};
+
+struct SequenceState {
+    std::vector<uint32_t> table;
+    uint32_t seq_len = 0;
+    bool active = true;
+    int priority = 2;  // Evictable 0, Low 1, Normal 2, High 3 (ref pool.rs:69-86)
+};
+
+struct Stats {
+    uint32_t blocks_in_use, total_blocks, total_physical_blocks, free_physical_blocks;
+    uint32_t active_sequences, num_layers, blocks_per_superblock, superblock_count;
+    uint32_t block_size, max_blocks_per_seq, block_bytes;
+    float physical_idle_ratio;
+};
+
+struct Metrics {
+    float ifr, pme, bu, rfi;
+    uint64_t gpu_blocks;
+};
+
+// One destination row of a KV write, resolved on the host.
+struct RowDst {
+    uint32_t src_row;      // row of the [batch][row] source
+    uint64_t page_offset;  // byte offset of the page inside each region
+    uint32_t slot;         // token offset inside the page
+};
+
+class PoolCore {
+public:
+    PoolCore(const PoolGeometry& g, std::unique_ptr<PageBacking> backing);
+    ~PoolCore();
+
+    const PoolGeometry& geo() const { return geo_; }
+    uint64_t va_k(size_t layer) const { return backing_->region_base(2 * layer); }
+    uint64_t va_v(size_t layer) const { return backing_->region_base(2 * layer + 1); }
+    int backing_kind() const { return backing_->kind(); }
+
+    // Allocation (ref pool.rs:456-476).  On failure nothing stays allocated.
+    bool alloc_blocks(uint32_t n, uint32_t* out, std::string* err);
+    // Decrement and release at zero, in table order (ref pool.rs:478-549).
+    void free_blocks(const uint32_t* ids, size_t n);
+
+    uint32_t register_sequence(const uint32_t* table, size_t n);
+    void unregister_sequence(uint32_t seq);
+    void touch(uint32_t seq);
+    void cool(uint32_t seq);
+    void set_priority(uint32_t seq, int prio);
+    bool has_sequence(uint32_t seq);
+    void update_seq_len(uint32_t seq, uint32_t len);
+    uint32_t get_seq_len(uint32_t seq);
+    bool append_block_to_sequence(uint32_t seq, uint32_t block);
+    bool get_block_table(uint32_t seq, std::vector<uint32_t>* out);
+
+    bool block_va_offset(uint32_t block, uint64_t* out);  // false if not in use
+    std::vector<uint64_t> all_offsets_f16();
+    std::vector<uint8_t> all_valid_flags();
+    bool table_va_offsets(uint32_t seq, std::vector<uint64_t>* out);
+    uint32_t refcount(uint32_t block);
+
+    // Copy-on-write support.
+    bool fork_sequence(uint32_t src, uint32_t* out_seq, std::string* err);
+    bool share_prefix(uint32_t src, uint32_t dst, uint32_t n, uint32_t* out, std::string* err);
+    int cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src, uint32_t* dst,
+                             std::string* err);
+    // Byte offsets of the pages of (src, dst) pairs; false if an id is not in use.
+    bool resolve_pairs(const uint32_t* pairs, size_t n, std::vector<uint64_t>* out,
+                       std::string* err);
+
+    // KV-write destination resolution (ref ffi.rs:1088-1200, 1217-1383).  Every
+    // row is validated before anything is returned (no partial writes).
+    bool resolve_positions(const uint32_t* seqs, const uint32_t* pos, uint32_t batch,
+                           std::vector<RowDst>* out, std::string* err);
+    bool resolve_slots(const int64_t* slots, uint32_t batch, std::vector<RowDst>* out,
+                       std::string* err);
+
+    Stats stats();
+    Metrics metrics();
+    bool below_low_watermark(float threshold);
+    bool has_free_blocks();
+    uint32_t blocks_in_use();
+    uint32_t total_blocks();
+    uint32_t free_physical_blocks();
+    uint32_t active_sequences();
+    uint64_t epoch();
+
+private:
+    bool ensure_capacity_locked(std::string* err);
+    bool alloc_one_locked(uint32_t* id, std::string* err);
+    void release_locked(const uint32_t* ids, size_t n);
+    uint32_t blocks_in_use_locked() const;
+
+    PoolGeometry geo_;
+    std::unique_ptr<PageBacking> backing_;
+    std::mutex mu_;
+    // Physical page handles (superblock, index) -- one list for all 2*L
+    // regions, which the reference keeps identical by construction
+    // ("lockstep", ref pool.rs:364-410).
+    std::vector<std::pair<uint32_t, uint32_t>> free_handles_;
+    size_t superblock_count_ = 0;
+    std::vector<BlockInfo> blocks_;
+    std::vector<uint32_t> free_ids_;
+    std::vector<SequenceState> seqs_;
+    uint64_t epoch_ = 0;
+};
+
+}  // namespace kcmm

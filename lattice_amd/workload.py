@@ -1,0 +1,207 @@
+"""Synthetic decode-step workloads built through the KCMM C ABI.
+
+Used by bench.py, __graft_entry__.smoke() and the GPU tests to lay out a
+paged KV cache the way a serving engine would: pages are allocated from the
+pool, shuffled with a seeded permutation, handed to sequences as block
+tables, and filled with N(0,1) values.  PRNG: numpy PCG64
+(np.random.default_rng(seed)); fixed seeds per configuration.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .bindings import KV_BF16, KV_F16, KV_FP8, KcmmLibrary, KcmmPool, make_config, memcpy_htod
+
+SB = 2 * 1024 * 1024
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (vectorised)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        r = np.where(nan, np.uint16(0x7FC0), r)
+    return r
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def encode16(dtype: int, x: np.ndarray) -> np.ndarray:
+    return f32_to_f16_bits(x) if dtype == KV_F16 else f32_to_bf16_bits(x)
+
+
+def encode_fp8_page(blk: np.ndarray):
+    """A whole page [bs][Hkv][D] at once (prefill-style): scale per kv head =
+    amax/448 (1 for an all-zero head), e4m3fn RNE via torch's cast."""
+    amax = np.abs(blk).max(axis=(0, 2)).astype(np.float32)
+    scales = np.where(amax > 0, amax / np.float32(448.0), np.float32(1.0)).astype(np.float32)
+    y = torch.from_numpy((blk / scales[None, :, None]).astype(np.float32))
+    data = y.to(torch.float8_e4m3fn).view(torch.uint8).numpy().reshape(-1)
+    return data, scales
+
+
+@dataclass
+class DecodeCase:
+    lib: KcmmLibrary
+    pool: KcmmPool
+    dtype: int
+    batch: int
+    num_q_heads: int
+    kv_heads: int
+    head_dim: int
+    block_size: int
+    num_layers: int
+    seq_lens: np.ndarray            # int32 [B], tokens attended (incl. the appended one)
+    block_tables: np.ndarray        # int32 [B][mbps]
+    offsets_f16: np.ndarray         # uint64 [n_ids]
+    q_bits: np.ndarray              # uint16 [B][Hq][D]
+    k_mirror: list = field(default_factory=list)   # per layer host copy of the K region
+    v_mirror: list = field(default_factory=list)
+    dev: dict = field(default_factory=dict)        # torch device tensors
+
+    @property
+    def mbps(self) -> int:
+        return self.block_tables.shape[1]
+
+    @property
+    def geometry(self) -> dict:
+        st = self.pool.stats()
+        elem = 1 if self.dtype == KV_FP8 else 2
+        row_bytes = self.kv_heads * self.head_dim * elem
+        return dict(block_bytes=st["block_bytes"], row_bytes=row_bytes,
+                    data_bytes=row_bytes * self.block_size,
+                    mapped_bytes=st["superblock_count"] * SB)
+
+    def kv_bytes(self) -> int:
+        """Algorithmic K+V bytes one decode attention step reads (one layer)."""
+        elem = 1 if self.dtype == KV_FP8 else 2
+        return int(self.seq_lens.astype(np.int64).sum()) * 2 * self.kv_heads * self.head_dim * elem
+
+    def run_attention(self, layer: int = 0, stream_ptr: int | None = None, scale=None) -> None:
+        scale = 1.0 / math.sqrt(self.head_dim) if scale is None else scale
+        d = self.dev
+        self.pool.paged_attn_decode(
+            layer_idx=layer, query_ptr=d["q"].data_ptr(), out_ptr=d["out"].data_ptr(),
+            block_tables_ptr=d["bt"].data_ptr(), seq_lens_ptr=d["sl"].data_ptr(),
+            block_offsets_f16_ptr=d["offs"].data_ptr(), batch=self.batch,
+            num_q_heads=self.num_q_heads, kv_heads=self.kv_heads, head_dim=self.head_dim,
+            block_size=self.block_size, max_blocks_per_seq=self.mbps, scale=scale,
+            stream_ptr=stream_ptr)
+
+    def out_bits(self) -> np.ndarray:
+        return self.dev["out"].cpu().numpy().view(np.uint16)
+
+
+def _fill_pages_host(case: DecodeCase, rng: np.random.Generator, layer_tokens) -> None:
+    """Write N(0,1) K/V for every attended token into host mirrors of the
+    regions, then upload the mapped part of each region."""
+    g = case.geometry
+    hk, d, bs = case.kv_heads, case.head_dim, case.block_size
+    for layer in range(case.num_layers):
+        mk = np.zeros(g["mapped_bytes"], dtype=np.uint8)
+        mv = np.zeros(g["mapped_bytes"], dtype=np.uint8)
+        for b in range(case.batch):
+            L = int(layer_tokens[b])
+            if L <= 0:
+                continue
+            n_pages = -(-L // bs)
+            for which, mirror in ((0, mk), (1, mv)):
+                x = rng.standard_normal((n_pages * bs, hk, d)).astype(np.float32)
+                x[L:] = 0.0
+                for pi in range(n_pages):
+                    page = int(case.offsets_f16[case.block_tables[b, pi]]) * 2
+                    blk = x[pi * bs:(pi + 1) * bs]
+                    if case.dtype == KV_FP8:
+                        data, scales = encode_fp8_page(blk)
+                        mirror[page:page + data.size] = data
+                        mirror[page + g["data_bytes"]:page + g["data_bytes"] + 4 * hk] = \
+                            scales.view(np.uint8)
+                    else:
+                        data = encode16(case.dtype, blk).view(np.uint8).reshape(-1)
+                        mirror[page:page + data.size] = data
+        memcpy_htod(case.pool.va_k(layer), mk)
+        memcpy_htod(case.pool.va_v(layer), mv)
+        case.k_mirror.append(mk)
+        case.v_mirror.append(mv)
+
+
+def build_decode_case(lib: KcmmLibrary, *, batch: int, num_q_heads: int, kv_heads: int,
+                      head_dim: int, block_size: int, ctx_lens, dtype: int = KV_BF16,
+                      num_layers: int = 1, seed: int = 0, host_mirror: bool = True,
+                      extra_seq_len: int = 0, device: str = "cuda") -> DecodeCase:
+    """Allocate pages for `ctx_lens` tokens per sequence (+ `extra_seq_len`
+    page headroom), shuffle them over the pool, fill them and upload q."""
+    if dtype == KV_FP8 and not host_mirror:
+        raise ValueError("fp8 pools are filled through the host mirror")
+    rng = np.random.default_rng(seed)
+    ctx = np.asarray(ctx_lens, dtype=np.int64)
+    max_len = int(max(1, ctx.max() + extra_seq_len))
+    cfg = make_config(num_layers=num_layers, kv_heads=kv_heads, head_dim=head_dim,
+                      max_batch=batch, max_seq_len=max_len, block_size=block_size)
+    pool = lib.create_pool(cfg, dtype)
+    pages = [max(1, -(-int(L + extra_seq_len) // block_size)) for L in ctx]
+    ids = []
+    total = sum(pages)
+    for start in range(0, total, 4096):
+        ids += pool.alloc_blocks(min(4096, total - start))
+    perm = rng.permutation(np.asarray(ids, dtype=np.int64))
+    mbps = -(-max_len // block_size)
+    bt = np.zeros((batch, mbps), dtype=np.int32)
+    pos = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[pos:pos + n]
+        pos += n
+        s = pool.register_sequence(bt[b, :n].tolist())
+        pool.update_seq_len(s, int(ctx[b]))
+    offs = np.asarray(pool.all_block_offsets_f16(), dtype=np.uint64)
+    qdt = KV_F16 if dtype == KV_F16 else KV_BF16   # fp8 pools take bf16 queries
+    q = encode16(qdt, rng.standard_normal((batch, num_q_heads, head_dim)).astype(np.float32))
+    case = DecodeCase(lib=lib, pool=pool, dtype=dtype, batch=batch, num_q_heads=num_q_heads,
+                      kv_heads=kv_heads, head_dim=head_dim, block_size=block_size,
+                      num_layers=num_layers, seq_lens=ctx.astype(np.int32), block_tables=bt,
+                      offsets_f16=offs, q_bits=q)
+    if host_mirror:
+        _fill_pages_host(case, rng, ctx)
+    else:
+        fill_regions_on_device(case, seed)
+    tdt = torch.float16 if dtype == KV_F16 else torch.bfloat16
+    case.dev = {
+        "q": torch.from_numpy(q.view(np.int16)).view(tdt).to(device),
+        "out": torch.zeros((batch, num_q_heads, head_dim), dtype=tdt, device=device),
+        "bt": torch.from_numpy(bt).to(device),
+        "sl": torch.from_numpy(case.seq_lens.copy()).to(device),
+        "offs": torch.from_numpy(offs.view(np.int64)).to(device),
+    }
+    return case
+
+
+def fill_regions_on_device(case: DecodeCase, seed: int) -> None:
+    """Fill every mapped byte of every region with N(0,1) 16-bit values
+    generated on the GPU (torch), for workloads too large for a host mirror."""
+    g = case.geometry
+    n = g["mapped_bytes"] // 2
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    tdt = torch.float16 if case.dtype == KV_F16 else torch.bfloat16
+    import ctypes
+    from .bindings import hip
+    h = hip()
+    h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    for layer in range(case.num_layers):
+        for base in (case.pool.va_k(layer), case.pool.va_v(layer)):
+            chunk = 64 << 20
+            for off in range(0, n, chunk):
+                m = min(chunk, n - off)
+                t = torch.randn(m, generator=gen, device="cuda", dtype=torch.float32).to(tdt)
+                rc = h.hipMemcpy(ctypes.c_void_p(base + 2 * off), ctypes.c_void_p(t.data_ptr()),
+                                 2 * m, 3)
+                if rc != 0:
+                    raise RuntimeError(f"hipMemcpy D2D failed ({rc})")
+    torch.cuda.synchronize()

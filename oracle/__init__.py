@@ -1,0 +1,278 @@
+"""Python access to the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker used by tests/, by
+__graft_entry__.smoke() and by bench.py's cpu_baseline leg.  Nothing in the
+lattice_amd package imports this module, and no product code path may fall
+back to it.  See oracle.h for what each function restates and DESIGN.md for
+how each one is pinned.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+F16, BF16, FP8, F32 = 0, 1, 2, 3
+_NP_STORAGE = {F16: np.uint16, BF16: np.uint16, FP8: np.uint8, F32: np.float32}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle` (or __graft_entry__.build())")
+        _lib = C.CDLL(str(LIB_PATH))
+        _bind(_lib)
+    return _lib
+
+
+def build() -> None:
+    import subprocess
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+P = C.c_void_p
+U32, U64, I32, F = C.c_uint32, C.c_uint64, C.c_int32, C.c_float
+
+
+def _bind(l: C.CDLL) -> None:
+    sig = {
+        "oracle_f32_to_bf16": ([F], C.c_uint16), "oracle_bf16_to_f32": ([C.c_uint16], F),
+        "oracle_f32_to_f16": ([F], C.c_uint16), "oracle_f16_to_f32": ([C.c_uint16], F),
+        "oracle_f32_to_e4m3": ([F], C.c_uint8), "oracle_e4m3_to_f32": ([C.c_uint8], F),
+        "oracle_encode_array": ([C.c_int, P, P, C.c_size_t], None),
+        "oracle_decode_array": ([C.c_int, P, P, C.c_size_t], None),
+        "opool_new": ([C.c_size_t] * 6 + [C.c_int, C.c_int], P),
+        "opool_delete": ([P], None),
+        "opool_alloc": ([P, U32, P], C.c_int),
+        "opool_release": ([P, P, U32], None),
+        "opool_register": ([P, P, U32], U32),
+        "opool_unregister": ([P, U32], None),
+        "opool_append_block": ([P, U32, U32], C.c_int),
+        "opool_update_seq_len": ([P, U32, U32], None),
+        "opool_block_table": ([P, U32, P, U32, P], C.c_int),
+        "opool_block_offset": ([P, U32, P], C.c_int),
+        "opool_offsets_f16": ([P, P, U32], U32),
+        "opool_valid_flags": ([P, P, U32], U32),
+        "opool_table_offsets": ([P, U32, P, U32, P], C.c_int),
+        "opool_fork": ([P, U32, P], C.c_int),
+        "opool_share_prefix": ([P, U32, U32, U32, P], C.c_int),
+        "opool_cow": ([P, U32, U32, P, P], C.c_int),
+        "opool_refcount": ([P, U32], U32),
+        "opool_stats": ([P, P], None),
+        "opool_metrics": ([P, P], None),
+        "opool_below_low_watermark": ([P, F], C.c_int),
+        "oracle_kv_write_rows": ([C.c_int, P, P, P, P, P, P, P, U32, U32, U32, U32, U32], C.c_int),
+        "oracle_kv_write_device_slots": ([C.c_int, P, P, P, P, P, U32, P, P, U32, U32, U32, U32,
+                                          U32, U32, P], C.c_int),
+        "oracle_copy_pages": ([P, U32, P, U32, U32], None),
+        "oracle_attn_decode_f64": ([C.c_int, P, P, P, P, P, P, P] + [U32] * 8 + [C.c_double],
+                                   C.c_int),
+        "oracle_attn_decode_ref_f32": ([C.c_int, P, P, P, P, P, P, P] + [U32] * 7 + [F, C.c_int],
+                                       C.c_int),
+        "oracle_gemm_bf16_f64": ([P, P, P, U32, U32, U32], None),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(l, name)
+        fn.argtypes = args
+        fn.restype = res
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ---- numeric formats -------------------------------------------------------
+
+def encode(dtype: int, x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=_NP_STORAGE[dtype])
+    lib().oracle_encode_array(dtype, _p(x), _p(out), x.size)
+    return out
+
+
+def decode(dtype: int, x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=_NP_STORAGE[dtype])
+    out = np.empty(x.shape, dtype=np.float32)
+    lib().oracle_decode_array(dtype, _p(x), _p(out), x.size)
+    return out
+
+
+# ---- page allocator ----------------------------------------------------------
+
+class OraclePool:
+    """Restatement of the reference allocator (ref superblock.rs, pool.rs)."""
+
+    def __init__(self, block_size, num_layers, kv_heads, head_dim, max_batch, max_seq_len,
+                 dtype=F16, rollback_on_failure=True):
+        self._h = lib().opool_new(block_size, num_layers, kv_heads, head_dim, max_batch,
+                                  max_seq_len, dtype, int(rollback_on_failure))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().opool_delete(self._h)
+            self._h = None
+
+    def alloc(self, n: int) -> list[int] | None:
+        out = np.zeros(max(n, 1), dtype=np.uint32)
+        return None if lib().opool_alloc(self._h, n, _p(out)) else out[:n].tolist()
+
+    def release(self, ids):
+        a = np.asarray(ids, dtype=np.uint32)
+        lib().opool_release(self._h, _p(a), a.size)
+
+    def register(self, table) -> int:
+        a = np.asarray(table, dtype=np.uint32)
+        return lib().opool_register(self._h, _p(a) if a.size else None, a.size)
+
+    def unregister(self, seq):
+        lib().opool_unregister(self._h, seq)
+
+    def append_block(self, seq, blk) -> int:
+        return lib().opool_append_block(self._h, seq, blk)
+
+    def update_seq_len(self, seq, n):
+        lib().opool_update_seq_len(self._h, seq, n)
+
+    def block_table(self, seq, max_blocks=1 << 16):
+        out = np.zeros(max_blocks, dtype=np.uint32)
+        cnt = C.c_uint32(0)
+        rc = lib().opool_block_table(self._h, seq, _p(out), max_blocks, C.byref(cnt))
+        return None if rc else out[: cnt.value].tolist()
+
+    def block_offset(self, blk):
+        v = C.c_uint64(0)
+        return None if lib().opool_block_offset(self._h, blk, C.byref(v)) else v.value
+
+    def offsets_f16(self, max_blocks=1 << 20):
+        out = np.zeros(max_blocks, dtype=np.uint64)
+        n = lib().opool_offsets_f16(self._h, _p(out), max_blocks)
+        return out[:n]
+
+    def valid_flags(self, max_blocks=1 << 20):
+        out = np.zeros(max_blocks, dtype=np.uint8)
+        n = lib().opool_valid_flags(self._h, _p(out), max_blocks)
+        return out[:n]
+
+    def table_offsets(self, seq, max_blocks=1 << 16):
+        out = np.zeros(max_blocks, dtype=np.uint64)
+        cnt = C.c_uint32(0)
+        rc = lib().opool_table_offsets(self._h, seq, _p(out), max_blocks, C.byref(cnt))
+        return None if rc else out[: cnt.value].tolist()
+
+    def fork(self, src):
+        v = C.c_uint32(0)
+        return None if lib().opool_fork(self._h, src, C.byref(v)) else v.value
+
+    def share_prefix(self, src, dst, n):
+        out = np.zeros(max(n, 1), dtype=np.uint32)
+        return None if lib().opool_share_prefix(self._h, src, dst, n, _p(out)) else out[:n].tolist()
+
+    def cow(self, seq, logical):
+        s, d = C.c_uint32(0), C.c_uint32(0)
+        rc = lib().opool_cow(self._h, seq, logical, C.byref(s), C.byref(d))
+        return rc, (s.value, d.value)
+
+    def refcount(self, blk) -> int:
+        return lib().opool_refcount(self._h, blk)
+
+    def stats(self) -> dict:
+        st = np.zeros(14, dtype=np.uint64)
+        lib().opool_stats(self._h, _p(st))
+        keys = ["blocks_in_use", "total_blocks", "total_physical_blocks", "free_physical_blocks",
+                "active_sequences", "num_layers", "blocks_per_superblock", "superblock_count",
+                "block_size", "max_blocks_per_seq", "block_bytes"]
+        d = {k: int(st[i]) for i, k in enumerate(keys)}
+        d["physical_idle_ratio"] = float(np.array([st[11]], dtype=np.uint32).view(np.float32)[0])
+        d["max_physical_blocks"] = int(st[12])
+        d["region_superblocks"] = int(st[13])
+        return d
+
+    def metrics(self) -> dict:
+        m = np.zeros(4, dtype=np.float32)
+        lib().opool_metrics(self._h, _p(m))
+        return dict(zip(["ifr", "pme", "bu", "rfi"], m.tolist()))
+
+    def below_low_watermark(self, t) -> bool:
+        return bool(lib().opool_below_low_watermark(self._h, t))
+
+
+# ---- KV write / page copy ------------------------------------------------------
+
+def kv_write_rows(dtype, k_region, v_region, k_src, v_src, page_offsets, slots, src_rows,
+                  kv_heads, head_dim, row_bytes, data_bytes):
+    po = np.ascontiguousarray(page_offsets, dtype=np.uint64)
+    sl = np.ascontiguousarray(slots, dtype=np.uint32)
+    sr = np.ascontiguousarray(src_rows, dtype=np.uint32)
+    lib().oracle_kv_write_rows(dtype, _p(k_region), _p(v_region), _p(k_src), _p(v_src), _p(po),
+                               _p(sl), _p(sr), po.size, kv_heads, head_dim, row_bytes, data_bytes)
+
+
+def kv_write_device_slots(dtype, k_region, v_region, k_src, v_src, slots, offsets_f16, valid,
+                          block_size, kv_heads, head_dim, row_bytes, data_bytes) -> int:
+    s = np.ascontiguousarray(slots, dtype=np.int64)
+    o = np.ascontiguousarray(offsets_f16, dtype=np.uint64)
+    v = None if valid is None else np.ascontiguousarray(valid, dtype=np.uint8)
+    status = np.zeros(1, dtype=np.int32)
+    lib().oracle_kv_write_device_slots(dtype, _p(k_region), _p(v_region), _p(k_src), _p(v_src),
+                                       _p(s), s.size, _p(o), _p(v), o.size, block_size, kv_heads,
+                                       head_dim, row_bytes, data_bytes, _p(status))
+    return int(status[0])
+
+
+def copy_pages(regions: list[np.ndarray], pairs, block_bytes: int) -> None:
+    ptrs = (C.c_void_p * len(regions))(*[r.ctypes.data for r in regions])
+    pr = np.ascontiguousarray(pairs, dtype=np.uint64).reshape(-1)
+    lib().oracle_copy_pages(C.cast(ptrs, C.c_void_p), len(regions), _p(pr), pr.size // 2,
+                            block_bytes)
+
+
+# ---- attention / GEMM ------------------------------------------------------------
+
+def attn_decode_f64(dtype, q, k_region, v_region, block_tables, seq_lens, offsets_f16,
+                    num_q_heads, kv_heads, head_dim, block_size, row_bytes, data_bytes, scale):
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    of = np.ascontiguousarray(offsets_f16, dtype=np.uint64)
+    q = np.ascontiguousarray(q)
+    batch, mbps = bt.shape
+    out = np.zeros((batch, num_q_heads, head_dim), dtype=np.float64)
+    lib().oracle_attn_decode_f64(dtype, _p(q), _p(out), _p(k_region), _p(v_region), _p(bt),
+                                 _p(sl), _p(of), batch, num_q_heads, kv_heads, head_dim,
+                                 block_size, mbps, row_bytes, data_bytes, scale)
+    return out
+
+
+def attn_decode_ref_f32(dtype, q, k_region, v_region, block_tables, seq_lens, offsets_f16,
+                        num_q_heads, kv_heads, head_dim, block_size, row_bytes, scale,
+                        threads=0, out=None):
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    of = np.ascontiguousarray(offsets_f16, dtype=np.uint64)
+    q = np.ascontiguousarray(q)
+    batch, mbps = bt.shape
+    if out is None:
+        out = np.zeros((batch, num_q_heads, head_dim), dtype=np.float32)
+    rc = lib().oracle_attn_decode_ref_f32(dtype, _p(q), _p(out), _p(k_region), _p(v_region),
+                                          _p(bt), _p(sl), _p(of), batch, num_q_heads, kv_heads,
+                                          head_dim, block_size, mbps, row_bytes, scale, threads)
+    if rc:
+        raise ValueError("oracle_attn_decode_ref_f32: unsupported dtype/head_dim")
+    return out
+
+
+def gemm_bf16_f64(x_bits: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    m, k = x.shape
+    n, k2 = w.shape
+    assert k == k2
+    y = np.zeros((m, n), dtype=np.float64)
+    lib().oracle_gemm_bf16_f64(_p(x), _p(w), _p(y), m, n, k)
+    return y

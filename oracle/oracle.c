@@ -1,0 +1,721 @@
+/*
+ * oracle.c -- CPU restatement of the reference's decode-step data path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for tests/, smoke()
+ * and the CPU baseline of bench.py.  Never linked into the product.
+ *
+ * Build: make -C oracle   (gcc -O3 -fopenmp; no reference sources are used)
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define SB_BYTES ((size_t)2 * 1024 * 1024)
+
+/* ======================================================================
+ * Numeric formats (the reference is f16-only, ref pool.rs:203-204; bf16 and
+ * fp8 follow their published definitions: bf16 = upper half of IEEE binary32
+ * with round-to-nearest-even, OCP FP8 e4m3fn with RNE and saturation).
+ * ====================================================================== */
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+uint16_t oracle_f32_to_bf16(float x) {
+    uint32_t u = f2u(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* IEEE binary16 with RNE, gradual underflow and overflow to infinity
+ * (ref: half 2.7.1 f16::from_f32, used at llama_transformer.rs:70). */
+uint16_t oracle_f32_to_f16(float x) {
+    uint32_t u = f2u(x);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7e00u;          /* NaN */
+    if (a >= 0x477ff000u) return sign | 0x7c00u;         /* >= 65520 rounds to inf */
+    if (a < 0x38800000u) {                               /* below 2^-14: subnormal */
+        /* value = a * 2^24 in units of the f16 subnormal step 2^-24 */
+        float v = u2f(a) * 16777216.0f;                  /* exact scaling */
+        float r = rintf(v);                              /* RNE */
+        return sign | (uint16_t)r;
+    }
+    uint32_t e = (a >> 23) - 112;                        /* rebias 127 -> 15 */
+    uint32_t m = a & 0x7fffffu;
+    uint32_t q = m >> 13, rem = m & 0x1fffu;
+    uint32_t h = (e << 10) | q;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) h += 1;  /* carry may bump e */
+    return sign | (uint16_t)h;
+}
+
+float oracle_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    if (e == 0) {
+        float v = ldexpf((float)m, -24);
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+    return u2f(sign | ((e + 112) << 23) | (m << 13));
+}
+
+uint8_t oracle_f32_to_e4m3(float x) {
+    uint32_t bits = f2u(x);
+    uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
+    float a = fabsf(x);
+    if (a != a) return sign | 0x7fu;
+    if (a >= 448.0f) return sign | 0x7eu;
+    if (a < 0.015625f) return sign | (uint8_t)rintf(a * 512.0f);  /* 2^-9 grid */
+    uint32_t ab = f2u(a);
+    int e = (int)(ab >> 23) - 127;
+    uint32_t mant = ab & 0x7fffffu, q = mant >> 20, rem = mant & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) ++q;
+    if (q == 8) { q = 0; ++e; }
+    uint32_t code = ((uint32_t)(e + 7) << 3) | q;
+    if (code > 0x7eu) code = 0x7eu;
+    return sign | (uint8_t)code;
+}
+
+float oracle_e4m3_to_f32(uint8_t b) {
+    int s = b & 0x80, e = (b >> 3) & 0xf, m = b & 7;
+    float v;
+    if (e == 0xf && m == 7) return NAN;
+    if (e == 0) v = ldexpf((float)m, -9);
+    else v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    return s ? -v : v;
+}
+
+void oracle_encode_array(int dtype, const float *src, void *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        switch (dtype) {
+            case 0: ((uint16_t *)dst)[i] = oracle_f32_to_f16(src[i]); break;
+            case 1: ((uint16_t *)dst)[i] = oracle_f32_to_bf16(src[i]); break;
+            case 2: ((uint8_t *)dst)[i] = oracle_f32_to_e4m3(src[i]); break;
+            default: ((float *)dst)[i] = src[i]; break;
+        }
+    }
+}
+
+void oracle_decode_array(int dtype, const void *src, float *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        switch (dtype) {
+            case 0: dst[i] = oracle_f16_to_f32(((const uint16_t *)src)[i]); break;
+            case 1: dst[i] = oracle_bf16_to_f32(((const uint16_t *)src)[i]); break;
+            case 2: dst[i] = oracle_e4m3_to_f32(((const uint8_t *)src)[i]); break;
+            default: dst[i] = ((const float *)src)[i]; break;
+        }
+    }
+}
+
+static size_t esize_of(int dtype) { return dtype == 2 ? 1 : (dtype == 3 ? 4 : 2); }
+
+/* ======================================================================
+ * Page allocator, restated from the reference's structure: one free stack of
+ * (superblock, index) handles per layer and per K/V (ref superblock.rs:40-142,
+ * LayerKvPool :151-171), moved in lockstep (ref pool.rs:364-410); logical
+ * block ids with a recycled-id stack (ref pool.rs:412-454); sequences
+ * (ref pool.rs:551-572).  Reference counts are this build's CoW extension.
+ * ====================================================================== */
+
+typedef struct { uint32_t sb, idx; } Handle;
+
+typedef struct {
+    Handle *free;    /* LIFO stack */
+    size_t nfree;
+    size_t sb_count;
+} LayerPool;
+
+typedef struct {
+    uint64_t va;
+    uint32_t sb, idx;
+    uint32_t refcount;
+    int in_use;
+} OBlock;
+
+typedef struct {
+    uint32_t *table;
+    size_t n, cap;
+    uint32_t seq_len;
+} OSeq;
+
+struct OPool {
+    size_t block_size, num_layers, kv_heads, head_dim;
+    size_t elem_per_block, block_bytes, bps, max_blocks_per_seq, max_blocks_total;
+    size_t max_physical, region_bytes;
+    int rollback;
+    LayerPool *pools;        /* 2*L: K pools then V pools */
+    OBlock *blocks;
+    size_t nblocks, cap_blocks;
+    uint32_t *free_ids;
+    size_t nfree_ids, cap_free_ids;
+    OSeq *seqs;
+    size_t nseqs, cap_seqs;
+};
+
+static void *grow(void *p, size_t *cap, size_t need, size_t elem) {
+    if (need <= *cap) return p;
+    size_t c = *cap ? *cap : 16;
+    while (c < need) c *= 2;
+    *cap = c;
+    return realloc(p, c * elem);
+}
+
+OPool *opool_new(size_t block_size, size_t num_layers, size_t kv_heads, size_t head_dim,
+                 size_t max_batch, size_t max_seq_len, int dtype, int rollback) {
+    OPool *p = (OPool *)calloc(1, sizeof(OPool));
+    p->block_size = block_size ? block_size : 16;              /* ref ffi.rs:477 */
+    p->num_layers = num_layers;
+    p->kv_heads = kv_heads;
+    p->head_dim = head_dim;
+    p->elem_per_block = kv_heads * p->block_size * head_dim;   /* ref pool.rs:202 */
+    size_t data = p->elem_per_block * esize_of(dtype);
+    p->block_bytes = dtype == 2 ? (data + kv_heads * 4 + 255) / 256 * 256 : data;
+    p->bps = SB_BYTES / p->block_bytes;                        /* ref superblock.rs:78 */
+    p->max_blocks_per_seq = (max_seq_len + p->block_size - 1) / p->block_size;
+    p->max_blocks_total = max_batch * p->max_blocks_per_seq;  /* ref pool.rs:206-207 */
+    size_t sbs = (p->max_blocks_total + p->bps - 1) / p->bps;
+    p->max_physical = sbs * p->bps;                            /* ref pool.rs:1145-1152 */
+    size_t ref_va = (p->max_blocks_total * p->block_bytes + SB_BYTES - 1) / SB_BYTES * SB_BYTES;
+    p->region_bytes = ref_va > sbs * SB_BYTES ? ref_va : sbs * SB_BYTES;
+    p->rollback = rollback;
+    p->pools = (LayerPool *)calloc(2 * num_layers, sizeof(LayerPool));
+    for (size_t l = 0; l < 2 * num_layers; ++l)
+        p->pools[l].free = (Handle *)malloc((p->max_physical + 1) * sizeof(Handle));
+    return p;
+}
+
+void opool_delete(OPool *p) {
+    if (!p) return;
+    for (size_t l = 0; l < 2 * p->num_layers; ++l) free(p->pools[l].free);
+    for (size_t s = 0; s < p->nseqs; ++s) free(p->seqs[s].table);
+    free(p->pools); free(p->blocks); free(p->free_ids); free(p->seqs);
+    free(p);
+}
+
+/* ref pool.rs:323-362 */
+static int ensure_capacity(OPool *p) {
+    if (p->pools[0].nfree > 0) return 0;
+    if (p->pools[0].sb_count * p->bps >= p->max_physical) return -1;
+    for (size_t l = 0; l < 2 * p->num_layers; ++l) {
+        LayerPool *lp = &p->pools[l];
+        uint32_t sb = (uint32_t)lp->sb_count++;              /* ref superblock.rs:103-116 */
+        for (size_t i = 0; i < p->bps; ++i) {
+            lp->free[lp->nfree].sb = sb;
+            lp->free[lp->nfree].idx = (uint32_t)i;
+            lp->nfree++;
+        }
+    }
+    return 0;
+}
+
+/* ref pool.rs:364-454 */
+static int alloc_one(OPool *p, uint32_t *id_out) {
+    if (ensure_capacity(p)) return -1;
+    Handle h = {0, 0};
+    for (size_t l = 0; l < 2 * p->num_layers; ++l) {
+        LayerPool *lp = &p->pools[l];
+        Handle x = lp->free[--lp->nfree];
+        if (l == 0) h = x;
+        else if (x.sb != h.sb || x.idx != h.idx) abort();  /* lockstep broken */
+    }
+    OBlock b;
+    b.va = (uint64_t)h.sb * SB_BYTES + (uint64_t)h.idx * p->block_bytes;
+    b.sb = h.sb; b.idx = h.idx; b.refcount = 1; b.in_use = 1;
+    uint32_t id;
+    if (p->nfree_ids > 0) {
+        id = p->free_ids[--p->nfree_ids];
+        p->blocks[id] = b;
+    } else {
+        p->blocks = (OBlock *)grow(p->blocks, &p->cap_blocks, p->nblocks + 1, sizeof(OBlock));
+        id = (uint32_t)p->nblocks++;
+        p->blocks[id] = b;
+    }
+    *id_out = id;
+    return 0;
+}
+
+static void push_handle(OPool *p, uint32_t sb, uint32_t idx) {
+    for (size_t l = 0; l < 2 * p->num_layers; ++l) {
+        LayerPool *lp = &p->pools[l];
+        lp->free[lp->nfree].sb = sb;
+        lp->free[lp->nfree].idx = idx;
+        lp->nfree++;
+    }
+}
+
+int opool_alloc(OPool *p, uint32_t n, uint32_t *out) {
+    size_t before = p->nblocks;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (alloc_one(p, &out[i])) {
+            if (p->rollback) {
+                for (uint32_t j = i; j-- > 0;) {
+                    OBlock *b = &p->blocks[out[j]];
+                    push_handle(p, b->sb, b->idx);
+                    if (out[j] >= before) {
+                        p->nblocks--;
+                    } else {
+                        memset(b, 0, sizeof(*b));
+                        p->free_ids = (uint32_t *)grow(p->free_ids, &p->cap_free_ids,
+                                                       p->nfree_ids + 1, sizeof(uint32_t));
+                        p->free_ids[p->nfree_ids++] = out[j];
+                    }
+                }
+            }
+            return -1;
+        }
+    }
+    return 0;
+}
+
+/* ref pool.rs:478-549 (+ reference counts) */
+void opool_release(OPool *p, const uint32_t *ids, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t id = ids[i];
+        if (id >= p->nblocks) continue;
+        OBlock *b = &p->blocks[id];
+        if (!b->in_use) continue;
+        if (b->refcount > 1) { b->refcount--; continue; }
+        b->in_use = 0;
+        b->refcount = 0;
+        push_handle(p, b->sb, b->idx);
+        p->free_ids = (uint32_t *)grow(p->free_ids, &p->cap_free_ids, p->nfree_ids + 1,
+                                       sizeof(uint32_t));
+        p->free_ids[p->nfree_ids++] = id;
+    }
+}
+
+static OSeq *new_seq(OPool *p) {
+    p->seqs = (OSeq *)grow(p->seqs, &p->cap_seqs, p->nseqs + 1, sizeof(OSeq));
+    OSeq *s = &p->seqs[p->nseqs++];
+    memset(s, 0, sizeof(*s));
+    return s;
+}
+
+static void seq_push(OSeq *s, uint32_t v) {
+    s->table = (uint32_t *)grow(s->table, &s->cap, s->n + 1, sizeof(uint32_t));
+    s->table[s->n++] = v;
+}
+
+uint32_t opool_register(OPool *p, const uint32_t *table, uint32_t n) {
+    OSeq *s = new_seq(p);
+    for (uint32_t i = 0; i < n; ++i) seq_push(s, table[i]);
+    return (uint32_t)(p->nseqs - 1);
+}
+
+void opool_unregister(OPool *p, uint32_t seq) {
+    if (seq >= p->nseqs) return;
+    OSeq *s = &p->seqs[seq];
+    uint32_t *t = s->table;
+    size_t n = s->n;
+    s->table = NULL; s->n = 0; s->cap = 0; s->seq_len = 0;
+    if (n) opool_release(p, t, (uint32_t)n);
+    free(t);
+}
+
+int opool_append_block(OPool *p, uint32_t seq, uint32_t blk) {
+    if (seq >= p->nseqs) return -1;
+    seq_push(&p->seqs[seq], blk);
+    return 0;
+}
+
+void opool_update_seq_len(OPool *p, uint32_t seq, uint32_t len) {
+    if (seq < p->nseqs) p->seqs[seq].seq_len = len;
+}
+
+int opool_block_table(OPool *p, uint32_t seq, uint32_t *out, uint32_t max, uint32_t *count) {
+    if (seq >= p->nseqs) { *count = 0; return -1; }
+    uint32_t n = (uint32_t)(p->seqs[seq].n < max ? p->seqs[seq].n : max);
+    memcpy(out, p->seqs[seq].table, n * sizeof(uint32_t));
+    *count = n;
+    return 0;
+}
+
+int opool_block_offset(OPool *p, uint32_t blk, uint64_t *out) {
+    if (blk >= p->nblocks || !p->blocks[blk].in_use) return -1;
+    *out = p->blocks[blk].va;
+    return 0;
+}
+
+/* ref pool.rs:724-748 */
+uint32_t opool_offsets_f16(OPool *p, uint64_t *out, uint32_t max) {
+    uint32_t n = (uint32_t)(p->nblocks < max ? p->nblocks : max);
+    for (uint32_t i = 0; i < n; ++i) out[i] = p->blocks[i].in_use ? p->blocks[i].va / 2 : 0;
+    return n;
+}
+
+uint32_t opool_valid_flags(OPool *p, uint8_t *out, uint32_t max) {
+    uint32_t n = (uint32_t)(p->nblocks < max ? p->nblocks : max);
+    for (uint32_t i = 0; i < n; ++i) out[i] = p->blocks[i].in_use ? 1 : 0;
+    return n;
+}
+
+int opool_table_offsets(OPool *p, uint32_t seq, uint64_t *out, uint32_t max, uint32_t *count) {
+    *count = 0;
+    if (seq >= p->nseqs) return -1;
+    OSeq *s = &p->seqs[seq];
+    for (size_t i = 0; i < s->n; ++i) {
+        uint32_t id = s->table[i];
+        if (id >= p->nblocks || !p->blocks[id].in_use) return -1;
+    }
+    uint32_t n = (uint32_t)(s->n < max ? s->n : max);
+    for (uint32_t i = 0; i < n; ++i) out[i] = p->blocks[s->table[i]].va;
+    *count = n;
+    return 0;
+}
+
+/* Copy-on-write extension (vLLM fork / clear_copy_on_writes semantics,
+ * ref patch_vllm.py:1083-1101, shadow_allocator.py:63-118). */
+int opool_fork(OPool *p, uint32_t src, uint32_t *out_seq) {
+    if (src >= p->nseqs) return -1;
+    OSeq *d = new_seq(p);
+    OSeq *s = &p->seqs[src];
+    for (size_t i = 0; i < s->n; ++i) {
+        uint32_t id = s->table[i];
+        seq_push(d, id);
+        if (id < p->nblocks && p->blocks[id].in_use) p->blocks[id].refcount++;
+    }
+    d->seq_len = s->seq_len;
+    *out_seq = (uint32_t)(p->nseqs - 1);
+    return 0;
+}
+
+int opool_share_prefix(OPool *p, uint32_t src, uint32_t dst, uint32_t n, uint32_t *out) {
+    if (src >= p->nseqs || dst >= p->nseqs || p->seqs[src].n < n) return -1;
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t id = p->seqs[src].table[i];
+        if (id >= p->nblocks || !p->blocks[id].in_use) return -1;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t id = p->seqs[src].table[i];
+        p->blocks[id].refcount++;
+        seq_push(&p->seqs[dst], id);
+        out[i] = id;
+    }
+    return 0;
+}
+
+int opool_cow(OPool *p, uint32_t seq, uint32_t logical, uint32_t *src, uint32_t *dst) {
+    if (seq >= p->nseqs || logical >= p->seqs[seq].n) return -1;
+    uint32_t old = p->seqs[seq].table[logical];
+    if (old >= p->nblocks || !p->blocks[old].in_use) return -1;
+    if (p->blocks[old].refcount <= 1) return 0;
+    uint32_t nid;
+    if (alloc_one(p, &nid)) return -1;
+    p->seqs[seq].table[logical] = nid;
+    p->blocks[old].refcount--;
+    *src = old;
+    *dst = nid;
+    return 1;
+}
+
+uint32_t opool_refcount(OPool *p, uint32_t blk) {
+    if (blk >= p->nblocks || !p->blocks[blk].in_use) return 0;
+    return p->blocks[blk].refcount;
+}
+
+static uint64_t in_use_count(OPool *p) {
+    uint64_t n = 0;
+    for (size_t i = 0; i < p->nblocks; ++i) n += p->blocks[i].in_use ? 1 : 0;
+    return n;
+}
+
+void opool_stats(OPool *p, uint64_t *st) {
+    uint64_t in_use = in_use_count(p);
+    size_t sbc = p->pools[0].sb_count;
+    st[0] = in_use;
+    st[1] = p->nblocks;
+    st[2] = sbc * p->bps;
+    st[3] = p->pools[0].nfree;
+    st[4] = p->nseqs;
+    st[5] = p->num_layers;
+    st[6] = p->bps;
+    st[7] = sbc;
+    st[8] = p->block_size;
+    st[9] = p->max_blocks_per_seq;
+    st[10] = p->block_bytes;
+    /* ref pool.rs:1160-1172 */
+    float idle = 0.0f;
+    if (sbc > 0) {
+        uint64_t total = (uint64_t)sbc * SB_BYTES * p->num_layers * 2;
+        uint64_t used = in_use * p->block_bytes * p->num_layers * 2;
+        if (used < total) idle = (float)(total - used) / (float)total;
+    }
+    uint32_t ib;
+    memcpy(&ib, &idle, 4);
+    st[11] = ib;
+    st[12] = p->max_physical;
+    st[13] = p->region_bytes / SB_BYTES;
+}
+
+/* ref pool.rs:1179-1240, metrics.rs:142-162 (all f32) */
+void opool_metrics(OPool *p, float *m) {
+    uint64_t total_physical = p->pools[0].sb_count * p->bps;
+    uint64_t in_use = in_use_count(p);
+    uint64_t used = 0, tokens = 0;
+    for (size_t s = 0; s < p->nseqs; ++s) { used += p->seqs[s].n; tokens += p->seqs[s].seq_len; }
+    uint64_t L2 = p->num_layers * 2;
+    uint64_t actual = p->pools[0].sb_count * SB_BYTES * L2;
+    uint64_t slots = used * p->block_size;
+    m[0] = slots ? (float)((int64_t)slots - (int64_t)tokens) / (float)slots : 0.0f;
+    uint64_t ideal = tokens * (p->elem_per_block / p->block_size * L2);
+    m[1] = actual ? (float)ideal / (float)actual : 1.0f;
+    m[2] = total_physical ? (float)in_use / (float)total_physical : 0.0f;
+    uint64_t act_sb = (in_use + p->bps - 1) / p->bps;
+    uint64_t act_bytes = act_sb * SB_BYTES * L2;
+    m[3] = act_bytes ? 1.0f - (float)ideal / (float)act_bytes : 0.0f;
+}
+
+int opool_below_low_watermark(OPool *p, float threshold) {
+    uint64_t total = p->pools[0].sb_count * p->bps;
+    if (!total) return 0;
+    return (float)p->pools[0].nfree / (float)total < threshold;
+}
+
+/* ======================================================================
+ * KV write
+ * ====================================================================== */
+
+/* fp8 page write of one kv head row (this build's fp8 contract, stated in
+ * include/kcmm_mi355x.h and the kernel source; no reference counterpart). */
+static void fp8_write_head(uint8_t *page, uint32_t slot, uint32_t kvh, const uint16_t *src,
+                           uint32_t D, uint32_t row_bytes, uint32_t data_bytes) {
+    float x[512];
+    float amax = 0.0f;
+    for (uint32_t d = 0; d < D; ++d) {
+        x[d] = oracle_bf16_to_f32(src[d]);
+        float a = fabsf(x[d]);
+        if (a > amax) amax = a;
+    }
+    uint8_t *sp = page + data_bytes + kvh * 4;
+    float scale;
+    if (slot == 0) {
+        scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+    } else {
+        float old;
+        memcpy(&old, sp, 4);
+        scale = old;
+        if (amax > 448.0f * old) {
+            scale = amax / 448.0f;
+            for (uint32_t u = 0; u < slot; ++u) {
+                uint8_t *row = page + (uint64_t)u * row_bytes + kvh * D;
+                for (uint32_t d = 0; d < D; ++d) {
+                    float y = oracle_e4m3_to_f32(row[d]) * old;
+                    row[d] = oracle_f32_to_e4m3(y / scale);
+                }
+            }
+        }
+    }
+    uint8_t *row = page + (uint64_t)slot * row_bytes + kvh * D;
+    for (uint32_t d = 0; d < D; ++d) row[d] = oracle_f32_to_e4m3(x[d] / scale);
+    memcpy(sp, &scale, 4);
+}
+
+static void write_row(int dtype, uint8_t *k_region, uint8_t *v_region, const uint8_t *k_src,
+                      const uint8_t *v_src, uint64_t page, uint32_t slot, uint32_t src_row,
+                      uint32_t kv_heads, uint32_t D, uint32_t row_bytes, uint32_t data_bytes) {
+    if (dtype == 2) {
+        for (uint32_t g = 0; g < kv_heads; ++g) {
+            const uint16_t *ks = (const uint16_t *)k_src + ((uint64_t)src_row * kv_heads + g) * D;
+            const uint16_t *vs = (const uint16_t *)v_src + ((uint64_t)src_row * kv_heads + g) * D;
+            fp8_write_head(k_region + page, slot, g, ks, D, row_bytes, data_bytes);
+            fp8_write_head(v_region + page, slot, g, vs, D, row_bytes, data_bytes);
+        }
+        return;
+    }
+    /* ref pool.rs:1073-1091: dst = region + va_offset + off*step*2, one row copy */
+    uint64_t dst = page + (uint64_t)slot * row_bytes;
+    memcpy(k_region + dst, k_src + (uint64_t)src_row * row_bytes, row_bytes);
+    memcpy(v_region + dst, v_src + (uint64_t)src_row * row_bytes, row_bytes);
+}
+
+int oracle_kv_write_rows(int dtype, uint8_t *k_region, uint8_t *v_region, const uint8_t *k_src,
+                         const uint8_t *v_src, const uint64_t *page_offsets,
+                         const uint32_t *slots, const uint32_t *src_rows, uint32_t n,
+                         uint32_t kv_heads, uint32_t head_dim, uint32_t row_bytes,
+                         uint32_t data_bytes) {
+    for (uint32_t i = 0; i < n; ++i)
+        write_row(dtype, k_region, v_region, k_src, v_src, page_offsets[i], slots[i],
+                  src_rows[i], kv_heads, head_dim, row_bytes, data_bytes);
+    return 0;
+}
+
+/* ref kcmm_vllm_kv_write.cu:8-66: padding skipped, id >= len -> status 1,
+ * inactive id -> status 2, first error wins. */
+int oracle_kv_write_device_slots(int dtype, uint8_t *k_region, uint8_t *v_region,
+                                 const uint8_t *k_src, const uint8_t *v_src, const int64_t *slots,
+                                 uint32_t batch, const uint64_t *offsets_f16,
+                                 const uint8_t *valid, uint32_t offsets_len, uint32_t block_size,
+                                 uint32_t kv_heads, uint32_t head_dim, uint32_t row_bytes,
+                                 uint32_t data_bytes, int32_t *status) {
+    for (uint32_t r = 0; r < batch; ++r) {
+        int64_t slot = slots[r];
+        if (slot < 0) continue;
+        int64_t id = slot / block_size;
+        if (id >= (int64_t)offsets_len) { if (status && *status == 0) *status = 1; continue; }
+        if (valid && valid[id] == 0) { if (status && *status == 0) *status = 2; continue; }
+        write_row(dtype, k_region, v_region, k_src, v_src, offsets_f16[id] * 2,
+                  (uint32_t)(slot % block_size), r, kv_heads, head_dim, row_bytes, data_bytes);
+    }
+    return 0;
+}
+
+void oracle_copy_pages(uint8_t *const *regions, uint32_t n_regions, const uint64_t *pairs,
+                       uint32_t n_pairs, uint32_t block_bytes) {
+    for (uint32_t p = 0; p < n_pairs; ++p)
+        for (uint32_t r = 0; r < n_regions; ++r)
+            memmove(regions[r] + pairs[2 * p + 1], regions[r] + pairs[2 * p], block_bytes);
+}
+
+/* ======================================================================
+ * Paged decode attention
+ * ====================================================================== */
+
+static double q_elem(int dtype, const void *q, size_t i) {
+    if (dtype == 0) return oracle_f16_to_f32(((const uint16_t *)q)[i]);
+    if (dtype == 3) return ((const float *)q)[i];
+    return oracle_bf16_to_f32(((const uint16_t *)q)[i]);  /* bf16 and fp8 pools */
+}
+
+static double kv_elem(int dtype, const uint8_t *page, uint64_t off, uint32_t d,
+                      uint32_t data_bytes, uint32_t kvh) {
+    switch (dtype) {
+        case 0: { uint16_t h; memcpy(&h, page + off + 2 * d, 2); return oracle_f16_to_f32(h); }
+        case 1: { uint16_t h; memcpy(&h, page + off + 2 * d, 2); return oracle_bf16_to_f32(h); }
+        case 2: {
+            float s;
+            memcpy(&s, page + data_bytes + 4 * kvh, 4);
+            return (double)oracle_e4m3_to_f32(page[off + d]) * (double)s;
+        }
+        default: { float f; memcpy(&f, page + off + 4 * d, 4); return f; }
+    }
+}
+
+int oracle_attn_decode_f64(int dtype, const void *q, double *out, const uint8_t *k_region,
+                           const uint8_t *v_region, const int32_t *block_tables,
+                           const int32_t *seq_lens, const uint64_t *offsets_f16, uint32_t batch,
+                           uint32_t hq, uint32_t hkv, uint32_t D, uint32_t bs, uint32_t mbps,
+                           uint32_t row_bytes, uint32_t data_bytes, double scale) {
+    size_t es = esize_of(dtype);
+    #pragma omp parallel for schedule(dynamic)
+    for (long long task = 0; task < (long long)batch * hq; ++task) {
+        uint32_t b = (uint32_t)(task / hq), h = (uint32_t)(task % hq);
+        uint32_t kvh = h * hkv / hq;                       /* ref kcmm_vllm_paged_attn.cu:40 */
+        int64_t L = seq_lens[b];
+        if (L > (int64_t)mbps * bs) L = (int64_t)mbps * bs;
+        double *o = out + ((size_t)b * hq + h) * D;
+        if (L <= 0) { for (uint32_t d = 0; d < D; ++d) o[d] = 0.0; continue; }
+        double *s = (double *)malloc((size_t)L * sizeof(double));
+        const size_t qi = ((size_t)b * hq + h) * D;
+        double mx = -INFINITY;
+        for (int64_t t = 0; t < L; ++t) {
+            int32_t blk = block_tables[(size_t)b * mbps + t / bs];
+            uint64_t page = offsets_f16[blk] * 2;
+            uint64_t off = (uint64_t)(t % bs) * row_bytes + (uint64_t)kvh * D * es;
+            double acc = 0.0;
+            for (uint32_t d = 0; d < D; ++d)
+                acc += q_elem(dtype, q, qi + d) * kv_elem(dtype, k_region + page, off, d, data_bytes, kvh);
+            s[t] = acc * scale;
+            if (s[t] > mx) mx = s[t];
+        }
+        double z = 0.0;
+        for (int64_t t = 0; t < L; ++t) { s[t] = exp(s[t] - mx); z += s[t]; }
+        for (uint32_t d = 0; d < D; ++d) o[d] = 0.0;
+        for (int64_t t = 0; t < L; ++t) {
+            int32_t blk = block_tables[(size_t)b * mbps + t / bs];
+            uint64_t page = offsets_f16[blk] * 2;
+            uint64_t off = (uint64_t)(t % bs) * row_bytes + (uint64_t)kvh * D * es;
+            double w = s[t] / z;
+            for (uint32_t d = 0; d < D; ++d)
+                o[d] += w * kv_elem(dtype, v_region + page, off, d, data_bytes, kvh);
+        }
+        free(s);
+    }
+    return 0;
+}
+
+/* The reference kernel's loop (ref kcmm_vllm_paged_attn.cu:38-101): m starts
+ * at -1e30, per token dot*scale, m=max, e=exp(dot-m), corr=exp(old_m-m),
+ * s=s*corr+e, acc=acc*corr+e*v; out=acc/s.  16-bit K/V only. */
+int oracle_attn_decode_ref_f32(int dtype, const void *q, float *out, const uint8_t *k_region,
+                               const uint8_t *v_region, const int32_t *block_tables,
+                               const int32_t *seq_lens, const uint64_t *offsets_f16,
+                               uint32_t batch, uint32_t hq, uint32_t hkv, uint32_t D,
+                               uint32_t bs, uint32_t mbps, uint32_t row_bytes, float scale,
+                               int threads) {
+    if (D > 256 || (dtype != 0 && dtype != 1)) return -1;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#endif
+    #pragma omp parallel for schedule(dynamic, 4)
+    for (long long task = 0; task < (long long)batch * hq; ++task) {
+        uint32_t b = (uint32_t)(task / hq), h = (uint32_t)(task % hq);
+        uint32_t kvh = h * hkv / hq;
+        int32_t L = seq_lens[b];
+        float *o = out + ((size_t)b * hq + h) * D;
+        if (L <= 0) { for (uint32_t d = 0; d < D; ++d) o[d] = 0.0f; continue; }
+        float qv[256], acc[256];
+        for (uint32_t d = 0; d < D; ++d) {
+            uint16_t x = ((const uint16_t *)q)[((size_t)b * hq + h) * D + d];
+            qv[d] = dtype == 0 ? oracle_f16_to_f32(x) : oracle_bf16_to_f32(x);
+            acc[d] = 0.0f;
+        }
+        float m = -1e30f, s = 0.0f;
+        for (int32_t pos = 0; pos < L; ++pos) {
+            int32_t blk = block_tables[(size_t)b * mbps + pos / bs];
+            uint64_t base = offsets_f16[blk] * 2 + (uint64_t)(pos % bs) * row_bytes +
+                            (uint64_t)kvh * D * 2;
+            const uint16_t *kr = (const uint16_t *)(k_region + base);
+            const uint16_t *vr = (const uint16_t *)(v_region + base);
+            float dot = 0.0f;
+            if (dtype == 1) {
+                for (uint32_t d = 0; d < D; ++d) dot += qv[d] * u2f((uint32_t)kr[d] << 16);
+            } else {
+                for (uint32_t d = 0; d < D; ++d) dot += qv[d] * oracle_f16_to_f32(kr[d]);
+            }
+            dot *= scale;
+            float old_m = m;
+            m = fmaxf(m, dot);
+            float e = expf(dot - m);
+            float corr = expf(old_m - m);
+            s = s * corr + e;
+            if (dtype == 1) {
+                for (uint32_t d = 0; d < D; ++d) acc[d] = acc[d] * corr + e * u2f((uint32_t)vr[d] << 16);
+            } else {
+                for (uint32_t d = 0; d < D; ++d) acc[d] = acc[d] * corr + e * oracle_f16_to_f32(vr[d]);
+            }
+        }
+        float inv = 1.0f / s;
+        for (uint32_t d = 0; d < D; ++d) o[d] = acc[d] * inv;
+    }
+    return 0;
+}
+
+/* ======================================================================
+ * GEMM: Y = X W^T (the HF Linear product ref llama_transformer.rs:115-120
+ * intends; ref runtime.rs:17-41 delegates it to cuBLAS).
+ * ====================================================================== */
+void oracle_gemm_bf16_f64(const uint16_t *x, const uint16_t *w, double *y, uint32_t m,
+                          uint32_t n, uint32_t k) {
+    #pragma omp parallel for schedule(static)
+    for (long long i = 0; i < (long long)m; ++i) {
+        double *xr = (double *)malloc(k * sizeof(double));
+        for (uint32_t t = 0; t < k; ++t) xr[t] = oracle_bf16_to_f32(x[(size_t)i * k + t]);
+        for (uint32_t j = 0; j < n; ++j) {
+            const uint16_t *wr = w + (size_t)j * k;
+            double acc = 0.0;
+            for (uint32_t t = 0; t < k; ++t) acc += xr[t] * (double)oracle_bf16_to_f32(wr[t]);
+            y[(size_t)i * n + j] = acc;
+        }
+        free(xr);
+    }
+}

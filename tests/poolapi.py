@@ -1,0 +1,169 @@
+"""One interface over the oracle allocator and the product's pool ABI, so the
+same allocation scenarios run against both and their observable state can be
+compared after every operation."""
+from __future__ import annotations
+
+import oracle as O
+from lattice_amd.bindings import KcmmError, KcmmLibrary, make_config
+
+STAT_KEYS = ["blocks_in_use", "total_blocks", "total_physical_blocks", "free_physical_blocks",
+             "active_sequences", "num_layers", "blocks_per_superblock", "superblock_count",
+             "block_size", "max_blocks_per_seq", "block_bytes"]
+
+
+class OracleAdapter:
+    def __init__(self, *, block_size, num_layers, kv_heads, head_dim, max_batch, max_seq_len,
+                 dtype=O.F16, rollback=True):
+        self.p = O.OraclePool(block_size, num_layers, kv_heads, head_dim, max_batch, max_seq_len,
+                              dtype, rollback)
+
+    def alloc(self, n):
+        return self.p.alloc(n)
+
+    def free(self, ids):
+        self.p.release(ids)
+
+    def register(self, t):
+        return self.p.register(t)
+
+    def unregister(self, s):
+        self.p.unregister(s)
+
+    def append_block(self, s, b):
+        return self.p.append_block(s, b) == 0
+
+    def update_seq_len(self, s, n):
+        self.p.update_seq_len(s, n)
+
+    def block_table(self, s):
+        return self.p.block_table(s)
+
+    def block_offset(self, b):
+        return self.p.block_offset(b)
+
+    def offsets_f16(self):
+        return self.p.offsets_f16().tolist()
+
+    def valid(self):
+        return self.p.valid_flags().tolist()
+
+    def table_offsets(self, s):
+        return self.p.table_offsets(s)
+
+    def fork(self, s):
+        return self.p.fork(s)
+
+    def share_prefix(self, src, dst, n):
+        return self.p.share_prefix(src, dst, n)
+
+    def cow(self, s, logical):
+        rc, pair = self.p.cow(s, logical)
+        return rc, (pair if rc == 1 else None)
+
+    def refcount(self, b):
+        return self.p.refcount(b)
+
+    def stats(self):
+        st = self.p.stats()
+        return {k: st[k] for k in STAT_KEYS} | {"physical_idle_ratio": st["physical_idle_ratio"]}
+
+    def metrics(self):
+        return self.p.metrics()
+
+    def below(self, t):
+        return self.p.below_low_watermark(t)
+
+
+class ProductAdapter:
+    def __init__(self, lib: KcmmLibrary, *, block_size, num_layers, kv_heads, head_dim, max_batch,
+                 max_seq_len, dtype=0):
+        cfg = make_config(num_layers=num_layers, kv_heads=kv_heads, head_dim=head_dim,
+                          max_batch=max_batch, max_seq_len=max_seq_len, block_size=block_size)
+        self.pool = lib.create_pool(cfg, dtype)
+
+    def close(self):
+        self.pool.destroy()
+
+    def alloc(self, n):
+        try:
+            return self.pool.alloc_blocks(n)
+        except KcmmError:
+            return None
+
+    def free(self, ids):
+        self.pool.free_blocks(ids)
+
+    def register(self, t):
+        return self.pool.register_sequence(t)
+
+    def unregister(self, s):
+        self.pool.unregister_sequence(s)
+
+    def append_block(self, s, b):
+        try:
+            self.pool.append_block_to_sequence(s, b)
+            return True
+        except KcmmError:
+            return False
+
+    def update_seq_len(self, s, n):
+        self.pool.update_seq_len(s, n)
+
+    def block_table(self, s):
+        try:
+            return self.pool.block_table(s)
+        except KcmmError:
+            return None
+
+    def block_offset(self, b):
+        v = self.pool.block_va_offset(b)
+        return v if v != 0 else (0 if self._in_use(b) else None)
+
+    def _in_use(self, b):
+        flags = self.pool.all_block_valid_flags()
+        return b < len(flags) and flags[b] == 1
+
+    def offsets_f16(self):
+        return self.pool.all_block_offsets_f16() if self.pool.total_blocks() else []
+
+    def valid(self):
+        return self.pool.all_block_valid_flags() if self.pool.total_blocks() else []
+
+    def table_offsets(self, s):
+        try:
+            return self.pool.block_table_va_offsets(s)
+        except KcmmError:
+            return None
+
+    def fork(self, s):
+        try:
+            return self.pool.fork_sequence(s)
+        except KcmmError:
+            return None
+
+    def share_prefix(self, src, dst, n):
+        try:
+            return self.pool.share_prefix(src, dst, n)
+        except KcmmError:
+            return None
+
+    def cow(self, s, logical):
+        try:
+            pair = self.pool.cow_block_for_append(s, logical)
+        except KcmmError:
+            return -1, None
+        return (1, pair) if pair else (0, None)
+
+    def refcount(self, b):
+        return self.pool.refcount(b)
+
+    def stats(self):
+        st = self.pool.stats()
+        return {k: st[k] for k in STAT_KEYS} | {"physical_idle_ratio": st["physical_idle_ratio"]}
+
+    def metrics(self):
+        m = self.pool.metrics()
+        return {k: m[k] for k in ("ifr", "pme", "bu", "rfi")}
+
+    def below(self, t):
+        return bool(self.pool.lib.kcmm_below_low_watermark(self.pool.handle, t))

@@ -1,0 +1,193 @@
+"""Paged decode attention on the GPU through the C ABI vs the oracle.
+
+Tolerance (relative to the output's scale, max|got-ref| / max|ref|): bf16
+1e-2, fp8 KV 3e-2 (against the oracle on the same dequantized pages), f16
+1e-2 (BASELINE tolerances; f16 shares bf16's since outputs and P are 16-bit).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lattice_amd.bindings import KV_BF16, KV_F16, KV_FP8, memcpy_dtoh
+from lattice_amd.workload import build_decode_case
+
+pytestmark = pytest.mark.gpu
+
+TOL = {KV_BF16: 1e-2, KV_F16: 1e-2, KV_FP8: 3e-2}
+
+
+def oracle_out(case, layer=0, scale=None, regions=None):
+    g = case.geometry
+    scale = 1 / math.sqrt(case.head_dim) if scale is None else scale
+    kreg, vreg = regions if regions else (case.k_mirror[layer], case.v_mirror[layer])
+    return O.attn_decode_f64(case.dtype, case.q_bits, kreg, vreg, case.block_tables,
+                             case.seq_lens, case.offsets_f16, case.num_q_heads, case.kv_heads,
+                             case.head_dim, case.block_size, g["row_bytes"], g["data_bytes"],
+                             scale)
+
+
+def gpu_out(case):
+    bits = case.out_bits()
+    return O.decode(O.F16 if case.dtype == KV_F16 else O.BF16, bits).astype(np.float64)
+
+
+def rel_err(got, ref):
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def check(case, **kw):
+    import torch
+    case.dev["out"].fill_(float("nan"))
+    case.run_attention(**kw)
+    torch.cuda.synchronize()
+    got, ref = gpu_out(case), oracle_out(case, scale=kw.get("scale"))
+    err = rel_err(got, ref)
+    print(f"shape B={case.batch} Hq={case.num_q_heads} Hkv={case.kv_heads} D={case.head_dim} "
+          f"bs={case.block_size} dtype={case.dtype} max_len={case.seq_lens.max()} err={err:.3e}",
+          flush=True)
+    assert np.isfinite(got).all()
+    assert err <= TOL[case.dtype], err
+    zero = case.seq_lens <= 0
+    assert not got[zero].any()
+    return err
+
+
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_F16])
+def test_llama3_8b_shape_reduced_batch(gpu_lib, dtype):
+    rng = np.random.default_rng(100 + dtype)
+    ctx = rng.integers(512, 4097, size=8) + 1          # BASELINE configs[1], 8 of 64 seqs
+    case = build_decode_case(gpu_lib, batch=8, num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=dtype, seed=1)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_F16])
+def test_ragged_lengths_and_chunk_edges(gpu_lib, dtype):
+    ctx = [0, 1, 2, 15, 16, 17, 31, 32, 33, 63, 255, 256, 257, 511, 512, 513, 1024, 1025, -3]
+    case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=dtype, seed=2)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [
+    (8, 8, 64, 16),      # BASELINE configs[0] geometry (MHA)
+    (16, 8, 128, 16),
+    (32, 2, 128, 16),    # group 16 (largest MFMA path)
+    (8, 1, 256, 16),
+    (32, 8, 128, 32),    # block size not 16: runtime divide path
+    (12, 4, 64, 8),
+])
+def test_mfma_path_shapes(gpu_lib, hq, hkv, d, bs):
+    rng = np.random.default_rng(hq * d + bs)
+    ctx = rng.integers(1, 700, size=5)
+    case = build_decode_case(gpu_lib, batch=5, num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=bs, ctx_lens=ctx, dtype=KV_BF16, seed=3)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [(6, 4, 80, 8), (32, 1, 96, 16), (40, 8, 128, 16)])
+def test_generic_path_shapes(gpu_lib, hq, hkv, d, bs):
+    # head_dim not in {64,128,256}, Hq not a multiple of Hkv, or group > 16
+    ctx = [1, 40, 129, 0]
+    case = build_decode_case(gpu_lib, batch=4, num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=bs, ctx_lens=ctx, dtype=KV_F16, seed=4)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+def test_fp8_pages(gpu_lib):
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(1, 900, size=6)
+    case = build_decode_case(gpu_lib, batch=6, num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_FP8, seed=5)
+    try:
+        import torch
+        case.dev["out"].fill_(float("nan"))
+        case.run_attention(stream_ptr=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        err = rel_err(gpu_out(case), oracle_out(case))
+        print(f"fp8 err={err:.3e}", flush=True)
+        assert err <= TOL[KV_FP8]
+    finally:
+        case.pool.destroy()
+
+
+@pytest.mark.parametrize("dtype", [KV_F16, KV_BF16])
+def test_seq_len_one_returns_v_row_exactly(gpu_lib, dtype):
+    """ref non_default_stream_ffi_smoke.py:172-179,334-343 (q = 0, exact)."""
+    import torch
+    case = build_decode_case(gpu_lib, batch=3, num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=[1, 1, 1], dtype=dtype, seed=6)
+    try:
+        case.dev["q"].zero_()
+        case.run_attention(scale=1.0, stream_ptr=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        out = case.out_bits()
+        g = case.geometry
+        for b in range(3):
+            page = int(case.offsets_f16[case.block_tables[b, 0]]) * 2
+            v = case.v_mirror[0][page:page + g["row_bytes"]].view(np.uint16).reshape(8, 128)
+            for h in range(32):
+                assert np.array_equal(out[b, h], v[h * 8 // 32]), (b, h)
+    finally:
+        case.pool.destroy()
+
+
+def test_entry_point_variants_agree(gpu_lib):
+    import torch
+    ctx = [300, 5, 2000]
+    case = build_decode_case(gpu_lib, batch=3, num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_F16, seed=7)
+    try:
+        outs = []
+        s = torch.cuda.Stream()
+        for kw in [dict(), dict(stream_ptr=s.cuda_stream),
+                   dict(stream_ptr=s.cuda_stream, variant="current_context")]:
+            case.dev["out"].zero_()
+            torch.cuda.synchronize()
+            d = case.dev
+            case.pool.paged_attn_decode(
+                layer_idx=0, query_ptr=d["q"].data_ptr(), out_ptr=d["out"].data_ptr(),
+                block_tables_ptr=d["bt"].data_ptr(), seq_lens_ptr=d["sl"].data_ptr(),
+                block_offsets_f16_ptr=d["offs"].data_ptr(), batch=3, num_q_heads=32, kv_heads=8,
+                head_dim=128, block_size=16, max_blocks_per_seq=case.mbps, scale=0.088, **kw)
+            torch.cuda.synchronize()
+            outs.append(case.out_bits().copy())
+        assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    finally:
+        case.pool.destroy()
+
+
+def test_full_llama3_8b_decode_shape(gpu_lib):
+    """BASELINE configs[1] at full size (64 seqs, ctx U[512,4096] + 1): the
+    GPU result against the oracle run on the device regions read back."""
+    import torch
+    rng = np.random.default_rng(2024)
+    ctx = rng.integers(512, 4097, size=64) + 1
+    case = build_decode_case(gpu_lib, batch=64, num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=8,
+                             host_mirror=False)
+    try:
+        case.run_attention(stream_ptr=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        g = case.geometry
+        kreg = memcpy_dtoh(case.pool.va_k(0), g["mapped_bytes"])
+        vreg = memcpy_dtoh(case.pool.va_v(0), g["mapped_bytes"])
+        err = rel_err(gpu_out(case), oracle_out(case, regions=(kreg, vreg)))
+        print(f"full Cfg2 err={err:.3e}", flush=True)
+        assert err <= TOL[KV_BF16]
+    finally:
+        case.pool.destroy()

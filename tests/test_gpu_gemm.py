@@ -1,0 +1,55 @@
+"""Projection GEMM Y = X W^T (bf16, fp32 accumulate) on the GPU vs the
+oracle (fp64) on small shapes and vs a torch fp32 matmul at the Llama-3-8B
+decode shapes.  Tolerance: max|Y-ref| / max|ref| <= 1e-2 (bf16)."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_err(got, ref):
+    return float(np.abs(got - ref).max() / np.abs(ref).max())
+
+
+def run(gpu_lib, x, w):
+    import torch
+    m, k = x.shape
+    n = w.shape[0]
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.gemm_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k,
+                      torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 256), (17, 192, 512), (64, 256, 1024),
+                                   (100, 128, 768), (256, 320, 2048)])
+def test_vs_oracle(gpu_lib, m, n, k):
+    import torch
+    rng = np.random.default_rng(m + n + k)
+    xb = O.encode(O.BF16, rng.standard_normal((m, k)))
+    wb = O.encode(O.BF16, rng.standard_normal((n, k)) * 0.02)
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    w = torch.from_numpy(wb.view(np.int16)).view(torch.bfloat16).cuda()
+    y = run(gpu_lib, x, w)
+    got = O.decode(O.BF16, y.cpu().view(torch.int16).numpy().view(np.uint16))
+    err = rel_err(got, O.gemm_bf16_f64(xb, wb))
+    print(f"gemm {m}x{n}x{k} err={err:.3e}", flush=True)
+    assert err <= 1e-2
+
+
+@pytest.mark.parametrize("m", [64, 256])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)])
+def test_llama3_8b_projections(gpu_lib, m, n, k):
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m * 7 + n + k)
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    y = run(gpu_lib, x, w).float()
+    ref = x.float() @ w.float().t()
+    err = float((y - ref).abs().max() / ref.abs().max())
+    print(f"gemm {m}x{n}x{k} err={err:.3e}", flush=True)
+    assert err <= 1e-2

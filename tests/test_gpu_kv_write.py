@@ -1,0 +1,182 @@
+"""KV append on the GPU through the C ABI: the reference's KAT (ref
+scripts/kcmm/kv_write_ffi_smoke.py) replayed on libkcmm.so, region bytes
+compared bit-exactly with the oracle after every step; then randomized
+appends (16-bit and fp8 pages) against the oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+from lattice_amd.bindings import (KV_BF16, KV_F16, KV_FP8, make_config, memcpy_dtoh,
+                                  memset_d8)
+from tests import kat_kv_write as K
+
+pytestmark = pytest.mark.gpu
+
+SB = 2 * 1024 * 1024
+
+
+def region_bytes(pool, layer=0):
+    n = pool.stats()["superblock_count"] * SB
+    return memcpy_dtoh(pool.va_k(layer), n), memcpy_dtoh(pool.va_v(layer), n)
+
+
+def zero_regions(pool):
+    n = pool.stats()["superblock_count"] * SB
+    for l in range(pool.stats()["num_layers"]):
+        memset_d8(pool.va_k(l), 0, n)
+        memset_d8(pool.va_v(l), 0, n)
+
+
+def t16(bits, torch):
+    return torch.from_numpy(bits.view(np.int16)).view(torch.float16).cuda()
+
+
+def test_kat_bit_exact_vs_oracle(gpu_lib):
+    import torch
+    ref = K.run_oracle()
+    c = K.KAT["config"]
+    bs, step = c["block_size"], c["kv_heads"] * c["head_dim"]
+    pool = gpu_lib.create_pool(make_config(block_size=bs, max_blocks=c["max_blocks"],
+                                           num_layers=c["num_layers"], kv_heads=c["kv_heads"],
+                                           head_dim=c["head_dim"], max_batch=c["max_batch"],
+                                           max_seq_len=c["max_seq_len"]), KV_F16)
+    try:
+        ids = pool.alloc_blocks(K.KAT["setup"]["alloc"])
+        inactive = ids[K.KAT["setup"]["free_index"]]
+        pool.free_blocks([inactive])
+        blocks = ids[: K.KAT["setup"]["register_first"]]
+        seq = pool.register_sequence(blocks)
+        assert (blocks, inactive, seq) == (ref["blocks"], ref["inactive"], ref["seq"])
+        assert pool.block_table(seq, 4) == blocks
+        zero_regions(pool)
+        stream = torch.cuda.current_stream()
+
+        pw = K.KAT["position_write"]
+        k, v = t16(K.f16_rows(2, step, pw["k_offset"]), torch), t16(K.f16_rows(2, step, pw["v_offset"]), torch)
+        torch.cuda.synchronize()
+        pool.append_kv_step(0, [seq, seq], pw["positions"], k.data_ptr(), v.data_ptr())
+        pool.synchronize()
+        got = region_bytes(pool)
+        assert np.array_equal(got[0], ref["steps"][0][1]) and np.array_equal(got[1], ref["steps"][0][2])
+
+        hs = K.KAT["host_slot_write"]
+        k, v = t16(K.f16_rows(3, step, hs["k_offset"]), torch), t16(K.f16_rows(3, step, hs["v_offset"]), torch)
+        pool.append_kv_slots(0, K.resolve_slots(hs["slots"], blocks, bs), k.data_ptr(), v.data_ptr(),
+                             stream_ptr=stream.cuda_stream)
+        stream.synchronize()
+        got = region_bytes(pool)
+        assert np.array_equal(got[0], ref["steps"][1][1]) and np.array_equal(got[1], ref["steps"][1][2])
+
+        ds = K.KAT["device_slot_write"]
+        k, v = t16(K.f16_rows(3, step, ds["k_offset"]), torch), t16(K.f16_rows(3, step, ds["v_offset"]), torch)
+        offs = pool.all_block_offsets_f16()
+        valid = pool.all_block_valid_flags()
+        assert offs == ref["offsets"] and valid == ref["valid"]
+        slots_t = torch.tensor(K.resolve_slots(ds["slots"], blocks, bs), dtype=torch.int64, device="cuda")
+        offs_t = torch.tensor(offs, dtype=torch.int64, device="cuda")
+        valid_t = torch.tensor(valid, dtype=torch.uint8, device="cuda")
+        status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        common = dict(layer_idx=0, block_offsets_f16_ptr=offs_t.data_ptr(),
+                      valid_blocks_ptr=valid_t.data_ptr(), block_offsets_f16_len=len(offs),
+                      stream_ptr=stream.cuda_stream)
+        pool.append_kv_device_slots_on_stream(slot_mapping_ptr=slots_t.data_ptr(), batch=3,
+                                              k_src_ptr=k.data_ptr(), v_src_ptr=v.data_ptr(),
+                                              status_ptr=status.data_ptr(), **common)
+        stream.synchronize()
+        assert int(status.item()) == ref["steps"][2][3] == 0
+        got = region_bytes(pool)
+        assert np.array_equal(got[0], ref["steps"][2][1]) and np.array_equal(got[1], ref["steps"][2][2])
+
+        # bad slots (ref kv_write_ffi_smoke.py:423-505)
+        invalid_slot = c["max_blocks"] * bs
+        with pytest.raises(Exception):
+            pool.append_kv_slots(0, [invalid_slot], k[:1].data_ptr(), v[:1].data_ptr(),
+                                 stream_ptr=stream.cuda_stream)
+        for slot, expect in ((inactive * bs, ref["inactive_status"]), (invalid_slot, ref["invalid_status"])):
+            st = torch.zeros(1, dtype=torch.int32, device="cuda")
+            sl = torch.tensor([slot], dtype=torch.int64, device="cuda")
+            pool.append_kv_device_slots_on_stream(slot_mapping_ptr=sl.data_ptr(), batch=1,
+                                                  k_src_ptr=k.data_ptr(), v_src_ptr=v.data_ptr(),
+                                                  status_ptr=st.data_ptr(), **common)
+            stream.synchronize()
+            assert int(st.item()) == expect
+        got = region_bytes(pool)
+        assert np.array_equal(got[0], ref["final"][0]) and np.array_equal(got[1], ref["final"][1])
+        pool.unregister_sequence(seq)
+        assert pool.stats()["blocks_in_use"] == ref["blocks_in_use_after"] == 0
+    finally:
+        pool.destroy()
+
+
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_FP8])
+def test_random_decode_appends_vs_oracle(gpu_lib, dtype):
+    """Many decode steps of 1 token per sequence (device slots) into shuffled
+    pages; region bytes bit-exact with the oracle after the run.  For fp8 the
+    rows grow in magnitude now and then, exercising page re-scaling."""
+    import torch
+    rng = np.random.default_rng(10 + dtype)
+    B, hk, d, bs, L = 6, 8, 128, 16, 2
+    pool = gpu_lib.create_pool(make_config(num_layers=L, kv_heads=hk, head_dim=d, max_batch=B,
+                                           max_seq_len=80), dtype)
+    opool = O.OraclePool(bs, L, hk, d, B, 80, dtype)
+    try:
+        n_pages = 5
+        ids = pool.alloc_blocks(B * n_pages)
+        assert ids == opool.alloc(B * n_pages)
+        perm = rng.permutation(ids)
+        tables = [perm[i * n_pages:(i + 1) * n_pages].tolist() for i in range(B)]
+        zero_regions(pool)
+        nb = pool.stats()["superblock_count"] * SB
+        oreg = [[np.zeros(nb, np.uint8), np.zeros(nb, np.uint8)] for _ in range(L)]
+        offs = pool.all_block_offsets_f16()
+        offs_t = torch.tensor(offs, dtype=torch.int64, device="cuda")
+        g_row = hk * d * (1 if dtype == KV_FP8 else 2)
+        data_bytes = g_row * bs
+        stream = torch.cuda.current_stream()
+        for t in range(70):
+            pos = np.full(B, t)
+            slots = [tables[b][t // bs] * bs + t % bs for b in range(B)]
+            for layer in range(L):
+                mag = 4.0 if (dtype == KV_FP8 and rng.random() < 0.1) else 1.0
+                x = (rng.standard_normal((2, B, hk * d)) * mag).astype(np.float32)
+                bits = O.encode(O.BF16, x)
+                k = torch.from_numpy(bits[0].view(np.int16)).view(torch.bfloat16).cuda()
+                v = torch.from_numpy(bits[1].view(np.int16)).view(torch.bfloat16).cuda()
+                sl = torch.tensor(slots, dtype=torch.int64, device="cuda")
+                pool.append_kv_device_slots_on_stream(
+                    layer_idx=layer, slot_mapping_ptr=sl.data_ptr(),
+                    block_offsets_f16_ptr=offs_t.data_ptr(), valid_blocks_ptr=0,
+                    block_offsets_f16_len=len(offs), batch=B, k_src_ptr=k.data_ptr(),
+                    v_src_ptr=v.data_ptr(), status_ptr=0, stream_ptr=stream.cuda_stream)
+                O.kv_write_device_slots(dtype, oreg[layer][0], oreg[layer][1], bits[0], bits[1],
+                                        slots, np.asarray(offs, np.uint64), None, bs, hk, d,
+                                        g_row, data_bytes)
+                stream.synchronize()   # keep sources alive until the kernel ran
+        for layer in range(L):
+            gk, gv = region_bytes(pool, layer)
+            assert np.array_equal(gk, oreg[layer][0]), f"K layer {layer}"
+            assert np.array_equal(gv, oreg[layer][1]), f"V layer {layer}"
+    finally:
+        pool.destroy()
+
+
+def test_host_variants_validate_before_writing(gpu_lib):
+    """All rows are checked before any is enqueued (the reference applies
+    the rows before a bad one, ref ffi.rs:1325-1343 -- not replicated)."""
+    import torch
+    pool = gpu_lib.create_pool(make_config(num_layers=1, kv_heads=2, head_dim=64, max_batch=2,
+                                           max_seq_len=64), KV_BF16)
+    try:
+        ids = pool.alloc_blocks(2)
+        seq = pool.register_sequence(ids[:1])
+        zero_regions(pool)
+        k = torch.ones((2, 128), dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(Exception):
+            pool.append_kv_step(0, [seq, seq], [0, 16], k.data_ptr(), k.data_ptr())  # 2nd row: no block
+        with pytest.raises(Exception):
+            pool.append_kv_slots(0, [ids[0] * 16, 999 * 16], k.data_ptr(), k.data_ptr())
+        pool.synchronize()
+        kr, vr = region_bytes(pool)
+        assert not kr.any() and not vr.any()
+    finally:
+        pool.destroy()
