@@ -37,9 +37,10 @@ kcmm_pool_t *kcmm_pool_create_typed(const kcmm_config_t *config, int32_t kv_dtyp
 /** Pool element type (kcmm_kv_dtype_t), or -1 for NULL. */
 int32_t kcmm_get_kv_dtype(kcmm_pool_t *pool);
 
-/** 0 = pages backed by HIP VMM 2 MiB superblocks mapped on demand (the
- *  reference design, ref cuda_vmm.rs), 1 = one hipMalloc per region (used
- *  when VMM is unavailable or KCMM_BACKING=flat), -1 for NULL. */
+/** 1 = one hipMalloc per region holding the full capacity (default),
+ *  0 = HIP VMM 2 MiB superblocks mapped on demand (the reference design, ref
+ *  cuda_vmm.rs; selected with KCMM_BACKING=vmm), -1 for NULL.  Block ids and
+ *  offsets are identical for both. */
 int32_t kcmm_get_backing_kind(kcmm_pool_t *pool);
 
 /** Why the last kcmm_pool_create* on this thread returned NULL (the reference
@@ -120,7 +121,7 @@ int kcmm_copy_blocks_device_on_stream(kcmm_pool_t *pool, uint64_t pairs_ptr,
  *  ref llama_transformer.rs:115-120), bf16 inputs and output, fp32
  *  accumulation on MFMA.  Replaces the cuBLAS call of ref runtime.rs:17-41
  *  (whose column-major arguments equal this product only at m == 1).
- *  Enqueue only; requires k % 64 == 0 and n % 64 == 0. */
+ *  Enqueue only; requires k % 256 == 0 and n % 64 == 0. */
 int kcmm_gemm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
                              uint32_t m, uint32_t n, uint32_t k,
                              uint64_t stream_ptr);

@@ -2,6 +2,10 @@
 // error channel and return conventions follow the reference's Rust FFI
 // (ref src/kcmm/ffi.rs); bookkeeping is PoolCore, device work goes through
 // device_api.hpp.  This file has no HIP dependency.
+#include <execinfo.h>
+#include <unistd.h>
+
+#include <csignal>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -30,6 +34,28 @@ struct kcmm_pool_t {
 namespace {
 
 thread_local std::string g_create_error;
+
+// KCMM_CRASH_TRACE=1: print a native backtrace on SIGSEGV/SIGBUS before the
+// default action, to locate host-side crashes inside the library.
+void crash_trace_handler(int sig) {
+    void* frames[64];
+    const int n = backtrace(frames, 64);
+    const char msg[] = "\n[kcmm] fatal signal; native backtrace:\n";
+    (void)!write(2, msg, sizeof(msg) - 1);
+    backtrace_symbols_fd(frames, n, 2);
+    signal(sig, SIG_DFL);
+    raise(sig);
+}
+
+struct CrashTraceInstaller {
+    CrashTraceInstaller() {
+        const char* e = std::getenv("KCMM_CRASH_TRACE");
+        if (e != nullptr && e[0] == '1') {
+            signal(SIGSEGV, crash_trace_handler);
+            signal(SIGBUS, crash_trace_handler);
+        }
+    }
+} g_crash_trace_installer;
 
 size_t write_c_str(char* buf, size_t max_len, const std::string& s) {
     // ref ffi.rs:412-422: copy at most max_len-1 bytes and terminate.

@@ -1,12 +1,16 @@
 // Device page backing for a KCMM pool on MI355X.
 //
-// HipVmmBacking restates the reference's CUDA-VMM design (ref
-// src/cache/cuda_vmm.rs:6-234, pool.rs:211-221,287-322) with HIP VMM: each of
-// the 2*L regions is one virtual-address reservation, and a 2 MiB physical
-// superblock is created and mapped at byte sb*2MiB of every region when the
-// allocator grows.  HipFlatBacking backs each region with one hipMalloc of
-// the full capacity; it is used when the device reports no VMM support or
-// KCMM_BACKING=flat, and yields the same block ids and offsets.
+// Two backings with identical block ids and offsets:
+//  * HipFlatBacking (default): each of the 2*L regions is one hipMalloc of
+//    the pool's full capacity.  MI355X carries 288 GB of HBM per GPU, so the
+//    configured capacity is committed up front and growth costs nothing.
+//  * HipVmmBacking (KCMM_BACKING=vmm): the reference's CUDA-VMM design (ref
+//    src/cache/cuda_vmm.rs:6-234, pool.rs:211-221,287-322) on HIP VMM -- one
+//    virtual-address reservation per region, and a 2 MiB physical superblock
+//    created and mapped at byte sb*2MiB of every region when the allocator
+//    grows.  Opt-in: with the HIP runtime PyTorch-ROCm 7.0 ships, a process
+//    that created and destroyed a dozen VMM pools saw hipMemSetAccess fail
+//    with "invalid argument" and a crash inside pool teardown.
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -130,14 +134,16 @@ namespace dev {
 
 std::unique_ptr<PageBacking> make_backing(int device, std::string* err) {
     const char* env = std::getenv("KCMM_BACKING");
-    if (env != nullptr && std::strcmp(env, "flat") == 0)
-        return std::unique_ptr<PageBacking>(new HipFlatBacking());
-    int vmm = 0;
-    if (hipDeviceGetAttribute(&vmm, hipDeviceAttributeVirtualMemoryManagementSupported,
-                              device) != hipSuccess)
-        vmm = 0;
-    if (vmm) return std::unique_ptr<PageBacking>(new HipVmmBacking(device));
-    (void)err;
+    if (env != nullptr && std::strcmp(env, "vmm") == 0) {
+        int vmm = 0;
+        if (hipDeviceGetAttribute(&vmm, hipDeviceAttributeVirtualMemoryManagementSupported,
+                                  device) != hipSuccess || !vmm) {
+            (void)hipGetLastError();
+            *err = "KCMM_BACKING=vmm but the device reports no HIP VMM support";
+            return nullptr;
+        }
+        return std::unique_ptr<PageBacking>(new HipVmmBacking(device));
+    }
     return std::unique_ptr<PageBacking>(new HipFlatBacking());
 }
 

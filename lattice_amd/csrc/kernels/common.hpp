@@ -73,6 +73,7 @@ __device__ __forceinline__ float fp8e4m3_to_f32(uint32_t b) {
     do {                                                                        \
         hipError_t e_ = (expr);                                                 \
         if (e_ != hipSuccess) {                                                 \
+            (void)hipGetLastError(); /* do not leave the error for the caller */ \
             if (errp) *(errp) = std::string(#expr) + ": " + hipGetErrorString(e_); \
             return false;                                                       \
         }                                                                       \

@@ -96,7 +96,7 @@ class DecodeCase:
             stream_ptr=stream_ptr)
 
     def out_bits(self) -> np.ndarray:
-        return self.dev["out"].cpu().numpy().view(np.uint16)
+        return self.dev["out"].cpu().view(torch.int16).numpy().view(np.uint16)
 
 
 def _fill_pages_host(case: DecodeCase, rng: np.random.Generator, layer_tokens) -> None:
