@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--attn-only", action="store_true", help="time attention (+append) only")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
     return ap.parse_args()
 
 
@@ -165,6 +167,14 @@ def main():
         "down": lambda l: gemm("down", l),
     }
 
+    if args.calib_copy:
+        src = torch.empty(128 << 20, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        dst.copy_(src)                               # 256 MiB read + 256 MiB written
+        torch.cuda.synchronize()
+        del src, dst
     for i in range(args.warmup):
         for n in names:
             calls[n](i % args.layers)

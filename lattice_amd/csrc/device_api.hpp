@@ -19,9 +19,10 @@ std::unique_ptr<PageBacking> make_backing(int device, std::string* err);
 
 bool set_device(int device, std::string* err);
 
-// Per-(device, stream, slot) device scratch for split-K partials; grown on
-// demand (slot 0: decode attention, slot 1: GEMM).
-bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, std::string* err);
+// Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
+// attention partials, 1: GEMM partials, 2: decode attention counters).
+bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
+                      std::string* err);
 bool synchronize_device(int device, std::string* err);
 
 // Paged decode attention over one layer's K/V regions.

@@ -17,8 +17,9 @@
 //    softmax in the log2 domain with cross-lane max by lane shuffles;
 //  * O^T += V^T P^T on the same MFMA: V goes through wave-private LDS to be
 //    read transposed; P^T is already in B-operand layout in registers;
-//  * waves of a workgroup merge in LDS; chunks of one (b, g) merge in a
-//    second kernel by log-sum-exp (split-K over long contexts).
+//  * waves of a workgroup merge in LDS; the chunks of one (b, g) merge by
+//    log-sum-exp in whichever workgroup finishes last (split-K over long
+//    contexts in a single launch).
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -39,6 +40,7 @@ struct AttnParams {
     const uint64_t* offsets_f16;
     float* part_acc;        // [B][Hkv][max_chunks][G][D]
     float* part_ml;         // [B][Hkv][max_chunks][G][2]
+    int* counters;          // [B][Hkv] chunk arrivals (zero between launches)
     int batch, num_q_heads, kv_heads, group, block_size, mbps, max_chunks;
     int row_bytes, data_bytes;
     float scale_log2;       // scale * log2(e)
@@ -82,15 +84,123 @@ __device__ __forceinline__ uint64_t token_offset(const AttnParams& p, int b, int
 
 constexpr int kPad = 4;  // LDS row padding (elements): keeps transposed reads conflict-free
 
+// One 32-token tile: 2 halves of 16 tokens, KC 16-byte fragments per lane each.
+template <int KC>
+struct Tile {
+    u32x4 k[2][KC];
+    u32x4 v[2][KC];
+};
+
+template <int KC>
+__device__ __forceinline__ void load_tile(Tile<KC>& t, const uint8_t* k_base,
+                                          const uint8_t* v_base, const uint64_t off[2],
+                                          int lg) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint8_t* kr = k_base + off[h] + lg * 16;
+        const uint8_t* vr = v_base + off[h] + lg * 16;
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            t.k[h][kc] = *reinterpret_cast<const u32x4*>(kr + kc * 64);
+            t.v[h][kc] = *reinterpret_cast<const u32x4*>(vr + kc * 64);
+        }
+    }
+}
+
+// Online-softmax update of one tile (see the file comment for the layouts).
+template <int DT, int D>
+__device__ __forceinline__ void compute_tile(const Tile<D / 32>& t, const u32x4* qf, int tbase,
+                                             int L, float scale_log2, float& m_run,
+                                             float& l_run, f32x4* acc, uint16_t* vl, int ln,
+                                             int lg) {
+    constexpr int KC = D / 32;
+    constexpr int DB = D / 16;
+    constexpr int ROW = D + kPad;
+    f32x4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        s[h] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) s[h] = mfma16x16x32<DT>(t.k[h][kc], qf[kc], s[h]);
+    }
+    float sv[8];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = tbase + h * 16 + lg * 4 + r;
+            const float x = tok < L ? s[h][r] * scale_log2 : -INFINITY;
+            sv[h * 4 + r] = x;
+            mt = fmaxf(mt, x);
+        }
+    }
+    mt = wave_max_across_groups(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+    float pv[8];
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_new);
+        psum += pv[i];
+    }
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int i = 0; i < DB; ++i) acc[i] *= corr;
+
+    // P^T as the B operand: k-slot (lg, i) = token (i<4 ? 4lg+i : 16+4lg+i-4).
+    u32x4 pf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        pf[i] = f32_to_elem<DT>(pv[2 * i]) | (f32_to_elem<DT>(pv[2 * i + 1]) << 16);
+
+    // V rows into wave-private LDS (row = token in tile), then V^T reads.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            uint16_t* dst = vl + (h * 16 + ln) * ROW + kc * 32 + lg * 8;
+            reinterpret_cast<u32x2*>(dst)[0] = u32x2{t.v[h][kc][0], t.v[h][kc][1]};
+            reinterpret_cast<u32x2*>(dst)[1] = u32x2{t.v[h][kc][2], t.v[h][kc][3]};
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        const uint16_t* col = vl + db * 16 + ln;
+        u32x4 va;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t0 = (2 * i < 4) ? 4 * lg + 2 * i : 16 + 4 * lg + 2 * i - 4;
+            const uint32_t lo = col[t0 * ROW];
+            const uint32_t hi = col[(t0 + 1) * ROW];
+            va[i] = lo | (hi << 16);
+        }
+        acc[db] = mfma16x16x32<DT>(va, pf, acc[db]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// Workgroup = WAVES wavefronts on one (sequence b, kv head, chunk of CHUNK
+// tokens); wave w owns tiles [w*TPW, (w+1)*TPW) of the chunk.  Chunks of a
+// sequence longer than CHUNK write fp32 partials (unnormalised output, max,
+// denominator); the last workgroup of that (b, kv head) to finish -- found
+// with a device-scope counter -- merges them by log-sum-exp and resets the
+// counter, so one launch does split-K end to end.
 template <int DT, int D, int BS, int WAVES, int TPW>
 __global__ __launch_bounds__(WAVES * 64) void attn_decode_mfma(AttnParams p) {
-    constexpr int KC = D / 32;     // 32-wide k chunks of the head dimension
-    constexpr int DB = D / 16;     // 16-wide output blocks
+    constexpr int KC = D / 32;
+    constexpr int DB = D / 16;
     constexpr int CHUNK = WAVES * TPW * 32;
-    constexpr int ROW = D + kPad;  // LDS row stride in elements
+    constexpr int ROW = D + kPad;
     constexpr int HEAD_BYTES = D * 2;
+    constexpr int LDS_ELEMS = WAVES * 32 * ROW;
+    static_assert((WAVES * D * 16 + WAVES * 32) * 4 <= LDS_ELEMS * 2, "merge area exceeds LDS");
 
-    __shared__ __attribute__((aligned(16))) uint16_t lds[WAVES * 32 * ROW];
+    __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
+    __shared__ int last_flag;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -103,7 +213,8 @@ __global__ __launch_bounds__(WAVES * 64) void attn_decode_mfma(AttnParams p) {
     const int b = bid % p.batch;
     const int chunk = bid / p.batch;
     const int G = p.group;
-    const int L = min(p.seq_lens[b], p.mbps * (BS > 0 ? BS : p.block_size));
+    const int bs = BS > 0 ? BS : p.block_size;
+    const int L = min(p.seq_lens[b], p.mbps * bs);
 
     if (L <= 0) {
         if (chunk == 0) {
@@ -115,6 +226,20 @@ __global__ __launch_bounds__(WAVES * 64) void attn_decode_mfma(AttnParams p) {
     }
     const int n_chunks = (L + CHUNK - 1) / CHUNK;
     if (chunk >= n_chunks) return;
+
+    const int tok0 = chunk * CHUNK + wave * TPW * 32;
+    const int ntiles = max(0, min(TPW, (L - tok0 + 31) / 32));
+
+    // Page addresses of every tile this wave will read, fetched up front so
+    // the dependent table -> offset -> data loads are not paid per tile.
+    uint64_t toff[TPW][2];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int pos = min(tok0 + t * 32 + h * 16 + ln, L - 1);
+            toff[t][h] = token_offset<BS>(p, b, kvh, pos, HEAD_BYTES);
+        }
 
     // Q^T as the B operand: lane (head ln, group lg) holds Q[ln][kc*32+8lg .. +8].
     u32x4 qf[KC];
@@ -134,98 +259,25 @@ __global__ __launch_bounds__(WAVES * 64) void attn_decode_mfma(AttnParams p) {
     f32x4 acc[DB];
 #pragma unroll
     for (int i = 0; i < DB; ++i) acc[i] = f32x4{0, 0, 0, 0};
-
     uint16_t* vl = lds + wave * 32 * ROW;
-    const int tok0 = chunk * CHUNK + wave * TPW * 32;
 
-    for (int t = 0; t < TPW; ++t) {
-        const int tbase = tok0 + t * 32;
-        if (tbase >= L) break;  // wave-uniform
-
-        // Each lane fetches token tbase + h*16 + ln (clamped into [0, L)).
-        u32x4 kf[2][KC], vf[2][KC];
+    // Two tiles in flight: the loads of tile t+1 are issued before tile t is
+    // consumed.
+    Tile<KC> ta, tb;
+    if (ntiles > 0) load_tile<KC>(ta, p.k_base, p.v_base, toff[0], lg);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int pos = min(tbase + h * 16 + ln, L - 1);
-            const uint64_t off = token_offset<BS>(p, b, kvh, pos, HEAD_BYTES);
-            const uint8_t* kr = p.k_base + off + lg * 16;
-            const uint8_t* vr = p.v_base + off + lg * 16;
-#pragma unroll
-            for (int kc = 0; kc < KC; ++kc) {
-                kf[h][kc] = *reinterpret_cast<const u32x4*>(kr + kc * 64);
-                vf[h][kc] = *reinterpret_cast<const u32x4*>(vr + kc * 64);
-            }
+    for (int t = 0; t < TPW; t += 2) {
+        if (t < ntiles) {
+            if (t + 1 < ntiles) load_tile<KC>(tb, p.k_base, p.v_base, toff[t + 1], lg);
+            compute_tile<DT, D>(ta, qf, tok0 + t * 32, L, p.scale_log2, m_run, l_run, acc, vl, ln,
+                                lg);
         }
-
-        // S^T: lane (head ln, group lg) gets rows 4lg..4lg+3 (tokens) of each half.
-        f32x4 s[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            s[h] = f32x4{0, 0, 0, 0};
-#pragma unroll
-            for (int kc = 0; kc < KC; ++kc) s[h] = mfma16x16x32<DT>(kf[h][kc], qf[kc], s[h]);
+        if (t + 1 < ntiles) {
+            if (t + 2 < ntiles && t + 2 < TPW)
+                load_tile<KC>(ta, p.k_base, p.v_base, toff[(t + 2) % TPW], lg);
+            compute_tile<DT, D>(tb, qf, tok0 + (t + 1) * 32, L, p.scale_log2, m_run, l_run, acc,
+                                vl, ln, lg);
         }
-
-        float sv[8];
-        float mt = -INFINITY;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = tbase + h * 16 + lg * 4 + r;
-                const float x = tok < L ? s[h][r] * p.scale_log2 : -INFINITY;
-                sv[h * 4 + r] = x;
-                mt = fmaxf(mt, x);
-            }
-        }
-        mt = wave_max_across_groups(mt);
-        const float m_new = fmaxf(m_run, mt);
-        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-        float pv[8];
-        float psum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_new);
-            psum += pv[i];
-        }
-        l_run = l_run * corr + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int i = 0; i < DB; ++i) acc[i] *= corr;
-
-        // P^T as the B operand: k-slot (lg, i) = token (i<4 ? 4lg+i : 16+4lg+i-4).
-        u32x4 pf;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            pf[i] = f32_to_elem<DT>(pv[2 * i]) | (f32_to_elem<DT>(pv[2 * i + 1]) << 16);
-
-        // V rows into wave-private LDS: row = token in tile, row-major dims.
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int kc = 0; kc < KC; ++kc) {
-                uint16_t* dst = vl + (h * 16 + ln) * ROW + kc * 32 + lg * 8;
-                reinterpret_cast<u32x2*>(dst)[0] = u32x2{vf[h][kc][0], vf[h][kc][1]};
-                reinterpret_cast<u32x2*>(dst)[1] = u32x2{vf[h][kc][2], vf[h][kc][3]};
-            }
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-
-        // V^T as the A operand: lane (dim ln, group lg), k-slot i -> token as above.
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            const uint16_t* col = vl + db * 16 + ln;
-            u32x4 va;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t0 = (2 * i < 4) ? 4 * lg + 2 * i : 16 + 4 * lg + 2 * i - 4;
-                const uint32_t lo = col[t0 * ROW];
-                const uint32_t hi = col[(t0 + 1) * ROW];
-                va[i] = lo | (hi << 16);
-            }
-            acc[db] = mfma16x16x32<DT>(va, pf, acc[db]);
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 
     l_run = wave_sum_across_groups(l_run);
@@ -244,7 +296,9 @@ __global__ __launch_bounds__(WAVES * 64) void attn_decode_mfma(AttnParams p) {
     }
     __syncthreads();
 
-    const bool single = (n_chunks == 1);
+    uint16_t* out_bh = reinterpret_cast<uint16_t*>(p.out) +
+                       (static_cast<size_t>(b) * p.num_q_heads + kvh * G) * D;
+    const size_t unit0 = (static_cast<size_t>(b) * p.kv_heads + kvh) * p.max_chunks;
     for (int i = threadIdx.x; i < G * D; i += WAVES * 64) {
         const int j = i / D;
         const int d = i - j * D;
@@ -259,55 +313,56 @@ __global__ __launch_bounds__(WAVES * 64) void attn_decode_mfma(AttnParams p) {
             lsum += wgt * mrg_ml[(w * 16 + j) * 2 + 1];
             o += wgt * mrg[(w * D + d) * 16 + j];
         }
-        if (single) {
-            uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) +
-                            (static_cast<size_t>(b) * p.num_q_heads + kvh * G + j) * D + d;
-            *dst = static_cast<uint16_t>(f32_to_elem<DT>(o / lsum));
+        if (n_chunks == 1) {
+            out_bh[i] = static_cast<uint16_t>(f32_to_elem<DT>(o / lsum));
         } else {
-            const size_t unit = (static_cast<size_t>(b) * p.kv_heads + kvh) * p.max_chunks + chunk;
-            p.part_acc[(unit * G + j) * D + d] = o;
+            // Agent-scope stores write through to the device coherence point,
+            // so the merging workgroup (possibly on another XCD) sees them
+            // without a whole-L2 write-back.
+            const size_t u = (unit0 + chunk) * G + j;
+            __hip_atomic_store(&p.part_acc[u * D + d], o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (d == 0) {
-                p.part_ml[(unit * G + j) * 2 + 0] = M;
-                p.part_ml[(unit * G + j) * 2 + 1] = lsum;
+                __hip_atomic_store(&p.part_ml[u * 2 + 0], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&p.part_ml[u * 2 + 1], lsum, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
-}
+    if (n_chunks == 1) return;
 
-// Log-sum-exp merge of the chunk partials of every (b, query head) whose
-// sequence spans more than one chunk.  One wavefront per (b, head).
-template <int DT, int D>
-__global__ __launch_bounds__(64) void attn_decode_merge(AttnParams p, int chunk_tokens) {
-    const int bh = blockIdx.x;
-    const int b = bh / p.num_q_heads;
-    const int h = bh - b * p.num_q_heads;
-    const int L = min(p.seq_lens[b], p.mbps * p.block_size);
-    if (L <= 0) return;
-    const int n_chunks = (L + chunk_tokens - 1) / chunk_tokens;
-    if (n_chunks <= 1) return;
-    const int kvh = h / p.group;
-    const int j = h - kvh * p.group;
-    const size_t unit0 = (static_cast<size_t>(b) * p.kv_heads + kvh) * p.max_chunks;
-    float M = -INFINITY;
-    for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, p.part_ml[((unit0 + c) * p.group + j) * 2]);
-    constexpr int PER = D / 64;
-    float o[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) o[i] = 0.0f;
-    float lsum = 0.0f;
-    for (int c = 0; c < n_chunks; ++c) {
-        const size_t base = (unit0 + c) * p.group + j;
-        const float wgt = __builtin_amdgcn_exp2f(p.part_ml[base * 2] - M);
-        lsum += wgt * p.part_ml[base * 2 + 1];
-#pragma unroll
-        for (int i = 0; i < PER; ++i) o[i] += wgt * p.part_acc[base * D + threadIdx.x + 64 * i];
+    // ---- split-K: the last chunk of (b, kv head) to arrive merges ----
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // partial stores acknowledged
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(&p.counters[b * p.kv_heads + kvh], 1,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = (prev == n_chunks - 1);
     }
-    uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) +
-                    (static_cast<size_t>(b) * p.num_q_heads + h) * D;
-    const float inv = 1.0f / lsum;
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-        dst[threadIdx.x + 64 * i] = static_cast<uint16_t>(f32_to_elem<DT>(o[i] * inv));
+    __syncthreads();
+    if (!last_flag) return;
+    for (int i = threadIdx.x; i < G * D; i += WAVES * 64) {
+        const int j = i / D;
+        const int d = i - j * D;
+        float M = -INFINITY;
+        for (int c = 0; c < n_chunks; ++c)
+            M = fmaxf(M, __hip_atomic_load(&p.part_ml[((unit0 + c) * G + j) * 2], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+        float lsum = 0.0f, o = 0.0f;
+        for (int c = 0; c < n_chunks; ++c) {
+            const size_t u = (unit0 + c) * G + j;
+            const float mc = __hip_atomic_load(&p.part_ml[u * 2], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+            const float wgt = __builtin_amdgcn_exp2f(mc - M);
+            lsum += wgt * __hip_atomic_load(&p.part_ml[u * 2 + 1], __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+            o += wgt * __hip_atomic_load(&p.part_acc[u * D + d], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+        }
+        out_bh[i] = static_cast<uint16_t>(f32_to_elem<DT>(o / lsum));
+    }
+    if (threadIdx.x == 0)   // ready for the next launch
+        __hip_atomic_store(&p.counters[b * p.kv_heads + kvh], 0, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Any-shape fallback (head_dim <= 256, any GQA map, any block size, fp8
@@ -397,8 +452,8 @@ constexpr int kWaves = 4;
 int tiles_per_wave() {
     static int v = [] {
         const char* e = std::getenv("KCMM_ATTN_TPW");
-        int x = e ? std::atoi(e) : 2;
-        return (x == 1 || x == 2 || x == 4 || x == 8) ? x : 2;
+        int x = e ? std::atoi(e) : 4;
+        return (x == 1 || x == 2 || x == 4 || x == 8) ? x : 4;
     }();
     return v;
 }
@@ -415,22 +470,22 @@ bool launch_mfma_tpw(AttnParams& p, hipStream_t s, std::string* err) {
         return false;
     }
     const size_t units = static_cast<size_t>(p.batch) * p.kv_heads * p.max_chunks * p.group;
-    void* ws = nullptr;
     if (p.max_chunks > 1) {
+        void* ws = nullptr;
+        void* cnt = nullptr;
         if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 0,
-                                   units * (D + 2) * sizeof(float), &ws, err))
+                                   units * (D + 2) * sizeof(float), &ws, false, err) ||
+            !dev::stream_workspace(reinterpret_cast<uint64_t>(s), 2,
+                                   static_cast<size_t>(p.batch) * p.kv_heads * sizeof(int), &cnt,
+                                   true, err))
             return false;
-        p.part_acc = static_cast<float*>(ws);
-        p.part_ml = p.part_acc + units * D;
+        p.part_ml = static_cast<float*>(ws);
+        p.part_acc = p.part_ml + units * 2;
+        p.counters = static_cast<int*>(cnt);
     }
     hipLaunchKernelGGL((attn_decode_mfma<DT, D, BS, kWaves, TPW>), dim3(static_cast<unsigned>(grid)),
                        dim3(kWaves * 64), 0, s, p);
     KCMM_HIP_CHECK(hipGetLastError(), err);
-    if (p.max_chunks > 1) {
-        hipLaunchKernelGGL((attn_decode_merge<DT, D>), dim3(p.batch * p.num_q_heads), dim3(64), 0,
-                           s, p, CHUNK);
-        KCMM_HIP_CHECK(hipGetLastError(), err);
-    }
     return true;
 }
 
@@ -438,9 +493,9 @@ template <int DT, int D, int BS>
 bool launch_mfma(AttnParams& p, hipStream_t s, std::string* err) {
     switch (tiles_per_wave()) {
         case 1: return launch_mfma_tpw<DT, D, BS, 1>(p, s, err);
-        case 4: return launch_mfma_tpw<DT, D, BS, 4>(p, s, err);
         case 8: return launch_mfma_tpw<DT, D, BS, 8>(p, s, err);
-        default: return launch_mfma_tpw<DT, D, BS, 2>(p, s, err);
+        case 2: return launch_mfma_tpw<DT, D, BS, 2>(p, s, err);
+        default: return launch_mfma_tpw<DT, D, BS, 4>(p, s, err);
     }
 }
 

@@ -152,10 +152,12 @@ bool set_device(int device, std::string* err) {
     return true;
 }
 
-// Device scratch for split-K partials, one buffer per (device, stream, user
-// slot) so launches on different streams never share one.  Grows on demand;
-// the old buffer is released only after its stream has drained.
-bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, std::string* err) {
+// Device scratch for split-K partials and arrival counters, one buffer per
+// (device, stream, user slot) so launches on different streams never share
+// one.  Grows on demand; the old buffer is released only after its stream has
+// drained; `zero_fill` buffers start zeroed (their users restore zero).
+bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
+                      std::string* err) {
     struct Ws {
         void* ptr = nullptr;
         size_t bytes = 0;
@@ -176,6 +178,9 @@ bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, std::
         const size_t want = bytes + bytes / 4;
         KCMM_HIP_CHECK(hipMalloc(&w.ptr, want), err);
         w.bytes = want;
+        if (zero_fill)
+            KCMM_HIP_CHECK(hipMemsetAsync(w.ptr, 0, want, reinterpret_cast<hipStream_t>(stream)),
+                           err);
     }
     *out = w.ptr;
     return true;

@@ -151,7 +151,7 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
     if (splits > 1) {
         void* ws = nullptr;
         if (!stream_workspace(stream, 1, static_cast<size_t>(splits) * M * N * sizeof(float), &ws,
-                              err))
+                              false, err))
             return false;
         part = static_cast<float*>(ws);
     }

@@ -56,7 +56,9 @@ std::unique_ptr<PageBacking> make_backing(int, std::string*) {
 }
 bool set_device(int, std::string*) { return true; }
 bool synchronize_device(int, std::string*) { return true; }
-bool stream_workspace(uint64_t, int, size_t, void**, std::string* err) { return no_device(err); }
+bool stream_workspace(uint64_t, int, size_t, void**, bool, std::string* err) {
+    return no_device(err);
+}
 bool attn_decode(const AttnDecodeArgs&, std::string* err) { return no_device(err); }
 bool kv_write_rows(const KvRowsArgs&, std::string* err) { return no_device(err); }
 bool kv_write_device_slots(const KvDeviceSlotsArgs&, std::string* err) { return no_device(err); }
