@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--attn-only", action="store_true", help="time attention (+append) only")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-shuffle", action="store_true",
+                    help="give each sequence contiguous pages (locality experiment)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
     return ap.parse_args()
@@ -115,7 +117,8 @@ def main():
     t0 = time.perf_counter()
     case = build_decode_case(lib, batch=B, num_q_heads=HQ, kv_heads=HKV, head_dim=D,
                              block_size=BS, ctx_lens=L, dtype=KV_BF16, num_layers=args.layers,
-                             seed=args.seed + 1, host_mirror=False)
+                             seed=args.seed + 1, host_mirror=False,
+                             shuffle=not args.no_shuffle)
     log(f"workload built in {time.perf_counter() - t0:.1f}s: {case.pool.stats()['superblock_count']} "
         f"superblocks/region, backing={'vmm' if case.pool.backing_kind() == 0 else 'flat'}")
     stream = torch.cuda.current_stream()

@@ -8,21 +8,29 @@
 // region.  L <= 0 writes zeros.  Accumulation is fp32.
 //
 // MI355X design (the reference uses one scalar thread per (b, h)):
-//  * one workgroup of WAVES wavefronts per (b, kv head, chunk of CHUNK
-//    tokens); every page slice a workgroup reads serves all G = Hq/Hkv query
-//    heads of its kv head (GQA reuse: each K/V byte is read from HBM once);
-//  * a wave walks 32-token tiles; each lane issues 16-byte loads straight
-//    into MFMA operand layout -- no LDS for K;
+//  * the work is the list of 32-token tiles of every (sequence b, kv head g),
+//    b-major; every wave (one per workgroup) streams an equal contiguous
+//    slice of that list, so a ragged batch leaves no tail of idle CUs;
+//  * one tile read serves all G = Hq/Hkv query heads of its kv head (GQA
+//    reuse: each K/V byte is read from HBM once);
+//  * every load instruction covers eight tokens x 128 contiguous bytes (whole
+//    cache lines, nontemporal); one DPP row rotation and one select per dword
+//    then turn two such loads into MFMA operand layout (16 tokens x 64 bytes);
+//  * page addresses are wave-uniform scalar loads issued one tile ahead;
 //  * S^T = K Q^T on v_mfma_f32_16x16x32 (token rows x head columns), online
 //    softmax in the log2 domain with cross-lane max by lane shuffles;
-//  * O^T += V^T P^T on the same MFMA: V goes through wave-private LDS to be
-//    read transposed; P^T is already in B-operand layout in registers;
-//  * waves of a workgroup merge in LDS; the chunks of one (b, g) merge by
-//    log-sum-exp in whichever workgroup finishes last (split-K over long
-//    contexts in a single launch).
+//  * O^T += V^T P^T on the same MFMA: V^T is produced in registers by
+//    multiplying each V fragment with a 0/1 selection matrix (exact for
+//    16-bit values), so the kernel touches no LDS;
+//  * a (b, g) whose tiles lie inside one wave's slice is normalised and
+//    written by that wave; one that spans waves leaves fp32 partials
+//    (unnormalised output, max, denominator) that attn_decode_merge combines
+//    by log-sum-exp.
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 #include "../device_api.hpp"
 #include "common.hpp"
@@ -38,11 +46,12 @@ struct AttnParams {
     const int32_t* block_tables;
     const int32_t* seq_lens;
     const uint64_t* offsets_f16;
-    float* part_acc;        // [B][Hkv][max_chunks][G][D]
-    float* part_ml;         // [B][Hkv][max_chunks][G][2]
-    int* counters;          // [B][Hkv] chunk arrivals (zero between launches)
-    int batch, num_q_heads, kv_heads, group, block_size, mbps, max_chunks;
+    float* part_acc;        // [waves][2][G][D]  (slot 0: head of slice, 1: tail)
+    float* part_ml;         // [waves][2][G][2]  (max in log2 units, denominator)
+    int batch, num_q_heads, kv_heads, group, block_size, mbps;
     int row_bytes, data_bytes;
+    int total_waves;        // grid of the streaming kernel (one wave per workgroup)
+    int min_tiles;          // smallest slice a wave takes
     float scale_log2;       // scale * log2(e)
 };
 
@@ -59,6 +68,12 @@ __device__ __forceinline__ float wave_sum_across_groups(float x) {
     return x;
 }
 
+__device__ __forceinline__ int wave_sum(int x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
 template <int DT>
 __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
     if constexpr (DT == kDtF16)
@@ -70,52 +85,86 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
                                                        0);
 }
 
-// Byte offset (inside a region) of token `pos` of sequence b, kv head kvh.
-template <int BS>
-__device__ __forceinline__ uint64_t token_offset(const AttnParams& p, int b, int kvh, int pos,
-                                                 int head_bytes) {
-    const int bs = BS > 0 ? BS : p.block_size;
-    const int lb = pos / bs;
-    const int off = pos - lb * bs;
-    const int blk = p.block_tables[static_cast<size_t>(b) * p.mbps + lb];
-    return p.offsets_f16[blk] * 2ull + static_cast<uint64_t>(off) * p.row_bytes +
-           static_cast<uint64_t>(kvh) * head_bytes;
+// Tokens of sequence b that attention reads (ref kernel: the table holds at
+// most mbps * bs of them).
+__device__ __forceinline__ int clamp_len(int L, int cap) { return L < 0 ? 0 : (L > cap ? cap : L); }
+__device__ __forceinline__ int tiles_of(int L) { return (L + 31) >> 5; }
+
+// Slice length of one wave for `total` tiles; the attention and the merge
+// kernel must agree on it.
+__device__ __forceinline__ int wave_slice(int total, const AttnParams& p) {
+    const int per = (total + p.total_waves - 1) / p.total_waves;
+    return per > p.min_tiles ? per : p.min_tiles;
 }
 
-constexpr int kPad = 4;  // LDS row padding (elements): keeps transposed reads conflict-free
-
-// One 32-token tile: 2 halves of 16 tokens, KC 16-byte fragments per lane each.
+// One 32-token tile: 2 halves of 16 tokens, KC 16-byte fragments per lane
+// each; after fix_lines, k[h][kc] of lane (ln, lg) holds bytes
+// (4kc + lg)*16 .. +16 of token 16h + ln's head row (the MFMA A layout).
 template <int KC>
 struct Tile {
     u32x4 k[2][KC];
     u32x4 v[2][KC];
 };
 
-template <int KC>
-__device__ __forceinline__ void load_tile(Tile<KC>& t, const uint8_t* k_base,
-                                          const uint8_t* v_base, const uint64_t off[2],
-                                          int lg) {
+// Row rotation by 8 inside each 16-lane row (DPP row_ror:8; its own inverse).
+__device__ __forceinline__ uint32_t ror8(uint32_t x) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x128, 0xF, 0xF, false));
+}
+
+// x was loaded as: lane (r, lg) <- token (r & 7), bytes (4*(r >> 3) + lg)*16
+// of a 128-byte line; y the same for tokens 8..15.  Afterwards x holds the
+// first 64 bytes of tokens 0..15 and y the second 64 bytes, lane r = token r.
+__device__ __forceinline__ void fix_lines(u32x4& x, u32x4& y, bool low8) {
+    u32x4 nx, ny;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint8_t* kr = k_base + off[h] + lg * 16;
-        const uint8_t* vr = v_base + off[h] + lg * 16;
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-            t.k[h][kc] = *reinterpret_cast<const u32x4*>(kr + kc * 64);
-            t.v[h][kc] = *reinterpret_cast<const u32x4*>(vr + kc * 64);
-        }
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t rx = ror8(x[c]);
+        const uint32_t ry = ror8(y[c]);
+        nx[c] = low8 ? x[c] : ry;
+        ny[c] = low8 ? rx : y[c];
+    }
+    x = nx;
+    y = ny;
+}
+
+__device__ __forceinline__ u32x4 load_stream(const uint8_t* a) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a));
+}
+
+// B operand of a 16x16x32 MFMA that selects 16 consecutive k indices:
+// E[k][j] = (k == 16*sub + j).  Multiplying an A operand by it returns the
+// selected A columns in C layout, i.e. transposed relative to the A layout.
+template <int DT>
+__device__ __forceinline__ u32x4 select_operand(int sub, int ln, int lg) {
+    constexpr uint32_t one = DT == kDtF16 ? 0x3C00u : 0x3F80u;
+    u32x4 e = u32x4{0, 0, 0, 0};
+    const int k = 16 * sub + ln;          // the k that column ln selects
+    if ((k >> 3) == lg) {
+        const int t = k & 7;              // item within the lane's 8 k values
+        e[t >> 1] = (t & 1) ? (one << 16) : one;
+    }
+    return e;
+}
+
+// Two fp32 values that hold exactly representable 16-bit values -> packed pair.
+template <int DT>
+__device__ __forceinline__ uint32_t pack_exact(float lo, float hi) {
+    if constexpr (DT == kDtF16) {
+        return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+    } else {
+        return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
     }
 }
 
 // Online-softmax update of one tile (see the file comment for the layouts).
 template <int DT, int D>
-__device__ __forceinline__ void compute_tile(const Tile<D / 32>& t, const u32x4* qf, int tbase,
-                                             int L, float scale_log2, float& m_run,
-                                             float& l_run, f32x4* acc, uint16_t* vl, int ln,
-                                             int lg) {
+__device__ __forceinline__ void compute_tile(const Tile<D / 32>& t, const u32x4* qf,
+                                             const u32x4* esel, int tbase, int L,
+                                             float scale_log2, float& m_run, float& l_run,
+                                             f32x4* acc, int lg) {
     constexpr int KC = D / 32;
     constexpr int DB = D / 16;
-    constexpr int ROW = D + kPad;
     f32x4 s[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -155,214 +204,368 @@ __device__ __forceinline__ void compute_tile(const Tile<D / 32>& t, const u32x4*
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         pf[i] = f32_to_elem<DT>(pv[2 * i]) | (f32_to_elem<DT>(pv[2 * i + 1]) << 16);
-
-    // V rows into wave-private LDS (row = token in tile), then V^T reads.
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-            uint16_t* dst = vl + (h * 16 + ln) * ROW + kc * 32 + lg * 8;
-            reinterpret_cast<u32x2*>(dst)[0] = u32x2{t.v[h][kc][0], t.v[h][kc][1]};
-            reinterpret_cast<u32x2*>(dst)[1] = u32x2{t.v[h][kc][2], t.v[h][kc][3]};
-        }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // V^T for the PV product, by selection MFMAs, one 16-dim block at a time
+    // (keeps few transposed values live): lane (dim ln, group lg) receives
+    // V[h*16 + 4lg + r][16db + ln] for r = 0..3 from half h.
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-        const uint16_t* col = vl + db * 16 + ln;
+        const f32x4 v0 = mfma16x16x32<DT>(t.v[0][db >> 1], esel[db & 1], f32x4{0, 0, 0, 0});
+        const f32x4 v1 = mfma16x16x32<DT>(t.v[1][db >> 1], esel[db & 1], f32x4{0, 0, 0, 0});
         u32x4 va;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t0 = (2 * i < 4) ? 4 * lg + 2 * i : 16 + 4 * lg + 2 * i - 4;
-            const uint32_t lo = col[t0 * ROW];
-            const uint32_t hi = col[(t0 + 1) * ROW];
-            va[i] = lo | (hi << 16);
-        }
+        va[0] = pack_exact<DT>(v0[0], v0[1]);
+        va[1] = pack_exact<DT>(v0[2], v0[3]);
+        va[2] = pack_exact<DT>(v1[0], v1[1]);
+        va[3] = pack_exact<DT>(v1[2], v1[3]);
         acc[db] = mfma16x16x32<DT>(va, pf, acc[db]);
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
-// Workgroup = WAVES wavefronts on one (sequence b, kv head, chunk of CHUNK
-// tokens); wave w owns tiles [w*TPW, (w+1)*TPW) of the chunk.  Chunks of a
-// sequence longer than CHUNK write fp32 partials (unnormalised output, max,
-// denominator); the last workgroup of that (b, kv head) to finish -- found
-// with a device-scope counter -- merges them by log-sum-exp and resets the
-// counter, so one launch does split-K end to end.
-template <int DT, int D, int BS, int WAVES, int TPW>
-__global__ __launch_bounds__(WAVES * 64) void attn_decode_mfma(AttnParams p) {
+// Streaming decode attention: one wave per workgroup, each on the slice
+// [gw*per, gw*per + per) of the b-major tile list, with P tiles in flight.
+// Read-only tables come as separate restrict arguments so that wave-uniform
+// reads of them compile to scalar loads, which do not wait behind the vector
+// loads in flight.  Past the end of its slice a wave keeps issuing loads, of
+// `idle` (a small workspace region that stays in L2), so that every step has
+// the same loads outstanding and the waits stay exact.
+template <int DT, int D, int BS, int P>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P == 2 ? 2 : 1)))
+void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
+                        const int32_t* __restrict__ sl, const uint64_t* __restrict__ offs,
+                        const uint8_t* __restrict__ idle) {
     constexpr int KC = D / 32;
+    constexpr int LINES = D / 64;
     constexpr int DB = D / 16;
-    constexpr int CHUNK = WAVES * TPW * 32;
-    constexpr int ROW = D + kPad;
-    constexpr int HEAD_BYTES = D * 2;
-    constexpr int LDS_ELEMS = WAVES * 32 * ROW;
-    static_assert((WAVES * D * 16 + WAVES * 32) * 4 <= LDS_ELEMS * 2, "merge area exceeds LDS");
-
-    __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
-    __shared__ int last_flag;
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x;
     const int ln = lane & 15;
     const int lg = lane >> 4;
-
-    int bid = blockIdx.x;
-    const int kvh = bid % p.kv_heads;
-    bid /= p.kv_heads;
-    const int b = bid % p.batch;
-    const int chunk = bid / p.batch;
-    const int G = p.group;
     const int bs = BS > 0 ? BS : p.block_size;
-    const int L = min(p.seq_lens[b], p.mbps * bs);
+    const int cap = p.mbps * bs;
+    const int Hkv = p.kv_heads;
+    const int G = p.group;
 
-    if (L <= 0) {
-        if (chunk == 0) {
-            uint16_t* o = reinterpret_cast<uint16_t*>(p.out) +
-                          (static_cast<size_t>(b) * p.num_q_heads + kvh * G) * D;
-            for (int i = threadIdx.x; i < G * D; i += WAVES * 64) o[i] = 0;
+    // ---- this wave's slice of the tile list ----
+    // lane i of chunk c describes sequence c + i: clamped length, tiles
+    auto chunk_vals = [&](int c, int& Lc, int& v) {
+        const int bb = c + lane;
+        Lc = bb < p.batch ? clamp_len(sl[bb], cap) : 0;
+        v = Hkv * tiles_of(Lc);
+    };
+    auto inclusive_scan = [&](int v) {
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(v, o);
+            if (lane >= o) v += y;
         }
-        return;
+        return v;
+    };
+    int L0, v0;
+    chunk_vals(0, L0, v0);
+    const int incl0 = inclusive_scan(v0);
+    int total = __shfl(incl0, 63);
+    for (int c = 64; c < p.batch; c += 64) {
+        int Lc, v;
+        chunk_vals(c, Lc, v);
+        total += wave_sum(v);
     }
-    const int n_chunks = (L + CHUNK - 1) / CHUNK;
-    if (chunk >= n_chunks) return;
+    total = __builtin_amdgcn_readfirstlane(total);
+    const int per = wave_slice(total, p);
+    const int t0 = static_cast<int>(blockIdx.x) * per;
+    if (t0 >= total) return;
+    const int n = min(per, total - t0);
 
-    const int tok0 = chunk * CHUNK + wave * TPW * 32;
-    const int ntiles = max(0, min(TPW, (L - tok0 + 31) / 32));
-
-    // Page addresses of every tile this wave will read, fetched up front so
-    // the dependent table -> offset -> data loads are not paid per tile.
-    uint64_t toff[TPW][2];
-#pragma unroll
-    for (int t = 0; t < TPW; ++t)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int pos = min(tok0 + t * 32 + h * 16 + ln, L - 1);
-            toff[t][h] = token_offset<BS>(p, b, kvh, pos, HEAD_BYTES);
-        }
-
-    // Q^T as the B operand: lane (head ln, group lg) holds Q[ln][kc*32+8lg .. +8].
-    u32x4 qf[KC];
+    // sequence holding tile t0, its first tile and its length
+    int b = 0, start = 0, Lb = 0;
     {
-        const bool valid = ln < G;
-        const uint8_t* qrow =
-            p.q + (static_cast<size_t>(b) * p.num_q_heads + kvh * G + (valid ? ln : 0)) * D * 2;
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-            u32x4 v = *reinterpret_cast<const u32x4*>(qrow + (kc * 32 + lg * 8) * 2);
-            qf[kc] = valid ? v : u32x4{0, 0, 0, 0};
+        unsigned long long hit = __ballot(incl0 > t0);
+        if (hit) {
+            const int j = __ffsll(static_cast<long long>(hit)) - 1;
+            b = j;
+            start = __shfl(incl0 - v0, j);
+            Lb = __shfl(L0, j);
+        } else {
+            int base = __shfl(incl0, 63);
+            for (int c = 64; c < p.batch; c += 64) {
+                int Lc, v;
+                chunk_vals(c, Lc, v);
+                const int incl = inclusive_scan(v);
+                hit = __ballot(base + incl > t0);
+                if (hit) {
+                    const int j = __ffsll(static_cast<long long>(hit)) - 1;
+                    b = c + j;
+                    start = base + __shfl(incl - v, j);
+                    Lb = __shfl(Lc, j);
+                    break;
+                }
+                base += __shfl(incl, 63);
+            }
         }
     }
 
+    // Cursor over the tile list: (sequence, kv head, tile, length, tiles).
+    struct Cur {
+        int b, g, t, L, nt;
+    };
+    Cur ic;  // next tile to issue
+    ic.b = __builtin_amdgcn_readfirstlane(b);
+    ic.L = __builtin_amdgcn_readfirstlane(Lb);
+    ic.nt = tiles_of(ic.L);
+    {
+        const int rem = t0 - __builtin_amdgcn_readfirstlane(start);
+        ic.g = rem / ic.nt;
+        ic.t = rem - ic.g * ic.nt;
+    }
+    auto advance = [&](Cur& c) {
+        if (++c.t < c.nt) return;
+        c.t = 0;
+        if (++c.g < Hkv) return;
+        c.g = 0;
+        ++c.b;
+        c.L = clamp_len(sl[c.b], cap);
+        c.nt = tiles_of(c.L);
+        // sequences without tokens own no tiles (the slice never ends in them)
+        while (c.nt == 0 && c.b + 1 < p.batch) {
+            ++c.b;
+            c.L = clamp_len(sl[c.b], cap);
+            c.nt = tiles_of(c.L);
+        }
+    };
+    // Page-relative byte address of each 8-token group of a tile; groups past
+    // the sequence re-read its last group (masked).
+    auto group_bases = [&](const Cur& c, uint64_t* gb) {
+        const int last8 = (c.L - 1) & ~7;
+        const int32_t* row = bt + static_cast<size_t>(c.b) * p.mbps;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int tok = min(c.t * 32 + q * 8, last8);
+            const int lb = tok / bs;
+            gb[q] = offs[row[lb]] * 2ull +
+                    static_cast<uint32_t>((tok - lb * bs) * p.row_bytes + c.g * D * 2);
+        }
+    };
+
+    const uint32_t lo = static_cast<uint32_t>((ln & 7) * p.row_bytes + ((ln >> 3) * 4 + lg) * 16);
+    const bool low8 = ln < 8;
+    auto issue = [&](Tile<KC>& tl, bool real, const uint64_t* gb) {
+        const uint8_t* kb = real ? p.k_base : idle;
+        const uint8_t* vb = real ? p.v_base : idle;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int c2 = 0; c2 < LINES; ++c2) {
+                const uint32_t o = lo + c2 * 128;
+                const uint64_t g0 = real ? gb[2 * h] : 0;
+                const uint64_t g1 = real ? gb[2 * h + 1] : 0;
+                tl.k[h][2 * c2] = load_stream(kb + g0 + o);
+                tl.k[h][2 * c2 + 1] = load_stream(kb + g1 + o);
+                tl.v[h][2 * c2] = load_stream(vb + g0 + o);
+                tl.v[h][2 * c2 + 1] = load_stream(vb + g1 + o);
+            }
+    };
+    // Q^T as the B operand: lane (head ln, group lg) holds Q[ln][kc*32+8lg .. +8].
+    // Columns ln >= G repeat head G-1; they are computed and never stored.
+    auto load_q = [&](u32x4* qd, const Cur& c) {
+        const uint8_t* qrow = p.q + (static_cast<size_t>(c.b) * p.num_q_heads + c.g * G +
+                                     min(ln, G - 1)) * D * 2;
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+            qd[kc] = *reinterpret_cast<const u32x4*>(qrow + (kc * 32 + lg * 8) * 2);
+    };
+
+    const u32x4 esel[2] = {select_operand<DT>(0, ln, lg), select_operand<DT>(1, ln, lg)};
     float m_run = -INFINITY;  // running max (log2 domain) of column ln
     float l_run = 0.0f;       // this lane's share of the softmax denominator
     f32x4 acc[DB];
 #pragma unroll
     for (int i = 0; i < DB; ++i) acc[i] = f32x4{0, 0, 0, 0};
-    uint16_t* vl = lds + wave * 32 * ROW;
 
-    // Two tiles in flight: the loads of tile t+1 are issued before tile t is
-    // consumed.
-    Tile<KC> ta, tb;
-    if (ntiles > 0) load_tile<KC>(ta, p.k_base, p.v_base, toff[0], lg);
+    // Segment end: normalise and store, or leave a partial in slot
+    // 0 (segment began in an earlier slice) / 1 (continues in a later one).
+    auto flush = [&](const Cur& c, bool began_here) {
+        const float l = wave_sum_across_groups(l_run);
+        const bool complete = began_here && c.t == c.nt - 1;
+        if (ln < G) {
+            if (complete) {
+                const float inv = 1.0f / l;
+                uint16_t* o = reinterpret_cast<uint16_t*>(p.out) +
+                              (static_cast<size_t>(c.b) * p.num_q_heads + c.g * G + ln) * D + 4 * lg;
 #pragma unroll
-    for (int t = 0; t < TPW; t += 2) {
-        if (t < ntiles) {
-            if (t + 1 < ntiles) load_tile<KC>(tb, p.k_base, p.v_base, toff[t + 1], lg);
-            compute_tile<DT, D>(ta, qf, tok0 + t * 32, L, p.scale_log2, m_run, l_run, acc, vl, ln,
-                                lg);
-        }
-        if (t + 1 < ntiles) {
-            if (t + 2 < ntiles && t + 2 < TPW)
-                load_tile<KC>(ta, p.k_base, p.v_base, toff[(t + 2) % TPW], lg);
-            compute_tile<DT, D>(tb, qf, tok0 + (t + 1) * 32, L, p.scale_log2, m_run, l_run, acc,
-                                vl, ln, lg);
-        }
-    }
-
-    l_run = wave_sum_across_groups(l_run);
-
-    // ---- merge the waves of this workgroup in LDS ----
-    __syncthreads();
-    float* mrg = reinterpret_cast<float*>(lds);   // [WAVES][D][16] then [WAVES][16][2]
-    float* mrg_ml = mrg + WAVES * D * 16;
+                for (int db = 0; db < DB; ++db) {
+                    u32x2 w;
+                    w[0] = f32_to_elem<DT>(acc[db][0] * inv) | (f32_to_elem<DT>(acc[db][1] * inv) << 16);
+                    w[1] = f32_to_elem<DT>(acc[db][2] * inv) | (f32_to_elem<DT>(acc[db][3] * inv) << 16);
+                    *reinterpret_cast<u32x2*>(o + 16 * db) = w;
+                }
+            } else {
+                const size_t unit = static_cast<size_t>(blockIdx.x) * 2 + (began_here ? 1 : 0);
+                float* pa = p.part_acc + (unit * G + ln) * D + 4 * lg;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mrg[(wave * D + db * 16 + lg * 4 + r) * 16 + ln] = acc[db][r];
-    if (lg == 0) {
-        mrg_ml[(wave * 16 + ln) * 2 + 0] = m_run;
-        mrg_ml[(wave * 16 + ln) * 2 + 1] = l_run;
-    }
-    __syncthreads();
-
-    uint16_t* out_bh = reinterpret_cast<uint16_t*>(p.out) +
-                       (static_cast<size_t>(b) * p.num_q_heads + kvh * G) * D;
-    const size_t unit0 = (static_cast<size_t>(b) * p.kv_heads + kvh) * p.max_chunks;
-    for (int i = threadIdx.x; i < G * D; i += WAVES * 64) {
-        const int j = i / D;
-        const int d = i - j * D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, mrg_ml[(w * 16 + j) * 2]);
-        float lsum = 0.0f, o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-            const float mw = mrg_ml[(w * 16 + j) * 2];
-            const float wgt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            lsum += wgt * mrg_ml[(w * 16 + j) * 2 + 1];
-            o += wgt * mrg[(w * D + d) * 16 + j];
-        }
-        if (n_chunks == 1) {
-            out_bh[i] = static_cast<uint16_t>(f32_to_elem<DT>(o / lsum));
-        } else {
-            // Agent-scope stores write through to the device coherence point,
-            // so the merging workgroup (possibly on another XCD) sees them
-            // without a whole-L2 write-back.
-            const size_t u = (unit0 + chunk) * G + j;
-            __hip_atomic_store(&p.part_acc[u * D + d], o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (d == 0) {
-                __hip_atomic_store(&p.part_ml[u * 2 + 0], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&p.part_ml[u * 2 + 1], lsum, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(pa + 16 * db) = acc[db];
+                if (lg == 0) {
+                    p.part_ml[(unit * G + ln) * 2 + 0] = m_run;
+                    p.part_ml[(unit * G + ln) * 2 + 1] = l;
+                }
             }
         }
-    }
-    if (n_chunks == 1) return;
+        m_run = -INFINITY;
+        l_run = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DB; ++i) acc[i] = f32x4{0, 0, 0, 0};
+    };
 
-    // ---- split-K: the last chunk of (b, kv head) to arrive merges ----
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // partial stores acknowledged
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int prev = __hip_atomic_fetch_add(&p.counters[b * p.kv_heads + kvh], 1,
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = (prev == n_chunks - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    for (int i = threadIdx.x; i < G * D; i += WAVES * 64) {
-        const int j = i / D;
-        const int d = i - j * D;
-        float M = -INFINITY;
-        for (int c = 0; c < n_chunks; ++c)
-            M = fmaxf(M, __hip_atomic_load(&p.part_ml[((unit0 + c) * G + j) * 2], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT));
-        float lsum = 0.0f, o = 0.0f;
-        for (int c = 0; c < n_chunks; ++c) {
-            const size_t u = (unit0 + c) * G + j;
-            const float mc = __hip_atomic_load(&p.part_ml[u * 2], __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-            const float wgt = __builtin_amdgcn_exp2f(mc - M);
-            lsum += wgt * __hip_atomic_load(&p.part_ml[u * 2 + 1], __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-            o += wgt * __hip_atomic_load(&p.part_acc[u * D + d], __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
+    // ---- pipeline: buf[k] holds tile i with i % P == k; while tile i is
+    // consumed, tiles i+1 .. i+P-1 are in flight and the page addresses of
+    // tile i+P are being fetched ----
+    u32x4 qf[KC];
+    Cur cq[P];
+    Tile<KC> buf[P];
+    uint64_t gb[4];
+    load_q(qf, ic);
+    bool began_here = ic.t == 0;
+    group_bases(ic, gb);
+#pragma unroll
+    for (int k = 0; k < P - 1; ++k) {
+        cq[k] = ic;
+        issue(buf[k], k < n, gb);
+        if (k + 1 < n) {
+            advance(ic);
+            group_bases(ic, gb);
         }
-        out_bh[i] = static_cast<uint16_t>(f32_to_elem<DT>(o / lsum));
     }
-    if (threadIdx.x == 0)   // ready for the next launch
-        __hip_atomic_store(&p.counters[b * p.kv_heads + kvh], 0, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+
+    // With P >= 3 the Q of a new (b, g) is read ahead into qn, before the
+    // tile loads of the step, so that waiting for it never drains the tiles
+    // in flight behind it (P == 2 has no such tile: qf is refilled directly).
+    u32x4 qn[P > 2 ? KC : 1];
+    bool q_ready = false;
+    auto step = [&](auto phase, int i) {
+        constexpr int j = decltype(phase)::value;
+        constexpr int jn = (j + P - 1) % P;
+        if constexpr (P > 2) {
+            // take the Q read ahead for this tile before qn is refilled
+            if (q_ready) {
+#pragma unroll
+                for (int kc = 0; kc < KC; ++kc) qf[kc] = qn[kc];
+                q_ready = false;
+            }
+            if (i + 1 < n && cq[(j + 1) % P].t == 0) load_q(qn, cq[(j + 1) % P]);
+        }
+        cq[jn] = ic;
+        issue(buf[jn], i + P - 1 < n, gb);
+        if (i + P < n) {
+            advance(ic);
+            group_bases(ic, gb);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < n) {
+            const Cur c = cq[j];
+            Tile<KC>& now = buf[j];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int c2 = 0; c2 < LINES; ++c2) {
+                    fix_lines(now.k[h][2 * c2], now.k[h][2 * c2 + 1], low8);
+                    fix_lines(now.v[h][2 * c2], now.v[h][2 * c2 + 1], low8);
+                }
+            const int tbase = c.t * 32;
+            if (tbase + 32 > c.L) {
+                // rows past the sequence may hold anything (even NaN): zero
+                // the V rows so that the selection products stay exact
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const bool dead = tbase + h * 16 + ln >= c.L;
+#pragma unroll
+                    for (int kc = 0; kc < KC; ++kc)
+                        if (dead) now.v[h][kc] = u32x4{0, 0, 0, 0};
+                }
+            }
+            compute_tile<DT, D>(now, qf, esel, tbase, c.L, p.scale_log2, m_run, l_run, acc, lg);
+            if (i == n - 1 || c.t == c.nt - 1) flush(c, began_here);
+            if (i + 1 < n && cq[(j + 1) % P].t == 0) {
+                // a new (b, g) starts with tile i+1
+                if constexpr (P > 2) q_ready = true;
+                else load_q(qf, cq[(j + 1) % P]);  // waited for with tile i+1
+                began_here = true;
+            }
+        }
+    };
+    for (int i = 0; i < n; i += P) {
+        step(std::integral_constant<int, 0>{}, i);
+        step(std::integral_constant<int, 1>{}, i + 1);
+        if constexpr (P > 2) step(std::integral_constant<int, 2>{}, i + 2);
+        if constexpr (P > 3) step(std::integral_constant<int, 3>{}, i + 3);
+    }
+}
+
+constexpr int kMaxMergeParts = 256;  // partial weights the merge kernel stages in LDS
+
+// Log-sum-exp merge, one workgroup per (b, kv head): a (b, g) whose tiles
+// span waves wa..wb has partials in wave wa's slot 1 and in slot 0 of waves
+// wa+1..wb.  Also writes the zeros of sequences with no tokens.
+template <int DT, int D, int BS>
+__global__ __launch_bounds__(256) void attn_decode_merge(AttnParams p,
+                                                         const int32_t* __restrict__ sl) {
+    __shared__ float wgt[kMaxMergeParts * 16];
+    __shared__ float gmax[16];
+    __shared__ float inv_l[16];
+    __shared__ int red[2][4];
+    const int bs = BS > 0 ? BS : p.block_size;
+    const int cap = p.mbps * bs;
+    const int Hkv = p.kv_heads;
+    const int G = p.group;
+    const int kvh = blockIdx.x % Hkv;
+    const int b = blockIdx.x / Hkv;
+    int before = 0, total = 0;
+    for (int i = threadIdx.x; i < p.batch; i += 256) {
+        const int v = Hkv * tiles_of(clamp_len(sl[i], cap));
+        total += v;
+        if (i < b) before += v;
+    }
+    before = wave_sum(before);
+    total = wave_sum(total);
+    if ((threadIdx.x & 63) == 0) {
+        red[0][threadIdx.x >> 6] = before;
+        red[1][threadIdx.x >> 6] = total;
+    }
+    __syncthreads();
+    before = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    total = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    const int nt = tiles_of(clamp_len(sl[b], cap));
+    uint16_t* out_bh = reinterpret_cast<uint16_t*>(p.out) +
+                       (static_cast<size_t>(b) * p.num_q_heads + kvh * G) * D;
+    if (nt == 0) {
+        for (int i = threadIdx.x; i < G * D; i += 256) out_bh[i] = 0;
+        return;
+    }
+    const int per = wave_slice(total, p);
+    const int s = before + kvh * nt;
+    const int wa = s / per;
+    const int np = (s + nt - 1) / per - wa + 1;
+    if (np == 1) return;  // written by its wave
+    const float* ml = p.part_ml;
+    const float* pa = p.part_acc;
+    auto unit = [&](int k) { return static_cast<size_t>(wa + k) * 2 + (k == 0 ? 1 : 0); };
+    for (int j = threadIdx.x; j < G; j += 256) {
+        float M = -INFINITY;
+        for (int k = 0; k < np; ++k) M = fmaxf(M, ml[(unit(k) * G + j) * 2]);
+        float l = 0.0f;
+        for (int k = 0; k < np; ++k) {
+            const float w = __builtin_amdgcn_exp2f(ml[(unit(k) * G + j) * 2] - M);
+            if (k < kMaxMergeParts) wgt[k * 16 + j] = w;
+            l += w * ml[(unit(k) * G + j) * 2 + 1];
+        }
+        gmax[j] = M;
+        inv_l[j] = 1.0f / l;
+    }
+    __syncthreads();
+    const int staged = min(np, kMaxMergeParts);
+    for (int i = threadIdx.x; i < G * D; i += 256) {
+        const int j = i / D;
+        float o = 0.0f;
+        for (int k = 0; k < staged; ++k) o += wgt[k * 16 + j] * pa[unit(k) * G * D + i];
+        for (int k = staged; k < np; ++k)
+            o += __builtin_amdgcn_exp2f(ml[(unit(k) * G + j) * 2] - gmax[j]) * pa[unit(k) * G * D + i];
+        out_bh[i] = static_cast<uint16_t>(f32_to_elem<DT>(o * inv_l[j]));
+    }
 }
 
 // Any-shape fallback (head_dim <= 256, any GQA map, any block size, fp8
@@ -445,76 +648,66 @@ __global__ __launch_bounds__(64) void attn_decode_generic(AttnParams p, int head
     }
 }
 
-constexpr int kWaves = 4;
-
-// Tiles (of 32 tokens) per wave; the chunk of one workgroup is
-// kWaves * tpw * 32 tokens.  KCMM_ATTN_TPW overrides the default.
-int tiles_per_wave() {
-    static int v = [] {
-        const char* e = std::getenv("KCMM_ATTN_TPW");
-        int x = e ? std::atoi(e) : 4;
-        return (x == 1 || x == 2 || x == 4 || x == 8) ? x : 4;
-    }();
-    return v;
+int env_int(const char* name, int dflt, int lo, int hi) {
+    const char* e = std::getenv(name);
+    if (!e) return dflt;
+    const int x = std::atoi(e);
+    return x < lo || x > hi ? dflt : x;
 }
 
-template <int DT, int D, int BS, int TPW>
-bool launch_mfma_tpw(AttnParams& p, hipStream_t s, std::string* err) {
-    constexpr int CHUNK = kWaves * TPW * 32;
-    const int bs = BS > 0 ? BS : p.block_size;
-    const long long max_tok = static_cast<long long>(p.mbps) * bs;
-    p.max_chunks = static_cast<int>((max_tok + CHUNK - 1) / CHUNK);
-    const long long grid = static_cast<long long>(p.kv_heads) * p.batch * p.max_chunks;
-    if (grid > 0x7fffffffLL) {
-        *err = "decode attention grid too large";
+// Tunables, read on every call (getenv is cheap next to a launch):
+// KCMM_ATTN_WAVES waves of the streaming kernel, KCMM_ATTN_MIN_TILES the
+// smallest slice a wave takes, KCMM_ATTN_DEPTH tiles in flight (2 or 3).
+int stream_waves() { return env_int("KCMM_ATTN_WAVES", 1024, 1, 1 << 20); }
+int stream_min_tiles() { return env_int("KCMM_ATTN_MIN_TILES", 8, 1, 1 << 16); }
+int stream_depth() { return env_int("KCMM_ATTN_DEPTH", 2, 2, 3); }
+
+template <int DT, int D, int BS>
+bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
+    static_assert(D % 64 == 0, "head rows are whole 128-byte lines");
+    const long long cap = static_cast<long long>(p.mbps) * p.block_size;
+    const long long tmax = static_cast<long long>(p.batch) * p.kv_heads * ((cap + 31) / 32);
+    if (cap > INT_MAX || tmax > (1LL << 30)) {
+        *err = "decode attention: batch x context too large";
         return false;
     }
-    const size_t units = static_cast<size_t>(p.batch) * p.kv_heads * p.max_chunks * p.group;
-    if (p.max_chunks > 1) {
-        void* ws = nullptr;
-        void* cnt = nullptr;
-        if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 0,
-                                   units * (D + 2) * sizeof(float), &ws, false, err) ||
-            !dev::stream_workspace(reinterpret_cast<uint64_t>(s), 2,
-                                   static_cast<size_t>(p.batch) * p.kv_heads * sizeof(int), &cnt,
-                                   true, err))
-            return false;
-        p.part_ml = static_cast<float*>(ws);
-        p.part_acc = p.part_ml + units * 2;
-        p.counters = static_cast<int*>(cnt);
-    }
-    hipLaunchKernelGGL((attn_decode_mfma<DT, D, BS, kWaves, TPW>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kWaves * 64), 0, s, p);
+    if (p.batch == 0) return true;
+    p.min_tiles = stream_min_tiles();
+    const long long want = (tmax + p.min_tiles - 1) / p.min_tiles;
+    p.total_waves = static_cast<int>(std::max(1LL, std::min<long long>(stream_waves(), want)));
+    const size_t units = static_cast<size_t>(p.total_waves) * 2 * p.group;
+    // idle-load region first: it must cover one tile's lane addresses
+    const size_t idle_bytes = (static_cast<size_t>(8) * p.row_bytes + 1023) & ~static_cast<size_t>(255);
+    void* ws = nullptr;
+    if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 0,
+                               idle_bytes + units * (D + 2) * sizeof(float), &ws, false, err))
+        return false;
+    const uint8_t* idle = static_cast<const uint8_t*>(ws);
+    p.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + idle_bytes);
+    p.part_acc = p.part_ml + units * 2;
+    if (stream_depth() == 3)
+        hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 3>), dim3(p.total_waves), dim3(64), 0, s,
+                           p, p.block_tables, p.seq_lens, p.offsets_f16, idle);
+    else
+        hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 2>), dim3(p.total_waves), dim3(64), 0, s,
+                           p, p.block_tables, p.seq_lens, p.offsets_f16, idle);
+    KCMM_HIP_CHECK(hipGetLastError(), err);
+    hipLaunchKernelGGL((attn_decode_merge<DT, D, BS>), dim3(p.batch * p.kv_heads), dim3(256), 0, s,
+                       p, p.seq_lens);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     return true;
 }
 
-template <int DT, int D, int BS>
-bool launch_mfma(AttnParams& p, hipStream_t s, std::string* err) {
-    switch (tiles_per_wave()) {
-        case 1: return launch_mfma_tpw<DT, D, BS, 1>(p, s, err);
-        case 8: return launch_mfma_tpw<DT, D, BS, 8>(p, s, err);
-        case 2: return launch_mfma_tpw<DT, D, BS, 2>(p, s, err);
-        default: return launch_mfma_tpw<DT, D, BS, 4>(p, s, err);
-    }
-}
-
 template <int DT, int D>
-bool launch_mfma_bs(AttnParams& p, hipStream_t s, std::string* err) {
-    if (p.block_size == 16) return launch_mfma<DT, D, 16>(p, s, err);
-    return launch_mfma<DT, D, 0>(p, s, err);
+bool launch_stream_bs(AttnParams& p, hipStream_t s, std::string* err) {
+    if (p.block_size == 16) return launch_stream<DT, D, 16>(p, s, err);
+    return launch_stream<DT, D, 0>(p, s, err);
 }
 
 template <int DT>
 bool launch_dt(AttnParams& p, int head_dim, hipStream_t s, std::string* err) {
-    switch (head_dim) {
-        case 64: return launch_mfma_bs<DT, 64>(p, s, err);
-        case 128: return launch_mfma_bs<DT, 128>(p, s, err);
-        case 256: return launch_mfma_bs<DT, 256>(p, s, err);
-        default: break;
-    }
-    *err = "unsupported head_dim for the MFMA path";
-    return false;
+    if (head_dim == 64) return launch_stream_bs<DT, 64>(p, s, err);
+    return launch_stream_bs<DT, 128>(p, s, err);
 }
 
 }  // namespace
@@ -541,10 +734,12 @@ bool attn_decode(const AttnDecodeArgs& a, std::string* err) {
     p.scale_log2 = a.scale * 1.4426950408889634f;
     hipStream_t s = reinterpret_cast<hipStream_t>(a.stream);
 
+    // Streaming MFMA path: 16-bit pages, whole GQA groups of at most 16 heads,
+    // head_dim 64 or 128, pages made of 8-token groups.
     const bool grouped = p.num_q_heads % p.kv_heads == 0 && p.group <= 16;
-    const bool mfma_dim = a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256;
+    const bool stream_dim = a.head_dim == 64 || a.head_dim == 128;
     const bool force_generic = std::getenv("KCMM_ATTN_GENERIC") != nullptr;
-    if (a.dtype != kDtFP8 && grouped && mfma_dim && !force_generic) {
+    if (a.dtype != kDtFP8 && grouped && stream_dim && a.block_size % 8 == 0 && !force_generic) {
         if (a.dtype == kDtF16) return launch_dt<kDtF16>(p, a.head_dim, s, err);
         return launch_dt<kDtBF16>(p, a.head_dim, s, err);
     }

@@ -135,7 +135,8 @@ def _fill_pages_host(case: DecodeCase, rng: np.random.Generator, layer_tokens) -
 def build_decode_case(lib: KcmmLibrary, *, batch: int, num_q_heads: int, kv_heads: int,
                       head_dim: int, block_size: int, ctx_lens, dtype: int = KV_BF16,
                       num_layers: int = 1, seed: int = 0, host_mirror: bool = True,
-                      extra_seq_len: int = 0, device: str = "cuda") -> DecodeCase:
+                      extra_seq_len: int = 0, device: str = "cuda",
+                      shuffle: bool = True) -> DecodeCase:
     """Allocate pages for `ctx_lens` tokens per sequence (+ `extra_seq_len`
     page headroom), shuffle them over the pool, fill them and upload q."""
     if dtype == KV_FP8 and not host_mirror:
@@ -152,6 +153,8 @@ def build_decode_case(lib: KcmmLibrary, *, batch: int, num_q_heads: int, kv_head
     for start in range(0, total, 4096):
         ids += pool.alloc_blocks(min(4096, total - start))
     perm = rng.permutation(np.asarray(ids, dtype=np.int64))
+    if not shuffle:   # pages of a sequence contiguous in allocation order
+        perm = np.asarray(ids, dtype=np.int64)
     mbps = -(-max_len // block_size)
     bt = np.zeros((batch, mbps), dtype=np.int32)
     pos = 0

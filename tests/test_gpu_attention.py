@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lattice_amd.bindings import KV_BF16, KV_F16, KV_FP8, memcpy_dtoh
+from lattice_amd.bindings import KV_BF16, KV_F16, KV_FP8, memcpy_dtoh, memcpy_htod
 from lattice_amd.workload import build_decode_case
 
 pytestmark = pytest.mark.gpu
@@ -167,6 +167,77 @@ def test_entry_point_variants_agree(gpu_lib):
             torch.cuda.synchronize()
             outs.append(case.out_bits().copy())
         assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    finally:
+        case.pool.destroy()
+
+
+@pytest.fixture(params=["default", "depth3", "many_waves"])
+def stream_tuning(request, monkeypatch):
+    """Streaming-kernel settings: the default, three tiles in flight, and a
+    tiny slice per wave (every (b, kv head) split over many waves, so the
+    log-sum-exp merge runs everywhere)."""
+    if request.param == "depth3":
+        monkeypatch.setenv("KCMM_ATTN_DEPTH", "3")
+    elif request.param == "many_waves":
+        monkeypatch.setenv("KCMM_ATTN_WAVES", "4096")
+        monkeypatch.setenv("KCMM_ATTN_MIN_TILES", "1")
+    return request.param
+
+
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_F16])
+def test_stream_settings_ragged(gpu_lib, stream_tuning, dtype):
+    ctx = [0, 1, 33, 4100, 31, 32, 64, 2049, -1, 700, 17, 1500]
+    case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=dtype, seed=9)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+def test_many_short_sequences(gpu_lib, stream_tuning):
+    """130 sequences (three 64-lane chunks of the slice lookup) of 0..40
+    tokens: most (b, kv head) pairs are a single tile, so the query rows
+    switch at nearly every tile."""
+    rng = np.random.default_rng(10)
+    ctx = rng.integers(-2, 41, size=130)
+    ctx[[0, 64, 65, 129]] = 0
+    case = build_decode_case(gpu_lib, batch=130, num_q_heads=16, kv_heads=4, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=10)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+def test_head_dim_64_stream(gpu_lib, stream_tuning):
+    rng = np.random.default_rng(11)
+    ctx = rng.integers(1, 900, size=9)
+    case = build_decode_case(gpu_lib, batch=9, num_q_heads=8, kv_heads=8, head_dim=64,
+                             block_size=16, ctx_lens=ctx, dtype=KV_F16, seed=11)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+def test_nan_in_unused_page_rows(gpu_lib):
+    """Rows of a sequence's last page past seq_len may hold any bits; they
+    must not reach the output (the kernel reads whole 8-token groups)."""
+    ctx = [5, 17, 40, 100, 1]
+    case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=12)
+    try:
+        g = case.geometry
+        nan_row = np.full(g["row_bytes"] // 2, 0x7FC1, dtype=np.uint16)
+        for b, L in enumerate(ctx):
+            last = (L - 1) // 16
+            page = int(case.offsets_f16[case.block_tables[b, last]]) * 2
+            for slot in range(L - last * 16, 16):
+                off = page + slot * g["row_bytes"]
+                memcpy_htod(case.pool.va_k(0) + off, nan_row)
+                memcpy_htod(case.pool.va_v(0) + off, nan_row)
+        check(case)
     finally:
         case.pool.destroy()
 
