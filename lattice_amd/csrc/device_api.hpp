@@ -20,7 +20,7 @@ std::unique_ptr<PageBacking> make_backing(int device, std::string* err);
 bool set_device(int device, std::string* err);
 
 // Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
-// attention partials, 1: GEMM partials, 2: decode attention counters).
+// attention partials, 1: GEMM partials, 2: decode attention segment table).
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);

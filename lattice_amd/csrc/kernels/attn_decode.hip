@@ -48,6 +48,7 @@ struct AttnParams {
     const uint64_t* offsets_f16;
     float* part_acc;        // [waves][2][G][D]  (slot 0: head of slice, 1: tail)
     float* part_ml;         // [waves][2][G][2]  (max in log2 units, denominator)
+    int2* seg_info;         // [B][Hkv]: (first wave, waves) of each (b, g); waves <= 1: no merge
     int batch, num_q_heads, kv_heads, group, block_size, mbps;
     int row_bytes, data_bytes;
     int total_waves;        // grid of the streaming kernel (one wave per workgroup)
@@ -269,7 +270,17 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     }
     total = __builtin_amdgcn_readfirstlane(total);
     const int per = wave_slice(total, p);
-    const int t0 = static_cast<int>(blockIdx.x) * per;
+
+    // sequences without tokens: zero rows, nothing to merge
+    for (int bb = blockIdx.x; bb < p.batch; bb += gridDim.x) {
+        if (clamp_len(sl[bb], cap) > 0) continue;
+        uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + static_cast<size_t>(bb) * p.num_q_heads * D;
+        for (int e = lane; e < p.num_q_heads * D; e += 64) o[e] = 0;
+        if (lane < Hkv) p.seg_info[bb * Hkv + lane] = int2{0, 0};
+    }
+
+    const int slice = static_cast<int>(blockIdx.x);
+    const int t0 = slice * per;
     if (t0 >= total) return;
     const int n = min(per, total - t0);
 
@@ -380,9 +391,15 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
 
     // Segment end: normalise and store, or leave a partial in slot
     // 0 (segment began in an earlier slice) / 1 (continues in a later one).
-    auto flush = [&](const Cur& c, bool began_here) {
+    auto flush = [&](const Cur& c, bool began_here, int i) {
         const float l = wave_sum_across_groups(l_run);
         const bool complete = began_here && c.t == c.nt - 1;
+        if (began_here && lane == 0) {
+            // the wave where (b, g) begins tells the merge where its parts are
+            const int first = t0 + i - c.t;
+            const int waves = complete ? 1 : (first + c.nt - 1) / per - slice + 1;
+            p.seg_info[c.b * Hkv + c.g] = int2{slice, waves};
+        }
         if (ln < G) {
             if (complete) {
                 const float inv = 1.0f / l;
@@ -396,7 +413,7 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
                     *reinterpret_cast<u32x2*>(o + 16 * db) = w;
                 }
             } else {
-                const size_t unit = static_cast<size_t>(blockIdx.x) * 2 + (began_here ? 1 : 0);
+                const size_t unit = static_cast<size_t>(slice) * 2 + (began_here ? 1 : 0);
                 float* pa = p.part_acc + (unit * G + ln) * D + 4 * lg;
 #pragma unroll
                 for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(pa + 16 * db) = acc[db];
@@ -479,7 +496,7 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
                 }
             }
             compute_tile<DT, D>(now, qf, esel, tbase, c.L, p.scale_log2, m_run, l_run, acc, lg);
-            if (i == n - 1 || c.t == c.nt - 1) flush(c, began_here);
+            if (i == n - 1 || c.t == c.nt - 1) flush(c, began_here, i);
             if (i + 1 < n && cq[(j + 1) % P].t == 0) {
                 // a new (b, g) starts with tile i+1
                 if constexpr (P > 2) q_ready = true;
@@ -496,76 +513,94 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     }
 }
 
-constexpr int kMaxMergeParts = 256;  // partial weights the merge kernel stages in LDS
-
-// Log-sum-exp merge, one workgroup per (b, kv head): a (b, g) whose tiles
-// span waves wa..wb has partials in wave wa's slot 1 and in slot 0 of waves
-// wa+1..wb.  Also writes the zeros of sequences with no tokens.
-template <int DT, int D, int BS>
-__global__ __launch_bounds__(256) void attn_decode_merge(AttnParams p,
-                                                         const int32_t* __restrict__ sl) {
-    __shared__ float wgt[kMaxMergeParts * 16];
-    __shared__ float gmax[16];
-    __shared__ float inv_l[16];
-    __shared__ int red[2][4];
-    const int bs = BS > 0 ? BS : p.block_size;
-    const int cap = p.mbps * bs;
-    const int Hkv = p.kv_heads;
+// Log-sum-exp merge, one wave per (b, kv head) that spans several waves of
+// the streaming kernel: its partials sit in slot 1 of its first wave wa and
+// in slot 0 of waves wa+1 .. wa+np-1.  All (max, denominator) pairs of up to
+// 64 parts are read at once (one part per lane); the weights go through LDS.
+// NO = outputs per lane rounded up to a power of two; every load is issued
+// unconditionally (clamped index) so that none waits behind a branch.
+template <int DT, int D, int NO>
+__global__ __launch_bounds__(64) void attn_decode_merge(AttnParams p,
+                                                        const int2* __restrict__ info) {
+    constexpr int NJ = NO * 64 / D > 0 ? NO * 64 / D : 1;  // heads covered (power of two)
+    __shared__ float sw[64 * NJ];
+    const int2 si = info[blockIdx.x];
+    const int wa = si.x, np = si.y;
+    if (np <= 1) return;
+    const int lane = threadIdx.x;
     const int G = p.group;
-    const int kvh = blockIdx.x % Hkv;
-    const int b = blockIdx.x / Hkv;
-    int before = 0, total = 0;
-    for (int i = threadIdx.x; i < p.batch; i += 256) {
-        const int v = Hkv * tiles_of(clamp_len(sl[i], cap));
-        total += v;
-        if (i < b) before += v;
-    }
-    before = wave_sum(before);
-    total = wave_sum(total);
-    if ((threadIdx.x & 63) == 0) {
-        red[0][threadIdx.x >> 6] = before;
-        red[1][threadIdx.x >> 6] = total;
-    }
-    __syncthreads();
-    before = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-    total = red[1][0] + red[1][1] + red[1][2] + red[1][3];
-    const int nt = tiles_of(clamp_len(sl[b], cap));
-    uint16_t* out_bh = reinterpret_cast<uint16_t*>(p.out) +
-                       (static_cast<size_t>(b) * p.num_q_heads + kvh * G) * D;
-    if (nt == 0) {
-        for (int i = threadIdx.x; i < G * D; i += 256) out_bh[i] = 0;
-        return;
-    }
-    const int per = wave_slice(total, p);
-    const int s = before + kvh * nt;
-    const int wa = s / per;
-    const int np = (s + nt - 1) / per - wa + 1;
-    if (np == 1) return;  // written by its wave
-    const float* ml = p.part_ml;
-    const float* pa = p.part_acc;
+    const int b = blockIdx.x / p.kv_heads;
+    const int g = blockIdx.x - b * p.kv_heads;
+    const int n_out = G * D / 64;      // lane holds outputs lane + 64e, e < n_out
     auto unit = [&](int k) { return static_cast<size_t>(wa + k) * 2 + (k == 0 ? 1 : 0); };
-    for (int j = threadIdx.x; j < G; j += 256) {
-        float M = -INFINITY;
-        for (int k = 0; k < np; ++k) M = fmaxf(M, ml[(unit(k) * G + j) * 2]);
-        float l = 0.0f;
-        for (int k = 0; k < np; ++k) {
-            const float w = __builtin_amdgcn_exp2f(ml[(unit(k) * G + j) * 2] - M);
-            if (k < kMaxMergeParts) wgt[k * 16 + j] = w;
-            l += w * ml[(unit(k) * G + j) * 2 + 1];
+
+    float mx[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) mx[j] = -INFINITY;
+    for (int k0 = 0; k0 < np; k0 += 64) {
+        const int k = min(k0 + lane, np - 1);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            mx[j] = fmaxf(mx[j], p.part_ml[(unit(k) * G + min(j, G - 1)) * 2]);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx[j] = fmaxf(mx[j], __shfl_xor(mx[j], o));
+
+    float ls[NJ], acc[NO];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) ls[j] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < NO; ++e) acc[e] = 0.0f;
+    for (int k0 = 0; k0 < np; k0 += 64) {
+        const bool live = k0 + lane < np;
+        const int k = min(k0 + lane, np - 1);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const size_t u = (unit(k) * G + min(j, G - 1)) * 2;
+            const float w = live ? __builtin_amdgcn_exp2f(p.part_ml[u] - mx[j]) : 0.0f;
+            ls[j] += w * p.part_ml[u + 1];
+            sw[lane * NJ + j] = w;
         }
-        gmax[j] = M;
-        inv_l[j] = 1.0f / l;
+        __syncthreads();
+        const int kn = min(64, np - k0);
+#pragma unroll 4
+        for (int kk = 0; kk < kn; ++kk) {
+            const float* pa = p.part_acc + unit(k0 + kk) * G * D + lane;
+#pragma unroll
+            for (int e = 0; e < NO; ++e)
+                acc[e] += sw[kk * NJ + e * 64 / D] * pa[min(e, n_out - 1) * 64];
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    const int staged = min(np, kMaxMergeParts);
-    for (int i = threadIdx.x; i < G * D; i += 256) {
-        const int j = i / D;
-        float o = 0.0f;
-        for (int k = 0; k < staged; ++k) o += wgt[k * 16 + j] * pa[unit(k) * G * D + i];
-        for (int k = staged; k < np; ++k)
-            o += __builtin_amdgcn_exp2f(ml[(unit(k) * G + j) * 2] - gmax[j]) * pa[unit(k) * G * D + i];
-        out_bh[i] = static_cast<uint16_t>(f32_to_elem<DT>(o * inv_l[j]));
-    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ls[j] += __shfl_xor(ls[j], o);
+    uint16_t* out = reinterpret_cast<uint16_t*>(p.out) +
+                    (static_cast<size_t>(b) * p.num_q_heads + g * G) * D + lane;
+#pragma unroll
+    for (int e = 0; e < NO; ++e)
+        if (e < n_out) out[e * 64] = static_cast<uint16_t>(f32_to_elem<DT>(acc[e] / ls[e * 64 / D]));
+}
+
+template <int DT, int D>
+void launch_merge(AttnParams& p, hipStream_t s) {
+    const int n_out = p.group * D / 64;
+    const dim3 grid(p.batch * p.kv_heads), block(64);
+    if (n_out <= 1)
+        hipLaunchKernelGGL((attn_decode_merge<DT, D, 1>), grid, block, 0, s, p, p.seg_info);
+    else if (n_out <= 2)
+        hipLaunchKernelGGL((attn_decode_merge<DT, D, 2>), grid, block, 0, s, p, p.seg_info);
+    else if (n_out <= 4)
+        hipLaunchKernelGGL((attn_decode_merge<DT, D, 4>), grid, block, 0, s, p, p.seg_info);
+    else if (n_out <= 8)
+        hipLaunchKernelGGL((attn_decode_merge<DT, D, 8>), grid, block, 0, s, p, p.seg_info);
+    else if (n_out <= 16)
+        hipLaunchKernelGGL((attn_decode_merge<DT, D, 16>), grid, block, 0, s, p, p.seg_info);
+    else
+        hipLaunchKernelGGL((attn_decode_merge<DT, D, 32>), grid, block, 0, s, p, p.seg_info);
 }
 
 // Any-shape fallback (head_dim <= 256, any GQA map, any block size, fp8
@@ -685,6 +720,12 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
     const uint8_t* idle = static_cast<const uint8_t*>(ws);
     p.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + idle_bytes);
     p.part_acc = p.part_ml + units * 2;
+    void* info = nullptr;
+    if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 2,
+                               static_cast<size_t>(p.batch) * p.kv_heads * sizeof(int2), &info,
+                               false, err))
+        return false;
+    p.seg_info = static_cast<int2*>(info);
     if (stream_depth() == 3)
         hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 3>), dim3(p.total_waves), dim3(64), 0, s,
                            p, p.block_tables, p.seq_lens, p.offsets_f16, idle);
@@ -692,8 +733,7 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
         hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 2>), dim3(p.total_waves), dim3(64), 0, s,
                            p, p.block_tables, p.seq_lens, p.offsets_f16, idle);
     KCMM_HIP_CHECK(hipGetLastError(), err);
-    hipLaunchKernelGGL((attn_decode_merge<DT, D, BS>), dim3(p.batch * p.kv_heads), dim3(256), 0, s,
-                       p, p.seq_lens);
+    launch_merge<DT, D>(p, s);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     return true;
 }
