@@ -16,6 +16,12 @@ Printed JSON: `value` is decode-attention KV GB/s (algorithmic K+V bytes of
 one layer-step / attention call time); decode tokens/s = 64 / (32 * t_layer)
 with t_layer the sum of the six calls (lm_head, sampling, norms, RoPE and
 SwiGLU glue are not in this path and are excluded).
+
+`roofline` prices the attention call (streaming kernel + log-sum-exp merge,
+timed by HIP events on the launch stream) against MI355X's 8 TB/s; its
+`traffic` (HBM bytes per call) is read from the rocprofv3 FETCH_SIZE /
+WRITE_SIZE summary committed in profiles/, which records the commands and the
+copy-kernel calibration it was scaled with.
 """
 from __future__ import annotations
 
@@ -57,6 +63,21 @@ def parse():
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "attn_decode_cfg2_hbm_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per attention call from the committed rocprofv3 counter
+    summary (None if the file is absent)."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_call:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
@@ -225,8 +246,10 @@ def main():
         "attn_us_per_layer_step": round(per["attn"] * 1e3, 2),
         "kv_bytes_per_layer_step": kv_bytes,
         "roofline": {"bound": "hbm", "achieved": round(kv_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(kv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "paged decode attention call (attn_decode_mfma + split merge)"},
+                     "unit": "GB/s", "frac": round(kv_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": "paged decode attention call (attn_decode_stream + attn_decode_merge)",
+                     "algorithmic_bytes": kv_bytes},
         "append_us": round(per["append"] * 1e3, 2),
         "wall_s_timed": round(wall, 3),
     }
