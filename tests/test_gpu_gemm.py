@@ -53,3 +53,23 @@ def test_llama3_8b_projections(gpu_lib, m, n, k):
     err = float((y - ref).abs().max() / ref.abs().max())
     print(f"gemm {m}x{n}x{k} err={err:.3e}", flush=True)
     assert err <= 1e-2
+
+
+@pytest.mark.parametrize("target", ["1", "64", "256", "100000"])
+@pytest.mark.parametrize("m,n,k", [(1, 128, 256), (17, 384, 512), (33, 1280, 2304),
+                                   (64, 256, 14336), (64, 6144, 4096), (48, 64, 1024)])
+def test_split_k_choices(gpu_lib, monkeypatch, target, m, n, k):
+    """The K split chosen for a target workgroup count (1 = never split,
+    100000 = as many splits as chunks allow) gives the same product: split
+    partials and their reduction are exact up to fp32 rounding."""
+    import torch
+    monkeypatch.setenv("KCMM_GEMM_WGS", target)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m * 31 + n + k + len(target))
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    y = run(gpu_lib, x, w).float()
+    ref = x.float() @ w.float().t()
+    err = float((y - ref).abs().max() / ref.abs().max())
+    print(f"gemm target={target} {m}x{n}x{k} err={err:.3e}", flush=True)
+    assert err <= 1e-2
