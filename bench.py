@@ -60,6 +60,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-shuffle", action="store_true",
                     help="give each sequence contiguous pages (locality experiment)")
+    ap.add_argument("--config", choices=["cfg2", "cfg5"], default="cfg2",
+                    help="cfg2: the headline bf16 decode layer-step; cfg5: fp8-e4m3 pages, "
+                         "B=128, ctx 80%% U[1024,8192] + 20%% U[16384,32768] (attention only)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
     return ap.parse_args()
@@ -133,11 +136,20 @@ def main():
     assert torch.cuda.is_available(), "bench needs a GPU"
     lib = KcmmLibrary()
     rng = np.random.default_rng(args.seed)
-    ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B)          # context before the appended token
+    global B
+    kv_dtype = KV_BF16
+    if args.config == "cfg5":
+        from lattice_amd.bindings import KV_FP8
+        B, kv_dtype, args.attn_only = 128, KV_FP8, True
+        args.layers = min(args.layers, 2)
+        long = rng.random(B) < 0.2
+        ctx = np.where(long, rng.integers(16384, 32769, size=B), rng.integers(1024, 8193, size=B))
+    else:
+        ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B)      # context before the appended token
     L = ctx + 1
     t0 = time.perf_counter()
     case = build_decode_case(lib, batch=B, num_q_heads=HQ, kv_heads=HKV, head_dim=D,
-                             block_size=BS, ctx_lens=L, dtype=KV_BF16, num_layers=args.layers,
+                             block_size=BS, ctx_lens=L, dtype=kv_dtype, num_layers=args.layers,
                              seed=args.seed + 1, host_mirror=False,
                              shuffle=not args.no_shuffle)
     log(f"workload built in {time.perf_counter() - t0:.1f}s: {case.pool.stats()['superblock_count']} "
@@ -235,13 +247,17 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "bf16" if args.config == "cfg2" else "fp8-e4m3 KV, bf16 MFMA",
         "data": "synthetic (seeded N(0,1) K/V, N(0,0.02) weights; no checkpoint)",
-        "config": {"workload": "llama3-8b-shape decode layer-step: paged attention + KV append "
-                               "+ QKV/O/gate_up/down GEMMs",
+        "config": {"workload": ("llama3-8b-shape decode layer-step: paged attention + KV append "
+                                "+ QKV/O/gate_up/down GEMMs") if args.config == "cfg2" else
+                               "cfg5: fp8-e4m3 paged decode attention + KV append, long-tail ctx",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "block_size": BS,
-                   "ctx": f"U[{CTX_LO},{CTX_HI}]+1", "mean_len": float(L.mean()),
-                   "kv_sets_cycled": args.layers, "kv_dtype": "bf16"},
+                   "ctx": f"U[{CTX_LO},{CTX_HI}]+1" if args.config == "cfg2" else
+                          "80% U[1024,8192] + 20% U[16384,32768], +1",
+                   "mean_len": float(L.mean()),
+                   "kv_sets_cycled": args.layers,
+                   "kv_dtype": "bf16" if args.config == "cfg2" else "fp8-e4m3 (page scales)"},
         "kv_frac_of_hbm_peak": round(kv_gbs / HBM_PEAK_GBS, 4),
         "attn_us_per_layer_step": round(per["attn"] * 1e3, 2),
         "kv_bytes_per_layer_step": kv_bytes,

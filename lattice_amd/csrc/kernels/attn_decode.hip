@@ -221,6 +221,110 @@ __device__ __forceinline__ void compute_tile(const Tile<D / 32>& t, const u32x4*
     }
 }
 
+// Eight e4m3 values (two dwords) -> eight bf16, exactly (every e4m3 value
+// is a bf16 value); the page scale is applied outside, in fp32.
+__device__ __forceinline__ u32x4 fp8x8_to_bf16(uint32_t d0, uint32_t d1) {
+    u32x4 r;
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, true));
+    return r;
+}
+
+// fp8 page tile (head_dim 128): t.k[h][0] holds bytes 16lg..16lg+15 and
+// t.k[h][1] bytes 64+16lg..+15 of token 16h + ln's head row.  MFMA k-step kc
+// takes the eight elements at (kc>>1)*64 + (kc&1)*8 + 16lg; Q is read in the
+// same order.  S is scaled by the K scale of each token's (page, kv head),
+// P by the V scale before the PV product (l uses the unscaled P), so the
+// result equals attention over the dequantized pages.  acc[db] then holds
+// the dims given by fp8_dim_offset.
+__device__ __forceinline__ void compute_tile_fp8(const Tile<2>& t, const u32x4* qf,
+                                                 const u32x4* esel, int tbase, int L,
+                                                 float scale_log2, const float* ks,
+                                                 const float* vs, float& m_run, float& l_run,
+                                                 f32x4* acc, int lg) {
+    f32x4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        s[h] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+            const u32x4& raw = t.k[h][kc >> 1];
+            const u32x4 a = (kc & 1) ? fp8x8_to_bf16(raw[2], raw[3]) : fp8x8_to_bf16(raw[0], raw[1]);
+            s[h] = mfma16x16x32<kDtBF16>(a, qf[kc], s[h]);
+        }
+    }
+    // rows 4lg + r of half h are tokens of 8-token group 2h (lg < 2) or 2h+1
+    float sv[8];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float kscale = (lg < 2 ? ks[2 * h] : ks[2 * h + 1]) * scale_log2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = tbase + h * 16 + lg * 4 + r;
+            const float x = tok < L ? s[h][r] * kscale : -INFINITY;
+            sv[h * 4 + r] = x;
+            mt = fmaxf(mt, x);
+        }
+    }
+    mt = wave_max_across_groups(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+    float pv[8];
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_new);
+        psum += pv[i];
+    }
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= corr;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float vscale = lg < 2 ? vs[2 * h] : vs[2 * h + 1];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pv[h * 4 + r] *= vscale;
+    }
+    u32x4 pf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        pf[i] = f32_to_elem<kDtBF16>(pv[2 * i]) | (f32_to_elem<kDtBF16>(pv[2 * i + 1]) << 16);
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+        const u32x4& r0 = t.v[0][kc >> 1];
+        const u32x4& r1 = t.v[1][kc >> 1];
+        const u32x4 f0 = (kc & 1) ? fp8x8_to_bf16(r0[2], r0[3]) : fp8x8_to_bf16(r0[0], r0[1]);
+        const u32x4 f1 = (kc & 1) ? fp8x8_to_bf16(r1[2], r1[3]) : fp8x8_to_bf16(r1[0], r1[1]);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const f32x4 v0 = mfma16x16x32<kDtBF16>(f0, esel[sub], f32x4{0, 0, 0, 0});
+            const f32x4 v1 = mfma16x16x32<kDtBF16>(f1, esel[sub], f32x4{0, 0, 0, 0});
+            u32x4 va;
+            va[0] = pack_exact<kDtBF16>(v0[0], v0[1]);
+            va[1] = pack_exact<kDtBF16>(v0[2], v0[3]);
+            va[2] = pack_exact<kDtBF16>(v1[0], v1[1]);
+            va[3] = pack_exact<kDtBF16>(v1[2], v1[3]);
+            acc[2 * kc + sub] = mfma16x16x32<kDtBF16>(va, pf, acc[2 * kc + sub]);
+        }
+    }
+}
+
+// First of the four consecutive dims that lane group lg holds in acc[db]
+// (rows 4lg .. 4lg+3 of the O^T block).
+template <bool F8>
+__device__ __forceinline__ int dim_offset(int db, int lg) {
+    if constexpr (F8) {
+        const int kc = db >> 1, sub = db & 1;
+        return (kc >> 1) * 64 + (kc & 1) * 8 + 32 * sub + 4 * lg + (lg >= 2 ? 8 : 0);
+    } else {
+        return 16 * db + 4 * lg;
+    }
+}
+
 // Streaming decode attention: one wave per workgroup, each on the slice
 // [gw*per, gw*per + per) of the b-major tile list, with P tiles in flight.
 // Read-only tables come as separate restrict arguments so that wave-uniform
@@ -232,10 +336,16 @@ template <int DT, int D, int BS, int P>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P == 2 ? 2 : 1)))
 void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
                         const int32_t* __restrict__ sl, const uint64_t* __restrict__ offs,
+                        const uint8_t* __restrict__ kreg, const uint8_t* __restrict__ vreg,
                         const uint8_t* __restrict__ idle) {
-    constexpr int KC = D / 32;
-    constexpr int LINES = D / 64;
+    constexpr bool F8 = DT == kDtFP8;
+    constexpr int MDT = F8 ? kDtBF16 : DT;     // MFMA, q and out element type
+    constexpr int EB = F8 ? 1 : 2;             // bytes per K/V element
+    constexpr int KC = D / 32;                 // MFMA k-steps per 16-token half
+    constexpr int LINES = D * EB / 128;        // 128-byte lines per head row
+    constexpr int TK = 2 * LINES;              // loaded fragments per half
     constexpr int DB = D / 16;
+    static_assert(!F8 || D == 128, "fp8 pages take the streaming path at head_dim 128");
     const int lane = threadIdx.x;
     const int ln = lane & 15;
     const int lg = lane >> 4;
@@ -315,6 +425,7 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     // Cursor over the tile list: (sequence, kv head, tile, length, tiles).
     struct Cur {
         int b, g, t, L, nt;
+        float ks[F8 ? 4 : 1], vs[F8 ? 4 : 1];   // fp8: page scales of the 8-token groups
     };
     Cur ic;  // next tile to issue
     ic.b = __builtin_amdgcn_readfirstlane(b);
@@ -342,23 +453,29 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     };
     // Page-relative byte address of each 8-token group of a tile; groups past
     // the sequence re-read its last group (masked).
-    auto group_bases = [&](const Cur& c, uint64_t* gb) {
+    // (fp8: also reads the groups' K / V page scales, a tile ahead of use)
+    auto group_bases = [&](Cur& c, uint64_t* gb) {
         const int last8 = (c.L - 1) & ~7;
         const int32_t* row = bt + static_cast<size_t>(c.b) * p.mbps;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int tok = min(c.t * 32 + q * 8, last8);
             const int lb = tok / bs;
-            gb[q] = offs[row[lb]] * 2ull +
-                    static_cast<uint32_t>((tok - lb * bs) * p.row_bytes + c.g * D * 2);
+            const uint64_t page = offs[row[lb]] * 2ull;
+            gb[q] = page + static_cast<uint32_t>((tok - lb * bs) * p.row_bytes + c.g * D * EB);
+            if constexpr (F8) {
+                const uint64_t sc = page + static_cast<uint32_t>(p.data_bytes + c.g * 4);
+                c.ks[q] = *reinterpret_cast<const float*>(kreg + sc);
+                c.vs[q] = *reinterpret_cast<const float*>(vreg + sc);
+            }
         }
     };
 
     const uint32_t lo = static_cast<uint32_t>((ln & 7) * p.row_bytes + ((ln >> 3) * 4 + lg) * 16);
     const bool low8 = ln < 8;
-    auto issue = [&](Tile<KC>& tl, bool real, const uint64_t* gb) {
-        const uint8_t* kb = real ? p.k_base : idle;
-        const uint8_t* vb = real ? p.v_base : idle;
+    auto issue = [&](Tile<TK>& tl, bool real, const uint64_t* gb) {
+        const uint8_t* kb = real ? kreg : idle;
+        const uint8_t* vb = real ? vreg : idle;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -378,11 +495,13 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
         const uint8_t* qrow = p.q + (static_cast<size_t>(c.b) * p.num_q_heads + c.g * G +
                                      min(ln, G - 1)) * D * 2;
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc)
-            qd[kc] = *reinterpret_cast<const u32x4*>(qrow + (kc * 32 + lg * 8) * 2);
+        for (int kc = 0; kc < KC; ++kc) {
+            const int e0 = F8 ? (kc >> 1) * 64 + (kc & 1) * 8 + 16 * lg : kc * 32 + lg * 8;
+            qd[kc] = *reinterpret_cast<const u32x4*>(qrow + e0 * 2);
+        }
     };
 
-    const u32x4 esel[2] = {select_operand<DT>(0, ln, lg), select_operand<DT>(1, ln, lg)};
+    const u32x4 esel[2] = {select_operand<MDT>(0, ln, lg), select_operand<MDT>(1, ln, lg)};
     float m_run = -INFINITY;  // running max (log2 domain) of column ln
     float l_run = 0.0f;       // this lane's share of the softmax denominator
     f32x4 acc[DB];
@@ -404,19 +523,20 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
             if (complete) {
                 const float inv = 1.0f / l;
                 uint16_t* o = reinterpret_cast<uint16_t*>(p.out) +
-                              (static_cast<size_t>(c.b) * p.num_q_heads + c.g * G + ln) * D + 4 * lg;
+                              (static_cast<size_t>(c.b) * p.num_q_heads + c.g * G + ln) * D;
 #pragma unroll
                 for (int db = 0; db < DB; ++db) {
                     u32x2 w;
-                    w[0] = f32_to_elem<DT>(acc[db][0] * inv) | (f32_to_elem<DT>(acc[db][1] * inv) << 16);
-                    w[1] = f32_to_elem<DT>(acc[db][2] * inv) | (f32_to_elem<DT>(acc[db][3] * inv) << 16);
-                    *reinterpret_cast<u32x2*>(o + 16 * db) = w;
+                    w[0] = f32_to_elem<MDT>(acc[db][0] * inv) | (f32_to_elem<MDT>(acc[db][1] * inv) << 16);
+                    w[1] = f32_to_elem<MDT>(acc[db][2] * inv) | (f32_to_elem<MDT>(acc[db][3] * inv) << 16);
+                    *reinterpret_cast<u32x2*>(o + dim_offset<F8>(db, lg)) = w;
                 }
             } else {
                 const size_t unit = static_cast<size_t>(slice) * 2 + (began_here ? 1 : 0);
-                float* pa = p.part_acc + (unit * G + ln) * D + 4 * lg;
+                float* pa = p.part_acc + (unit * G + ln) * D;
 #pragma unroll
-                for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(pa + 16 * db) = acc[db];
+                for (int db = 0; db < DB; ++db)
+                    *reinterpret_cast<f32x4*>(pa + dim_offset<F8>(db, lg)) = acc[db];
                 if (lg == 0) {
                     p.part_ml[(unit * G + ln) * 2 + 0] = m_run;
                     p.part_ml[(unit * G + ln) * 2 + 1] = l;
@@ -434,7 +554,7 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     // tile i+P are being fetched ----
     u32x4 qf[KC];
     Cur cq[P];
-    Tile<KC> buf[P];
+    Tile<TK> buf[P];
     uint64_t gb[4];
     load_q(qf, ic);
     bool began_here = ic.t == 0;
@@ -475,7 +595,7 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
         __builtin_amdgcn_sched_barrier(0);
         if (i < n) {
             const Cur c = cq[j];
-            Tile<KC>& now = buf[j];
+            Tile<TK>& now = buf[j];
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -491,11 +611,15 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
                 for (int h = 0; h < 2; ++h) {
                     const bool dead = tbase + h * 16 + ln >= c.L;
 #pragma unroll
-                    for (int kc = 0; kc < KC; ++kc)
+                    for (int kc = 0; kc < TK; ++kc)
                         if (dead) now.v[h][kc] = u32x4{0, 0, 0, 0};
                 }
             }
-            compute_tile<DT, D>(now, qf, esel, tbase, c.L, p.scale_log2, m_run, l_run, acc, lg);
+            if constexpr (F8)
+                compute_tile_fp8(now, qf, esel, tbase, c.L, p.scale_log2, c.ks, c.vs, m_run, l_run,
+                                 acc, lg);
+            else
+                compute_tile<DT, D>(now, qf, esel, tbase, c.L, p.scale_log2, m_run, l_run, acc, lg);
             if (i == n - 1 || c.t == c.nt - 1) flush(c, began_here, i);
             if (i + 1 < n && cq[(j + 1) % P].t == 0) {
                 // a new (b, g) starts with tile i+1
@@ -691,15 +815,21 @@ int env_int(const char* name, int dflt, int lo, int hi) {
 }
 
 // Tunables, read on every call (getenv is cheap next to a launch):
-// KCMM_ATTN_WAVES waves of the streaming kernel, KCMM_ATTN_MIN_TILES the
+// KCMM_ATTN_WAVES waves of the streaming kernel (default by page type), KCMM_ATTN_MIN_TILES the
 // smallest slice a wave takes, KCMM_ATTN_DEPTH tiles in flight (2 or 3).
-int stream_waves() { return env_int("KCMM_ATTN_WAVES", 1024, 1, 1 << 20); }
+// fp8 tiles carry half the bytes of 16-bit ones and use fewer registers
+// (3 waves per SIMD fit), so they need more waves to keep as many bytes in
+// flight (measured at the Llama-3-8B shape: 1024 waves best for 16-bit
+// pages, 3072 for fp8).
+int stream_waves(int dtype) {
+    return env_int("KCMM_ATTN_WAVES", dtype == kDtFP8 ? 3072 : 1024, 1, 1 << 20);
+}
 int stream_min_tiles() { return env_int("KCMM_ATTN_MIN_TILES", 8, 1, 1 << 16); }
 int stream_depth() { return env_int("KCMM_ATTN_DEPTH", 2, 2, 3); }
 
 template <int DT, int D, int BS>
 bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
-    static_assert(D % 64 == 0, "head rows are whole 128-byte lines");
+    static_assert(D * (DT == kDtFP8 ? 1 : 2) % 128 == 0, "head rows are whole 128-byte lines");
     const long long cap = static_cast<long long>(p.mbps) * p.block_size;
     const long long tmax = static_cast<long long>(p.batch) * p.kv_heads * ((cap + 31) / 32);
     if (cap > INT_MAX || tmax > (1LL << 30)) {
@@ -709,7 +839,7 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
     if (p.batch == 0) return true;
     p.min_tiles = stream_min_tiles();
     const long long want = (tmax + p.min_tiles - 1) / p.min_tiles;
-    p.total_waves = static_cast<int>(std::max(1LL, std::min<long long>(stream_waves(), want)));
+    p.total_waves = static_cast<int>(std::max(1LL, std::min<long long>(stream_waves(DT), want)));
     const size_t units = static_cast<size_t>(p.total_waves) * 2 * p.group;
     // idle-load region first: it must cover one tile's lane addresses
     const size_t idle_bytes = (static_cast<size_t>(8) * p.row_bytes + 1023) & ~static_cast<size_t>(255);
@@ -728,12 +858,12 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
     p.seg_info = static_cast<int2*>(info);
     if (stream_depth() == 3)
         hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 3>), dim3(p.total_waves), dim3(64), 0, s,
-                           p, p.block_tables, p.seq_lens, p.offsets_f16, idle);
+                           p, p.block_tables, p.seq_lens, p.offsets_f16, p.k_base, p.v_base, idle);
     else
         hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 2>), dim3(p.total_waves), dim3(64), 0, s,
-                           p, p.block_tables, p.seq_lens, p.offsets_f16, idle);
+                           p, p.block_tables, p.seq_lens, p.offsets_f16, p.k_base, p.v_base, idle);
     KCMM_HIP_CHECK(hipGetLastError(), err);
-    launch_merge<DT, D>(p, s);
+    launch_merge<DT == kDtFP8 ? kDtBF16 : DT, D>(p, s);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     return true;
 }
@@ -774,14 +904,15 @@ bool attn_decode(const AttnDecodeArgs& a, std::string* err) {
     p.scale_log2 = a.scale * 1.4426950408889634f;
     hipStream_t s = reinterpret_cast<hipStream_t>(a.stream);
 
-    // Streaming MFMA path: 16-bit pages, whole GQA groups of at most 16 heads,
-    // head_dim 64 or 128, pages made of 8-token groups.
+    // Streaming MFMA path: whole GQA groups of at most 16 heads, pages made of
+    // 8-token groups; 16-bit pages at head_dim 64 or 128, fp8 pages at 128.
     const bool grouped = p.num_q_heads % p.kv_heads == 0 && p.group <= 16;
     const bool stream_dim = a.head_dim == 64 || a.head_dim == 128;
     const bool force_generic = std::getenv("KCMM_ATTN_GENERIC") != nullptr;
-    if (a.dtype != kDtFP8 && grouped && stream_dim && a.block_size % 8 == 0 && !force_generic) {
-        if (a.dtype == kDtF16) return launch_dt<kDtF16>(p, a.head_dim, s, err);
-        return launch_dt<kDtBF16>(p, a.head_dim, s, err);
+    if (grouped && a.block_size % 8 == 0 && !force_generic) {
+        if (a.dtype == kDtFP8 && a.head_dim == 128) return launch_stream_bs<kDtFP8, 128>(p, s, err);
+        if (a.dtype == kDtF16 && stream_dim) return launch_dt<kDtF16>(p, a.head_dim, s, err);
+        if (a.dtype == kDtBF16 && stream_dim) return launch_dt<kDtBF16>(p, a.head_dim, s, err);
     }
     const dim3 grid(a.batch * a.num_q_heads);
     switch (a.dtype) {

@@ -139,8 +139,6 @@ def build_decode_case(lib: KcmmLibrary, *, batch: int, num_q_heads: int, kv_head
                       shuffle: bool = True) -> DecodeCase:
     """Allocate pages for `ctx_lens` tokens per sequence (+ `extra_seq_len`
     page headroom), shuffle them over the pool, fill them and upload q."""
-    if dtype == KV_FP8 and not host_mirror:
-        raise ValueError("fp8 pools are filled through the host mirror")
     rng = np.random.default_rng(seed)
     ctx = np.asarray(ctx_lens, dtype=np.int64)
     max_len = int(max(1, ctx.max() + extra_seq_len))
@@ -185,26 +183,67 @@ def build_decode_case(lib: KcmmLibrary, *, batch: int, num_q_heads: int, kv_head
     return case
 
 
-def fill_regions_on_device(case: DecodeCase, seed: int) -> None:
-    """Fill every mapped byte of every region with N(0,1) 16-bit values
-    generated on the GPU (torch), for workloads too large for a host mirror."""
-    g = case.geometry
-    n = g["mapped_bytes"] // 2
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(seed)
-    tdt = torch.float16 if case.dtype == KV_F16 else torch.bfloat16
+def _region_copy(dst: int, src, nbytes: int) -> None:
     import ctypes
     from .bindings import hip
     h = hip()
     h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    rc = h.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src.data_ptr()), nbytes, 3)
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy D2D failed ({rc})")
+
+
+def fill_regions_on_device(case: DecodeCase, seed: int) -> None:
+    """Fill the regions on the GPU (torch), for workloads too large for a host
+    mirror: every mapped byte of a 16-bit pool with N(0,1) values; every
+    allocated page of an fp8 pool with N(0,1) rows quantized per (page, kv
+    head) exactly as encode_fp8_page does (scale = amax/448, e4m3fn RNE),
+    scales in the page footer."""
+    g = case.geometry
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    if case.dtype == KV_FP8:
+        _fill_fp8_on_device(case, gen)
+        torch.cuda.synchronize()
+        return
+    n = g["mapped_bytes"] // 2
+    tdt = torch.float16 if case.dtype == KV_F16 else torch.bfloat16
     for layer in range(case.num_layers):
         for base in (case.pool.va_k(layer), case.pool.va_v(layer)):
             chunk = 64 << 20
             for off in range(0, n, chunk):
                 m = min(chunk, n - off)
                 t = torch.randn(m, generator=gen, device="cuda", dtype=torch.float32).to(tdt)
-                rc = h.hipMemcpy(ctypes.c_void_p(base + 2 * off), ctypes.c_void_p(t.data_ptr()),
-                                 2 * m, 3)
-                if rc != 0:
-                    raise RuntimeError(f"hipMemcpy D2D failed ({rc})")
+                _region_copy(base + 2 * off, t, 2 * m)
     torch.cuda.synchronize()
+
+
+def _fill_fp8_on_device(case: DecodeCase, gen) -> None:
+    g = case.geometry
+    bb, data_bytes = g["block_bytes"], g["data_bytes"]
+    hk, d, bs = case.kv_heads, case.head_dim, case.block_size
+    bps = SB // bb
+    ids = np.asarray([i for b in range(case.batch)
+                      for i in case.block_tables[b, :max(1, -(-int(case.seq_lens[b]) // bs))]],
+                     dtype=np.int64)
+    ids = np.unique(ids)
+    off = case.offsets_f16[ids].astype(np.int64) * 2
+    sb = torch.from_numpy(off // SB).cuda()
+    idx = torch.from_numpy((off % SB) // bb).cuda()
+    n_sb = g["mapped_bytes"] // SB
+    for layer in range(case.num_layers):
+        for base in (case.pool.va_k(layer), case.pool.va_v(layer)):
+            image = torch.zeros(g["mapped_bytes"], dtype=torch.uint8, device="cuda")
+            view = image.view(n_sb, SB)[:, :bps * bb].view(n_sb, bps, bb)
+            for c0 in range(0, len(ids), 4096):
+                c1 = min(len(ids), c0 + 4096)
+                x = torch.randn((c1 - c0, bs, hk, d), generator=gen, device="cuda")
+                amax = x.abs().amax(dim=(1, 3))
+                scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+                q8 = (x / scale[:, None, :, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+                page = torch.zeros((c1 - c0, bb), dtype=torch.uint8, device="cuda")
+                page[:, :data_bytes] = q8.reshape(c1 - c0, -1)
+                page[:, data_bytes:data_bytes + 4 * hk] = scale.contiguous().view(torch.uint8).reshape(c1 - c0, -1)
+                view[sb[c0:c1], idx[c0:c1]] = page
+            _region_copy(base, image, g["mapped_bytes"])
+            del image

@@ -108,11 +108,15 @@ def test_generic_path_shapes(gpu_lib, hq, hkv, d, bs):
         case.pool.destroy()
 
 
-def test_fp8_pages(gpu_lib):
-    rng = np.random.default_rng(5)
+@pytest.mark.parametrize("bs", [16, 32, 8])
+def test_fp8_pages(gpu_lib, bs):
+    """fp8-e4m3 pages (per (page, kv head) scales in the page footer) against
+    the oracle over the same dequantized pages; block sizes 16, 32 and 8
+    move the 8-token groups across page boundaries differently."""
+    rng = np.random.default_rng(5 + bs)
     ctx = rng.integers(1, 900, size=6)
     case = build_decode_case(gpu_lib, batch=6, num_q_heads=32, kv_heads=8, head_dim=128,
-                             block_size=16, ctx_lens=ctx, dtype=KV_FP8, seed=5)
+                             block_size=bs, ctx_lens=ctx, dtype=KV_FP8, seed=5)
     try:
         import torch
         case.dev["out"].fill_(float("nan"))
@@ -184,7 +188,7 @@ def stream_tuning(request, monkeypatch):
     return request.param
 
 
-@pytest.mark.parametrize("dtype", [KV_BF16, KV_F16])
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_F16, KV_FP8])
 def test_stream_settings_ragged(gpu_lib, stream_tuning, dtype):
     ctx = [0, 1, 33, 4100, 31, 32, 64, 2049, -1, 700, 17, 1500]
     case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
@@ -195,7 +199,8 @@ def test_stream_settings_ragged(gpu_lib, stream_tuning, dtype):
         case.pool.destroy()
 
 
-def test_many_short_sequences(gpu_lib, stream_tuning):
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_FP8])
+def test_many_short_sequences(gpu_lib, stream_tuning, dtype):
     """130 sequences (three 64-lane chunks of the slice lookup) of 0..40
     tokens: most (b, kv head) pairs are a single tile, so the query rows
     switch at nearly every tile."""
@@ -203,7 +208,7 @@ def test_many_short_sequences(gpu_lib, stream_tuning):
     ctx = rng.integers(-2, 41, size=130)
     ctx[[0, 64, 65, 129]] = 0
     case = build_decode_case(gpu_lib, batch=130, num_q_heads=16, kv_heads=4, head_dim=128,
-                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=10)
+                             block_size=16, ctx_lens=ctx, dtype=dtype, seed=10)
     try:
         check(case)
     finally:
@@ -221,15 +226,19 @@ def test_head_dim_64_stream(gpu_lib, stream_tuning):
         case.pool.destroy()
 
 
-def test_nan_in_unused_page_rows(gpu_lib):
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_FP8])
+def test_nan_in_unused_page_rows(gpu_lib, dtype):
     """Rows of a sequence's last page past seq_len may hold any bits; they
     must not reach the output (the kernel reads whole 8-token groups)."""
     ctx = [5, 17, 40, 100, 1]
     case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
-                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=12)
+                             block_size=16, ctx_lens=ctx, dtype=dtype, seed=12)
     try:
         g = case.geometry
-        nan_row = np.full(g["row_bytes"] // 2, 0x7FC1, dtype=np.uint16)
+        if dtype == KV_FP8:
+            nan_row = np.full(g["row_bytes"], 0x7F, dtype=np.uint8)      # e4m3 NaN
+        else:
+            nan_row = np.full(g["row_bytes"] // 2, 0x7FC1, dtype=np.uint16)
         for b, L in enumerate(ctx):
             last = (L - 1) // 16
             page = int(case.offsets_f16[case.block_tables[b, last]]) * 2
@@ -260,5 +269,28 @@ def test_full_llama3_8b_decode_shape(gpu_lib):
         err = rel_err(gpu_out(case), oracle_out(case, regions=(kreg, vreg)))
         print(f"full Cfg2 err={err:.3e}", flush=True)
         assert err <= TOL[KV_BF16]
+    finally:
+        case.pool.destroy()
+
+
+def test_fp8_device_filled_long_contexts(gpu_lib):
+    """fp8 pages quantized on the device (the Cfg5 fill) at a larger shape:
+    32 sequences of up to 6000 tokens, regions read back for the oracle."""
+    import torch
+    rng = np.random.default_rng(2025)
+    ctx = rng.integers(512, 6001, size=32)
+    ctx[3] = 16 * 7 + 1            # one page plus one token
+    case = build_decode_case(gpu_lib, batch=32, num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_FP8, seed=13,
+                             host_mirror=False)
+    try:
+        case.run_attention(stream_ptr=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        g = case.geometry
+        kreg = memcpy_dtoh(case.pool.va_k(0), g["mapped_bytes"])
+        vreg = memcpy_dtoh(case.pool.va_v(0), g["mapped_bytes"])
+        err = rel_err(gpu_out(case), oracle_out(case, regions=(kreg, vreg)))
+        print(f"fp8 device-filled err={err:.3e}", flush=True)
+        assert err <= TOL[KV_FP8]
     finally:
         case.pool.destroy()
