@@ -45,6 +45,7 @@ B, HQ, HKV, D, BS = 64, 32, 8, 128, 16
 CTX_LO, CTX_HI = 512, 4096
 MODEL_LAYERS = 32
 HIDDEN, INTER = 4096, 14336
+KV_BF16_CODE = 1
 GEMMS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
 
 
@@ -60,9 +61,11 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-shuffle", action="store_true",
                     help="give each sequence contiguous pages (locality experiment)")
-    ap.add_argument("--config", choices=["cfg2", "cfg5"], default="cfg2",
-                    help="cfg2: the headline bf16 decode layer-step; cfg5: fp8-e4m3 pages, "
-                         "B=128, ctx 80%% U[1024,8192] + 20%% U[16384,32768] (attention only)")
+    ap.add_argument("--config", choices=["cfg2", "cfg3", "cfg5"], default="cfg2",
+                    help="cfg2: the headline bf16 decode layer-step; cfg3: chunked prefill, "
+                         "16 seqs x 256-token chunk over a shared 1024-token prefix; cfg5: "
+                         "fp8-e4m3 pages, B=128, ctx 80%% U[1024,8192] + 20%% U[16384,32768] "
+                         "(attention only)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
     return ap.parse_args()
@@ -123,12 +126,57 @@ def cpu_baseline(case, seconds, threads):
                         f"{t * 1e3:.1f} ms per pass"))
 
 
+def bench_prefill(args):
+    """Cfg3: causal chunked prefill over shared-prefix pages; MFMA-bound."""
+    import torch
+    from lattice_amd.bindings import KcmmLibrary
+    from lattice_amd.workload import build_prefix_shared_case
+    lib = KcmmLibrary()
+    case = build_prefix_shared_case(lib, batch=16, prefix_tokens=1024, suffix_tokens=256,
+                                    chunk=256, num_q_heads=HQ, kv_heads=HKV, head_dim=D,
+                                    block_size=BS, dtype=KV_BF16_CODE, num_layers=args.layers,
+                                    seed=args.seed)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    for i in range(args.warmup):
+        case.run(layer=i % args.layers, stream_ptr=sp)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    ev[0].record(stream)
+    for i in range(args.steps):
+        case.run(layer=i % args.layers, stream_ptr=sp)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    ms = float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]))
+    flops = case.flops()
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"prefill per-call ms: {ms:.4f}, {flops / 1e9:.1f} GFLOP")
+    result = {
+        "metric": "chunked prefill attention TFLOP/s (% bf16 MFMA peak), 1 GPU",
+        "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "cfg3: 16 seqs share a refcounted 1024-token prefix + own 256 "
+                               "tokens; causal 256-token chunk each",
+                   "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "block_size": BS},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "gflop_per_call": round(flops / 1e9, 2),
+        "cpu_baseline": None,
+    }
+    case.pool.destroy()
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
                           "(multi-GPU sharding is described in DESIGN.md, not run)"}))
         sys.exit(2)
+    if args.config == "cfg3":
+        return bench_prefill(args)
     import torch
     from lattice_amd.bindings import KV_BF16, KcmmLibrary, make_config
     from lattice_amd.workload import build_decode_case

@@ -77,6 +77,27 @@ int kcmm_paged_attn_decode_fp8_on_stream(
     uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
     uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
 
+/* ---- chunked prefill attention ----------------------------------------- */
+
+/**
+ * Causal chunked-prefill attention over the pool's pages (the reference
+ * prefills one token per decode step, ref transformer.rs:50-65; this is the
+ * varlen-with-paged-KV form of vLLM's chunked prefill).  Sequence b holds
+ * seq_lens[b] cached tokens, the last (query_start_loc[b+1] -
+ * query_start_loc[b]) of which are this chunk's queries, already appended.
+ * Query i of b (row query_start_loc[b] + i of q/out, [rows][Hq][D]) is at
+ * position seq_lens[b] - len_b + i and attends to keys 0..position.  q/out
+ * are f16 for f16 pools and bf16 otherwise; seq_lens and query_start_loc are
+ * device int32 arrays; rows without a valid position are written as zeros.
+ * Enqueue only.
+ */
+int kcmm_paged_attn_prefill_on_stream(
+    kcmm_pool_t *pool, uint32_t layer_idx, uint64_t query_ptr, uint64_t out_ptr,
+    uint64_t block_tables_ptr, uint64_t seq_lens_ptr, uint64_t query_start_loc_ptr,
+    uint64_t block_offsets_f16_ptr, uint32_t batch, uint32_t total_query_tokens,
+    uint32_t num_q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
+    uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
+
 /* ---- copy-on-write fork ------------------------------------------------- */
 
 /** Fork `src_seq` (beam search): a new sequence holding the same block ids

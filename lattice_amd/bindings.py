@@ -123,6 +123,9 @@ SIGNATURES = {
     "kcmm_paged_attn_decode_bf16": (_ATTN, C.c_int),
     "kcmm_paged_attn_decode_bf16_on_stream": (_ATTN + [_U64], C.c_int),
     "kcmm_paged_attn_decode_fp8_on_stream": (_ATTN + [_U64], C.c_int),
+    "kcmm_paged_attn_prefill_on_stream": ([_P, _U32, _U64, _U64, _U64, _U64, _U64, _U64, _U32,
+                                           _U32, _U32, _U32, _U32, _U32, _U32, C.c_float, _U64],
+                                          C.c_int),
     "kcmm_precompile_paged_attn_decode_f16": ([_P], C.c_int),
     "kcmm_evict_blocks": ([_P, _U32], _U32),
     "kcmm_restore_evicted_block": ([_P, _U32], _U64),
@@ -372,6 +375,17 @@ class KcmmPool:
         else:
             rc = self.lib.kcmm_paged_attn_decode_fp8_on_stream(*args, stream_ptr or 0)
         self._check(rc, "paged_attn_decode")
+
+    def paged_attn_prefill(self, *, layer_idx, query_ptr, out_ptr, block_tables_ptr,
+                           seq_lens_ptr, query_start_loc_ptr, block_offsets_f16_ptr, batch,
+                           total_query_tokens, num_q_heads, kv_heads, head_dim, block_size,
+                           max_blocks_per_seq, scale, stream_ptr=0) -> None:
+        """Causal chunked prefill (q/out f16 for f16 pools, bf16 otherwise)."""
+        rc = self.lib.kcmm_paged_attn_prefill_on_stream(
+            self.handle, layer_idx, query_ptr, out_ptr, block_tables_ptr, seq_lens_ptr,
+            query_start_loc_ptr, block_offsets_f16_ptr, batch, total_query_tokens, num_q_heads,
+            kv_heads, head_dim, block_size, max_blocks_per_seq, C.c_float(scale), stream_ptr)
+        self._check(rc, "paged_attn_prefill")
 
     # -- copy-on-write --
     def fork_sequence(self, src: int) -> int:

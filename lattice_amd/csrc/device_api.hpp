@@ -41,6 +41,23 @@ struct AttnDecodeArgs {
 };
 bool attn_decode(const AttnDecodeArgs& a, std::string* err);
 
+// Causal chunked-prefill attention over one layer's K/V regions: sequence b's
+// last qsl[b+1]-qsl[b] cached tokens are the queries (rows qsl[b]..).
+struct AttnPrefillArgs {
+    int32_t dtype;            // pool dtype (kF16: f16 q/out; kBF16, kFP8: bf16 q/out)
+    uint64_t q, out;          // [total_query_tokens][num_q_heads][head_dim]
+    uint64_t k_base, v_base;
+    uint64_t block_tables;    // int32 [batch][mbps]
+    uint64_t seq_lens;        // int32 [batch], cached tokens including the chunk
+    uint64_t query_start_loc; // int32 [batch + 1]
+    uint64_t offsets_f16;
+    uint32_t batch, total_query_tokens, num_q_heads, kv_heads, head_dim, block_size, mbps;
+    uint32_t row_bytes, data_bytes;
+    float scale;
+    uint64_t stream;
+};
+bool attn_prefill(const AttnPrefillArgs& a, std::string* err);
+
 // KV append of host-resolved rows: source row r (elements of the pool dtype;
 // bf16 for fp8 pools) lands at page_offset + slot*row_bytes in both regions.
 struct KvRowsArgs {

@@ -558,6 +558,69 @@ int kcmm_paged_attn_decode_fp8_on_stream(KCMM_ATTN_ARGS, uint64_t stream) {
                      false, true);
 }
 
+int kcmm_paged_attn_prefill_on_stream(kcmm_pool_t* pool, uint32_t layer_idx, uint64_t q,
+                                      uint64_t out, uint64_t bt, uint64_t sl, uint64_t qsl,
+                                      uint64_t offs, uint32_t batch, uint32_t total,
+                                      uint32_t hq, uint32_t hkv, uint32_t d, uint32_t bs,
+                                      uint32_t mbps, float scale, uint64_t stream) {
+    const char* fn = "kcmm_paged_attn_prefill_on_stream";
+    if (pool == nullptr || q == 0 || out == 0 || bt == 0 || sl == 0 || qsl == 0 || offs == 0) {
+        if (pool) pool->set_error(std::string(fn) + ": null pointer argument");
+        return -1;
+    }
+    if (batch == 0 || hq == 0 || hkv == 0 || d == 0 || bs == 0 || mbps == 0) {
+        pool->set_error(std::string(fn) + ": shape arguments must be positive");
+        return -1;
+    }
+    if (d > 256 || hq % hkv != 0 || hq > 0xFFFF || mbps > 0xFFFF) {
+        pool->set_error(std::string(fn) + ": head_dim <= 256, q heads a multiple of kv heads "
+                                          "and packed shapes <= 65535 required");
+        return -1;
+    }
+    if (static_cast<uint64_t>(total) * hq > 0x7fffffffull) {
+        pool->set_error(std::string(fn) + ": too many query rows");
+        return -1;
+    }
+    if (!layer_ok(pool, layer_idx, fn)) return -1;
+    const kcmm::PoolGeometry& g = pool->core->geo();
+    if (hkv != g.kv_heads || d != g.head_dim || bs != g.block_size) {
+        pool->set_error(std::string(fn) +
+                        ": kv_heads/head_dim/block_size differ from the pool's geometry");
+        return -1;
+    }
+    std::string err;
+    if (!kcmm::dev::set_device(pool->device, &err)) {
+        pool->set_error(std::string(fn) + ": bind device failed: " + err);
+        return -1;
+    }
+    kcmm::dev::AttnPrefillArgs a{};
+    a.dtype = g.dtype;
+    a.q = q;
+    a.out = out;
+    a.k_base = pool->core->va_k(layer_idx);
+    a.v_base = pool->core->va_v(layer_idx);
+    a.block_tables = bt;
+    a.seq_lens = sl;
+    a.query_start_loc = qsl;
+    a.offsets_f16 = offs;
+    a.batch = batch;
+    a.total_query_tokens = total;
+    a.num_q_heads = hq;
+    a.kv_heads = hkv;
+    a.head_dim = d;
+    a.block_size = bs;
+    a.mbps = mbps;
+    a.row_bytes = static_cast<uint32_t>(g.row_bytes);
+    a.data_bytes = static_cast<uint32_t>(g.data_bytes);
+    a.scale = scale;
+    a.stream = stream;
+    if (!kcmm::dev::attn_prefill(a, &err)) {
+        pool->set_error(std::string(fn) + ": launch failed: " + err);
+        return -1;
+    }
+    return 0;
+}
+
 int kcmm_precompile_paged_attn_decode_f16(kcmm_pool_t* pool) { return pool ? 0 : -1; }
 
 // ---- tiering: not built (every block stays resident in HBM) ----------------------

@@ -247,3 +247,103 @@ def _fill_fp8_on_device(case: DecodeCase, gen) -> None:
                 view[sb[c0:c1], idx[c0:c1]] = page
             _region_copy(base, image, g["mapped_bytes"])
             del image
+
+
+@dataclass
+class PrefillCase:
+    """Chunked-prefill workload: sequences' pages (some shared), the chunk's
+    queries and the device tensors the prefill entry point takes."""
+    pool: KcmmPool
+    dtype: int
+    num_q_heads: int
+    kv_heads: int
+    head_dim: int
+    block_size: int
+    block_tables: np.ndarray        # int32 [B][mbps]
+    seq_lens: np.ndarray            # int32 [B], cached tokens incl. the chunk
+    qsl: np.ndarray                 # int32 [B+1]
+    offsets_f16: np.ndarray
+    q_bits: np.ndarray              # uint16 [T][Hq][D]
+    dev: dict = field(default_factory=dict)
+
+    @property
+    def mbps(self) -> int:
+        return self.block_tables.shape[1]
+
+    def flops(self) -> float:
+        """Algorithmic FLOPs: QK^T and PV over keys 0..p for every query."""
+        hq, d = self.num_q_heads, self.head_dim
+        total = 0
+        for b in range(len(self.seq_lens)):
+            n = int(self.qsl[b + 1] - self.qsl[b])
+            first = int(self.seq_lens[b]) - n
+            total += sum(first + i + 1 for i in range(n))
+        return 4.0 * hq * d * total
+
+    def run(self, layer: int = 0, stream_ptr: int = 0, scale=None) -> None:
+        scale = 1.0 / math.sqrt(self.head_dim) if scale is None else scale
+        d = self.dev
+        self.pool.paged_attn_prefill(
+            layer_idx=layer, query_ptr=d["q"].data_ptr(), out_ptr=d["out"].data_ptr(),
+            block_tables_ptr=d["bt"].data_ptr(), seq_lens_ptr=d["sl"].data_ptr(),
+            query_start_loc_ptr=d["qsl"].data_ptr(), block_offsets_f16_ptr=d["offs"].data_ptr(),
+            batch=len(self.seq_lens), total_query_tokens=int(self.qsl[-1]),
+            num_q_heads=self.num_q_heads, kv_heads=self.kv_heads, head_dim=self.head_dim,
+            block_size=self.block_size, max_blocks_per_seq=self.mbps, scale=scale,
+            stream_ptr=stream_ptr)
+
+
+def build_prefix_shared_case(lib: KcmmLibrary, *, batch: int, prefix_tokens: int,
+                             suffix_tokens: int, chunk: int, num_q_heads: int, kv_heads: int,
+                             head_dim: int, block_size: int, dtype: int = KV_BF16,
+                             num_layers: int = 1, seed: int = 0,
+                             device: str = "cuda") -> PrefillCase:
+    """`batch` sequences share `prefix_tokens` of refcounted pages (sequence 0
+    owns them, the others take them with kcmm_share_prefix) and own
+    `suffix_tokens` each; the chunk is the last `chunk` tokens of every
+    sequence.  Regions are filled on the device."""
+    assert prefix_tokens % block_size == 0
+    rng = np.random.default_rng(seed)
+    total = prefix_tokens + suffix_tokens
+    cfg = make_config(num_layers=num_layers, kv_heads=kv_heads, head_dim=head_dim,
+                      max_batch=batch, max_seq_len=total, block_size=block_size)
+    pool = lib.create_pool(cfg, dtype)
+    npre = prefix_tokens // block_size
+    nsuf = -(-suffix_tokens // block_size)
+    mbps = npre + nsuf
+    bt = np.zeros((batch, mbps), dtype=np.int32)
+    pre = pool.alloc_blocks(npre) if npre else []
+    for b in range(batch):
+        own = pool.alloc_blocks(nsuf)
+        if b == 0:
+            s = pool.register_sequence(pre + own)
+        else:
+            s = pool.register_sequence([])
+            pool.share_prefix(0, s, npre)
+            for blk in own:
+                pool.append_block_to_sequence(s, blk)
+        pool.update_seq_len(s, total)
+        bt[b] = pool.block_table(s)
+    offs = np.asarray(pool.all_block_offsets_f16(), dtype=np.uint64)
+    sl = np.full(batch, total, dtype=np.int32)
+    qsl = (np.arange(batch + 1) * chunk).astype(np.int32)
+    qdt = KV_F16 if dtype == KV_F16 else KV_BF16
+    q = encode16(qdt, rng.standard_normal((batch * chunk, num_q_heads, head_dim)).astype(np.float32))
+    case = PrefillCase(pool=pool, dtype=dtype, num_q_heads=num_q_heads, kv_heads=kv_heads,
+                       head_dim=head_dim, block_size=block_size, block_tables=bt, seq_lens=sl,
+                       qsl=qsl, offsets_f16=offs, q_bits=q)
+    shim = DecodeCase(lib=lib, pool=pool, dtype=dtype, batch=batch, num_q_heads=num_q_heads,
+                      kv_heads=kv_heads, head_dim=head_dim, block_size=block_size,
+                      num_layers=num_layers, seq_lens=sl, block_tables=bt, offsets_f16=offs,
+                      q_bits=q)
+    fill_regions_on_device(shim, seed + 1)
+    tdt = torch.float16 if dtype == KV_F16 else torch.bfloat16
+    case.dev = {
+        "q": torch.from_numpy(q.view(np.int16)).view(tdt).to(device),
+        "out": torch.zeros((batch * chunk, num_q_heads, head_dim), dtype=tdt, device=device),
+        "bt": torch.from_numpy(bt).to(device),
+        "sl": torch.from_numpy(sl.copy()).to(device),
+        "qsl": torch.from_numpy(qsl.copy()).to(device),
+        "offs": torch.from_numpy(offs.view(np.int64)).to(device),
+    }
+    return case

@@ -76,6 +76,8 @@ def _bind(l: C.CDLL) -> None:
                                    C.c_int),
         "oracle_attn_decode_ref_f32": ([C.c_int, P, P, P, P, P, P, P] + [U32] * 7 + [F, C.c_int],
                                        C.c_int),
+        "oracle_attn_prefill_f64": ([C.c_int, P, P, P, P, P, P, P, P] + [U32] * 8 + [C.c_double],
+                                    C.c_int),
         "oracle_gemm_bf16_f64": ([P, P, P, U32, U32, U32], None),
     }
     for name, (args, res) in sig.items():
@@ -246,6 +248,23 @@ def attn_decode_f64(dtype, q, k_region, v_region, block_tables, seq_lens, offset
     lib().oracle_attn_decode_f64(dtype, _p(q), _p(out), _p(k_region), _p(v_region), _p(bt),
                                  _p(sl), _p(of), batch, num_q_heads, kv_heads, head_dim,
                                  block_size, mbps, row_bytes, data_bytes, scale)
+    return out
+
+
+def attn_prefill_f64(dtype, q, k_region, v_region, block_tables, seq_lens, query_start_loc,
+                     offsets_f16, num_q_heads, kv_heads, head_dim, block_size, row_bytes,
+                     data_bytes, scale):
+    """Causal chunked prefill (fp64): q/out [total_rows][Hq][D]."""
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    qsl = np.ascontiguousarray(query_start_loc, dtype=np.int32)
+    of = np.ascontiguousarray(offsets_f16, dtype=np.uint64)
+    q = np.ascontiguousarray(q)
+    batch, mbps = bt.shape
+    out = np.zeros((int(qsl[-1]), num_q_heads, head_dim), dtype=np.float64)
+    lib().oracle_attn_prefill_f64(dtype, _p(q), _p(out), _p(k_region), _p(v_region), _p(bt),
+                                  _p(sl), _p(qsl), _p(of), batch, num_q_heads, kv_heads,
+                                  head_dim, block_size, mbps, row_bytes, data_bytes, scale)
     return out
 
 

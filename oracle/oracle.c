@@ -643,6 +643,63 @@ int oracle_attn_decode_f64(int dtype, const void *q, double *out, const uint8_t 
     return 0;
 }
 
+/* Causal chunked-prefill attention over paged K/V.  The reference has no
+ * chunked prefill (prefill is one token per decode step, ref
+ * transformer.rs:50-65); this is the north star's extension, restated as the
+ * textbook definition: sequence b holds seq_lens[b] tokens in the cache, the
+ * last len_b = qsl[b+1] - qsl[b] of which are this chunk's queries (their K/V
+ * already appended).  Query i of b sits at position p = seq_lens[b] - len_b + i
+ * and attends to keys 0..p; GQA head map as in decode.  Two-pass softmax in
+ * fp64.  q/out rows are [qsl[b] + i][hq][D]. */
+int oracle_attn_prefill_f64(int dtype, const void *q, double *out, const uint8_t *k_region,
+                            const uint8_t *v_region, const int32_t *block_tables,
+                            const int32_t *seq_lens, const int32_t *qsl,
+                            const uint64_t *offsets_f16, uint32_t batch, uint32_t hq,
+                            uint32_t hkv, uint32_t D, uint32_t bs, uint32_t mbps,
+                            uint32_t row_bytes, uint32_t data_bytes, double scale) {
+    size_t es = esize_of(dtype);
+    const int64_t total = qsl[batch];
+    #pragma omp parallel for schedule(dynamic)
+    for (long long task = 0; task < (long long)total * hq; ++task) {
+        const int64_t row = task / hq;
+        const uint32_t h = (uint32_t)(task % hq);
+        uint32_t b = 0;
+        while ((int64_t)qsl[b + 1] <= row) ++b;
+        const int64_t len = qsl[b + 1] - qsl[b];
+        const int64_t pos = (int64_t)seq_lens[b] - len + (row - qsl[b]);
+        const uint32_t kvh = h * hkv / hq;
+        double *o = out + ((size_t)row * hq + h) * D;
+        for (uint32_t d = 0; d < D; ++d) o[d] = 0.0;
+        if (pos < 0 || pos >= (int64_t)mbps * bs) continue;
+        const int64_t L = pos + 1;
+        double *s = (double *)malloc((size_t)L * sizeof(double));
+        const size_t qi = ((size_t)row * hq + h) * D;
+        double mx = -INFINITY;
+        for (int64_t t = 0; t < L; ++t) {
+            int32_t blk = block_tables[(size_t)b * mbps + t / bs];
+            uint64_t page = offsets_f16[blk] * 2;
+            uint64_t off = (uint64_t)(t % bs) * row_bytes + (uint64_t)kvh * D * es;
+            double acc = 0.0;
+            for (uint32_t d = 0; d < D; ++d)
+                acc += q_elem(dtype, q, qi + d) * kv_elem(dtype, k_region + page, off, d, data_bytes, kvh);
+            s[t] = acc * scale;
+            if (s[t] > mx) mx = s[t];
+        }
+        double z = 0.0;
+        for (int64_t t = 0; t < L; ++t) { s[t] = exp(s[t] - mx); z += s[t]; }
+        for (int64_t t = 0; t < L; ++t) {
+            int32_t blk = block_tables[(size_t)b * mbps + t / bs];
+            uint64_t page = offsets_f16[blk] * 2;
+            uint64_t off = (uint64_t)(t % bs) * row_bytes + (uint64_t)kvh * D * es;
+            double w = s[t] / z;
+            for (uint32_t d = 0; d < D; ++d)
+                o[d] += w * kv_elem(dtype, v_region + page, off, d, data_bytes, kvh);
+        }
+        free(s);
+    }
+    return 0;
+}
+
 /* The reference kernel's loop (ref kcmm_vllm_paged_attn.cu:38-101): m starts
  * at -1e30, per token dot*scale, m=max, e=exp(dot-m), corr=exp(old_m-m),
  * s=s*corr+e, acc=acc*corr+e*v; out=acc/s.  16-bit K/V only. */

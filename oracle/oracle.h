@@ -90,6 +90,15 @@ int oracle_attn_decode_f64(int dtype, const void *q, double *out, const uint8_t 
                            uint32_t num_q_heads, uint32_t kv_heads, uint32_t head_dim,
                            uint32_t block_size, uint32_t mbps, uint32_t row_bytes,
                            uint32_t data_bytes, double scale);
+/* Causal chunked prefill over paged K/V (textbook; the reference has no
+ * chunked prefill).  qsl = int32 [batch+1] query row offsets; the queries of
+ * b are the last qsl[b+1]-qsl[b] of its seq_lens[b] cached tokens. */
+int oracle_attn_prefill_f64(int dtype, const void *q, double *out, const uint8_t *k_region,
+                            const uint8_t *v_region, const int32_t *block_tables,
+                            const int32_t *seq_lens, const int32_t *qsl,
+                            const uint64_t *offsets_f16, uint32_t batch, uint32_t num_q_heads,
+                            uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
+                            uint32_t mbps, uint32_t row_bytes, uint32_t data_bytes, double scale);
 /* The reference kernel's own loop (one task per (b, q head), online softmax
  * in fp32) parallelised over tasks with OpenMP: the CPU baseline. */
 int oracle_attn_decode_ref_f32(int dtype, const void *q, float *out, const uint8_t *k_region,

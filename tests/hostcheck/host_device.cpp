@@ -60,6 +60,7 @@ bool stream_workspace(uint64_t, int, size_t, void**, bool, std::string* err) {
     return no_device(err);
 }
 bool attn_decode(const AttnDecodeArgs&, std::string* err) { return no_device(err); }
+bool attn_prefill(const AttnPrefillArgs&, std::string* err) { return no_device(err); }
 bool kv_write_rows(const KvRowsArgs&, std::string* err) { return no_device(err); }
 bool kv_write_device_slots(const KvDeviceSlotsArgs&, std::string* err) { return no_device(err); }
 bool copy_pages(const std::vector<uint64_t>&, const uint64_t*, size_t, uint32_t, uint64_t,
