@@ -8,18 +8,25 @@
 // p = seq_lens[b] - len_b + i and attends to keys 0..p.  q/out rows are
 // [qsl[b] + i][Hq][D]; GQA head map g = h / (Hq/Hkv).  Accumulation is fp32.
 //
-// MI355X design (the decode kernel's tile machinery, with query columns):
+// MI355X design (flash attention over LDS-staged pages):
 //  * workgroup = 4 waves on one (sequence b, kv head g, block of query
-//    tokens); wave w takes 2 blocks of 16 MFMA columns, a column being one
-//    (query token, head of the GQA group) pair, heads fastest;
-//  * each wave walks 32-key tiles up to its last query's position, the next
-//    tile in flight while one is consumed; a tile's keys come in whole
-//    128-byte lines (8 keys per load) put into MFMA layout by one DPP row
-//    rotation + select per dword (the four waves read the same keys, so the
-//    loads are cached ones);
-//  * S^T = K Q^T on v_mfma_f32_16x16x32, causal mask per column, online
-//    softmax in the log2 domain per column; O^T += V^T P^T with V^T made by
-//    0/1 selection MFMAs once per tile and shared by both column blocks.
+//    tokens); wave w owns 64 MFMA columns (4 blocks of 16), a column being
+//    one (query token, head of the GQA group) pair, heads fastest, with its
+//    Q rows held in registers for the whole key loop;
+//  * the workgroup walks 32-key tiles up to its last query's position: the
+//    256 threads gather a tile's K and V rows (16 B each, coalesced per row)
+//    into registers one tile ahead, store them to a double-buffered,
+//    XOR-swizzled LDS tile, and every wave computes from LDS, so each key
+//    row leaves L2 once per workgroup instead of once per wave;
+//  * page bases come two tiles ahead (block table one tile before offsets),
+//    so no load waits on a dependent load inside the loop;
+//  * S^T = K Q^T on v_mfma_f32_16x16x32 (K rows by ds_read_b128); V^T comes
+//    straight from the row-major V tile by the gfx950 transposing LDS read
+//    ds_read_b64_tr_b16, then O^T += V^T P^T; one V^T fragment serves the
+//    4 column blocks;
+//  * causal masking only on tiles that cross a column's position; online
+//    softmax in the log2 domain, rescaling only when a column's maximum grows
+//    by more than 8 (until then P <= 2^8, harmless in fp32 / 16-bit).
 #include <algorithm>
 #include <climits>
 #include <cmath>
@@ -34,10 +41,14 @@ struct PrefillParams {
     const uint8_t* q;
     uint8_t* out;
     int batch, num_q_heads, kv_heads, group, block_size, mbps;
-    int row_bytes, data_bytes, head_dim;
+    int row_bytes, data_bytes, head_dim, bs_shift;
     float scale_log2;
     float scale;
 };
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 template <int DT>
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
@@ -50,80 +61,86 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                        0);
 }
 
-__device__ __forceinline__ uint32_t ror8(uint32_t x) {
-    return static_cast<uint32_t>(
-        __builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x128, 0xF, 0xF, false));
-}
-
-// x: lane (r, lg) <- key (r & 7), bytes (4*(r >> 3) + lg)*16 of a 128-byte
-// line; y: keys 8..15.  Afterwards lane r = key r, x bytes 16lg..+15 and y
-// bytes 64+16lg..+15 of the line (MFMA A layout).
-__device__ __forceinline__ void fix_lines(u32x4& x, u32x4& y, bool low8) {
-    u32x4 nx, ny;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t rx = ror8(x[c]);
-        const uint32_t ry = ror8(y[c]);
-        nx[c] = low8 ? x[c] : ry;
-        ny[c] = low8 ? rx : y[c];
-    }
-    x = nx;
-    y = ny;
-}
-
-// E[k][j] = (k == 16*sub + j): selects 16 consecutive k indices (transposes).
+// Two fp32 -> one dword of 16-bit elements (round to nearest even).
 template <int DT>
-__device__ __forceinline__ u32x4 select_operand(int sub, int ln, int lg) {
-    constexpr uint32_t one = DT == kDtF16 ? 0x3C00u : 0x3F80u;
-    u32x4 e = u32x4{0, 0, 0, 0};
-    const int k = 16 * sub + ln;
-    if ((k >> 3) == lg) {
-        const int t = k & 7;
-        e[t >> 1] = (t & 1) ? (one << 16) : one;
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    if constexpr (DT == kDtF16) {
+        const f16x2 v = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+        return __builtin_bit_cast(uint32_t, v);
+    } else {
+        const bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+        return __builtin_bit_cast(uint32_t, v);
     }
-    return e;
 }
 
-template <int DT>
-__device__ __forceinline__ uint32_t pack_exact(float lo, float hi) {
-    if constexpr (DT == kDtF16) return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
-    else return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+// Maximum / sum over the 4 lanes (l, l^16, l^32, l^48) holding one MFMA
+// output column.  v_permlane16_swap(x, x) leaves x[l] in one result and
+// x[l ^ 16] in the other (v_permlane32_swap: x[l ^ 32]), so a symmetric
+// operation of the pair reduces across rows with VALU ops only.
+__device__ __forceinline__ float xor16_pair(float x, bool mx) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    const float a = __uint_as_float(r[0]), c = __uint_as_float(r[1]);
+    return mx ? fmaxf(a, c) : a + c;
+}
+__device__ __forceinline__ float xor32_pair(float x, bool mx) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    const float a = __uint_as_float(r[0]), c = __uint_as_float(r[1]);
+    return mx ? fmaxf(a, c) : a + c;
+}
+__device__ __forceinline__ float col_max(float x) { return xor32_pair(xor16_pair(x, true), true); }
+__device__ __forceinline__ float col_sum(float x) { return xor32_pair(xor16_pair(x, false), false); }
+
+// ds_read_b64_tr_b16 on a 16-lane group: lane (a + 4s) gives the address of
+// 4 consecutive 16-bit elements M[a + 4s][0..3]; lane (4a + e) receives
+// M[a][e], M[a + 4][e], M[a + 8][e], M[a + 12][e].  With lane a + 4s pointing
+// at V[key0 + s][d0 + 4a], lane i gets V[key0 + 0..3][d0 + i].
+__device__ __forceinline__ u32x2 lds_read_tr(const uint8_t* p) {
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+    return __builtin_bit_cast(u32x2, v);
 }
 
-__device__ __forceinline__ float col_max(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16));
-    return fmaxf(x, __shfl_xor(x, 32));
-}
-
-template <int KC>
-struct KvTile {
-    u32x4 k[2][KC];
-    u32x4 v[2][KC];
+template <int D>
+struct Shape {
+    static constexpr int CH = D / 8;          // 16-byte chunks per key row
+    static constexpr int KC = D / 32;         // k-steps of S^T = K Q^T
+    static constexpr int DB = D / 16;         // 16-row blocks of O^T
+    static constexpr int RPB = 256 / (2 * D); // key rows per 256-byte bank window
+    static constexpr int TILE = 32 * D * 2;   // bytes of one K (or V) tile
+    // physical chunk of logical chunk c of key row k: K rows are read 16 keys
+    // x 16 B at a time, V rows 8 keys x 32 B (transposing reads)
+    __device__ static int swz_k(int k, int c) { return c ^ ((k / RPB) & (CH - 1)); }
+    __device__ static int swz_v(int k, int c) { return c ^ (2 * ((k / RPB) & (CH / 2 - 1))); }
 };
 
 // Workgroups over (query-token block, kv head), kv head fastest: blockIdx.x
 // = block * Hkv + g.  Workgroups are dealt to the 8 XCDs round-robin, so with
 // 8 kv heads every XCD serves one head and its L2 holds that head's pages
 // (shared prefixes included) for all sequences.
-template <int DT, int D, int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+template <int DT, int D, int G, int NW, int NCB>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4)))
 void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                        const uint8_t* __restrict__ vreg, const int32_t* __restrict__ bt,
                        const int32_t* __restrict__ sl, const int32_t* __restrict__ qsl,
                        const uint64_t* __restrict__ offs) {
-    constexpr int KC = D / 32;
-    constexpr int LINES = D / 64;
-    constexpr int DB = D / 16;
-    constexpr int TPB = 16 / G;          // query tokens per 16-column block
-    constexpr int TW = 2 * TPB;          // per wave
-    constexpr int TWG = 4 * TW;          // per workgroup
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    using S = Shape<D>;
+    constexpr int KC = S::KC, DB = S::DB, CH = S::CH;
+    constexpr int NT = NW * 64;          // threads
+    constexpr int CPT = 64 * CH / NT;    // 16-byte chunks per thread per tile (K and V)
+    static_assert(CPT >= 1 && 64 * CH % NT == 0, "tile does not split over the threads");
+    constexpr int TPB = 16 / G;          // query tokens per column block
+    constexpr int TPW = NCB * TPB;       // per wave
+    constexpr int TWG = NW * TPW;        // per workgroup
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][S::TILE];   // [buffer][K, V]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ln = lane & 15, lg = lane >> 4;
-    const bool low8 = ln < 8;
     const int g = static_cast<int>(blockIdx.x) % p.kv_heads;
     const int item = static_cast<int>(blockIdx.x) / p.kv_heads;
-    const int bs = p.block_size;
 
     // ---- sequence and token block of this workgroup ----
     int b = -1, blk = 0;
@@ -150,170 +167,237 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         }
     }
     b = __builtin_amdgcn_readfirstlane(b);
-    if (b < 0) return;
+    if (b < 0) return;                     // whole workgroup: uniform
     blk = __builtin_amdgcn_readfirstlane(blk);
     const int q0 = qsl[b];
     const int len = qsl[b + 1] - q0;
-    const int L = min(sl[b], p.mbps * bs);
-    const int first_pos = L - len;           // position of the chunk's first query
-    const int tok0 = blk * TWG + wave * TW;  // this wave's first query (chunk index)
-    if (tok0 >= len) return;
+    const int L = min(sl[b], p.mbps << p.bs_shift);
+    const int first_pos = L - len;         // position of the chunk's first query
+    const int tok0_wg = blk * TWG;
     // queries before position 0 (more queries than cached tokens) see no key;
     // their rows are written as zeros
-    const int tok_last = min(tok0 + TW, len) - 1;
-    const int nkeys = max(0, first_pos + tok_last + 1);
-    const int ntiles = (nkeys + 31) / 32;
+    const int nt_wg = (max(0, first_pos + min(tok0_wg + TWG, len)) + 31) / 32;
+    const int tok0 = tok0_wg + wave * TPW;  // this wave's first query (chunk index)
+    const bool wave_live = tok0 < len;
+    const int tok_last = min(tok0 + TPW, len) - 1;
+    const int nt_w = wave_live ? (max(0, first_pos + tok_last + 1) + 31) / 32 : 0;
+    const int qmin = first_pos + tok0;     // smallest position among the wave's columns
 
     // ---- columns: query token (clamped into the chunk; extra columns are
     // computed on a duplicate and never stored) and its position ----
-    int qpos[2];
-    u32x4 qf[2][KC];
+    int qpos[NCB];
+    u32x4 qf[NCB][KC];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-        const int t = min(tok0 + qb * TPB + ln / G, len - 1);
-        qpos[qb] = first_pos + t;
+    for (int cb = 0; cb < NCB; ++cb) {
+        const int t = max(0, min(tok0 + cb * TPB + ln / G, len - 1));
+        qpos[cb] = first_pos + t;
         const uint8_t* qrow =
             p.q + ((static_cast<size_t>(q0) + t) * p.num_q_heads + g * G + ln % G) * D * 2;
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc)
-            qf[qb][kc] = *reinterpret_cast<const u32x4*>(qrow + (kc * 32 + lg * 8) * 2);
+            qf[cb][kc] = *reinterpret_cast<const u32x4*>(qrow + (kc * 32 + lg * 8) * 2);
     }
+    // Q loads stay first: the first tile store then waits for them too, and
+    // no wait inside the key loop is left counting them
+    __builtin_amdgcn_sched_barrier(0);
 
+    // ---- tile gather: chunk q = tid + NT * i of the tile's 2 x 32 x CH
+    // chunks is (tensor q / (32 CH), key (q / CH) % 32, chunk q % CH); keys
+    // past the sequence read its last row (finite; P = 0 there) ----
+    auto c_tensor = [&](int i) { return (tid + NT * i) / (32 * CH); };
+    auto c_key = [&](int i) { return ((tid + NT * i) / CH) % 32; };
+    const int tc = tid % CH;
     const int32_t* row = bt + static_cast<size_t>(b) * p.mbps;
-    const uint32_t lo = static_cast<uint32_t>((ln & 7) * p.row_bytes + ((ln >> 3) * 4 + lg) * 16);
-    const int last8 = (L - 1) & ~7;
-    auto load_tile = [&](KvTile<KC>& tl, int kt) {
-        uint64_t gb[4];
+    const int bmask = (1 << p.bs_shift) - 1;
+    const uint32_t head_off = static_cast<uint32_t>(g * D * 2 + tc * 16);
+    auto key_tok = [&](int kt, int i) { return min(kt * 32 + c_key(i), L - 1); };
+    auto page_entry = [&](int kt, int i) { return row[key_tok(kt, i) >> p.bs_shift]; };
+    // Loaded values pass through an empty asm where they are used, so the
+    // compiler cannot fold their arithmetic back next to the load (which
+    // would wait there for the loads issued just before).
+    auto page_offs = [&](int entry) {
+        asm volatile("" : "+v"(entry));
+        return offs[entry];
+    };
+    u32x4 gch[CPT];
+    auto gather = [&](int kt, const uint64_t (&pg)[CPT]) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int tok = min(kt * 32 + q * 8, last8);
-            const int lb = tok / bs;
-            gb[q] = offs[row[lb]] * 2ull +
-                    static_cast<uint32_t>((tok - lb * bs) * p.row_bytes + g * D * 2);
+        for (int i = 0; i < CPT; ++i) {
+            uint64_t page = pg[i];
+            asm volatile("" : "+v"(page));
+            const uint64_t a = page * 2ull +
+                               static_cast<uint32_t>((key_tok(kt, i) & bmask) * p.row_bytes) +
+                               head_off;
+            gch[i] = *reinterpret_cast<const u32x4*>((c_tensor(i) ? vreg : kreg) + a);
         }
+    };
+    auto store_tile = [&](int buf) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int c2 = 0; c2 < LINES; ++c2) {
-                const uint32_t o = lo + c2 * 128;
-                tl.k[h][2 * c2] = *reinterpret_cast<const u32x4*>(kreg + gb[2 * h] + o);
-                tl.k[h][2 * c2 + 1] = *reinterpret_cast<const u32x4*>(kreg + gb[2 * h + 1] + o);
-                tl.v[h][2 * c2] = *reinterpret_cast<const u32x4*>(vreg + gb[2 * h] + o);
-                tl.v[h][2 * c2 + 1] = *reinterpret_cast<const u32x4*>(vreg + gb[2 * h + 1] + o);
-            }
+        for (int i = 0; i < CPT; ++i) {
+            const int k = c_key(i);
+            const int pc = c_tensor(i) ? S::swz_v(k, tc) : S::swz_k(k, tc);
+            *reinterpret_cast<u32x4*>(&lds[buf][c_tensor(i)][k * D * 2 + pc * 16]) = gch[i];
+        }
     };
 
-    const u32x4 esel[2] = {select_operand<DT>(0, ln, lg), select_operand<DT>(1, ln, lg)};
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.0f, 0.0f};
-    f32x4 acc[2][DB];
+    float m_run[NCB], l_run[NCB];
+    f32x4 acc[NCB][DB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int cb = 0; cb < NCB; ++cb) {
+        m_run[cb] = -INFINITY;
+        l_run[cb] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < DB; ++i) acc[qb][i] = f32x4{0, 0, 0, 0};
+        for (int i = 0; i < DB; ++i) acc[cb][i] = f32x4{0, 0, 0, 0};
+    }
 
-    auto consume = [&](KvTile<KC>& t, int kt) {
+    // LDS byte offsets of this lane's K fragments (tile-invariant)
+    int k_off[2][KC];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            const int k = 16 * h + ln;
+            k_off[h][kc] = k * D * 2 + S::swz_k(k, 4 * kc + lg) * 16;
+        }
+    // V^T fragment (db, h): lane a + 4s reads V[key 16h + 4lg + s][d 16db + 4a]
+    const int va = ln & 3, vsi = ln >> 2;
+    auto v_off = [&](int db, int h) {
+        const int k = 16 * h + 4 * lg + vsi;
+        const int d = 16 * db + 4 * va;
+        return k * D * 2 + S::swz_v(k, d >> 3) * 16 + (d & 7) * 2;
+    };
+
+    // One 32-key tile.  Only a tile that crosses some column's position
+    // applies the causal mask.
+    auto compute = [&](int buf, int kt) {
+        const uint8_t* kb = lds[buf][0];
+        const uint8_t* vb = lds[buf][1];
+        u32x4 kf[2][KC];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int c2 = 0; c2 < LINES; ++c2) {
-                fix_lines(t.k[h][2 * c2], t.k[h][2 * c2 + 1], low8);
-                fix_lines(t.v[h][2 * c2], t.v[h][2 * c2 + 1], low8);
-            }
-        const int kbase = kt * 32;
-        if (kbase + 32 > L) {
-            // key rows past the sequence may hold anything: zero V for exact selection
+            for (int kc = 0; kc < KC; ++kc)
+                kf[h][kc] = *reinterpret_cast<const u32x4*>(kb + k_off[h][kc]);
+        f32x4 s[NCB][2];
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const bool dead = kbase + h * 16 + ln >= L;
+                s[cb][h] = f32x4{0, 0, 0, 0};
 #pragma unroll
                 for (int kc = 0; kc < KC; ++kc)
-                    if (dead) t.v[h][kc] = u32x4{0, 0, 0, 0};
+                    s[cb][h] = mfma16<DT>(kf[h][kc], qf[cb][kc], s[cb][h]);
+            }
+        // V^T fragments: in flight during the softmax
+        u32x4 vf[DB];
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const u32x2 lo = lds_read_tr(vb + v_off(db, 0));
+            const u32x2 hi = lds_read_tr(vb + v_off(db, 1));
+            vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+        if (kt * 32 + 31 > qmin) {
+            const int key0 = kt * 32 + 4 * lg;
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (key0 + 16 * h + r > qpos[cb]) s[cb][h][r] = -INFINITY;
+        }
+        // column maxima of the raw scores (scale > 0), masked keys -inf
+        float mt[NCB];
+        bool grow[NCB];
+        bool any_grow = false;
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            float x = fmaxf(fmaxf(fmaxf(s[cb][0][0], s[cb][0][1]), fmaxf(s[cb][0][2], s[cb][0][3])),
+                            fmaxf(fmaxf(s[cb][1][0], s[cb][1][1]), fmaxf(s[cb][1][2], s[cb][1][3])));
+            mt[cb] = col_max(x) * p.scale_log2;
+            // rescale only when the column maximum grows by more than 8
+            grow[cb] = mt[cb] > m_run[cb] + 8.0f;
+            any_grow |= grow[cb];
+        }
+        if (__builtin_amdgcn_ballot_w64(any_grow)) {
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+                if (!__builtin_amdgcn_ballot_w64(grow[cb])) continue;
+                // (a column that does not grow keeps its scale exactly)
+                const float corr = grow[cb] ? __builtin_amdgcn_exp2f(m_run[cb] - mt[cb]) : 1.0f;
+                l_run[cb] *= corr;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) acc[cb][db] *= corr;
+                m_run[cb] = grow[cb] ? mt[cb] : m_run[cb];
             }
         }
-        u32x4 pf[2];
-        float corr[2];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            f32x4 s[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                s[h] = f32x4{0, 0, 0, 0};
-#pragma unroll
-                for (int kc = 0; kc < KC; ++kc) s[h] = mfma16<DT>(t.k[h][kc], qf[qb][kc], s[h]);
-            }
-            float sv[8];
-            float mt = -INFINITY;
+        for (int cb = 0; cb < NCB; ++cb) {
+            // a column with no visible key yet keeps m = -inf and P = 0
+            const float nmu = m_run[cb] == -INFINITY ? 0.0f : -m_run[cb];
+            float pv[8];
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int key = kbase + h * 16 + lg * 4 + r;
-                    const float x = key <= qpos[qb] ? s[h][r] * p.scale_log2 : -INFINITY;
-                    sv[h * 4 + r] = x;
-                    mt = fmaxf(mt, x);
-                }
-            mt = col_max(mt);
-            const float m_new = fmaxf(m_run[qb], mt);
-            // a column with no key yet (m_new = -inf) keeps weight 0
-            corr[qb] = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-            float psum = 0.0f;
-            float pv[8];
+                for (int r = 0; r < 4; ++r)
+                    pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[cb][h][r], p.scale_log2, nmu));
+            l_run[cb] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+            u32x4 pf;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                pv[i] = m_new == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[i] - m_new);
-                psum += pv[i];
-            }
-            l_run[qb] = l_run[qb] * corr[qb] + psum;
-            m_run[qb] = m_new;
+            for (int i = 0; i < 4; ++i) pf[i] = pack2<DT>(pv[2 * i], pv[2 * i + 1]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                pf[qb][i] = f32_to_elem<DT>(pv[2 * i]) | (f32_to_elem<DT>(pv[2 * i + 1]) << 16);
-        }
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            const f32x4 v0 = mfma16<DT>(t.v[0][db >> 1], esel[db & 1], f32x4{0, 0, 0, 0});
-            const f32x4 v1 = mfma16<DT>(t.v[1][db >> 1], esel[db & 1], f32x4{0, 0, 0, 0});
-            u32x4 va;
-            va[0] = pack_exact<DT>(v0[0], v0[1]);
-            va[1] = pack_exact<DT>(v0[2], v0[3]);
-            va[2] = pack_exact<DT>(v1[0], v1[1]);
-            va[3] = pack_exact<DT>(v1[2], v1[3]);
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) acc[qb][db] = mfma16<DT>(va, pf[qb], acc[qb][db] * corr[qb]);
+            for (int db = 0; db < DB; ++db) acc[cb][db] = mfma16<DT>(vf[db], pf, acc[cb][db]);
         }
     };
 
-    if (ntiles > 0) {   // (no tile at all: the sequence has no visible key)
-        KvTile<KC> ta, tb;
-        load_tile(ta, 0);
-        int kt = 0;
-        for (; kt + 1 < ntiles; kt += 2) {
-            load_tile(tb, kt + 1);
-            __builtin_amdgcn_sched_barrier(0);
-            consume(ta, kt);
-            if (kt + 2 < ntiles) load_tile(ta, kt + 2);
-            __builtin_amdgcn_sched_barrier(0);
-            consume(tb, kt + 1);
+    if (nt_wg > 0) {   // (no tile at all: no column has a visible key)
+        uint64_t pg[CPT];
+        int ent[CPT];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) pg[i] = page_offs(page_entry(0, i));
+        gather(0, pg);
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) pg[i] = page_offs(page_entry(1, i));
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) ent[i] = page_entry(2, i);
+        store_tile(0);
+        gather(1, pg);
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) pg[i] = page_offs(ent[i]);       // tile 2
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) ent[i] = page_entry(3, i);        // tile 3
+        __syncthreads();
+        // Gathers past the last tile read clamped (valid) rows and are never
+        // consumed; issuing them unconditionally keeps every iteration's
+        // load sequence identical, so the compiler's counter waits stay exact.
+        for (int kt = 0; kt < nt_wg; ++kt) {
+            if (kt < nt_w) compute(kt & 1, kt);
+            store_tile((kt + 1) & 1);
+            __syncthreads();
+            gather(kt + 2, pg);
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) pg[i] = page_offs(ent[i]);   // tile kt + 3
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) ent[i] = page_entry(kt + 4, i);
         }
-        if (kt < ntiles) consume(ta, kt);
     }
 
     // ---- store the columns that are real queries ----
+    if (!wave_live) return;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-        const float l = l_run[qb] + __shfl_xor(l_run[qb], 16);
-        const float lt = l + __shfl_xor(l, 32);
-        const int t = tok0 + qb * TPB + ln / G;
+    for (int cb = 0; cb < NCB; ++cb) {
+        const float lt = col_sum(l_run[cb]);
+        const int t = tok0 + cb * TPB + ln / G;
         if (t < len) {
             const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
             uint16_t* o = reinterpret_cast<uint16_t*>(p.out) +
-                          ((static_cast<size_t>(q0) + t) * p.num_q_heads + g * G + ln % G) * D + 4 * lg;
+                          ((static_cast<size_t>(q0) + t) * p.num_q_heads + g * G + ln % G) * D +
+                          4 * lg;
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 u32x2 w;
-                w[0] = f32_to_elem<DT>(acc[qb][db][0] * inv) | (f32_to_elem<DT>(acc[qb][db][1] * inv) << 16);
-                w[1] = f32_to_elem<DT>(acc[qb][db][2] * inv) | (f32_to_elem<DT>(acc[qb][db][3] * inv) << 16);
+                w[0] = pack2<DT>(acc[cb][db][0] * inv, acc[cb][db][1] * inv);
+                w[1] = pack2<DT>(acc[cb][db][2] * inv, acc[cb][db][3] * inv);
                 *reinterpret_cast<u32x2*>(o + 16 * db) = w;
             }
         }
@@ -406,15 +490,16 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
 
 template <int DT, int D, int G>
 bool launch_mfma(const dev::AttnPrefillArgs& a, PrefillParams& p, hipStream_t s, std::string* err) {
-    constexpr int TWG = 4 * 2 * (16 / G);
+    constexpr int NW = 8, NCB = 2;   // 8 waves of 32 columns: 2 waves per SIMD
+    constexpr int TWG = NW * NCB * (16 / G);
     const long long blocks =
         (static_cast<long long>(a.total_query_tokens) / TWG + a.batch + 1) * p.kv_heads;
     if (blocks > INT_MAX) {
         *err = "prefill: too many query tokens";
         return false;
     }
-    hipLaunchKernelGGL((attn_prefill_mfma<DT, D, G>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(256), 0, s, p, reinterpret_cast<const uint8_t*>(a.k_base),
+    hipLaunchKernelGGL((attn_prefill_mfma<DT, D, G, NW, NCB>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(NW * 64), 0, s, p, reinterpret_cast<const uint8_t*>(a.k_base),
                        reinterpret_cast<const uint8_t*>(a.v_base),
                        reinterpret_cast<const int32_t*>(a.block_tables),
                        reinterpret_cast<const int32_t*>(a.seq_lens),
@@ -452,6 +537,8 @@ bool attn_prefill(const AttnPrefillArgs& a, std::string* err) {
     p.row_bytes = static_cast<int>(a.row_bytes);
     p.data_bytes = static_cast<int>(a.data_bytes);
     p.head_dim = static_cast<int>(a.head_dim);
+    p.bs_shift = 0;
+    while ((1u << p.bs_shift) < a.block_size) ++p.bs_shift;
     p.scale = a.scale;
     p.scale_log2 = a.scale * 1.4426950408889634f;
     hipStream_t s = reinterpret_cast<hipStream_t>(a.stream);
@@ -461,7 +548,9 @@ bool attn_prefill(const AttnPrefillArgs& a, std::string* err) {
     const bool mfma_group = p.num_q_heads % p.kv_heads == 0 && (G == 1 || G == 2 || G == 4 ||
                                                                 G == 8 || G == 16);
     const bool mfma_dim = a.head_dim == 64 || a.head_dim == 128;
-    if (a.dtype != kDtFP8 && mfma_group && mfma_dim && a.block_size % 8 == 0 &&
+    const bool pow2_bs = (1u << p.bs_shift) == a.block_size;
+    // (the MFMA kernel takes column maxima of the raw scores: scale > 0)
+    if (a.dtype != kDtFP8 && mfma_group && mfma_dim && pow2_bs && a.scale > 0.0f &&
         std::getenv("KCMM_ATTN_GENERIC") == nullptr) {
         if (a.dtype == kDtF16)
             return a.head_dim == 64 ? launch_group<kDtF16, 64>(a, p, s, err)
