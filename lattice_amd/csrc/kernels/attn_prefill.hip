@@ -73,6 +73,10 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
     }
 }
 
+// NaN-propagating maximum (v_maximum3_f32): unlike fmaxf it needs no
+// canonicalization of MFMA results.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Maximum / sum over the 4 lanes (l, l^16, l^32, l^48) holding one MFMA
 // output column.  v_permlane16_swap(x, x) leaves x[l] in one result and
 // x[l ^ 16] in the other (v_permlane32_swap: x[l ^ 32]), so a symmetric
@@ -81,16 +85,15 @@ __device__ __forceinline__ float xor16_pair(float x, bool mx) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
                                                     false, false);
     const float a = __uint_as_float(r[0]), c = __uint_as_float(r[1]);
-    return mx ? fmaxf(a, c) : a + c;
+    return mx ? vmax(a, c) : a + c;
 }
 __device__ __forceinline__ float xor32_pair(float x, bool mx) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
                                                     false, false);
     const float a = __uint_as_float(r[0]), c = __uint_as_float(r[1]);
-    return mx ? fmaxf(a, c) : a + c;
+    return mx ? vmax(a, c) : a + c;
 }
 __device__ __forceinline__ float col_max(float x) { return xor32_pair(xor16_pair(x, true), true); }
-__device__ __forceinline__ float col_sum(float x) { return xor32_pair(xor16_pair(x, false), false); }
 
 // ds_read_b64_tr_b16 on a 16-lane group: lane (a + 4s) gives the address of
 // 4 consecutive 16-bit elements M[a + 4s][0..3]; lane (4a + e) receives
@@ -107,12 +110,14 @@ struct Shape {
     static constexpr int CH = D / 8;          // 16-byte chunks per key row
     static constexpr int KC = D / 32;         // k-steps of S^T = K Q^T
     static constexpr int DB = D / 16;         // 16-row blocks of O^T
-    static constexpr int RPB = 256 / (2 * D); // key rows per 256-byte bank window
-    static constexpr int TILE = 32 * D * 2;   // bytes of one K (or V) tile
-    // physical chunk of logical chunk c of key row k: K rows are read 16 keys
-    // x 16 B at a time, V rows 8 keys x 32 B (transposing reads)
-    __device__ static int swz_k(int k, int c) { return c ^ ((k / RPB) & (CH - 1)); }
-    __device__ static int swz_v(int k, int c) { return c ^ (2 * ((k / RPB) & (CH / 2 - 1))); }
+    // Padded LDS rows: K is read 16 keys x 16 B at a time (ds_read_b128), V
+    // 8 keys x 32 B (transposing reads); a 16-byte (K) / 32-byte (V) pad puts
+    // those keys in distinct banks, and keeps every fragment offset linear in
+    // (key block, chunk) so it is an instruction immediate.
+    static constexpr int KROW = 2 * D + 16;
+    static constexpr int VROW = 2 * D + 32;
+    static constexpr int KTILE = 32 * KROW;
+    static constexpr int BUF = KTILE + 32 * VROW;   // one K + V tile
 };
 
 // Workgroups over (query-token block, kv head), kv head fastest: blockIdx.x
@@ -120,7 +125,7 @@ struct Shape {
 // 8 kv heads every XCD serves one head and its L2 holds that head's pages
 // (shared prefixes included) for all sequences.
 template <int DT, int D, int G, int NW, int NCB>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                        const uint8_t* __restrict__ vreg, const int32_t* __restrict__ bt,
                        const int32_t* __restrict__ sl, const int32_t* __restrict__ qsl,
@@ -133,7 +138,7 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     constexpr int TPB = 16 / G;          // query tokens per column block
     constexpr int TPW = NCB * TPB;       // per wave
     constexpr int TWG = NW * TPW;        // per workgroup
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][S::TILE];   // [buffer][K, V]
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * S::BUF];   // 2 x (K tile, V tile)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -225,9 +230,8 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         for (int i = 0; i < CPT; ++i) {
             uint64_t page = pg[i];
             asm volatile("" : "+v"(page));
-            const uint64_t a = page * 2ull +
-                               static_cast<uint32_t>((key_tok(kt, i) & bmask) * p.row_bytes) +
-                               head_off;
+            const uint64_t a =
+                page * 2ull + (__umul24(key_tok(kt, i) & bmask, p.row_bytes) + head_off);
             gch[i] = *reinterpret_cast<const u32x4*>((c_tensor(i) ? vreg : kreg) + a);
         }
     };
@@ -235,49 +239,44 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int k = c_key(i);
-            const int pc = c_tensor(i) ? S::swz_v(k, tc) : S::swz_k(k, tc);
-            *reinterpret_cast<u32x4*>(&lds[buf][c_tensor(i)][k * D * 2 + pc * 16]) = gch[i];
+            const int off = c_tensor(i) ? S::KTILE + k * S::VROW : k * S::KROW;
+            *reinterpret_cast<u32x4*>(&lds[buf * S::BUF + off + tc * 16]) = gch[i];
         }
     };
 
-    float m_run[NCB], l_run[NCB];
+    // l (the softmax denominator) accumulates on the MFMA as ones x P^T: every
+    // row of lsum[cb] holds the column sums of the 16-bit P used for O
+    const u32x4 ones = DT == kDtF16 ? u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}
+                                    : u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+    float m_run[NCB];
+    f32x4 lsum[NCB];
     f32x4 acc[NCB][DB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
         m_run[cb] = -INFINITY;
-        l_run[cb] = 0.0f;
+        lsum[cb] = f32x4{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < DB; ++i) acc[cb][i] = f32x4{0, 0, 0, 0};
     }
 
-    // LDS byte offsets of this lane's K fragments (tile-invariant)
-    int k_off[2][KC];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-            const int k = 16 * h + ln;
-            k_off[h][kc] = k * D * 2 + S::swz_k(k, 4 * kc + lg) * 16;
-        }
-    // V^T fragment (db, h): lane a + 4s reads V[key 16h + 4lg + s][d 16db + 4a]
-    const int va = ln & 3, vsi = ln >> 2;
-    auto v_off = [&](int db, int h) {
-        const int k = 16 * h + 4 * lg + vsi;
-        const int d = 16 * db + 4 * va;
-        return k * D * 2 + S::swz_v(k, d >> 3) * 16 + (d & 7) * 2;
-    };
+    // LDS byte offsets of this lane's fragments: K (key ln of a 16-key block,
+    // chunk lg of a 32-element k-step); V^T (lane a + 4s reads key 4lg + s of
+    // a 16-key block, elements 4a..4a+3 of a 16-element d block)
+    const int k_lane = ln * S::KROW + lg * 16;
+    const int v_lane = S::KTILE + (4 * lg + (ln >> 2)) * S::VROW + (ln & 3) * 8;
 
-    // One 32-key tile.  Only a tile that crosses some column's position
-    // applies the causal mask.
-    auto compute = [&](int buf, int kt) {
-        const uint8_t* kb = lds[buf][0];
-        const uint8_t* vb = lds[buf][1];
+    // One 32-key tile in two phases.  softmax_phase: S^T = K Q^T, causal
+    // mask (only on a tile that crosses some column's position), column
+    // maxima, lazy rescale, P into pf and l += ones x P^T.  pv_phase:
+    // O^T += V^T P^T.
+    auto softmax_phase = [&](int buf, int kt, u32x4 (&pf)[NCB]) {
+        const uint8_t* kb = lds + buf * S::BUF + k_lane;
         u32x4 kf[2][KC];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc)
-                kf[h][kc] = *reinterpret_cast<const u32x4*>(kb + k_off[h][kc]);
+                kf[h][kc] = *reinterpret_cast<const u32x4*>(kb + h * 16 * S::KROW + kc * 64);
         f32x4 s[NCB][2];
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb)
@@ -288,14 +287,6 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                 for (int kc = 0; kc < KC; ++kc)
                     s[cb][h] = mfma16<DT>(kf[h][kc], qf[cb][kc], s[cb][h]);
             }
-        // V^T fragments: in flight during the softmax
-        u32x4 vf[DB];
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            const u32x2 lo = lds_read_tr(vb + v_off(db, 0));
-            const u32x2 hi = lds_read_tr(vb + v_off(db, 1));
-            vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
         if (kt * 32 + 31 > qmin) {
             const int key0 = kt * 32 + 4 * lg;
 #pragma unroll
@@ -312,8 +303,8 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         bool any_grow = false;
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) {
-            float x = fmaxf(fmaxf(fmaxf(s[cb][0][0], s[cb][0][1]), fmaxf(s[cb][0][2], s[cb][0][3])),
-                            fmaxf(fmaxf(s[cb][1][0], s[cb][1][1]), fmaxf(s[cb][1][2], s[cb][1][3])));
+            const float x = vmax(vmax(vmax(s[cb][0][0], s[cb][0][1]), vmax(s[cb][0][2], s[cb][0][3])),
+                                 vmax(vmax(s[cb][1][0], s[cb][1][1]), vmax(s[cb][1][2], s[cb][1][3])));
             mt[cb] = col_max(x) * p.scale_log2;
             // rescale only when the column maximum grows by more than 8
             grow[cb] = mt[cb] > m_run[cb] + 8.0f;
@@ -325,7 +316,7 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                 if (!__builtin_amdgcn_ballot_w64(grow[cb])) continue;
                 // (a column that does not grow keeps its scale exactly)
                 const float corr = grow[cb] ? __builtin_amdgcn_exp2f(m_run[cb] - mt[cb]) : 1.0f;
-                l_run[cb] *= corr;
+                lsum[cb] *= corr;
 #pragma unroll
                 for (int db = 0; db < DB; ++db) acc[cb][db] *= corr;
                 m_run[cb] = grow[cb] ? mt[cb] : m_run[cb];
@@ -341,13 +332,24 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[cb][h][r], p.scale_log2, nmu));
-            l_run[cb] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-            u32x4 pf;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pf[i] = pack2<DT>(pv[2 * i], pv[2 * i + 1]);
-#pragma unroll
-            for (int db = 0; db < DB; ++db) acc[cb][db] = mfma16<DT>(vf[db], pf, acc[cb][db]);
+            for (int i = 0; i < 4; ++i) pf[cb][i] = pack2<DT>(pv[2 * i], pv[2 * i + 1]);
+            lsum[cb] = mfma16<DT>(ones, pf[cb], lsum[cb]);
         }
+    };
+    auto pv_phase = [&](int buf, const u32x4 (&pf)[NCB]) {
+        const uint8_t* vb = lds + buf * S::BUF + v_lane;
+        u32x4 vf[DB];
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const u32x2 lo = lds_read_tr(vb + db * 32);
+            const u32x2 hi = lds_read_tr(vb + 16 * S::VROW + db * 32);
+            vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) acc[cb][db] = mfma16<DT>(vf[db], pf[cb], acc[cb][db]);
     };
 
     if (nt_wg > 0) {   // (no tile at all: no column has a visible key)
@@ -370,15 +372,25 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         // Gathers past the last tile read clamped (valid) rows and are never
         // consumed; issuing them unconditionally keeps every iteration's
         // load sequence identical, so the compiler's counter waits stay exact.
-        for (int kt = 0; kt < nt_wg; ++kt) {
-            if (kt < nt_w) compute(kt & 1, kt);
-            store_tile((kt + 1) & 1);
+        // Two tiles per trip, so each LDS buffer index is a constant (an odd
+        // count runs one trip with nothing to compute on its second tile).
+        auto step = [&](int kt, int buf) {
+            if (kt < nt_w) {
+                u32x4 pf[NCB];
+                softmax_phase(buf, kt, pf);
+                pv_phase(buf, pf);
+            }
+            store_tile(buf ^ 1);
             __syncthreads();
             gather(kt + 2, pg);
 #pragma unroll
             for (int i = 0; i < CPT; ++i) pg[i] = page_offs(ent[i]);   // tile kt + 3
 #pragma unroll
             for (int i = 0; i < CPT; ++i) ent[i] = page_entry(kt + 4, i);
+        };
+        for (int kt = 0; kt < nt_wg; kt += 2) {
+            step(kt, 0);
+            step(kt + 1, 1);
         }
     }
 
@@ -386,7 +398,7 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     if (!wave_live) return;
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
-        const float lt = col_sum(l_run[cb]);
+        const float lt = lsum[cb][0];
         const int t = tok0 + cb * TPB + ln / G;
         if (t < len) {
             const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
@@ -490,7 +502,10 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
 
 template <int DT, int D, int G>
 bool launch_mfma(const dev::AttnPrefillArgs& a, PrefillParams& p, hipStream_t s, std::string* err) {
-    constexpr int NW = 8, NCB = 2;   // 8 waves of 32 columns: 2 waves per SIMD
+#ifndef KCMM_PREFILL_NW
+#define KCMM_PREFILL_NW 8
+#endif
+    constexpr int NW = KCMM_PREFILL_NW, NCB = 2;   // waves of 32 columns: 2 waves per SIMD
     constexpr int TWG = NW * NCB * (16 / G);
     const long long blocks =
         (static_cast<long long>(a.total_query_tokens) / TWG + a.batch + 1) * p.kv_heads;
