@@ -105,7 +105,7 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint8_t* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
-template <int D>
+template <int D, int KT>
 struct Shape {
     static constexpr int CH = D / 8;          // 16-byte chunks per key row
     static constexpr int KC = D / 32;         // k-steps of S^T = K Q^T
@@ -116,25 +116,27 @@ struct Shape {
     // (key block, chunk) so it is an instruction immediate.
     static constexpr int KROW = 2 * D + 16;
     static constexpr int VROW = 2 * D + 32;
-    static constexpr int KTILE = 32 * KROW;
-    static constexpr int BUF = KTILE + 32 * VROW;   // one K + V tile
+    static constexpr int KTILE = KT * KROW;
+    static constexpr int BUF = KTILE + KT * VROW;   // one K + V tile of KT keys
 };
 
 // Workgroups over (query-token block, kv head), kv head fastest: blockIdx.x
 // = block * Hkv + g.  Workgroups are dealt to the 8 XCDs round-robin, so with
 // 8 kv heads every XCD serves one head and its L2 holds that head's pages
 // (shared prefixes included) for all sequences.
-template <int DT, int D, int G, int NW, int NCB>
+template <int DT, int D, int G, int NW, int NCB, int KT>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                        const uint8_t* __restrict__ vreg, const int32_t* __restrict__ bt,
                        const int32_t* __restrict__ sl, const int32_t* __restrict__ qsl,
                        const uint64_t* __restrict__ offs) {
-    using S = Shape<D>;
+    using S = Shape<D, KT>;
     constexpr int KC = S::KC, DB = S::DB, CH = S::CH;
+    constexpr int NKB = KT / 16;         // 16-key blocks of S^T per tile
+    constexpr int NKS = KT / 32;         // 32-key k-steps of P V per tile
     constexpr int NT = NW * 64;          // threads
-    constexpr int CPT = 64 * CH / NT;    // 16-byte chunks per thread per tile (K and V)
-    static_assert(CPT >= 1 && 64 * CH % NT == 0, "tile does not split over the threads");
+    constexpr int CPT = 2 * KT * CH / NT;   // 16-byte chunks per thread per tile (K and V)
+    static_assert(CPT >= 1 && 2 * KT * CH % NT == 0, "tile does not split over the threads");
     constexpr int TPB = 16 / G;          // query tokens per column block
     constexpr int TPW = NCB * TPB;       // per wave
     constexpr int TWG = NW * TPW;        // per workgroup
@@ -181,11 +183,11 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     const int tok0_wg = blk * TWG;
     // queries before position 0 (more queries than cached tokens) see no key;
     // their rows are written as zeros
-    const int nt_wg = (max(0, first_pos + min(tok0_wg + TWG, len)) + 31) / 32;
+    const int nt_wg = (max(0, first_pos + min(tok0_wg + TWG, len)) + KT - 1) / KT;
     const int tok0 = tok0_wg + wave * TPW;  // this wave's first query (chunk index)
     const bool wave_live = tok0 < len;
     const int tok_last = min(tok0 + TPW, len) - 1;
-    const int nt_w = wave_live ? (max(0, first_pos + tok_last + 1) + 31) / 32 : 0;
+    const int nt_w = wave_live ? (max(0, first_pos + tok_last + 1) + KT - 1) / KT : 0;
     const int qmin = first_pos + tok0;     // smallest position among the wave's columns
 
     // ---- columns: query token (clamped into the chunk; extra columns are
@@ -206,16 +208,16 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     // no wait inside the key loop is left counting them
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- tile gather: chunk q = tid + NT * i of the tile's 2 x 32 x CH
-    // chunks is (tensor q / (32 CH), key (q / CH) % 32, chunk q % CH); keys
+    // ---- tile gather: chunk q = tid + NT * i of the tile's 2 x KT x CH
+    // chunks is (tensor q / (KT CH), key (q / CH) % KT, chunk q % CH); keys
     // past the sequence read its last row (finite; P = 0 there) ----
-    auto c_tensor = [&](int i) { return (tid + NT * i) / (32 * CH); };
-    auto c_key = [&](int i) { return ((tid + NT * i) / CH) % 32; };
+    auto c_tensor = [&](int i) { return (tid + NT * i) / (KT * CH); };
+    auto c_key = [&](int i) { return ((tid + NT * i) / CH) % KT; };
     const int tc = tid % CH;
     const int32_t* row = bt + static_cast<size_t>(b) * p.mbps;
     const int bmask = (1 << p.bs_shift) - 1;
     const uint32_t head_off = static_cast<uint32_t>(g * D * 2 + tc * 16);
-    auto key_tok = [&](int kt, int i) { return min(kt * 32 + c_key(i), L - 1); };
+    auto key_tok = [&](int kt, int i) { return min(kt * KT + c_key(i), L - 1); };
     auto page_entry = [&](int kt, int i) { return row[key_tok(kt, i) >> p.bs_shift]; };
     // Loaded values pass through an empty asm where they are used, so the
     // compiler cannot fold their arithmetic back next to the load (which
@@ -265,37 +267,36 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     const int k_lane = ln * S::KROW + lg * 16;
     const int v_lane = S::KTILE + (4 * lg + (ln >> 2)) * S::VROW + (ln & 3) * 8;
 
-    // One 32-key tile in two phases.  softmax_phase: S^T = K Q^T, causal
+    // One KT-key tile in two phases.  softmax_phase: S^T = K Q^T, causal
     // mask (only on a tile that crosses some column's position), column
     // maxima, lazy rescale, P into pf and l += ones x P^T.  pv_phase:
-    // O^T += V^T P^T.
-    auto softmax_phase = [&](int buf, int kt, u32x4 (&pf)[NCB]) {
+    // O^T += V^T P^T in 32-key k-steps.
+    auto softmax_phase = [&](int buf, int kt, u32x4 (&pf)[NCB][NKS]) {
         const uint8_t* kb = lds + buf * S::BUF + k_lane;
-        u32x4 kf[2][KC];
+        f32x4 s[NCB][NKB];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int hb = 0; hb < NKB; ++hb) {
+            u32x4 kf[KC];
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc)
-                kf[h][kc] = *reinterpret_cast<const u32x4*>(kb + h * 16 * S::KROW + kc * 64);
-        f32x4 s[NCB][2];
+                kf[kc] = *reinterpret_cast<const u32x4*>(kb + hb * 16 * S::KROW + kc * 64);
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                s[cb][h] = f32x4{0, 0, 0, 0};
+            for (int cb = 0; cb < NCB; ++cb) {
+                s[cb][hb] = f32x4{0, 0, 0, 0};
 #pragma unroll
                 for (int kc = 0; kc < KC; ++kc)
-                    s[cb][h] = mfma16<DT>(kf[h][kc], qf[cb][kc], s[cb][h]);
+                    s[cb][hb] = mfma16<DT>(kf[kc], qf[cb][kc], s[cb][hb]);
             }
-        if (kt * 32 + 31 > qmin) {
-            const int key0 = kt * 32 + 4 * lg;
+        }
+        if (kt * KT + KT - 1 > qmin) {
+            const int key0 = kt * KT + 4 * lg;
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-                for (int h = 0; h < 2; ++h)
+                for (int hb = 0; hb < NKB; ++hb)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (key0 + 16 * h + r > qpos[cb]) s[cb][h][r] = -INFINITY;
+                        if (key0 + 16 * hb + r > qpos[cb]) s[cb][hb][r] = -INFINITY;
         }
         // column maxima of the raw scores (scale > 0), masked keys -inf
         float mt[NCB];
@@ -303,8 +304,10 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         bool any_grow = false;
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) {
-            const float x = vmax(vmax(vmax(s[cb][0][0], s[cb][0][1]), vmax(s[cb][0][2], s[cb][0][3])),
-                                 vmax(vmax(s[cb][1][0], s[cb][1][1]), vmax(s[cb][1][2], s[cb][1][3])));
+            float x = -INFINITY;
+#pragma unroll
+            for (int hb = 0; hb < NKB; ++hb)
+                x = vmax(x, vmax(vmax(s[cb][hb][0], s[cb][hb][1]), vmax(s[cb][hb][2], s[cb][hb][3])));
             mt[cb] = col_max(x) * p.scale_log2;
             // rescale only when the column maximum grows by more than 8
             grow[cb] = mt[cb] > m_run[cb] + 8.0f;
@@ -326,30 +329,39 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         for (int cb = 0; cb < NCB; ++cb) {
             // a column with no visible key yet keeps m = -inf and P = 0
             const float nmu = m_run[cb] == -INFINITY ? 0.0f : -m_run[cb];
-            float pv[8];
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int j = 0; j < NKS; ++j) {
+                // k-step j: keys 4lg..+3 of block 2j, then of block 2j + 1
+                float pv[8];
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[cb][h][r], p.scale_log2, nmu));
+                for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pf[cb][i] = pack2<DT>(pv[2 * i], pv[2 * i + 1]);
-            lsum[cb] = mfma16<DT>(ones, pf[cb], lsum[cb]);
+                    for (int r = 0; r < 4; ++r)
+                        pv[4 * h + r] =
+                            __builtin_amdgcn_exp2f(fmaf(s[cb][2 * j + h][r], p.scale_log2, nmu));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pf[cb][j][i] = pack2<DT>(pv[2 * i], pv[2 * i + 1]);
+                lsum[cb] = mfma16<DT>(ones, pf[cb][j], lsum[cb]);
+            }
         }
     };
-    auto pv_phase = [&](int buf, const u32x4 (&pf)[NCB]) {
-        const uint8_t* vb = lds + buf * S::BUF + v_lane;
-        u32x4 vf[DB];
+    auto pv_phase = [&](int buf, const u32x4 (&pf)[NCB][NKS]) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            const u32x2 lo = lds_read_tr(vb + db * 32);
-            const u32x2 hi = lds_read_tr(vb + 16 * S::VROW + db * 32);
-            vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        for (int j = 0; j < NKS; ++j) {
+            const uint8_t* vb = lds + buf * S::BUF + v_lane + 32 * j * S::VROW;
+            u32x4 vf[DB];
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const u32x2 lo = lds_read_tr(vb + db * 32);
+                const u32x2 hi = lds_read_tr(vb + 16 * S::VROW + db * 32);
+                vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            }
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    acc[cb][db] = mfma16<DT>(vf[db], pf[cb][j], acc[cb][db]);
         }
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-            for (int db = 0; db < DB; ++db) acc[cb][db] = mfma16<DT>(vf[db], pf[cb], acc[cb][db]);
     };
 
     if (nt_wg > 0) {   // (no tile at all: no column has a visible key)
@@ -376,7 +388,7 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         // count runs one trip with nothing to compute on its second tile).
         auto step = [&](int kt, int buf) {
             if (kt < nt_w) {
-                u32x4 pf[NCB];
+                u32x4 pf[NCB][NKS];
                 softmax_phase(buf, kt, pf);
                 pv_phase(buf, pf);
             }
@@ -502,10 +514,10 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
 
 template <int DT, int D, int G>
 bool launch_mfma(const dev::AttnPrefillArgs& a, PrefillParams& p, hipStream_t s, std::string* err) {
-#ifndef KCMM_PREFILL_NW
-#define KCMM_PREFILL_NW 8
-#endif
-    constexpr int NW = KCMM_PREFILL_NW, NCB = 2;   // waves of 32 columns: 2 waves per SIMD
+    // 8 waves of 32 columns (2 waves per SIMD), 32 keys per tile.  Measured
+    // on Cfg3 (MI355X): 64-key tiles ~2% slower; 4-wave workgroups (two per
+    // CU) ~10% slower; 64 columns per wave does not fit 2 waves per SIMD.
+    constexpr int NW = 8, NCB = 2, KT = 32;
     constexpr int TWG = NW * NCB * (16 / G);
     const long long blocks =
         (static_cast<long long>(a.total_query_tokens) / TWG + a.batch + 1) * p.kv_heads;
@@ -513,7 +525,7 @@ bool launch_mfma(const dev::AttnPrefillArgs& a, PrefillParams& p, hipStream_t s,
         *err = "prefill: too many query tokens";
         return false;
     }
-    hipLaunchKernelGGL((attn_prefill_mfma<DT, D, G, NW, NCB>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((attn_prefill_mfma<DT, D, G, NW, NCB, KT>), dim3(static_cast<unsigned>(blocks)),
                        dim3(NW * 64), 0, s, p, reinterpret_cast<const uint8_t*>(a.k_base),
                        reinterpret_cast<const uint8_t*>(a.v_base),
                        reinterpret_cast<const int32_t*>(a.block_tables),
