@@ -639,15 +639,17 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
 
 // Log-sum-exp merge, one wave per (b, kv head) that spans several waves of
 // the streaming kernel: its partials sit in slot 1 of its first wave wa and
-// in slot 0 of waves wa+1 .. wa+np-1.  All (max, denominator) pairs of up to
-// 64 parts are read at once (one part per lane); the weights go through LDS.
-// NO = outputs per lane rounded up to a power of two; every load is issued
-// unconditionally (clamped index) so that none waits behind a branch.
+// in slot 0 of waves wa+1 .. wa+np-1.  Two dependent memory steps: the
+// segment record, then the (max, denominator) pairs of up to 64 parts (one
+// part per lane) together with the accumulators of the first QP parts; the
+// weights reach every lane through v_readlane.  NO = outputs per lane
+// rounded up to a power of two; every load is issued unconditionally
+// (clamped index) so that none waits behind a branch.
 template <int DT, int D, int NO>
 __global__ __launch_bounds__(64) void attn_decode_merge(AttnParams p,
                                                         const int2* __restrict__ info) {
-    constexpr int NJ = NO * 64 / D > 0 ? NO * 64 / D : 1;  // heads covered (power of two)
-    __shared__ float sw[64 * NJ];
+    constexpr int NJ = NO * 64 / D > 0 ? NO * 64 / D : 1;   // heads covered (power of two)
+    constexpr int QP = NO >= 16 ? 2 : 32 / NO > 4 ? 4 : 32 / NO;   // parts per round
     const int2 si = info[blockIdx.x];
     const int wa = si.x, np = si.y;
     if (np <= 1) return;
@@ -657,51 +659,67 @@ __global__ __launch_bounds__(64) void attn_decode_merge(AttnParams p,
     const int g = blockIdx.x - b * p.kv_heads;
     const int n_out = G * D / 64;      // lane holds outputs lane + 64e, e < n_out
     auto unit = [&](int k) { return static_cast<size_t>(wa + k) * 2 + (k == 0 ? 1 : 0); };
+    auto load_parts = [&](float (&v)[QP][NO], int k0) {
+#pragma unroll
+        for (int q = 0; q < QP; ++q) {
+            const float* pa = p.part_acc + unit(min(k0 + q, np - 1)) * G * D + lane;
+#pragma unroll
+            for (int e = 0; e < NO; ++e) v[q][e] = pa[min(e, n_out - 1) * 64];
+        }
+    };
 
-    float mx[NJ];
+    float mx[NJ], ls[NJ], acc[NO];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) mx[j] = -INFINITY;
-    for (int k0 = 0; k0 < np; k0 += 64) {
-        const int k = min(k0 + lane, np - 1);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-            mx[j] = fmaxf(mx[j], p.part_ml[(unit(k) * G + min(j, G - 1)) * 2]);
+    for (int j = 0; j < NJ; ++j) {
+        mx[j] = -INFINITY;
+        ls[j] = 0.0f;
     }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx[j] = fmaxf(mx[j], __shfl_xor(mx[j], o));
-
-    float ls[NJ], acc[NO];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) ls[j] = 0.0f;
 #pragma unroll
     for (int e = 0; e < NO; ++e) acc[e] = 0.0f;
     for (int k0 = 0; k0 < np; k0 += 64) {
         const bool live = k0 + lane < np;
         const int k = min(k0 + lane, np - 1);
+        float m[NJ], l[NJ], v[QP][NO];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const size_t u = (unit(k) * G + min(j, G - 1)) * 2;
-            const float w = live ? __builtin_amdgcn_exp2f(p.part_ml[u] - mx[j]) : 0.0f;
-            ls[j] += w * p.part_ml[u + 1];
-            sw[lane * NJ + j] = w;
+            m[j] = p.part_ml[u];
+            l[j] = p.part_ml[u + 1];
         }
-        __syncthreads();
-        const int kn = min(64, np - k0);
-#pragma unroll 4
-        for (int kk = 0; kk < kn; ++kk) {
-            const float* pa = p.part_acc + unit(k0 + kk) * G * D + lane;
+        load_parts(v, k0);   // in flight with the (max, denominator) loads
+        float w[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            float cm = live ? m[j] : -INFINITY;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
+            const float nm = fmaxf(mx[j], cm);
+            const float corr = mx[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mx[j] - nm);
+            w[j] = live ? __builtin_amdgcn_exp2f(m[j] - nm) : 0.0f;
+            float wl = w[j] * l[j];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) wl += __shfl_xor(wl, o);
+            ls[j] = ls[j] * corr + wl;
+            mx[j] = nm;
 #pragma unroll
             for (int e = 0; e < NO; ++e)
-                acc[e] += sw[kk * NJ + e * 64 / D] * pa[min(e, n_out - 1) * 64];
+                if (e * 64 / D == j) acc[e] *= corr;
         }
-        __syncthreads();
+        const int kn = min(64, np - k0);
+        for (int kk0 = 0; kk0 < kn; kk0 += QP) {
+            if (kk0 > 0) load_parts(v, k0 + kk0);
+#pragma unroll
+            for (int q = 0; q < QP; ++q) {
+                const int kk = min(kk0 + q, kn - 1);
+#pragma unroll
+                for (int e = 0; e < NO; ++e) {
+                    const float wt = __int_as_float(
+                        __builtin_amdgcn_readlane(__float_as_int(w[e * 64 / D]), kk));
+                    acc[e] += kk0 + q < kn ? wt * v[q][e] : 0.0f;
+                }
+            }
+        }
     }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ls[j] += __shfl_xor(ls[j], o);
     uint16_t* out = reinterpret_cast<uint16_t*>(p.out) +
                     (static_cast<size_t>(b) * p.num_q_heads + g * G) * D + lane;
 #pragma unroll
