@@ -57,8 +57,8 @@ __device__ __forceinline__ u32x4 load_stream(const uint8_t* a) {
 // (Measured alternatives that were slower at the Llama-3-8B decode shapes: a
 // persistent grid over (row block, k chunk) tiles with a 6-deep ring, and
 // direct-to-LDS activation loads with a 3-deep weight ring.)
-template <int MB, int KCH, int DEPTH>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEPTH == 3 ? 4 : 2)))
+template <int MB, int KCH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
                       uint16_t* __restrict__ Y, float* __restrict__ part, int M, int N, int K,
                       int klen) {
@@ -118,9 +118,6 @@ void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict
         for (int c2 = 0; c2 < LINES; ++c2) fix_lines(wa[2 * c2], wa[2 * c2 + 1], low8);
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
-            // (depth 3: one k-step of activation fragments live at a time)
-            if constexpr (DEPTH == 3)
-                if (kc > 0) __builtin_amdgcn_sched_barrier(0);
             const int pc = 4 * kc + lg;
 #pragma unroll
             for (int j = 0; j < MB; ++j) {
@@ -133,82 +130,6 @@ void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict
         }
     };
 
-    // acc[j][r] = Y[m_base + 16j + ln][n0 + 4lg + r]
-    auto store_out = [&]() {
-#pragma unroll
-        for (int j = 0; j < MB; ++j) {
-            const int m = m_base + 16 * j + ln;
-            if (m >= M) continue;
-            const int n = n0 + 4 * lg;
-            if (part == nullptr) {
-                u32x2 o;
-                o[0] = f32_to_bf16_bits(acc[j][0]) | (f32_to_bf16_bits(acc[j][1]) << 16);
-                o[1] = f32_to_bf16_bits(acc[j][2]) | (f32_to_bf16_bits(acc[j][3]) << 16);
-                *reinterpret_cast<u32x2*>(Y + static_cast<size_t>(m) * N + n) = o;
-            } else {
-                *reinterpret_cast<f32x4*>(part + (static_cast<size_t>(blockIdx.y) * M + m) * N +
-                                          n) = acc[j];
-            }
-        }
-    };
-
-    if constexpr (DEPTH == 3) {
-        // Three weight buffers: chunks c+1 and c+2 are in flight while c is
-        // consumed (twice the weight bytes in flight per wave).  Unrolled by
-        // three with a peeled tail, so every step's loads are fixed at
-        // compile time and the compiler's counter waits stay exact.
-        u32x4 w0[2 * LINES], w1[2 * LINES], w2[2 * LINES];
-        load_x(0);
-        load_w(w0, 0);
-        load_w(w1, 1);   // (nchunks >= 2 on this path)
-        __builtin_amdgcn_sched_barrier(0);
-        store_x(0);
-        __syncthreads();
-        auto step3 = [&](u32x4* now, u32x4* next2, int c, auto lx_tag, auto lw_tag) {
-            constexpr bool LX = decltype(lx_tag)::value;
-            constexpr bool LW = decltype(lw_tag)::value;
-            if constexpr (LX) load_x(c + 1);
-            if constexpr (LW) load_w(next2, c + 2);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(now, c & 1);
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (LX) {
-                store_x((c + 1) & 1);
-                __syncthreads();
-            }
-        };
-        using T = std::integral_constant<bool, true>;
-        using F = std::integral_constant<bool, false>;
-        int c = 0;
-        for (; c + 4 < nchunks; c += 3) {
-            step3(w0, w2, c, T{}, T{});
-            step3(w1, w0, c + 1, T{}, T{});
-            step3(w2, w1, c + 2, T{}, T{});
-        }
-        // here w0 = chunk c, w1 = chunk c + 1 and 1 <= nchunks - c <= 4
-        switch (nchunks - c) {
-            case 4:
-                step3(w0, w2, c, T{}, T{});
-                step3(w1, w0, c + 1, T{}, T{});
-                step3(w2, w1, c + 2, T{}, F{});
-                step3(w0, w1, c + 3, F{}, F{});
-                break;
-            case 3:
-                step3(w0, w2, c, T{}, T{});
-                step3(w1, w0, c + 1, T{}, F{});
-                step3(w2, w0, c + 2, F{}, F{});
-                break;
-            case 2:
-                step3(w0, w2, c, T{}, F{});
-                step3(w1, w2, c + 1, F{}, F{});
-                break;
-            default:
-                step3(w0, w2, c, F{}, F{});
-                break;
-        }
-        store_out();
-        return;
-    }
     u32x4 wa0[2 * LINES], wa1[2 * LINES];
     load_x(0);
     load_w(wa0, 0);
@@ -244,7 +165,22 @@ void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict
     } else {
         step(wa0, wa1, 0, c, Last{});
     }
-    store_out();
+
+    // acc[j][r] = Y[m_base + 16j + ln][n0 + 4lg + r]
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+        const int m = m_base + 16 * j + ln;
+        if (m >= M) continue;
+        const int n = n0 + 4 * lg;
+        if (part == nullptr) {
+            u32x2 o;
+            o[0] = f32_to_bf16_bits(acc[j][0]) | (f32_to_bf16_bits(acc[j][1]) << 16);
+            o[1] = f32_to_bf16_bits(acc[j][2]) | (f32_to_bf16_bits(acc[j][3]) << 16);
+            *reinterpret_cast<u32x2*>(Y + static_cast<size_t>(m) * N + n) = o;
+        } else {
+            *reinterpret_cast<f32x4*>(part + (static_cast<size_t>(blockIdx.y) * M + m) * N + n) = acc[j];
+        }
+    }
 }
 
 // Y = bf16(sum over splits of the fp32 partials); 4 outputs per thread.
@@ -289,8 +225,6 @@ int choose_splits(int N, int K, int kch, int mgroups) {
 template <int MB, int KCH>
 bool launch_gemm(const uint16_t* X, const uint16_t* W, uint16_t* Y, int M, int N, int K,
                  uint64_t stream, std::string* err) {
-    // weight pipeline depth (KCMM_GEMM_DEPTH, 2 or 3 chunks)
-    const int depth = env_int("KCMM_GEMM_DEPTH", 2) == 3 ? 3 : 2;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int mgroups = (M + 16 * MB - 1) / (16 * MB);
     const int splits = choose_splits(N, K, KCH, mgroups);
@@ -303,19 +237,8 @@ bool launch_gemm(const uint16_t* X, const uint16_t* W, uint16_t* Y, int M, int N
         part = static_cast<float*>(ws);
     }
     const dim3 grid(N / 64, splits, mgroups);
-    const int klen = K / splits;
-    // depth 3 runs 128-wide chunks (4 workgroups, 16 waves per CU) at M <= 64
-    bool launched = false;
-    if constexpr (MB <= 4) {
-        if (depth == 3 && klen / 128 >= 2) {
-            hipLaunchKernelGGL((gemm_bf16_stream<MB, 128, 3>), grid, dim3(256), 0, s, X, W, Y,
-                               part, M, N, K, klen);
-            launched = true;
-        }
-    }
-    if (!launched)
-        hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, 2>), grid, dim3(256), 0, s, X, W, Y, part,
-                           M, N, K, klen);
+    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH>), grid, dim3(256), 0, s, X, W, Y, part, M, N, K,
+                       K / splits);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     if (splits > 1) {
         const int MN = M * N;
