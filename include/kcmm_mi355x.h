@@ -147,6 +147,77 @@ int kcmm_gemm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
                              uint32_t m, uint32_t n, uint32_t k,
                              uint64_t stream_ptr);
 
+/** Y = R + X * W^T: the O / down projections with the residual add of ref
+ *  llama_transformer.rs:358,377 (add.cu) in the GEMM's store.  The product
+ *  is rounded to bf16 before the add, as a bf16 model computes it; R may be
+ *  the same buffer as Y.  Same shape rules as kcmm_gemm_bf16_on_stream. */
+int kcmm_gemm_bf16_add_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t residual_ptr,
+                                 uint64_t y_ptr, uint32_t m, uint32_t n, uint32_t k,
+                                 uint64_t stream_ptr);
+
+/* ---- decode-step glue and the layer step -------------------------------- */
+/* The steps of one decoder layer around the GEMMs and the attention (ref
+ * LlamaTransformer::forward_step_paged, llama_transformer.rs:262-391, and
+ * its rms_norm.cu / rope.cu / silu_mul.cu / add.cu), with Hugging Face Llama
+ * semantics.  bf16 activations, fp32 arithmetic, enqueue only; pointers are
+ * device addresses aligned to 16 bytes. */
+
+/** y[r] = w * bf16(x[r] * rsqrt(mean(x[r]^2) + eps)) for each of `rows` rows
+ *  of `hidden` elements (HF LlamaRMSNorm).  hidden % 8 == 0. */
+int kcmm_rmsnorm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
+                                uint32_t rows, uint32_t hidden, float eps,
+                                uint64_t stream_ptr);
+
+/** act[r][j] = silu(gate_up[r][j]) * gate_up[r][intermediate + j] (the fused
+ *  [gate | up] projection output).  intermediate % 8 == 0. */
+int kcmm_silu_mul_bf16_on_stream(uint64_t gate_up_ptr, uint64_t act_ptr, uint32_t rows,
+                                 uint32_t intermediate, uint64_t stream_ptr);
+
+/** RoPE fused with the KV append for the decode token of every sequence of a
+ *  bf16 pool: row b of qkv_ptr holds [q heads | k heads | v heads] x
+ *  head_dim; the token's position is seq_lens[b] - 1 (seq_lens include it).
+ *  q is rotated into q_out_ptr ([batch][num_q_heads][head_dim], the layout
+ *  the attention reads); k is rotated and written, with v, into the token's
+ *  page row (the vLLM reshape_and_cache slot block_tables[b][pos / bs] * bs
+ *  + pos % bs).  Rotation: HF rotate_half pairs (i, i + head_dim/2) at angle
+ *  pos * inv_freq[i], inv_freq an fp32 device array of head_dim/2 (so any
+ *  HF rope_type works).  Sequences with seq_lens <= 0 or a position past
+ *  the table are skipped.  The caller makes shared pages private first. */
+int kcmm_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, uint64_t qkv_ptr,
+                                    uint64_t q_out_ptr, uint64_t block_tables_ptr,
+                                    uint64_t seq_lens_ptr, uint64_t block_offsets_f16_ptr,
+                                    uint64_t inv_freq_ptr, uint32_t batch,
+                                    uint32_t num_q_heads, uint32_t max_blocks_per_seq,
+                                    uint64_t stream_ptr);
+
+/** Device addresses of one layer's weights (bf16, row-major [out][in]). */
+typedef struct kcmm_layer_weights {
+    uint64_t attn_norm; /**< [hidden] */
+    uint64_t qkv;       /**< [(Hq + 2 Hkv) head_dim][hidden]: q rows, k rows, v rows */
+    uint64_t o;         /**< [hidden][Hq head_dim] */
+    uint64_t mlp_norm;  /**< [hidden] */
+    uint64_t gate_up;   /**< [2 intermediate][hidden]: gate rows, then up rows */
+    uint64_t down;      /**< [hidden][intermediate] */
+} kcmm_layer_weights_t;
+
+/** One decoder layer of a decode step, in place on hidden_ptr
+ *  ([batch][hidden] bf16), for layer `layer_idx` of a bf16 pool (ref
+ *  LlamaTransformer::forward_step_paged, llama_transformer.rs:262-391, per
+ *  layer): h += o(attn(rope(qkv(rmsnorm(h))))), with this token's k / v
+ *  appended to the pages; h += down(silu(gate) * up(rmsnorm(h))).  kv
+ *  heads, head_dim and block size are the pool's; attention scale is
+ *  1/sqrt(head_dim).  seq_lens include the new token (its position is
+ *  seq_lens[b] - 1).  hidden, intermediate and q_heads * head_dim must be
+ *  multiples of 256.  Activations use a per-stream workspace of the library. */
+int kcmm_decode_layer_step_on_stream(kcmm_pool_t *pool, uint32_t layer_idx,
+                                     const kcmm_layer_weights_t *weights, uint64_t hidden_ptr,
+                                     uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+                                     uint64_t block_offsets_f16_ptr, uint64_t inv_freq_ptr,
+                                     uint32_t batch, uint32_t hidden_size,
+                                     uint32_t num_q_heads, uint32_t intermediate_size,
+                                     uint32_t max_blocks_per_seq, float rms_eps,
+                                     uint64_t stream_ptr);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,13 @@ def make_config(*, num_layers, kv_heads, head_dim, max_batch, max_seq_len, block
     return cfg
 
 
+class KcmmLayerWeights(C.Structure):
+    """kcmm_layer_weights_t (include/kcmm_mi355x.h): device addresses of one
+    layer's bf16 weights."""
+    _fields_ = [("attn_norm", C.c_uint64), ("qkv", C.c_uint64), ("o", C.c_uint64),
+                ("mlp_norm", C.c_uint64), ("gate_up", C.c_uint64), ("down", C.c_uint64)]
+
+
 _P, _U32, _U64, _I32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int32
 _ATTN = [_P, _U32, _U64, _U64, _U64, _U64, _U64] + [_U32] * 6 + [C.c_float]
 
@@ -151,6 +158,14 @@ SIGNATURES = {
     "kcmm_copy_blocks_on_stream": ([_P, _P, _U32, _U64], C.c_int),
     "kcmm_copy_blocks_device_on_stream": ([_P, _U64, _U64, _U32, _U64], C.c_int),
     "kcmm_gemm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
+    "kcmm_gemm_bf16_add_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
+    "kcmm_rmsnorm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, C.c_float, _U64], C.c_int),
+    "kcmm_silu_mul_bf16_on_stream": ([_U64, _U64, _U32, _U32, _U64], C.c_int),
+    "kcmm_rope_append_bf16_on_stream": ([_P, _U32, _U64, _U64, _U64, _U64, _U64, _U64, _U32,
+                                         _U32, _U32, _U64], C.c_int),
+    "kcmm_decode_layer_step_on_stream": ([_P, _U32, C.POINTER(KcmmLayerWeights), _U64, _U64, _U64,
+                                          _U64, _U64, _U32, _U32, _U32, _U32, _U32, C.c_float,
+                                          _U64], C.c_int),
     "kcmm_below_low_watermark": ([_P, C.c_float], C.c_int),
     "kcmm_synchronize": ([_P], C.c_int),
     "kcmm_get_block_size": ([_P], _U32),
@@ -192,6 +207,22 @@ class KcmmLibrary:
     def gemm_bf16(self, x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr=0) -> None:
         if self.lib.kcmm_gemm_bf16_on_stream(x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr) != 0:
             raise KcmmError("kcmm_gemm_bf16_on_stream failed")
+
+    def gemm_bf16_add(self, x_ptr, w_ptr, residual_ptr, y_ptr, m, n, k, stream_ptr=0) -> None:
+        """Y = R + X W^T (R may be Y)."""
+        if self.lib.kcmm_gemm_bf16_add_on_stream(x_ptr, w_ptr, residual_ptr, y_ptr, m, n, k,
+                                                 stream_ptr) != 0:
+            raise KcmmError("kcmm_gemm_bf16_add_on_stream failed")
+
+    def rmsnorm_bf16(self, x_ptr, w_ptr, y_ptr, rows, hidden, eps, stream_ptr=0) -> None:
+        if self.lib.kcmm_rmsnorm_bf16_on_stream(x_ptr, w_ptr, y_ptr, rows, hidden, C.c_float(eps),
+                                                stream_ptr) != 0:
+            raise KcmmError("kcmm_rmsnorm_bf16_on_stream failed")
+
+    def silu_mul_bf16(self, gate_up_ptr, act_ptr, rows, intermediate, stream_ptr=0) -> None:
+        if self.lib.kcmm_silu_mul_bf16_on_stream(gate_up_ptr, act_ptr, rows, intermediate,
+                                                 stream_ptr) != 0:
+            raise KcmmError("kcmm_silu_mul_bf16_on_stream failed")
 
 
 class KcmmPool:
@@ -386,6 +417,28 @@ class KcmmPool:
             query_start_loc_ptr, block_offsets_f16_ptr, batch, total_query_tokens, num_q_heads,
             kv_heads, head_dim, block_size, max_blocks_per_seq, C.c_float(scale), stream_ptr)
         self._check(rc, "paged_attn_prefill")
+
+    # -- decode-step glue and the layer step --
+    def rope_append(self, *, layer_idx, qkv_ptr, q_out_ptr, block_tables_ptr, seq_lens_ptr,
+                    block_offsets_f16_ptr, inv_freq_ptr, batch, num_q_heads, max_blocks_per_seq,
+                    stream_ptr=0) -> None:
+        """RoPE of the decode token's q / k, k and v appended to its page row."""
+        rc = self.lib.kcmm_rope_append_bf16_on_stream(
+            self.handle, layer_idx, qkv_ptr, q_out_ptr, block_tables_ptr, seq_lens_ptr,
+            block_offsets_f16_ptr, inv_freq_ptr, batch, num_q_heads, max_blocks_per_seq,
+            stream_ptr)
+        self._check(rc, "rope_append")
+
+    def decode_layer_step(self, *, layer_idx, weights: KcmmLayerWeights, hidden_ptr,
+                          block_tables_ptr, seq_lens_ptr, block_offsets_f16_ptr, inv_freq_ptr,
+                          batch, hidden_size, num_q_heads, intermediate_size, max_blocks_per_seq,
+                          rms_eps, stream_ptr=0) -> None:
+        """One decoder layer of a decode step, in place on hidden ([batch][hidden] bf16)."""
+        rc = self.lib.kcmm_decode_layer_step_on_stream(
+            self.handle, layer_idx, C.byref(weights), hidden_ptr, block_tables_ptr, seq_lens_ptr,
+            block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size, num_q_heads,
+            intermediate_size, max_blocks_per_seq, C.c_float(rms_eps), stream_ptr)
+        self._check(rc, "decode_layer_step")
 
     # -- copy-on-write --
     def fork_sequence(self, src: int) -> int:

@@ -41,7 +41,7 @@ CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-Wno-unused-para
 HOST_SOURCES = ["pool_core.cpp", "ffi.cpp"]
 HIP_SOURCES = ["kernels/backing.hip", "kernels/attn_decode.hip", "kernels/attn_prefill.hip",
                "kernels/kv_write.hip",
-               "kernels/page_copy.hip", "kernels/gemm.hip"]
+               "kernels/page_copy.hip", "kernels/gemm.hip", "kernels/glue.hip"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -20,7 +20,8 @@ std::unique_ptr<PageBacking> make_backing(int device, std::string* err);
 bool set_device(int device, std::string* err);
 
 // Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
-// attention partials, 1: GEMM partials, 2: decode attention segment table).
+// attention partials, 1: GEMM partials, 2: decode attention segment table,
+// 3: decode layer-step activations).
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);
@@ -88,9 +89,26 @@ bool copy_pages_device(const std::vector<uint64_t>& region_bases, uint64_t pairs
                        uint64_t offsets_f16, size_t num_pairs, uint32_t block_bytes,
                        uint64_t stream, std::string* err);
 
-// Y = X W^T, bf16, fp32 accumulate.
+// Y = X W^T (+ R when residual != 0; R may be Y), bf16, fp32 accumulate.  With a
+// residual the product is rounded to bf16 before the add, as a bf16 model does.
 bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
-               uint64_t stream, std::string* err);
+               uint64_t stream, std::string* err, uint64_t residual = 0);
+
+// Decode-step glue (kernels/glue.hip), bf16.
+bool rmsnorm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t rows, uint32_t hidden, float eps,
+                  uint64_t stream, std::string* err);
+struct RopeAppendArgs {
+    uint64_t qkv;             // [batch][(Hq + 2 Hkv) D]: q heads, k heads, v heads
+    uint64_t q_out;           // [batch][Hq][D]
+    uint64_t k_base, v_base;  // the layer's regions
+    uint64_t block_tables, seq_lens, offsets_f16;
+    uint64_t inv_freq;        // fp32 [D/2]
+    uint32_t batch, num_q_heads, kv_heads, head_dim, block_size, mbps, row_bytes;
+    uint64_t stream;
+};
+bool rope_append_bf16(const RopeAppendArgs& a, std::string* err);
+bool silu_mul_bf16(uint64_t gate_up, uint64_t act, uint32_t rows, uint32_t inter,
+                   uint64_t stream, std::string* err);
 
 }  // namespace dev
 }  // namespace kcmm

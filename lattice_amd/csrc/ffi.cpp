@@ -5,6 +5,7 @@
 #include <execinfo.h>
 #include <unistd.h>
 
+#include <cmath>
 #include <csignal>
 #include <cstdio>
 #include <cstdlib>
@@ -845,6 +846,216 @@ int kcmm_gemm_bf16_on_stream(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uin
     std::string err;
     if (!kcmm::dev::gemm_bf16(x, w, y, m, n, k, stream, &err)) {
         std::fprintf(stderr, "kcmm_gemm_bf16_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_gemm_bf16_add_on_stream(uint64_t x, uint64_t w, uint64_t residual, uint64_t y,
+                                 uint32_t m, uint32_t n, uint32_t k, uint64_t stream) {
+    if (x == 0 || w == 0 || residual == 0 || y == 0 || m == 0 || n == 0 || k == 0) return -1;
+    std::string err;
+    if (!kcmm::dev::gemm_bf16(x, w, y, m, n, k, stream, &err, residual)) {
+        std::fprintf(stderr, "kcmm_gemm_bf16_add_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+// ---- decode-step glue and the layer step ------------------------------------------------------
+
+int kcmm_rmsnorm_bf16_on_stream(uint64_t x, uint64_t w, uint64_t y, uint32_t rows,
+                                uint32_t hidden, float eps, uint64_t stream) {
+    if (x == 0 || w == 0 || y == 0 || rows == 0 || hidden == 0 || hidden % 8 != 0 ||
+        !(eps >= 0.0f))
+        return -1;
+    std::string err;
+    if (!kcmm::dev::rmsnorm_bf16(x, w, y, rows, hidden, eps, stream, &err)) {
+        std::fprintf(stderr, "kcmm_rmsnorm_bf16_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_silu_mul_bf16_on_stream(uint64_t gate_up, uint64_t act, uint32_t rows,
+                                 uint32_t intermediate, uint64_t stream) {
+    if (gate_up == 0 || act == 0 || rows == 0 || intermediate == 0 || intermediate % 8 != 0)
+        return -1;
+    std::string err;
+    if (!kcmm::dev::silu_mul_bf16(gate_up, act, rows, intermediate, stream, &err)) {
+        std::fprintf(stderr, "kcmm_silu_mul_bf16_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+namespace {
+
+// Shape checks shared by the RoPE/append and layer-step entry points; the
+// kv geometry is the pool's.
+bool step_shapes_ok(kcmm_pool_t* pool, const char* fn, uint32_t layer_idx, uint32_t batch,
+                    uint32_t hq, uint32_t mbps) {
+    if (!layer_ok(pool, layer_idx, fn)) return false;
+    const kcmm::PoolGeometry& g = pool->core->geo();
+    if (g.dtype != kcmm::kBF16) {
+        pool->set_error(std::string(fn) + ": needs a bf16 pool");
+        return false;
+    }
+    if (batch == 0 || hq == 0 || mbps == 0 || hq % g.kv_heads != 0 || hq > 0xFFFF ||
+        mbps > 0xFFFF) {
+        pool->set_error(std::string(fn) +
+                        ": batch, q heads (a multiple of kv heads) and max_blocks_per_seq must "
+                        "be positive (q heads and max_blocks_per_seq <= 65535)");
+        return false;
+    }
+    if (g.head_dim % 8 != 0 || g.head_dim > 256) {
+        pool->set_error(std::string(fn) + ": head_dim must be a multiple of 8, <= 256");
+        return false;
+    }
+    return true;
+}
+
+kcmm::dev::RopeAppendArgs rope_args(kcmm_pool_t* pool, uint32_t layer_idx, uint64_t qkv,
+                                    uint64_t q_out, uint64_t bt, uint64_t sl, uint64_t offs,
+                                    uint64_t inv_freq, uint32_t batch, uint32_t hq,
+                                    uint32_t mbps, uint64_t stream) {
+    const kcmm::PoolGeometry& g = pool->core->geo();
+    kcmm::dev::RopeAppendArgs a{};
+    a.qkv = qkv;
+    a.q_out = q_out;
+    a.k_base = pool->core->va_k(layer_idx);
+    a.v_base = pool->core->va_v(layer_idx);
+    a.block_tables = bt;
+    a.seq_lens = sl;
+    a.offsets_f16 = offs;
+    a.inv_freq = inv_freq;
+    a.batch = batch;
+    a.num_q_heads = hq;
+    a.kv_heads = static_cast<uint32_t>(g.kv_heads);
+    a.head_dim = static_cast<uint32_t>(g.head_dim);
+    a.block_size = static_cast<uint32_t>(g.block_size);
+    a.mbps = mbps;
+    a.row_bytes = static_cast<uint32_t>(g.row_bytes);
+    a.stream = stream;
+    return a;
+}
+
+}  // namespace
+
+int kcmm_rope_append_bf16_on_stream(kcmm_pool_t* pool, uint32_t layer_idx, uint64_t qkv,
+                                    uint64_t q_out, uint64_t block_tables, uint64_t seq_lens,
+                                    uint64_t offsets_f16, uint64_t inv_freq, uint32_t batch,
+                                    uint32_t num_q_heads, uint32_t max_blocks_per_seq,
+                                    uint64_t stream) {
+    const char* fn = "kcmm_rope_append_bf16_on_stream";
+    if (pool == nullptr || qkv == 0 || q_out == 0 || block_tables == 0 || seq_lens == 0 ||
+        offsets_f16 == 0 || inv_freq == 0) {
+        if (pool) pool->set_error(std::string(fn) + ": null pointer argument");
+        return -1;
+    }
+    if (!step_shapes_ok(pool, fn, layer_idx, batch, num_q_heads, max_blocks_per_seq)) return -1;
+    std::string err;
+    if (!kcmm::dev::set_device(pool->device, &err) ||
+        !kcmm::dev::rope_append_bf16(rope_args(pool, layer_idx, qkv, q_out, block_tables, seq_lens,
+                                               offsets_f16, inv_freq, batch, num_q_heads,
+                                               max_blocks_per_seq, stream),
+                                     &err)) {
+        pool->set_error(std::string(fn) + ": " + err);
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_decode_layer_step_on_stream(kcmm_pool_t* pool, uint32_t layer_idx,
+                                     const kcmm_layer_weights_t* w, uint64_t hidden,
+                                     uint64_t block_tables, uint64_t seq_lens,
+                                     uint64_t offsets_f16, uint64_t inv_freq, uint32_t batch,
+                                     uint32_t hidden_size, uint32_t num_q_heads,
+                                     uint32_t intermediate_size, uint32_t max_blocks_per_seq,
+                                     float rms_eps, uint64_t stream) {
+    const char* fn = "kcmm_decode_layer_step_on_stream";
+    if (pool == nullptr || w == nullptr || hidden == 0 || block_tables == 0 || seq_lens == 0 ||
+        offsets_f16 == 0 || inv_freq == 0 || w->attn_norm == 0 || w->qkv == 0 || w->o == 0 ||
+        w->mlp_norm == 0 || w->gate_up == 0 || w->down == 0) {
+        if (pool) pool->set_error(std::string(fn) + ": null pointer argument");
+        return -1;
+    }
+    if (!step_shapes_ok(pool, fn, layer_idx, batch, num_q_heads, max_blocks_per_seq)) return -1;
+    const kcmm::PoolGeometry& g = pool->core->geo();
+    const uint64_t D = g.head_dim, hkv = g.kv_heads, hq = num_q_heads;
+    const uint64_t H = hidden_size, I = intermediate_size;
+    const uint64_t qkv_n = (hq + 2 * hkv) * D, attn_k = hq * D;
+    // the projection GEMMs take n % 64 == 0 and k % 256 == 0
+    if (H == 0 || I == 0 || H % 256 != 0 || I % 256 != 0 || attn_k % 256 != 0 ||
+        qkv_n % 64 != 0 || !(rms_eps >= 0.0f)) {
+        pool->set_error(std::string(fn) +
+                        ": hidden, intermediate and q_heads*head_dim must be multiples of 256, "
+                        "(q_heads + 2 kv_heads)*head_dim a multiple of 64, eps >= 0");
+        return -1;
+    }
+    std::string err;
+    if (!kcmm::dev::set_device(pool->device, &err)) {
+        pool->set_error(std::string(fn) + ": bind device failed: " + err);
+        return -1;
+    }
+    // activations: normed [B][H], qkv [B][qkv_n], q [B][Hq D], attn [B][Hq D],
+    // gate_up [B][2I], act [B][I] (bf16), each 256-byte aligned
+    auto al = [](uint64_t bytes) { return (bytes + 255) & ~255ull; };
+    const uint64_t sz_norm = al(batch * H * 2), sz_qkv = al(batch * qkv_n * 2),
+                   sz_q = al(batch * attn_k * 2), sz_gu = al(batch * 2 * I * 2),
+                   sz_act = al(batch * I * 2);
+    void* ws = nullptr;
+    if (!kcmm::dev::stream_workspace(stream, 3, sz_norm + sz_qkv + 2 * sz_q + sz_gu + sz_act, &ws,
+                                     false, &err)) {
+        pool->set_error(std::string(fn) + ": workspace: " + err);
+        return -1;
+    }
+    const uint64_t base = reinterpret_cast<uint64_t>(ws);
+    const uint64_t normed = base, qkv = normed + sz_norm, q = qkv + sz_qkv, attn = q + sz_q,
+                   gu = attn + sz_q, act = gu + sz_gu;
+
+    kcmm::dev::AttnDecodeArgs at{};
+    at.dtype = g.dtype;
+    at.q = q;
+    at.out = attn;
+    at.k_base = pool->core->va_k(layer_idx);
+    at.v_base = pool->core->va_v(layer_idx);
+    at.block_tables = block_tables;
+    at.seq_lens = seq_lens;
+    at.offsets_f16 = offsets_f16;
+    at.batch = batch;
+    at.num_q_heads = num_q_heads;
+    at.kv_heads = static_cast<uint32_t>(hkv);
+    at.head_dim = static_cast<uint32_t>(D);
+    at.block_size = static_cast<uint32_t>(g.block_size);
+    at.mbps = max_blocks_per_seq;
+    at.row_bytes = static_cast<uint32_t>(g.row_bytes);
+    at.data_bytes = static_cast<uint32_t>(g.data_bytes);
+    at.scale = 1.0f / std::sqrt(static_cast<float>(D));
+    at.stream = stream;
+
+    const uint32_t B = batch;
+    const bool ok =
+        kcmm::dev::rmsnorm_bf16(hidden, w->attn_norm, normed, B, hidden_size, rms_eps, stream,
+                                &err) &&
+        kcmm::dev::gemm_bf16(normed, w->qkv, qkv, B, static_cast<uint32_t>(qkv_n), hidden_size,
+                             stream, &err) &&
+        kcmm::dev::rope_append_bf16(rope_args(pool, layer_idx, qkv, q, block_tables, seq_lens,
+                                              offsets_f16, inv_freq, B, num_q_heads,
+                                              max_blocks_per_seq, stream),
+                                    &err) &&
+        kcmm::dev::attn_decode(at, &err) &&
+        kcmm::dev::gemm_bf16(attn, w->o, hidden, B, hidden_size, static_cast<uint32_t>(attn_k),
+                             stream, &err, hidden) &&
+        kcmm::dev::rmsnorm_bf16(hidden, w->mlp_norm, normed, B, hidden_size, rms_eps, stream,
+                                &err) &&
+        kcmm::dev::gemm_bf16(normed, w->gate_up, gu, B, 2 * intermediate_size, hidden_size,
+                             stream, &err) &&
+        kcmm::dev::silu_mul_bf16(gu, act, B, intermediate_size, stream, &err) &&
+        kcmm::dev::gemm_bf16(act, w->down, hidden, B, hidden_size, intermediate_size, stream,
+                             &err, hidden);
+    if (!ok) {
+        pool->set_error(std::string(fn) + ": launch failed: " + err);
         return -1;
     }
     return 0;

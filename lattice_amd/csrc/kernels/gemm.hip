@@ -57,10 +57,23 @@ __device__ __forceinline__ u32x4 load_stream(const uint8_t* a) {
 // (Measured alternatives that were slower at the Llama-3-8B decode shapes: a
 // persistent grid over (row block, k chunk) tiles with a 6-deep ring, and
 // direct-to-LDS activation loads with a 3-deep weight ring.)
+// v (4 consecutive outputs) rounded to bf16, then + the residual row piece r,
+// in fp32 (the result is rounded once more by the store): the order of a bf16
+// model's "residual + o_proj(x)".
+__device__ __forceinline__ f32x4 add_residual(f32x4 v, const uint16_t* r) {
+    const u32x2 rr = *reinterpret_cast<const u32x2*>(r);
+    f32x4 o;
+    o[0] = bf16_bits_to_f32(f32_to_bf16_bits(v[0])) + __uint_as_float(rr[0] << 16);
+    o[1] = bf16_bits_to_f32(f32_to_bf16_bits(v[1])) + __uint_as_float(rr[0] & 0xffff0000u);
+    o[2] = bf16_bits_to_f32(f32_to_bf16_bits(v[2])) + __uint_as_float(rr[1] << 16);
+    o[3] = bf16_bits_to_f32(f32_to_bf16_bits(v[3])) + __uint_as_float(rr[1] & 0xffff0000u);
+    return o;
+}
+
 template <int MB, int KCH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
-                      uint16_t* __restrict__ Y, float* __restrict__ part, int M, int N, int K,
+                      uint16_t* Y, float* __restrict__ part, const uint16_t* R, int M, int N, int K,
                       int klen) {
     constexpr int LINES = KCH / 64;          // 128-byte lines per weight row per chunk
     constexpr int KC = KCH / 32;             // MFMA k-steps per chunk
@@ -173,9 +186,11 @@ void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict
         if (m >= M) continue;
         const int n = n0 + 4 * lg;
         if (part == nullptr) {
+            f32x4 v = acc[j];
+            if (R != nullptr) v = add_residual(v, R + static_cast<size_t>(m) * N + n);
             u32x2 o;
-            o[0] = f32_to_bf16_bits(acc[j][0]) | (f32_to_bf16_bits(acc[j][1]) << 16);
-            o[1] = f32_to_bf16_bits(acc[j][2]) | (f32_to_bf16_bits(acc[j][3]) << 16);
+            o[0] = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+            o[1] = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
             *reinterpret_cast<u32x2*>(Y + static_cast<size_t>(m) * N + n) = o;
         } else {
             *reinterpret_cast<f32x4*>(part + (static_cast<size_t>(blockIdx.y) * M + m) * N + n) = acc[j];
@@ -183,14 +198,15 @@ void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict
     }
 }
 
-// Y = bf16(sum over splits of the fp32 partials); 4 outputs per thread.
+// Y = bf16(sum over splits of the fp32 partials) (+ R); 4 outputs per thread.
 __global__ __launch_bounds__(256) void gemm_split_reduce(const float* __restrict__ part,
-                                                         uint16_t* __restrict__ Y, int MN,
+                                                         uint16_t* Y, const uint16_t* R, int MN,
                                                          int splits) {
     const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= MN) return;
     f32x4 s = *reinterpret_cast<const f32x4*>(part + i);
     for (int k = 1; k < splits; ++k) s += *reinterpret_cast<const f32x4*>(part + static_cast<size_t>(k) * MN + i);
+    if (R != nullptr) s = add_residual(s, R + i);
     u32x2 o;
     o[0] = f32_to_bf16_bits(s[0]) | (f32_to_bf16_bits(s[1]) << 16);
     o[1] = f32_to_bf16_bits(s[2]) | (f32_to_bf16_bits(s[3]) << 16);
@@ -223,8 +239,8 @@ int choose_splits(int N, int K, int kch, int mgroups) {
 }
 
 template <int MB, int KCH>
-bool launch_gemm(const uint16_t* X, const uint16_t* W, uint16_t* Y, int M, int N, int K,
-                 uint64_t stream, std::string* err) {
+bool launch_gemm(const uint16_t* X, const uint16_t* W, uint16_t* Y, const uint16_t* R, int M,
+                 int N, int K, uint64_t stream, std::string* err) {
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int mgroups = (M + 16 * MB - 1) / (16 * MB);
     const int splits = choose_splits(N, K, KCH, mgroups);
@@ -237,13 +253,13 @@ bool launch_gemm(const uint16_t* X, const uint16_t* W, uint16_t* Y, int M, int N
         part = static_cast<float*>(ws);
     }
     const dim3 grid(N / 64, splits, mgroups);
-    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH>), grid, dim3(256), 0, s, X, W, Y, part, M, N, K,
+    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH>), grid, dim3(256), 0, s, X, W, Y, part, R, M, N, K,
                        K / splits);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     if (splits > 1) {
         const int MN = M * N;
         hipLaunchKernelGGL(gemm_split_reduce, dim3((MN / 4 + 255) / 256), dim3(256), 0, s, part, Y,
-                           MN, splits);
+                           R, MN, splits);
         KCMM_HIP_CHECK(hipGetLastError(), err);
     }
     return true;
@@ -254,7 +270,7 @@ bool launch_gemm(const uint16_t* X, const uint16_t* W, uint16_t* Y, int M, int N
 namespace dev {
 
 bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
-               uint64_t stream, std::string* err) {
+               uint64_t stream, std::string* err, uint64_t residual) {
     if (m == 0 || n % 64 != 0 || k % 256 != 0 || n == 0 || k == 0) {
         *err = "gemm_bf16 needs m > 0, n % 64 == 0 and k % 256 == 0";
         return false;
@@ -267,13 +283,14 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
     const auto* X = reinterpret_cast<const uint16_t*>(x);
     const auto* W = reinterpret_cast<const uint16_t*>(w);
     auto* Y = reinterpret_cast<uint16_t*>(y);
+    const auto* R = reinterpret_cast<const uint16_t*>(residual);
     const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
     // token blocks per pass: the activation chunk (M x KCH bf16) is 32 KiB
-    if (M <= 16) return launch_gemm<1, 256>(X, W, Y, M, N, K, stream, err);
-    if (M <= 32) return launch_gemm<2, 256>(X, W, Y, M, N, K, stream, err);
-    if (M <= 64) return launch_gemm<4, 256>(X, W, Y, M, N, K, stream, err);
-    if (M <= 128) return launch_gemm<8, 128>(X, W, Y, M, N, K, stream, err);
-    return launch_gemm<16, 64>(X, W, Y, M, N, K, stream, err);
+    if (M <= 16) return launch_gemm<1, 256>(X, W, Y, R, M, N, K, stream, err);
+    if (M <= 32) return launch_gemm<2, 256>(X, W, Y, R, M, N, K, stream, err);
+    if (M <= 64) return launch_gemm<4, 256>(X, W, Y, R, M, N, K, stream, err);
+    if (M <= 128) return launch_gemm<8, 128>(X, W, Y, R, M, N, K, stream, err);
+    return launch_gemm<16, 64>(X, W, Y, R, M, N, K, stream, err);
 }
 
 }  // namespace dev

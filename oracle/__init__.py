@@ -295,3 +295,106 @@ def gemm_bf16_f64(x_bits: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
     y = np.zeros((m, n), dtype=np.float64)
     lib().oracle_gemm_bf16_f64(_p(x), _p(w), _p(y), m, n, k)
     return y
+
+
+# ---- decode-step glue and one decoder layer ----------------------------------
+# Restatement of one layer of ref LlamaTransformer::forward_step_paged
+# (src/model/llama_transformer.rs:262-391) with Hugging Face Llama semantics
+# (the reference's own rope.cu pairs and theta are not HF's): fp64 arithmetic,
+# activations rounded to bf16 wherever a bf16 model stores them.
+
+def bf16_round(x) -> np.ndarray:
+    return decode(BF16, encode(BF16, np.asarray(x, dtype=np.float64))).astype(np.float64)
+
+
+def rmsnorm_f64(x, w, eps, round_bf16=True):
+    """HF LlamaRMSNorm: w * (x * rsqrt(mean(x^2) + eps)), the normalised row
+    rounded to bf16 before the weight multiply when round_bf16."""
+    x = np.asarray(x, dtype=np.float64)
+    t = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    if round_bf16:
+        return bf16_round(np.asarray(w, dtype=np.float64) * bf16_round(t))
+    return np.asarray(w, dtype=np.float64) * t
+
+
+def default_inv_freq(theta: float, head_dim: int) -> np.ndarray:
+    """HF default rope: inv_freq[i] = theta^(-2i/head_dim), i < head_dim/2."""
+    return 1.0 / (theta ** (np.arange(0, head_dim, 2, dtype=np.float64) / head_dim))
+
+
+def rope_f64(x, pos, inv_freq):
+    """HF apply_rotary_pos_emb on the last axis: x*cos + rotate_half(x)*sin,
+    angle pos * inv_freq[i] for the pair (i, i + D/2).  pos broadcasts
+    against x's leading axes (x.shape[:-1])."""
+    x = np.asarray(x, dtype=np.float64)
+    d2 = x.shape[-1] // 2
+    ang = np.asarray(pos, dtype=np.float64)[..., None] * np.asarray(inv_freq, dtype=np.float64)
+    c = np.concatenate([np.cos(ang), np.cos(ang)], axis=-1)
+    s = np.concatenate([np.sin(ang), np.sin(ang)], axis=-1)
+    rot = np.concatenate([-x[..., d2:], x[..., :d2]], axis=-1)
+    return x * c + rot * s
+
+
+def silu_mul_f64(gate, up):
+    g = np.asarray(gate, dtype=np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(up, dtype=np.float64)
+
+
+def decode_layer_step_f64(hidden_bits, w, k_region, v_region, block_tables, seq_lens,
+                          offsets_f16, inv_freq, num_q_heads, kv_heads, head_dim,
+                          intermediate, block_size, row_bytes, eps, round_bf16=True):
+    """One decoder layer of a decode step for a bf16 pool.
+
+    hidden_bits [B][H] uint16 (bf16); w: dict of bf16-bit arrays attn_norm [H],
+    qkv [(Hq+2Hkv)D][H], o [H][Hq D], mlp_norm [H], gate_up [2I][H], down [H][I].
+    Sequence b's new token is at position seq_lens[b] - 1; its rotated k and v
+    are written (as bf16) into k_region / v_region (uint8 copies of the
+    layer's regions) and attention runs over rows 0..pos of its pages (the
+    new row at full precision when not round_bf16).  round_bf16 rounds every
+    stored activation to bf16 as a bf16 model does; without it the layer is
+    computed in fp64 throughout.  Returns the new hidden state (float64)."""
+    rnd = bf16_round if round_bf16 else (lambda a: np.asarray(a, dtype=np.float64))
+    f = lambda name: decode(BF16, w[name]).astype(np.float64)
+    hq, hkv, d = num_q_heads, kv_heads, head_dim
+    grp = hq // hkv
+    x = decode(BF16, hidden_bits).astype(np.float64)
+    bsz = x.shape[0]
+    pos = np.asarray(seq_lens, dtype=np.int64) - 1
+    bt = np.asarray(block_tables)
+    n1 = rmsnorm_f64(x, f("attn_norm"), eps, round_bf16)
+    qkv = rnd(n1 @ f("qkv").T)
+    q = qkv[:, :hq * d].reshape(bsz, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].reshape(bsz, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].reshape(bsz, hkv, d)
+    pe = np.maximum(pos, 0)[:, None].astype(np.float64)
+    q_r = rnd(rope_f64(q, pe, inv_freq))
+    k_r = rnd(rope_f64(k, pe, inv_freq))
+    att = np.zeros((bsz, hq, d), dtype=np.float64)
+    for b in range(bsz):
+        p = int(pos[b])
+        if p < 0 or p >= bt.shape[1] * block_size:
+            continue
+        rows_k, rows_v = [], []
+        for t in range(p + 1):
+            base = int(offsets_f16[bt[b, t // block_size]]) * 2 + (t % block_size) * row_bytes
+            if t == p:
+                k_region[base:base + hkv * d * 2] = encode(BF16, k_r[b].ravel()).view(np.uint8)
+                v_region[base:base + hkv * d * 2] = encode(BF16, v[b].ravel()).view(np.uint8)
+                rows_k.append(k_r[b])
+                rows_v.append(v[b])
+                continue
+            rows_k.append(decode(BF16, k_region[base:base + hkv * d * 2].view(np.uint16))
+                          .astype(np.float64).reshape(hkv, d))
+            rows_v.append(decode(BF16, v_region[base:base + hkv * d * 2].view(np.uint16))
+                          .astype(np.float64).reshape(hkv, d))
+        kk, vv = np.stack(rows_k), np.stack(rows_v)            # [p+1][Hkv][D]
+        for h in range(hq):
+            sc = kk[:, h // grp, :] @ q_r[b, h] / np.sqrt(d)
+            e = np.exp(sc - sc.max())
+            att[b, h] = (e / e.sum()) @ vv[:, h // grp, :]
+    att = rnd(att).reshape(bsz, hq * d)
+    h1 = rnd(x + rnd(att @ f("o").T))
+    n2 = rmsnorm_f64(h1, f("mlp_norm"), eps, round_bf16)
+    gu = rnd(n2 @ f("gate_up").T)
+    act = rnd(silu_mul_f64(gu[:, :intermediate], gu[:, intermediate:]))
+    return rnd(h1 + rnd(act @ f("down").T))

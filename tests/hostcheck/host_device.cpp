@@ -72,7 +72,15 @@ bool copy_pages_device(const std::vector<uint64_t>&, uint64_t, uint64_t, size_t,
     return no_device(err);
 }
 bool gemm_bf16(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t,
-               std::string* err) {
+               std::string* err, uint64_t) {
+    return no_device(err);
+}
+bool rmsnorm_bf16(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, float, uint64_t,
+                  std::string* err) {
+    return no_device(err);
+}
+bool rope_append_bf16(const RopeAppendArgs&, std::string* err) { return no_device(err); }
+bool silu_mul_bf16(uint64_t, uint64_t, uint32_t, uint32_t, uint64_t, std::string* err) {
     return no_device(err);
 }
 

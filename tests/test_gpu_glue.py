@@ -1,0 +1,238 @@
+"""Decode-step glue and the layer step on the GPU, through the C ABI, vs the
+oracle (which tests/test_oracle_glue.py pins against transformers' Llama
+modules).  Tolerances (bf16 activations): a kernel whose output the oracle
+rounds at the same point must agree to within one bf16 ulp of the value
+(2^-7 relative); GEMM-based results to 1e-2 of the max |value|; the V rows the
+RoPE/append kernel copies must be bit-exact and no other page byte may
+change."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, memcpy_dtoh
+from lattice_amd.workload import build_decode_case
+
+pytestmark = pytest.mark.gpu
+
+ULP = 2.0 ** -7
+
+
+def bf16_dev(torch, bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def bits_of(t):
+    import torch
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def within_ulp(got, ref, n=1):
+    return np.all(np.abs(got - ref) <= n * ULP * np.abs(ref) + 1e-30)
+
+
+def rel_err(got, ref):
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+@pytest.mark.parametrize("rows,hidden", [(7, 4096), (64, 4096), (3, 520)])
+def test_rmsnorm(gpu_lib, rows, hidden):
+    import torch
+    rng = np.random.default_rng(rows + hidden)
+    x = O.encode(O.BF16, rng.standard_normal((rows, hidden)) * 3)
+    w = O.encode(O.BF16, 1.0 + 0.1 * rng.standard_normal(hidden))
+    xd, wd = bf16_dev(torch, x), bf16_dev(torch, w)
+    yd = torch.full((rows, hidden), float("nan"), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.rmsnorm_bf16(xd.data_ptr(), wd.data_ptr(), yd.data_ptr(), rows, hidden, 1e-5,
+                         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = O.decode(O.BF16, bits_of(yd)).astype(np.float64)
+    ref = O.rmsnorm_f64(O.decode(O.BF16, x), O.decode(O.BF16, w), 1e-5)
+    # fp32 vs fp64 normalisation may flip the inner rounding: two roundings
+    assert within_ulp(got, ref, 2)
+    assert np.mean(got == ref) > 0.98
+
+
+@pytest.mark.parametrize("rows,inter", [(5, 14336), (64, 520)])
+def test_silu_mul(gpu_lib, rows, inter):
+    import torch
+    rng = np.random.default_rng(inter)
+    gu = O.encode(O.BF16, rng.standard_normal((rows, 2 * inter)) * 3)
+    gd = bf16_dev(torch, gu)
+    ad = torch.full((rows, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.silu_mul_bf16(gd.data_ptr(), ad.data_ptr(), rows, inter,
+                          torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = O.decode(O.BF16, bits_of(ad)).astype(np.float64)
+    g = O.decode(O.BF16, gu).astype(np.float64)
+    ref = O.bf16_round(O.silu_mul_f64(g[:, :inter], g[:, inter:]))
+    assert within_ulp(got, ref)
+
+
+@pytest.mark.parametrize("m,n,k,inplace", [(5, 256, 512, False), (64, 4096, 4096, True),
+                                           (64, 4096, 14336, True), (64, 28672, 4096, False)])
+def test_gemm_residual(gpu_lib, m, n, k, inplace):
+    """Y = R + X W^T with the product rounded to bf16 first; in place and
+    not, split-K (reduce kernel) and single-pass (GEMM store) paths."""
+    import torch
+    rng = np.random.default_rng(n + k)
+    x = O.encode(O.BF16, rng.standard_normal((m, k)))
+    w = O.encode(O.BF16, rng.standard_normal((n, k)) * 0.02)
+    r = O.encode(O.BF16, rng.standard_normal((m, n)))
+    xd, wd, rd = bf16_dev(torch, x), bf16_dev(torch, w), bf16_dev(torch, r)
+    yd = rd if inplace else torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.gemm_bf16_add(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), yd.data_ptr(), m, n, k,
+                          torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = O.decode(O.BF16, bits_of(yd)).astype(np.float64)
+    ref = O.bf16_round(O.decode(O.BF16, r) + O.bf16_round(O.gemm_bf16_f64(x, w)))
+    assert rel_err(got, ref) <= 1e-2
+
+
+def _region(case, which):
+    va = case.pool.va_k(0) if which == "k" else case.pool.va_v(0)
+    return memcpy_dtoh(va, case.geometry["mapped_bytes"])
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 2, 64), (12, 4, 80)])
+def test_rope_append(gpu_lib, hq, hkv, d):
+    """q rotated into q_out, k rotated and v copied into the new token's page
+    row; nothing else in the pages changes; a sequence with no token is
+    skipped."""
+    import torch
+    lens = [1, 16, 17, 300, 0]
+    case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=16, ctx_lens=lens, dtype=KV_BF16, seed=d)
+    try:
+        g = case.geometry
+        rng = np.random.default_rng(7)
+        qkv = O.encode(O.BF16, rng.standard_normal((len(lens), (hq + 2 * hkv) * d)))
+        inv = O.default_inv_freq(500000.0, d)
+        qkvd = bf16_dev(torch, qkv)
+        qo = torch.full((len(lens), hq, d), float("nan"), dtype=torch.bfloat16, device="cuda")
+        invd = torch.from_numpy(inv.astype(np.float32)).cuda()
+        k0, v0 = _region(case, "k"), _region(case, "v")
+        dv = case.dev
+        case.pool.rope_append(layer_idx=0, qkv_ptr=qkvd.data_ptr(), q_out_ptr=qo.data_ptr(),
+                              block_tables_ptr=dv["bt"].data_ptr(),
+                              seq_lens_ptr=dv["sl"].data_ptr(),
+                              block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                              inv_freq_ptr=invd.data_ptr(), batch=len(lens), num_q_heads=hq,
+                              max_blocks_per_seq=case.mbps,
+                              stream_ptr=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        k1, v1 = _region(case, "k"), _region(case, "v")
+        x = O.decode(O.BF16, qkv).astype(np.float64)
+        qg = O.decode(O.BF16, bits_of(qo)).astype(np.float64)
+        touched = np.zeros(k0.size, dtype=bool)
+        for b, L in enumerate(lens):
+            if L <= 0:
+                continue
+            pos = L - 1
+            ref_q = O.bf16_round(O.rope_f64(x[b, :hq * d].reshape(hq, d), np.full(hq, pos), inv))
+            assert rel_err(qg[b], ref_q) <= 1e-2, b
+            base = int(case.offsets_f16[case.block_tables[b, pos // 16]]) * 2 + (pos % 16) * g["row_bytes"]
+            seg = slice(base, base + hkv * d * 2)
+            touched[seg] = True
+            kg = O.decode(O.BF16, k1[seg].view(np.uint16)).astype(np.float64).reshape(hkv, d)
+            ref_k = O.bf16_round(O.rope_f64(x[b, hq * d:(hq + hkv) * d].reshape(hkv, d),
+                                            np.full(hkv, pos), inv))
+            assert rel_err(kg, ref_k) <= 1e-2, b
+            assert np.array_equal(v1[seg].view(np.uint16), qkv[b, (hq + hkv) * d:])
+        assert np.array_equal(k1[~touched], k0[~touched])
+        assert np.array_equal(v1[~touched], v0[~touched])
+    finally:
+        case.pool.destroy()
+
+
+def _layer_weights(torch, rng, h, inter, hq, hkv, d):
+    enc = lambda shape, std: O.encode(O.BF16, rng.standard_normal(shape) * std)
+    w = {"attn_norm": O.encode(O.BF16, 1.0 + 0.1 * rng.standard_normal(h)),
+         "qkv": enc(((hq + 2 * hkv) * d, h), 0.05), "o": enc((h, hq * d), 0.05),
+         "mlp_norm": O.encode(O.BF16, 1.0 + 0.1 * rng.standard_normal(h)),
+         "gate_up": enc((2 * inter, h), 0.05), "down": enc((h, inter), 0.05)}
+    dev = {k: bf16_dev(torch, v) for k, v in w.items()}
+    lw = KcmmLayerWeights(**{k: t.data_ptr() for k, t in dev.items()})
+    return w, dev, lw
+
+
+@pytest.mark.parametrize("hq,hkv,d,h,inter", [(8, 2, 64, 512, 768), (32, 8, 128, 4096, 1024)])
+def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter):
+    """One decoder layer through kcmm_decode_layer_step_on_stream vs the
+    oracle's bf16 layer (RMSNorm, QKV, RoPE + append, paged attention,
+    O + residual, RMSNorm, gate/up, SiLU*up, down + residual)."""
+    import torch
+    lens = [1, 16, 17, 130]
+    case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=16, ctx_lens=lens, dtype=KV_BF16, seed=h)
+    try:
+        g = case.geometry
+        rng = np.random.default_rng(11)
+        w, wdev, lw = _layer_weights(torch, rng, h, inter, hq, hkv, d)
+        hid = O.encode(O.BF16, rng.standard_normal((len(lens), h)))
+        hd = bf16_dev(torch, hid)
+        inv = O.default_inv_freq(500000.0, d)
+        invd = torch.from_numpy(inv.astype(np.float32)).cuda()
+        dv = case.dev
+        kreg, vreg = _region(case, "k"), _region(case, "v")
+        case.pool.decode_layer_step(layer_idx=0, weights=lw, hidden_ptr=hd.data_ptr(),
+                                    block_tables_ptr=dv["bt"].data_ptr(),
+                                    seq_lens_ptr=dv["sl"].data_ptr(),
+                                    block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                    inv_freq_ptr=invd.data_ptr(), batch=len(lens),
+                                    hidden_size=h, num_q_heads=hq, intermediate_size=inter,
+                                    max_blocks_per_seq=case.mbps, rms_eps=1e-5,
+                                    stream_ptr=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        got = O.decode(O.BF16, bits_of(hd)).astype(np.float64)
+        ref = O.decode_layer_step_f64(hid, w, kreg, vreg, case.block_tables, case.seq_lens,
+                                      case.offsets_f16, inv, hq, hkv, d, inter, 16,
+                                      g["row_bytes"], 1e-5)
+        x = O.decode(O.BF16, hid).astype(np.float64)
+        err = rel_err(got, ref)
+        upd = rel_err(got - x, ref - x)
+        print(f"layer step hq={hq} d={d} h={h}: err {err:.2e}, update err {upd:.2e}", flush=True)
+        assert np.isfinite(got).all() and err <= 1e-2 and upd <= 5e-2
+        # the new token's K / V rows hold what the oracle wrote (within bf16)
+        k1, v1 = _region(case, "k"), _region(case, "v")
+        for b, L in enumerate(lens):
+            pos = L - 1
+            base = int(case.offsets_f16[case.block_tables[b, pos // 16]]) * 2 + (pos % 16) * g["row_bytes"]
+            seg = slice(base, base + hkv * d * 2)
+            for got_r, ref_r in ((k1, kreg), (v1, vreg)):
+                a = O.decode(O.BF16, got_r[seg].view(np.uint16)).astype(np.float64)
+                r = O.decode(O.BF16, ref_r[seg].view(np.uint16)).astype(np.float64)
+                assert rel_err(a, r) <= 2e-2, b
+    finally:
+        case.pool.destroy()
+
+
+def test_layer_step_rejects_bad_shapes(gpu_lib):
+    import torch
+    case = build_decode_case(gpu_lib, batch=2, num_q_heads=8, kv_heads=2, head_dim=64,
+                             block_size=16, ctx_lens=[3, 4], dtype=KV_BF16, seed=1)
+    try:
+        rng = np.random.default_rng(1)
+        w, wdev, lw = _layer_weights(torch, rng, 512, 768, 8, 2, 64)
+        hd = torch.zeros((2, 512), dtype=torch.bfloat16, device="cuda")
+        invd = torch.zeros(32, dtype=torch.float32, device="cuda")
+        dv = case.dev
+        with pytest.raises(Exception):   # hidden not a multiple of 256
+            case.pool.decode_layer_step(layer_idx=0, weights=lw, hidden_ptr=hd.data_ptr(),
+                                        block_tables_ptr=dv["bt"].data_ptr(),
+                                        seq_lens_ptr=dv["sl"].data_ptr(),
+                                        block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                        inv_freq_ptr=invd.data_ptr(), batch=2, hidden_size=500,
+                                        num_q_heads=8, intermediate_size=768,
+                                        max_blocks_per_seq=case.mbps, rms_eps=1e-5)
+        with pytest.raises(Exception):   # q heads not a multiple of the pool's kv heads
+            case.pool.decode_layer_step(layer_idx=0, weights=lw, hidden_ptr=hd.data_ptr(),
+                                        block_tables_ptr=dv["bt"].data_ptr(),
+                                        seq_lens_ptr=dv["sl"].data_ptr(),
+                                        block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                        inv_freq_ptr=invd.data_ptr(), batch=2, hidden_size=512,
+                                        num_q_heads=7, intermediate_size=768,
+                                        max_blocks_per_seq=case.mbps, rms_eps=1e-5)
+    finally:
+        case.pool.destroy()
