@@ -8,14 +8,18 @@ pool holds several layers and consecutive steps cycle through them, so each
 step reads KV that is not resident in the 256 MB Infinity Cache -- as the 32
 layers of a real decode step do.
 
-A timed step = one transformer layer of a decode step through libkcmm.so:
-QKV GEMM -> KV append (device slots) -> paged attention -> O GEMM -> gate+up
-GEMM -> down GEMM.  HIP events on the launch stream time every call.
+A timed step = one decoder layer of a decode step through libkcmm.so, one
+C-ABI call per kernel: RMSNorm -> QKV GEMM -> RoPE + KV append into the page
+row -> paged attention -> O GEMM + residual -> RMSNorm -> gate+up GEMM ->
+SiLU*up -> down GEMM + residual.  HIP events on the launch stream time every
+call.  After the timed steps the same layer is timed through the single
+entry point kcmm_decode_layer_step_on_stream, and the standalone slot append
+(kcmm_append_kv_device_slots) on its own.
 
 Printed JSON: `value` is decode-attention KV GB/s (algorithmic K+V bytes of
 one layer-step / attention call time); decode tokens/s = 64 / (32 * t_layer)
-with t_layer the sum of the six calls (lm_head, sampling, norms, RoPE and
-SwiGLU glue are not in this path and are excluded).
+with t_layer the single-entry layer-step time (embedding, the final norm,
+lm_head and sampling are outside this path and excluded).
 
 `roofline` prices the attention call (streaming kernel + log-sum-exp merge,
 timed by HIP events on the launch stream) against MI355X's 8 TB/s; its
@@ -46,6 +50,7 @@ CTX_LO, CTX_HI = 512, 4096
 MODEL_LAYERS = 32
 HIDDEN, INTER = 4096, 14336
 KV_BF16_CODE = 1
+ROPE_THETA, RMS_EPS = 500000.0, 1e-5      # Llama-3-8B config.json
 GEMMS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
 
 
@@ -178,8 +183,8 @@ def main():
     if args.config == "cfg3":
         return bench_prefill(args)
     import torch
-    from lattice_amd.bindings import KV_BF16, KcmmLibrary, make_config
-    from lattice_amd.workload import build_decode_case
+    from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, KcmmLibrary
+    from lattice_amd.workload import build_decode_case, rope_inv_freq
 
     assert torch.cuda.is_available(), "bench needs a GPU"
     lib = KcmmLibrary()
@@ -216,15 +221,28 @@ def main():
     k_new = torch.randn((B, HKV * D), generator=g, device=dev).to(torch.bfloat16)
     v_new = torch.randn((B, HKV * D), generator=g, device=dev).to(torch.bfloat16)
 
-    # projection weights (two sets, alternating by layer) and activations
-    nw = 2
-    weights = [{name: (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16)
-                for name, n, k in GEMMS} for _ in range(nw)]
-    x_in = torch.randn((B, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
-    x_act = torch.randn((B, INTER), generator=g, device=dev).to(torch.bfloat16)
-    outs = {name: torch.empty((B, n), dtype=torch.bfloat16, device=dev) for name, n, _ in GEMMS}
+    # layer weights (two sets, alternating by layer; one set is 436 MB, above
+    # the 256 MB Infinity Cache) and activations
+    nw = 0 if args.attn_only else 2
+    weights = []
+    for _ in range(nw):
+        w = {name: (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+             for name, n, k in GEMMS}
+        for name in ("attn_norm", "mlp_norm"):
+            w[name] = (1.0 + 0.1 * torch.randn(HIDDEN, generator=g, device=dev)).to(torch.bfloat16)
+        weights.append(w)
+    layer_w = [KcmmLayerWeights(**{k: w[k].data_ptr() for k in
+                                   ("attn_norm", "qkv", "o", "mlp_norm", "gate_up", "down")})
+               for w in weights]
+    inv_freq = torch.from_numpy(rope_inv_freq(ROPE_THETA, D)).to(dev)
+    hidden = torch.randn((B, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
+    normed = torch.empty((B, HIDDEN), dtype=torch.bfloat16, device=dev)
+    qkv_out = torch.empty((B, (HQ + 2 * HKV) * D), dtype=torch.bfloat16, device=dev)
+    gate_up = torch.empty((B, 2 * INTER), dtype=torch.bfloat16, device=dev)
+    act = torch.empty((B, INTER), dtype=torch.bfloat16, device=dev)
     kv_bytes = case.kv_bytes()                     # identical for every layer
     scale = 1 / math.sqrt(D)
+    dv = case.dev
 
     def append(layer):
         case.pool.append_kv_device_slots_on_stream(
@@ -233,23 +251,48 @@ def main():
             block_offsets_f16_len=offs_t.numel(), batch=B, k_src_ptr=k_new.data_ptr(),
             v_src_ptr=v_new.data_ptr(), status_ptr=0, stream_ptr=sp)
 
-    def gemm(name, layer):
-        w = weights[layer % nw][name]
-        x = x_act if name == "down" else x_in       # [64][14336] or [64][4096] activations
-        n, k = w.shape
-        lib.gemm_bf16(x.data_ptr(), w.data_ptr(), outs[name].data_ptr(), B, n, k, sp)
+    def norm(name, layer):
+        lib.rmsnorm_bf16(hidden.data_ptr(), weights[layer % nw][name].data_ptr(),
+                         normed.data_ptr(), B, HIDDEN, RMS_EPS, sp)
 
-    names = ["qkv", "append", "attn", "o", "gate_up", "down"]
-    if args.attn_only:
-        names = ["append", "attn"]
+    def rope_append(layer):
+        case.pool.rope_append(layer_idx=layer, qkv_ptr=qkv_out.data_ptr(),
+                              q_out_ptr=dv["q"].data_ptr(), block_tables_ptr=dv["bt"].data_ptr(),
+                              seq_lens_ptr=dv["sl"].data_ptr(),
+                              block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                              inv_freq_ptr=inv_freq.data_ptr(), batch=B, num_q_heads=HQ,
+                              max_blocks_per_seq=case.mbps, stream_ptr=sp)
+
+    def layer_step(layer):
+        case.pool.decode_layer_step(layer_idx=layer, weights=layer_w[layer % nw],
+                                    hidden_ptr=hidden.data_ptr(),
+                                    block_tables_ptr=dv["bt"].data_ptr(),
+                                    seq_lens_ptr=dv["sl"].data_ptr(),
+                                    block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                    inv_freq_ptr=inv_freq.data_ptr(), batch=B,
+                                    hidden_size=HIDDEN, num_q_heads=HQ, intermediate_size=INTER,
+                                    max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
+
+    W = lambda layer, name: weights[layer % nw][name].data_ptr()
     calls = {
-        "qkv": lambda l: gemm("qkv", l),
+        "norm1": lambda l: norm("attn_norm", l),
+        "qkv": lambda l: lib.gemm_bf16(normed.data_ptr(), W(l, "qkv"), qkv_out.data_ptr(),
+                                       B, (HQ + 2 * HKV) * D, HIDDEN, sp),
+        "rope_append": rope_append,
         "append": append,
         "attn": lambda l: case.run_attention(layer=l, stream_ptr=sp, scale=scale),
-        "o": lambda l: gemm("o", l),
-        "gate_up": lambda l: gemm("gate_up", l),
-        "down": lambda l: gemm("down", l),
+        "o": lambda l: lib.gemm_bf16_add(dv["out"].data_ptr(), W(l, "o"), hidden.data_ptr(),
+                                         hidden.data_ptr(), B, HIDDEN, HQ * D, sp),
+        "norm2": lambda l: norm("mlp_norm", l),
+        "gate_up": lambda l: lib.gemm_bf16(normed.data_ptr(), W(l, "gate_up"),
+                                           gate_up.data_ptr(), B, 2 * INTER, HIDDEN, sp),
+        "silu": lambda l: lib.silu_mul_bf16(gate_up.data_ptr(), act.data_ptr(), B, INTER, sp),
+        "down": lambda l: lib.gemm_bf16_add(act.data_ptr(), W(l, "down"), hidden.data_ptr(),
+                                            hidden.data_ptr(), B, HIDDEN, INTER, sp),
     }
+    names = ["norm1", "qkv", "rope_append", "attn", "o", "norm2", "gate_up", "silu", "down"]
+    if args.attn_only:
+        names = ["append", "attn"]
 
     if args.calib_copy:
         src = torch.empty(128 << 20, dtype=torch.int16, device=dev)
@@ -282,6 +325,25 @@ def main():
     step_ms = float(np.mean([ev[i][0].elapsed_time(ev[i][-1]) for i in range(args.steps)]))
     log("per-call ms: " + ", ".join(f"{k}={v:.4f}" for k, v in per.items()))
 
+    extra = {}
+    if not args.attn_only:
+        # the same layer through the single entry point (what a serving loop
+        # calls 32 times per decode step), then the standalone slot append
+        for label, fn in (("layer_step", layer_step), ("append", append)):
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+            for i in range(args.warmup):
+                fn(i % args.layers)
+            torch.cuda.synchronize()
+            for i in range(args.steps):
+                evs[i].record(stream)
+                fn(i % args.layers)
+            evs[-1].record(stream)
+            torch.cuda.synchronize()
+            extra[label] = float(np.mean([evs[i].elapsed_time(evs[i + 1])
+                                          for i in range(args.steps)]))
+        log(f"layer step (one call) ms={extra['layer_step']:.4f}, append ms={extra['append']:.4f}")
+        assert torch.isfinite(hidden.float()).all(), "layer step produced non-finite hidden state"
+
     attn_s = per["attn"] / 1e3
     kv_gbs = kv_bytes / attn_s / 1e9
     result = {
@@ -297,8 +359,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16" if args.config == "cfg2" else "fp8-e4m3 KV, bf16 MFMA",
         "data": "synthetic (seeded N(0,1) K/V, N(0,0.02) weights; no checkpoint)",
-        "config": {"workload": ("llama3-8b-shape decode layer-step: paged attention + KV append "
-                                "+ QKV/O/gate_up/down GEMMs") if args.config == "cfg2" else
+        "config": {"workload": ("llama3-8b-shape decode layer-step: RMSNorm, QKV GEMM, RoPE + KV "
+                                "append, paged attention, O GEMM + residual, RMSNorm, gate_up "
+                                "GEMM, SiLU*up, down GEMM + residual") if args.config == "cfg2" else
                                "cfg5: fp8-e4m3 paged decode attention + KV append, long-tail ctx",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "block_size": BS,
                    "ctx": f"U[{CTX_LO},{CTX_HI}]+1" if args.config == "cfg2" else
@@ -314,18 +377,20 @@ def main():
                      "traffic": measured_traffic(),
                      "kernel": "paged decode attention call (attn_decode_stream + attn_decode_merge)",
                      "algorithmic_bytes": kv_bytes},
-        "append_us": round(per["append"] * 1e3, 2),
+        "append_us": round((per["append"] if args.attn_only else extra["append"]) * 1e3, 2),
         "wall_s_timed": round(wall, 3),
     }
     if not args.attn_only:
-        t_layer_s = sum(per[n] for n in names) / 1e3
+        t_layer_s = extra["layer_step"] / 1e3
         result["decode_tokens_per_s"] = round(B / (MODEL_LAYERS * t_layer_s), 1)
         result["t_layer_us"] = round(t_layer_s * 1e6, 2)
+        result["t_layer_components_us"] = {n: round(per[n] * 1e3, 2) for n in names}
         gem = {}
         for name, n, k in GEMMS:
             s = per[name] / 1e3
             flops = 2.0 * B * n * k
-            byts = 2.0 * (n * k + B * k + B * n)
+            # W, X and Y; O and down also read the residual they add
+            byts = 2.0 * (n * k + B * k + B * n * (2 if name in ("o", "down") else 1))
             ceiling = min(BF16_PEAK_TFLOPS * 1e12, HBM_PEAK_GBS * 1e9 * flops / byts)
             gem[name] = {"us": round(per[name] * 1e3, 2), "tflops": round(flops / s / 1e12, 1),
                          "gbs": round(byts / s / 1e9, 1),

@@ -347,3 +347,9 @@ def build_prefix_shared_case(lib: KcmmLibrary, *, batch: int, prefix_tokens: int
         "offs": torch.from_numpy(offs.view(np.int64)).to(device),
     }
     return case
+
+
+def rope_inv_freq(theta: float, head_dim: int) -> np.ndarray:
+    """Default (unscaled) RoPE frequencies, fp32: theta^(-2i/head_dim) for
+    i < head_dim/2, the rotate-half pairing (i, i + head_dim/2)."""
+    return (1.0 / (theta ** (np.arange(0, head_dim, 2, dtype=np.float64) / head_dim))).astype(np.float32)
