@@ -13,13 +13,15 @@ C-ABI call per kernel: RMSNorm -> QKV GEMM -> RoPE + KV append into the page
 row -> paged attention -> O GEMM + residual -> RMSNorm -> gate+up GEMM ->
 SiLU*up -> down GEMM + residual.  HIP events on the launch stream time every
 call.  After the timed steps the same layer is timed through the single
-entry point kcmm_decode_layer_step_on_stream, and the standalone slot append
-(kcmm_append_kv_device_slots) on its own.
+entry point kcmm_decode_layer_step_on_stream, the standalone slot append
+(kcmm_append_kv_device_slots) on its own, and a whole decode step -- all 32
+layers, each over its own KV -- through one kcmm_decode_layers_on_stream
+call.
 
 Printed JSON: `value` is decode-attention KV GB/s (algorithmic K+V bytes of
-one layer-step / attention call time); decode tokens/s = 64 / (32 * t_layer)
-with t_layer the single-entry layer-step time (embedding, the final norm,
-lm_head and sampling are outside this path and excluded).
+one layer-step / attention call time); decode tokens/s = 64 / t_step with
+t_step the 32-layer call (embedding, the final norm, lm_head and sampling
+are outside this path and excluded).
 
 `roofline` prices the attention call (streaming kernel + log-sum-exp merge,
 timed by HIP events on the launch stream) against MI355X's 8 TB/s; its
@@ -201,8 +203,10 @@ def main():
         ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B)      # context before the appended token
     L = ctx + 1
     t0 = time.perf_counter()
+    # the headline config holds all 32 layers' KV (19.6 GB) for the full-step timing
+    pool_layers = args.layers if args.attn_only else max(args.layers, MODEL_LAYERS)
     case = build_decode_case(lib, batch=B, num_q_heads=HQ, kv_heads=HKV, head_dim=D,
-                             block_size=BS, ctx_lens=L, dtype=kv_dtype, num_layers=args.layers,
+                             block_size=BS, ctx_lens=L, dtype=kv_dtype, num_layers=pool_layers,
                              seed=args.seed + 1, host_mirror=False,
                              shuffle=not args.no_shuffle)
     log(f"workload built in {time.perf_counter() - t0:.1f}s: {case.pool.stats()['superblock_count']} "
@@ -273,6 +277,16 @@ def main():
                                     hidden_size=HIDDEN, num_q_heads=HQ, intermediate_size=INTER,
                                     max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
 
+    def decode_step(_):
+        """All 32 layers of one decode step in one call (weight sets alternate)."""
+        case.pool.decode_layers(first_layer=0, weights=[layer_w[i % nw] for i in range(MODEL_LAYERS)],
+                                hidden_ptr=hidden.data_ptr(), block_tables_ptr=dv["bt"].data_ptr(),
+                                seq_lens_ptr=dv["sl"].data_ptr(),
+                                block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                inv_freq_ptr=inv_freq.data_ptr(), batch=B, hidden_size=HIDDEN,
+                                num_q_heads=HQ, intermediate_size=INTER,
+                                max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
+
     W = lambda layer, name: weights[layer % nw][name].data_ptr()
     calls = {
         "norm1": lambda l: norm("attn_norm", l),
@@ -329,19 +343,21 @@ def main():
     if not args.attn_only:
         # the same layer through the single entry point (what a serving loop
         # calls 32 times per decode step), then the standalone slot append
-        for label, fn in (("layer_step", layer_step), ("append", append)):
-            evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-            for i in range(args.warmup):
+        full_steps = max(4, args.steps // 8)
+        for label, fn, steps in (("layer_step", layer_step, args.steps), ("append", append, args.steps),
+                                 ("decode_step", decode_step, full_steps)):
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+            for i in range(min(args.warmup, steps)):
                 fn(i % args.layers)
             torch.cuda.synchronize()
-            for i in range(args.steps):
+            for i in range(steps):
                 evs[i].record(stream)
                 fn(i % args.layers)
             evs[-1].record(stream)
             torch.cuda.synchronize()
-            extra[label] = float(np.mean([evs[i].elapsed_time(evs[i + 1])
-                                          for i in range(args.steps)]))
-        log(f"layer step (one call) ms={extra['layer_step']:.4f}, append ms={extra['append']:.4f}")
+            extra[label] = float(np.mean([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]))
+        log(f"layer step (one call) ms={extra['layer_step']:.4f}, append ms={extra['append']:.4f}, "
+            f"32-layer decode step ms={extra['decode_step']:.4f}")
         assert torch.isfinite(hidden.float()).all(), "layer step produced non-finite hidden state"
 
     attn_s = per["attn"] / 1e3
@@ -381,9 +397,11 @@ def main():
         "wall_s_timed": round(wall, 3),
     }
     if not args.attn_only:
-        t_layer_s = extra["layer_step"] / 1e3
-        result["decode_tokens_per_s"] = round(B / (MODEL_LAYERS * t_layer_s), 1)
-        result["t_layer_us"] = round(t_layer_s * 1e6, 2)
+        t_step_s = extra["decode_step"] / 1e3
+        result["decode_tokens_per_s"] = round(B / t_step_s, 1)
+        result["t_decode_step_us"] = round(t_step_s * 1e6, 1)
+        result["t_layer_us"] = round(t_step_s / MODEL_LAYERS * 1e6, 2)
+        result["t_layer_single_call_us"] = round(extra["layer_step"] * 1e3, 2)
         result["t_layer_components_us"] = {n: round(per[n] * 1e3, 2) for n in names}
         gem = {}
         for name, n, k in GEMMS:

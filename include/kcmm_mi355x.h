@@ -162,16 +162,41 @@ int kcmm_gemm_bf16_add_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t residu
  * semantics.  bf16 activations, fp32 arithmetic, enqueue only; pointers are
  * device addresses aligned to 16 bytes. */
 
+/** The O projection with its residual add and the post-attention RMSNorm
+ *  (ref llama_transformer.rs:355-364: o GEMM, add.cu, rms_norm.cu):
+ *  hidden = bf16(hidden + bf16(x * w^T)) in place ([m][n]), then normed =
+ *  rmsnorm(hidden) with weight norm_w.  Bit-identical to
+ *  kcmm_gemm_bf16_add_on_stream followed by kcmm_rmsnorm_bf16_on_stream; the
+ *  split-K partial sums are finished inside the RMSNorm kernel.  n % 64 ==
+ *  0, k % 256 == 0. */
+int kcmm_gemm_bf16_add_rmsnorm_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t hidden_ptr,
+                                         uint64_t norm_w_ptr, uint64_t normed_ptr, uint32_t m,
+                                         uint32_t n, uint32_t k, float eps,
+                                         uint64_t stream_ptr);
+
 /** y[r] = w * bf16(x[r] * rsqrt(mean(x[r]^2) + eps)) for each of `rows` rows
  *  of `hidden` elements (HF LlamaRMSNorm).  hidden % 8 == 0. */
 int kcmm_rmsnorm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
                                 uint32_t rows, uint32_t hidden, float eps,
                                 uint64_t stream_ptr);
 
-/** act[r][j] = silu(gate_up[r][j]) * gate_up[r][intermediate + j] (the fused
- *  [gate | up] projection output).  intermediate % 8 == 0. */
+/** act[r][j] = bf16(bf16(silu(g)) * u) with g = gate_up[r][j] and
+ *  u = gate_up[r][intermediate + j] (the fused [gate | up] projection
+ *  output; F.silu on a bf16 tensor rounds before the multiply).
+ *  intermediate % 8 == 0. */
 int kcmm_silu_mul_bf16_on_stream(uint64_t gate_up_ptr, uint64_t act_ptr, uint32_t rows,
                                  uint32_t intermediate, uint64_t stream_ptr);
+
+/** The gate/up projection with SwiGLU in its store (ref
+ *  llama_transformer.rs:365-375: gate and up GEMMs, silu_mul.cu): act[m][j]
+ *  = bf16(bf16(silu(G)) * U) with G, U the bf16-rounded projections
+ *  x * w[j]^T and x * w[intermediate + j]^T; w_gate_up = [gate rows; up
+ *  rows], [2 intermediate][k].  Bit-identical to kcmm_gemm_bf16_on_stream
+ *  followed by kcmm_silu_mul_bf16_on_stream, without the [m][2 intermediate]
+ *  intermediate.  intermediate % 32 == 0, k % 256 == 0. */
+int kcmm_gemm_bf16_swiglu_on_stream(uint64_t x_ptr, uint64_t w_gate_up_ptr, uint64_t act_ptr,
+                                    uint32_t m, uint32_t intermediate, uint32_t k,
+                                    uint64_t stream_ptr);
 
 /** RoPE fused with the KV append for the decode token of every sequence of a
  *  bf16 pool: row b of qkv_ptr holds [q heads | k heads | v heads] x
@@ -189,6 +214,21 @@ int kcmm_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, uint6
                                     uint64_t inv_freq_ptr, uint32_t batch,
                                     uint32_t num_q_heads, uint32_t max_blocks_per_seq,
                                     uint64_t stream_ptr);
+
+/** The QKV projection of a decode step with RoPE and the KV append in its
+ *  store (ref llama_transformer.rs:300-340: q/k/v GEMMs, rope.cu, the cache
+ *  write): x_ptr [batch][hidden] times w_qkv_ptr [(Hq + 2 Hkv) head_dim]
+ *  [hidden] (q rows, k rows, v rows), each product rounded to bf16 and then
+ *  treated exactly as kcmm_rope_append_bf16_on_stream treats a qkv row, so
+ *  the pair gives identical bits without the qkv intermediate.  head_dim %
+ *  16 == 0, hidden % 256 == 0, (Hq + 2 Hkv) head_dim % 64 == 0. */
+int kcmm_qkv_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, uint64_t x_ptr,
+                                        uint64_t w_qkv_ptr, uint64_t q_out_ptr,
+                                        uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+                                        uint64_t block_offsets_f16_ptr, uint64_t inv_freq_ptr,
+                                        uint32_t batch, uint32_t hidden_size,
+                                        uint32_t num_q_heads, uint32_t max_blocks_per_seq,
+                                        uint64_t stream_ptr);
 
 /** Device addresses of one layer's weights (bf16, row-major [out][in]). */
 typedef struct kcmm_layer_weights {
@@ -217,6 +257,22 @@ int kcmm_decode_layer_step_on_stream(kcmm_pool_t *pool, uint32_t layer_idx,
                                      uint32_t num_q_heads, uint32_t intermediate_size,
                                      uint32_t max_blocks_per_seq, float rms_eps,
                                      uint64_t stream_ptr);
+
+/** Layers first_layer .. first_layer + num_layers - 1 of a decode step in one
+ *  call (the loop of ref LlamaTransformer::forward_step_paged over its
+ *  layers, llama_transformer.rs:262-391), in place on hidden_ptr: the same
+ *  arithmetic as num_layers calls of kcmm_decode_layer_step_on_stream, with
+ *  one kernel fewer per layer boundary (a layer's down projection leaves
+ *  fp32 partials whose residual add the next layer's first RMSNorm
+ *  finishes).  weights points to num_layers host structs; layer i uses
+ *  weights[i] and pool layer first_layer + i.  Same shape rules. */
+int kcmm_decode_layers_on_stream(kcmm_pool_t *pool, uint32_t first_layer, uint32_t num_layers,
+                                 const kcmm_layer_weights_t *weights, uint64_t hidden_ptr,
+                                 uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+                                 uint64_t block_offsets_f16_ptr, uint64_t inv_freq_ptr,
+                                 uint32_t batch, uint32_t hidden_size, uint32_t num_q_heads,
+                                 uint32_t intermediate_size, uint32_t max_blocks_per_seq,
+                                 float rms_eps, uint64_t stream_ptr);
 
 #ifdef __cplusplus
 }

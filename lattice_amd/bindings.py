@@ -161,11 +161,19 @@ SIGNATURES = {
     "kcmm_gemm_bf16_add_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_rmsnorm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, C.c_float, _U64], C.c_int),
     "kcmm_silu_mul_bf16_on_stream": ([_U64, _U64, _U32, _U32, _U64], C.c_int),
+    "kcmm_gemm_bf16_swiglu_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
+    "kcmm_gemm_bf16_add_rmsnorm_on_stream": ([_U64, _U64, _U64, _U64, _U64, _U32, _U32, _U32,
+                                              C.c_float, _U64], C.c_int),
+    "kcmm_qkv_rope_append_bf16_on_stream": ([_P, _U32, _U64, _U64, _U64, _U64, _U64, _U64, _U64,
+                                             _U32, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_rope_append_bf16_on_stream": ([_P, _U32, _U64, _U64, _U64, _U64, _U64, _U64, _U32,
                                          _U32, _U32, _U64], C.c_int),
     "kcmm_decode_layer_step_on_stream": ([_P, _U32, C.POINTER(KcmmLayerWeights), _U64, _U64, _U64,
                                           _U64, _U64, _U32, _U32, _U32, _U32, _U32, C.c_float,
                                           _U64], C.c_int),
+    "kcmm_decode_layers_on_stream": ([_P, _U32, _U32, C.POINTER(KcmmLayerWeights), _U64, _U64,
+                                      _U64, _U64, _U64, _U32, _U32, _U32, _U32, _U32, C.c_float,
+                                      _U64], C.c_int),
     "kcmm_below_low_watermark": ([_P, C.c_float], C.c_int),
     "kcmm_synchronize": ([_P], C.c_int),
     "kcmm_get_block_size": ([_P], _U32),
@@ -223,6 +231,21 @@ class KcmmLibrary:
         if self.lib.kcmm_silu_mul_bf16_on_stream(gate_up_ptr, act_ptr, rows, intermediate,
                                                  stream_ptr) != 0:
             raise KcmmError("kcmm_silu_mul_bf16_on_stream failed")
+
+    def gemm_bf16_add_rmsnorm(self, x_ptr, w_ptr, hidden_ptr, norm_w_ptr, normed_ptr, m, n, k,
+                              eps, stream_ptr=0) -> None:
+        """hidden += x W^T (bf16 rounding of a bf16 model); normed = rmsnorm(hidden)."""
+        if self.lib.kcmm_gemm_bf16_add_rmsnorm_on_stream(x_ptr, w_ptr, hidden_ptr, norm_w_ptr,
+                                                         normed_ptr, m, n, k, C.c_float(eps),
+                                                         stream_ptr) != 0:
+            raise KcmmError("kcmm_gemm_bf16_add_rmsnorm_on_stream failed")
+
+    def gemm_bf16_swiglu(self, x_ptr, w_gate_up_ptr, act_ptr, m, intermediate, k,
+                         stream_ptr=0) -> None:
+        """act = bf16(bf16(silu(x Wg^T)) * (x Wu^T)), W = [Wg; Wu]."""
+        if self.lib.kcmm_gemm_bf16_swiglu_on_stream(x_ptr, w_gate_up_ptr, act_ptr, m,
+                                                    intermediate, k, stream_ptr) != 0:
+            raise KcmmError("kcmm_gemm_bf16_swiglu_on_stream failed")
 
 
 class KcmmPool:
@@ -429,6 +452,16 @@ class KcmmPool:
             stream_ptr)
         self._check(rc, "rope_append")
 
+    def qkv_rope_append(self, *, layer_idx, x_ptr, w_qkv_ptr, q_out_ptr, block_tables_ptr,
+                        seq_lens_ptr, block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size,
+                        num_q_heads, max_blocks_per_seq, stream_ptr=0) -> None:
+        """QKV projection with RoPE and the KV append fused into its store."""
+        rc = self.lib.kcmm_qkv_rope_append_bf16_on_stream(
+            self.handle, layer_idx, x_ptr, w_qkv_ptr, q_out_ptr, block_tables_ptr, seq_lens_ptr,
+            block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size, num_q_heads,
+            max_blocks_per_seq, stream_ptr)
+        self._check(rc, "qkv_rope_append")
+
     def decode_layer_step(self, *, layer_idx, weights: KcmmLayerWeights, hidden_ptr,
                           block_tables_ptr, seq_lens_ptr, block_offsets_f16_ptr, inv_freq_ptr,
                           batch, hidden_size, num_q_heads, intermediate_size, max_blocks_per_seq,
@@ -439,6 +472,17 @@ class KcmmPool:
             block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size, num_q_heads,
             intermediate_size, max_blocks_per_seq, C.c_float(rms_eps), stream_ptr)
         self._check(rc, "decode_layer_step")
+
+    def decode_layers(self, *, first_layer, weights, hidden_ptr, block_tables_ptr, seq_lens_ptr,
+                      block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size, num_q_heads,
+                      intermediate_size, max_blocks_per_seq, rms_eps, stream_ptr=0) -> None:
+        """Layers first_layer .. first_layer + len(weights) - 1 in one call."""
+        arr = (KcmmLayerWeights * len(weights))(*weights)
+        rc = self.lib.kcmm_decode_layers_on_stream(
+            self.handle, first_layer, len(weights), arr, hidden_ptr, block_tables_ptr,
+            seq_lens_ptr, block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size, num_q_heads,
+            intermediate_size, max_blocks_per_seq, C.c_float(rms_eps), stream_ptr)
+        self._check(rc, "decode_layers")
 
     # -- copy-on-write --
     def fork_sequence(self, src: int) -> int:

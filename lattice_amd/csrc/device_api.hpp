@@ -20,8 +20,8 @@ std::unique_ptr<PageBacking> make_backing(int device, std::string* err);
 bool set_device(int device, std::string* err);
 
 // Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
-// attention partials, 1: GEMM partials, 2: decode attention segment table,
-// 3: decode layer-step activations).
+// attention partials, 1: GEMM split partials, 2: decode attention segment
+// table, 3: decode layer-step activations).
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);
@@ -109,6 +109,31 @@ struct RopeAppendArgs {
 bool rope_append_bf16(const RopeAppendArgs& a, std::string* err);
 bool silu_mul_bf16(uint64_t gate_up, uint64_t act, uint32_t rows, uint32_t inter,
                    uint64_t stream, std::string* err);
+
+// The same two steps fed by a split GEMM's fp32 partials [splits][rows][n]
+// (summed in split order and rounded to bf16 first, as the GEMM's own store
+// would): RoPE/append of the QKV projection, and the O projection's residual
+// add (hidden = bf16(hidden + bf16(sum)), written back) followed by RMSNorm.
+bool rope_append_from_partials(const RopeAppendArgs& a, const float* part, int splits,
+                               std::string* err);
+bool residual_rmsnorm_from_partials(const float* part, int splits, uint64_t hidden, uint64_t w,
+                                    uint64_t y, uint32_t rows, uint32_t H, float eps,
+                                    uint64_t stream, std::string* err);
+
+// X W^T as fp32 partials [*splits][m][n] in the stream's workspace (slot 1),
+// for a consumer that finishes the sum itself.
+bool gemm_bf16_partials(uint64_t x, uint64_t w, uint32_t m, uint32_t n, uint32_t k,
+                        uint64_t stream, float** part, int* splits, std::string* err);
+
+// Fused projections (kernels/gemm.hip): the QKV GEMM whose store does what
+// rope_append_bf16 does with its result (a.qkv unused; one token per
+// sequence, m == a.batch; head_dim % 16 == 0), and the gate/up GEMM whose
+// store does what silu_mul_bf16 does (w_gate_up = [gate; up], [2 inter][k]).
+// With a K split the finishing step runs as a second kernel over the partials.
+bool gemm_bf16_rope_append(uint64_t x, uint64_t w_qkv, uint32_t m, uint32_t k,
+                           const RopeAppendArgs& a, std::string* err);
+bool gemm_bf16_swiglu(uint64_t x, uint64_t w_gate_up, uint64_t act, uint32_t m, uint32_t inter,
+                      uint32_t k, uint64_t stream, std::string* err);
 
 }  // namespace dev
 }  // namespace kcmm

@@ -864,6 +864,35 @@ int kcmm_gemm_bf16_add_on_stream(uint64_t x, uint64_t w, uint64_t residual, uint
 
 // ---- decode-step glue and the layer step ------------------------------------------------------
 
+int kcmm_gemm_bf16_swiglu_on_stream(uint64_t x, uint64_t w_gate_up, uint64_t act, uint32_t m,
+                                    uint32_t intermediate, uint32_t k, uint64_t stream) {
+    if (x == 0 || w_gate_up == 0 || act == 0 || m == 0 || intermediate == 0 || k == 0) return -1;
+    std::string err;
+    if (!kcmm::dev::gemm_bf16_swiglu(x, w_gate_up, act, m, intermediate, k, stream, &err)) {
+        std::fprintf(stderr, "kcmm_gemm_bf16_swiglu_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_gemm_bf16_add_rmsnorm_on_stream(uint64_t x, uint64_t w, uint64_t hidden, uint64_t norm_w,
+                                         uint64_t normed, uint32_t m, uint32_t n, uint32_t k,
+                                         float eps, uint64_t stream) {
+    if (x == 0 || w == 0 || hidden == 0 || norm_w == 0 || normed == 0 || m == 0 || n == 0 ||
+        k == 0 || n % 8 != 0 || !(eps >= 0.0f))
+        return -1;
+    std::string err;
+    float* part = nullptr;
+    int splits = 1;
+    if (!kcmm::dev::gemm_bf16_partials(x, w, m, n, k, stream, &part, &splits, &err) ||
+        !kcmm::dev::residual_rmsnorm_from_partials(part, splits, hidden, norm_w, normed, m, n, eps,
+                                                   stream, &err)) {
+        std::fprintf(stderr, "kcmm_gemm_bf16_add_rmsnorm_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
 int kcmm_rmsnorm_bf16_on_stream(uint64_t x, uint64_t w, uint64_t y, uint32_t rows,
                                 uint32_t hidden, float eps, uint64_t stream) {
     if (x == 0 || w == 0 || y == 0 || rows == 0 || hidden == 0 || hidden % 8 != 0 ||
@@ -966,21 +995,61 @@ int kcmm_rope_append_bf16_on_stream(kcmm_pool_t* pool, uint32_t layer_idx, uint6
     return 0;
 }
 
-int kcmm_decode_layer_step_on_stream(kcmm_pool_t* pool, uint32_t layer_idx,
-                                     const kcmm_layer_weights_t* w, uint64_t hidden,
-                                     uint64_t block_tables, uint64_t seq_lens,
-                                     uint64_t offsets_f16, uint64_t inv_freq, uint32_t batch,
-                                     uint32_t hidden_size, uint32_t num_q_heads,
-                                     uint32_t intermediate_size, uint32_t max_blocks_per_seq,
-                                     float rms_eps, uint64_t stream) {
-    const char* fn = "kcmm_decode_layer_step_on_stream";
-    if (pool == nullptr || w == nullptr || hidden == 0 || block_tables == 0 || seq_lens == 0 ||
-        offsets_f16 == 0 || inv_freq == 0 || w->attn_norm == 0 || w->qkv == 0 || w->o == 0 ||
-        w->mlp_norm == 0 || w->gate_up == 0 || w->down == 0) {
+int kcmm_qkv_rope_append_bf16_on_stream(kcmm_pool_t* pool, uint32_t layer_idx, uint64_t x,
+                                        uint64_t w_qkv, uint64_t q_out, uint64_t block_tables,
+                                        uint64_t seq_lens, uint64_t offsets_f16, uint64_t inv_freq,
+                                        uint32_t batch, uint32_t hidden_size, uint32_t num_q_heads,
+                                        uint32_t max_blocks_per_seq, uint64_t stream) {
+    const char* fn = "kcmm_qkv_rope_append_bf16_on_stream";
+    if (pool == nullptr || x == 0 || w_qkv == 0 || q_out == 0 || block_tables == 0 ||
+        seq_lens == 0 || offsets_f16 == 0 || inv_freq == 0) {
         if (pool) pool->set_error(std::string(fn) + ": null pointer argument");
         return -1;
     }
     if (!step_shapes_ok(pool, fn, layer_idx, batch, num_q_heads, max_blocks_per_seq)) return -1;
+    std::string err;
+    if (!kcmm::dev::set_device(pool->device, &err) ||
+        !kcmm::dev::gemm_bf16_rope_append(x, w_qkv, batch, hidden_size,
+                                          rope_args(pool, layer_idx, 0, q_out, block_tables,
+                                                    seq_lens, offsets_f16, inv_freq, batch,
+                                                    num_q_heads, max_blocks_per_seq, stream),
+                                          &err)) {
+        pool->set_error(std::string(fn) + ": " + err);
+        return -1;
+    }
+    return 0;
+}
+
+namespace {
+
+// Layers first .. first + n - 1 of a decode step, in place on hidden.  Per
+// layer: RMSNorm -> QKV projection with RoPE + KV append -> paged attention
+// -> O projection (fp32 partials) -> residual add + RMSNorm -> gate/up with
+// SwiGLU -> down projection.  Between layers the down projection also leaves
+// partials, and the next layer's first RMSNorm finishes its residual add;
+// the last layer's down projection adds its residual itself.
+int run_decode_layers(kcmm_pool_t* pool, const char* fn, uint32_t first, uint32_t n,
+                      const kcmm_layer_weights_t* w, uint64_t hidden, uint64_t block_tables,
+                      uint64_t seq_lens, uint64_t offsets_f16, uint64_t inv_freq, uint32_t batch,
+                      uint32_t hidden_size, uint32_t num_q_heads, uint32_t intermediate_size,
+                      uint32_t max_blocks_per_seq, float rms_eps, uint64_t stream) {
+    if (pool == nullptr || w == nullptr || n == 0 || hidden == 0 || block_tables == 0 ||
+        seq_lens == 0 || offsets_f16 == 0 || inv_freq == 0) {
+        if (pool) pool->set_error(std::string(fn) + ": null pointer argument or no layers");
+        return -1;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        const kcmm_layer_weights_t& l = w[i];
+        if (l.attn_norm == 0 || l.qkv == 0 || l.o == 0 || l.mlp_norm == 0 || l.gate_up == 0 ||
+            l.down == 0) {
+            pool->set_error(std::string(fn) + ": null weight pointer");
+            return -1;
+        }
+    }
+    if (first + static_cast<uint64_t>(n) - 1 > 0xFFFFFFFFull ||
+        !step_shapes_ok(pool, fn, first, batch, num_q_heads, max_blocks_per_seq) ||
+        !step_shapes_ok(pool, fn, first + n - 1, batch, num_q_heads, max_blocks_per_seq))
+        return -1;
     const kcmm::PoolGeometry& g = pool->core->geo();
     const uint64_t D = g.head_dim, hkv = g.kv_heads, hq = num_q_heads;
     const uint64_t H = hidden_size, I = intermediate_size;
@@ -998,67 +1067,123 @@ int kcmm_decode_layer_step_on_stream(kcmm_pool_t* pool, uint32_t layer_idx,
         pool->set_error(std::string(fn) + ": bind device failed: " + err);
         return -1;
     }
-    // activations: normed [B][H], qkv [B][qkv_n], q [B][Hq D], attn [B][Hq D],
-    // gate_up [B][2I], act [B][I] (bf16), each 256-byte aligned
+    // activations: normed [B][H], qkv [B][qkv_n] (only when RoPE is not fused),
+    // q [B][Hq D], attn [B][Hq D], act [B][I] (bf16), each 256-byte aligned
     auto al = [](uint64_t bytes) { return (bytes + 255) & ~255ull; };
-    const uint64_t sz_norm = al(batch * H * 2), sz_qkv = al(batch * qkv_n * 2),
-                   sz_q = al(batch * attn_k * 2), sz_gu = al(batch * 2 * I * 2),
-                   sz_act = al(batch * I * 2);
+    const uint64_t sz_norm = al(batch * H * 2), sz_qkv = D % 16 == 0 ? 0 : al(batch * qkv_n * 2),
+                   sz_q = al(batch * attn_k * 2), sz_act = al(batch * I * 2);
     void* ws = nullptr;
-    if (!kcmm::dev::stream_workspace(stream, 3, sz_norm + sz_qkv + 2 * sz_q + sz_gu + sz_act, &ws,
-                                     false, &err)) {
+    if (!kcmm::dev::stream_workspace(stream, 3, sz_norm + sz_qkv + 2 * sz_q + sz_act, &ws, false,
+                                     &err)) {
         pool->set_error(std::string(fn) + ": workspace: " + err);
         return -1;
     }
     const uint64_t base = reinterpret_cast<uint64_t>(ws);
     const uint64_t normed = base, qkv = normed + sz_norm, q = qkv + sz_qkv, attn = q + sz_q,
-                   gu = attn + sz_q, act = gu + sz_gu;
-
-    kcmm::dev::AttnDecodeArgs at{};
-    at.dtype = g.dtype;
-    at.q = q;
-    at.out = attn;
-    at.k_base = pool->core->va_k(layer_idx);
-    at.v_base = pool->core->va_v(layer_idx);
-    at.block_tables = block_tables;
-    at.seq_lens = seq_lens;
-    at.offsets_f16 = offsets_f16;
-    at.batch = batch;
-    at.num_q_heads = num_q_heads;
-    at.kv_heads = static_cast<uint32_t>(hkv);
-    at.head_dim = static_cast<uint32_t>(D);
-    at.block_size = static_cast<uint32_t>(g.block_size);
-    at.mbps = max_blocks_per_seq;
-    at.row_bytes = static_cast<uint32_t>(g.row_bytes);
-    at.data_bytes = static_cast<uint32_t>(g.data_bytes);
-    at.scale = 1.0f / std::sqrt(static_cast<float>(D));
-    at.stream = stream;
-
+                   act = attn + sz_q;
     const uint32_t B = batch;
-    const bool ok =
-        kcmm::dev::rmsnorm_bf16(hidden, w->attn_norm, normed, B, hidden_size, rms_eps, stream,
-                                &err) &&
-        kcmm::dev::gemm_bf16(normed, w->qkv, qkv, B, static_cast<uint32_t>(qkv_n), hidden_size,
-                             stream, &err) &&
-        kcmm::dev::rope_append_bf16(rope_args(pool, layer_idx, qkv, q, block_tables, seq_lens,
-                                              offsets_f16, inv_freq, B, num_q_heads,
-                                              max_blocks_per_seq, stream),
-                                    &err) &&
-        kcmm::dev::attn_decode(at, &err) &&
-        kcmm::dev::gemm_bf16(attn, w->o, hidden, B, hidden_size, static_cast<uint32_t>(attn_k),
-                             stream, &err, hidden) &&
-        kcmm::dev::rmsnorm_bf16(hidden, w->mlp_norm, normed, B, hidden_size, rms_eps, stream,
-                                &err) &&
-        kcmm::dev::gemm_bf16(normed, w->gate_up, gu, B, 2 * intermediate_size, hidden_size,
-                             stream, &err) &&
-        kcmm::dev::silu_mul_bf16(gu, act, B, intermediate_size, stream, &err) &&
-        kcmm::dev::gemm_bf16(act, w->down, hidden, B, hidden_size, intermediate_size, stream,
-                             &err, hidden);
-    if (!ok) {
-        pool->set_error(std::string(fn) + ": launch failed: " + err);
-        return -1;
+
+    float* down_part = nullptr;   // previous layer's down-projection partials
+    int down_splits = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t layer = first + i;
+        const kcmm_layer_weights_t& l = w[i];
+        kcmm::dev::AttnDecodeArgs at{};
+        at.dtype = g.dtype;
+        at.q = q;
+        at.out = attn;
+        at.k_base = pool->core->va_k(layer);
+        at.v_base = pool->core->va_v(layer);
+        at.block_tables = block_tables;
+        at.seq_lens = seq_lens;
+        at.offsets_f16 = offsets_f16;
+        at.batch = batch;
+        at.num_q_heads = num_q_heads;
+        at.kv_heads = static_cast<uint32_t>(hkv);
+        at.head_dim = static_cast<uint32_t>(D);
+        at.block_size = static_cast<uint32_t>(g.block_size);
+        at.mbps = max_blocks_per_seq;
+        at.row_bytes = static_cast<uint32_t>(g.row_bytes);
+        at.data_bytes = static_cast<uint32_t>(g.data_bytes);
+        at.scale = 1.0f / std::sqrt(static_cast<float>(D));
+        at.stream = stream;
+        const auto ra = rope_args(pool, layer, qkv, q, block_tables, seq_lens, offsets_f16,
+                                  inv_freq, B, num_q_heads, max_blocks_per_seq, stream);
+        auto norm1 = [&]() {
+            if (down_part == nullptr)
+                return kcmm::dev::rmsnorm_bf16(hidden, l.attn_norm, normed, B, hidden_size, rms_eps,
+                                               stream, &err);
+            return kcmm::dev::residual_rmsnorm_from_partials(down_part, down_splits, hidden,
+                                                             l.attn_norm, normed, B, hidden_size,
+                                                             rms_eps, stream, &err);
+        };
+        // QKV projection with RoPE + KV append in its store (head_dim % 16 ==
+        // 0), else the projection then the standalone RoPE/append kernel
+        auto qkv_step = [&]() {
+            if (D % 16 == 0)
+                return kcmm::dev::gemm_bf16_rope_append(normed, l.qkv, B, hidden_size, ra, &err);
+            return kcmm::dev::gemm_bf16(normed, l.qkv, qkv, B, static_cast<uint32_t>(qkv_n),
+                                        hidden_size, stream, &err) &&
+                   kcmm::dev::rope_append_bf16(ra, &err);
+        };
+        // O projection as partials; the residual add is finished by the
+        // RMSNorm kernel that reads them
+        auto o_step = [&]() {
+            float* part = nullptr;
+            int splits = 1;
+            return kcmm::dev::gemm_bf16_partials(attn, l.o, B, hidden_size,
+                                                 static_cast<uint32_t>(attn_k), stream, &part,
+                                                 &splits, &err) &&
+                   kcmm::dev::residual_rmsnorm_from_partials(part, splits, hidden, l.mlp_norm,
+                                                             normed, B, hidden_size, rms_eps,
+                                                             stream, &err);
+        };
+        auto down_step = [&]() {
+            if (i + 1 == n) {
+                down_part = nullptr;
+                return kcmm::dev::gemm_bf16(act, l.down, hidden, B, hidden_size,
+                                            intermediate_size, stream, &err, hidden);
+            }
+            return kcmm::dev::gemm_bf16_partials(act, l.down, B, hidden_size, intermediate_size,
+                                                 stream, &down_part, &down_splits, &err);
+        };
+        const bool ok = norm1() && qkv_step() && kcmm::dev::attn_decode(at, &err) && o_step() &&
+                        kcmm::dev::gemm_bf16_swiglu(normed, l.gate_up, act, B, intermediate_size,
+                                                    hidden_size, stream, &err) &&
+                        down_step();
+        if (!ok) {
+            pool->set_error(std::string(fn) + ": launch failed at layer " + std::to_string(layer) +
+                            ": " + err);
+            return -1;
+        }
     }
     return 0;
+}
+
+}  // namespace
+
+int kcmm_decode_layer_step_on_stream(kcmm_pool_t* pool, uint32_t layer_idx,
+                                     const kcmm_layer_weights_t* w, uint64_t hidden,
+                                     uint64_t block_tables, uint64_t seq_lens,
+                                     uint64_t offsets_f16, uint64_t inv_freq, uint32_t batch,
+                                     uint32_t hidden_size, uint32_t num_q_heads,
+                                     uint32_t intermediate_size, uint32_t max_blocks_per_seq,
+                                     float rms_eps, uint64_t stream) {
+    return run_decode_layers(pool, "kcmm_decode_layer_step_on_stream", layer_idx, 1, w, hidden,
+                             block_tables, seq_lens, offsets_f16, inv_freq, batch, hidden_size,
+                             num_q_heads, intermediate_size, max_blocks_per_seq, rms_eps, stream);
+}
+
+int kcmm_decode_layers_on_stream(kcmm_pool_t* pool, uint32_t first_layer, uint32_t num_layers,
+                                 const kcmm_layer_weights_t* weights, uint64_t hidden,
+                                 uint64_t block_tables, uint64_t seq_lens, uint64_t offsets_f16,
+                                 uint64_t inv_freq, uint32_t batch, uint32_t hidden_size,
+                                 uint32_t num_q_heads, uint32_t intermediate_size,
+                                 uint32_t max_blocks_per_seq, float rms_eps, uint64_t stream) {
+    return run_decode_layers(pool, "kcmm_decode_layers_on_stream", first_layer, num_layers,
+                             weights, hidden, block_tables, seq_lens, offsets_f16, inv_freq, batch,
+                             hidden_size, num_q_heads, intermediate_size, max_blocks_per_seq,
+                             rms_eps, stream);
 }
 
 // ---- utilities ---------------------------------------------------------------------------------

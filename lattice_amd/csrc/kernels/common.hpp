@@ -67,6 +67,31 @@ __device__ __forceinline__ float fp8e4m3_to_f32(uint32_t b) {
     return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
 }
 
+__device__ __forceinline__ float bf16_round_f32(float f) {
+    return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+// Decoder-layer element arithmetic shared by the standalone glue kernels and
+// the GEMM epilogues that fuse them, so both give identical bits.
+//  * RoPE of one rotate-half pair (x1 = element i, x2 = element i + D/2):
+//    x1' = x1 c - x2 s, x2' = x2 c + x1 s, with c, s of pos * inv_freq[i];
+//  * SwiGLU: bf16(bf16(silu(g)) * u), the roundings of a bf16 model.
+__device__ __forceinline__ void rope_cos_sin(int pos, float inv_freq, float* c, float* s) {
+    const float ang = static_cast<float>(pos) * inv_freq;
+    *c = cosf(ang);
+    *s = sinf(ang);
+}
+__device__ __forceinline__ float rope_first(float x1, float x2, float c, float s) {
+    return __builtin_fmaf(x1, c, -(x2 * s));
+}
+__device__ __forceinline__ float rope_second(float x1, float x2, float c, float s) {
+    return __builtin_fmaf(x2, c, x1 * s);
+}
+__device__ __forceinline__ float swiglu_bf16(float g, float u) {
+    const float sg = bf16_round_f32(g / (1.0f + __expf(-g)));
+    return bf16_round_f32(sg * u);
+}
+
 }  // namespace kcmm
 
 #define KCMM_HIP_CHECK(expr, errp)                                              \

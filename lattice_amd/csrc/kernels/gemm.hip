@@ -6,8 +6,21 @@
 // At decode the token count M is small (64..256) and the weights dominate the
 // bytes: at M = 64 the arithmetic intensity is ~62 flop/B, far below the MFMA
 // ridge, so the kernel is a weight stream (see gemm_bf16_stream).  K is split
-// when N alone gives too few workgroups; fp32 split partials are summed by a
-// second small kernel.
+// when N alone gives too few workgroups: each split then writes fp32
+// partials and the kernel that consumes the product sums them (in split
+// order) as its first step -- a plain reduce, the SwiGLU finish here, or the
+// RoPE/append and residual/RMSNorm kernels of glue.hip -- so no workgroup
+// waits on another and no extra kernel is spent on the sum.
+//
+// Without a split, three epilogues run in the GEMM's own store:
+//  * plain: Y = bf16(acc), or Y = bf16(R + bf16(acc)) with a residual R;
+//  * rope_append (the fused QKV projection of a decode step): q heads are
+//    rotated into q_out, k heads rotated and v heads copied straight into the
+//    token's page row, so qkv never makes a round trip through HBM;
+//  * swiglu (the fused gate/up projection): act = bf16(bf16(silu(g)) * u).
+// The paired epilogues choose which weight rows a wave streams so that both
+// members of a pair (RoPE i and i + D/2; gate j and up I + j) land in the
+// same wave, 32 lanes apart.
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
@@ -15,8 +28,16 @@
 #include "../device_api.hpp"
 #include "common.hpp"
 
+#ifndef KCMM_GEMM_BUFFER_LOADS
+#define KCMM_GEMM_BUFFER_LOADS 0
+#endif
+
 namespace kcmm {
 namespace {
+
+constexpr int kEpiPlain = 0;
+constexpr int kEpiRope = 1;
+constexpr int kEpiSwiglu = 2;
 
 // Row rotation by 8 inside each 16-lane row (DPP row_ror:8; its own inverse).
 __device__ __forceinline__ uint32_t ror8(uint32_t x) {
@@ -44,81 +65,158 @@ __device__ __forceinline__ u32x4 load_stream(const uint8_t* a) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a));
 }
 
-// Weight-streaming GEMM.  Workgroup = 4 waves = 64 weight rows (16 per wave)
-// x up to 16*MB tokens x one K split of `klen`, walked in chunks of KCH:
-//  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
-//    whole-line nontemporal loads (8 rows x 128 B per instruction) and is put
-//    into MFMA A layout by fix_lines; chunk c+1 is in flight while chunk c is
-//    consumed, so every weight byte is read once and never touches LDS;
-//  * the activation chunk (M x KCH) is staged in LDS, double-buffered, 16-byte
-//    pieces XOR-swizzled by row so that B-operand reads are conflict-free; one
-//    barrier per chunk;
-//  * rows of X past M are clamped (their output columns are never stored).
-// (Measured alternatives that were slower at the Llama-3-8B decode shapes: a
-// persistent grid over (row block, k chunk) tiles with a 6-deep ring, and
-// direct-to-LDS activation loads with a 3-deep weight ring.)
-// v (4 consecutive outputs) rounded to bf16, then + the residual row piece r,
-// in fp32 (the result is rounded once more by the store): the order of a bf16
-// model's "residual + o_proj(x)".
-__device__ __forceinline__ f32x4 add_residual(f32x4 v, const uint16_t* r) {
-    const u32x2 rr = *reinterpret_cast<const u32x2*>(r);
-    f32x4 o;
-    o[0] = bf16_bits_to_f32(f32_to_bf16_bits(v[0])) + __uint_as_float(rr[0] << 16);
-    o[1] = bf16_bits_to_f32(f32_to_bf16_bits(v[1])) + __uint_as_float(rr[0] & 0xffff0000u);
-    o[2] = bf16_bits_to_f32(f32_to_bf16_bits(v[2])) + __uint_as_float(rr[1] << 16);
-    o[3] = bf16_bits_to_f32(f32_to_bf16_bits(v[3])) + __uint_as_float(rr[1] & 0xffff0000u);
+// Buffer resources: the range check makes rows past M read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+template <int POLICY>   // 2: streaming
+__device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POLICY));
+}
+
+__device__ __forceinline__ u32x2 pack4_bf16(f32x4 v) {
+    u32x2 o;
+    o[0] = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+    o[1] = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
     return o;
 }
 
-template <int MB, int KCH>
+// 4 consecutive outputs rounded to bf16, then + the residual piece r in fp32
+// (rounded once more by the store): the order of a bf16 model's
+// "residual + o_proj(x)".
+__device__ __forceinline__ f32x4 add_residual(f32x4 v, const uint16_t* r) {
+    const u32x2 rr = *reinterpret_cast<const u32x2*>(r);
+    f32x4 o;
+    o[0] = bf16_round_f32(v[0]) + __uint_as_float(rr[0] << 16);
+    o[1] = bf16_round_f32(v[1]) + __uint_as_float(rr[0] & 0xffff0000u);
+    o[2] = bf16_round_f32(v[2]) + __uint_as_float(rr[1] << 16);
+    o[3] = bf16_round_f32(v[3]) + __uint_as_float(rr[1] & 0xffff0000u);
+    return o;
+}
+
+struct GemmParams {
+    const uint16_t* X;   // [M][K]
+    const uint16_t* W;   // [N][K]
+    uint16_t* Y;         // plain: [M][N]; swiglu: act [M][N/2]
+    const uint16_t* R;   // plain: residual [M][N] or null (may equal Y)
+    float* part;         // non-null: write fp32 partials [split][M][N], no epilogue
+    int M, N, K, klen;
+    // rope_append
+    uint16_t* q_out;     // [M][Hq][D]
+    uint8_t* k_base;
+    uint8_t* v_base;
+    const int32_t* block_tables;
+    const int32_t* seq_lens;
+    const uint64_t* offsets_f16;
+    const float* inv_freq;
+    int hq, hkv, D, block_size, mbps, row_bytes;
+};
+
+// Weight-streaming GEMM.  Workgroup = 4 waves = 64 weight rows (16 per wave)
+// x up to 16*MB tokens x one K split of `klen`, walked in chunks of KCH:
+//  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
+//    whole-line streaming loads (8 rows x 128 B per instruction) and is put
+//    into MFMA A layout by fix_lines, one line at a time; chunk c+1 is in
+//    flight while chunk c is consumed, so every weight byte is read once and
+//    never touches LDS;
+//  * the activation chunk (M x KCH) is staged in LDS, double-buffered, laid
+//    out so that B-operand reads are conflict-free; one barrier per chunk;
+//  * activation rows past M are clamped or read as zero (their outputs are
+//    never stored).
+// (Measured alternatives that were not faster at the Llama-3-8B decode
+// shapes: a persistent grid over (row block, k chunk) tiles with a 6-deep
+// ring; direct-to-LDS activation loads with a 3-deep weight ring; 8-wave
+// workgroups at 2 or 4 waves per SIMD; summing the split partials inside
+// this kernel by the last workgroup of each tile, whose coherent stores and
+// arrival count put several memory round trips on every tile's tail.)
+template <int MB, int KCH, int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
-                      uint16_t* Y, float* __restrict__ part, const uint16_t* R, int M, int N, int K,
-                      int klen) {
+void gemm_bf16_stream(GemmParams p) {
+    constexpr int NT = 256;
     constexpr int LINES = KCH / 64;          // 128-byte lines per weight row per chunk
     constexpr int KC = KCH / 32;             // MFMA k-steps per chunk
     constexpr int PIECES = KCH / 8;          // 16-byte pieces per activation row
     constexpr int MROWS = 16 * MB;
-    constexpr int XLOADS = MROWS * PIECES / 256;
-    static_assert(XLOADS * 256 == MROWS * PIECES, "activation chunk must split over 256 threads");
-    __shared__ u32x4 xs[2][MROWS * PIECES];
+    constexpr int XLOADS = MROWS * PIECES / NT;
+    constexpr int XROWSTEP = NT / PIECES;    // activation rows per load round
+    static_assert(XLOADS * NT == MROWS * PIECES, "activation chunk must split over the threads");
+    constexpr bool BUF = KCMM_GEMM_BUFFER_LOADS != 0;
+    // LDS row: padded by 16 bytes (buffer form) or XOR-swizzled pieces
+    constexpr int ROWB = BUF ? (PIECES + 1) * 16 : PIECES * 16;
+    constexpr int XBUF = MROWS * ROWB;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2 * XBUF];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ln = lane & 15, lg = lane >> 4;
     const bool low8 = ln < 8;
-    const int n0 = blockIdx.x * 64 + wave * 16;
+    const int K = p.K;
     const int m_base = blockIdx.z * MROWS;
-    const int kbeg = blockIdx.y * klen;
-    const int nchunks = klen / KCH;
+    const int kbeg = blockIdx.y * p.klen;
+    const int nchunks = p.klen / KCH;
+    const uint32_t rowb = static_cast<uint32_t>(K) * 2;
 
-    const uint8_t* wx = reinterpret_cast<const uint8_t*>(W + static_cast<size_t>(n0 + (ln & 7)) * K + kbeg) +
-                        ((ln >> 3) * 4 + lg) * 16;
-    const size_t row8 = static_cast<size_t>(8) * K * 2;
+    // weight rows of this wave: rowA + 0..7 (MFMA rows 0..7), rowB + 0..7 (8..15)
+    const int gw = blockIdx.x * 4 + wave;
+    int rowA, rowB;
+    if constexpr (EPI == kEpiRope) {
+        const int wph = p.D / 16;            // waves per head: 8 rotation pairs each
+        const int head = gw / wph;
+        rowA = head * p.D + (gw - head * wph) * 8;
+        rowB = rowA + p.D / 2;
+    } else if constexpr (EPI == kEpiSwiglu) {
+        rowA = gw * 8;
+        rowB = p.N / 2 + gw * 8;
+    } else {
+        rowA = gw * 16;
+        rowB = rowA + 8;
+    }
+
+    const uint32_t piece = ((ln >> 3) * 4 + lg) * 16;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.W, static_cast<uint32_t>(p.N) * rowb);
+    const uint32_t wv0 = (rowA + (ln & 7)) * rowb + piece;
+    const uint32_t wv1 = (rowB + (ln & 7)) * rowb + piece;
+    const uint8_t* wp0 = reinterpret_cast<const uint8_t*>(p.W) + wv0 + static_cast<size_t>(kbeg) * 2;
+    const uint8_t* wp1 = reinterpret_cast<const uint8_t*>(p.W) + wv1 + static_cast<size_t>(kbeg) * 2;
     auto load_w = [&](u32x4* dst, int c) {
-        const uint8_t* q = wx + static_cast<size_t>(c) * KCH * 2;
 #pragma unroll
         for (int c2 = 0; c2 < LINES; ++c2) {
-            dst[2 * c2] = load_stream(q + c2 * 128);
-            dst[2 * c2 + 1] = load_stream(q + row8 + c2 * 128);
+            if constexpr (BUF) {
+                const uint32_t so = static_cast<uint32_t>(kbeg + c * KCH) * 2 + c2 * 128;
+                dst[2 * c2] = bload<2>(wr, wv0, so);
+                dst[2 * c2 + 1] = bload<2>(wr, wv1, so);
+            } else {
+                const size_t o = static_cast<size_t>(c) * KCH * 2 + c2 * 128;
+                dst[2 * c2] = load_stream(wp0 + o);
+                dst[2 * c2 + 1] = load_stream(wp1 + o);
+            }
         }
     };
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.X, static_cast<uint32_t>(p.M) * rowb);
     u32x4 xr[XLOADS];
     auto load_x = [&](int c) {
 #pragma unroll
         for (int i = 0; i < XLOADS; ++i) {
-            const int idx = tid + 256 * i;
-            const int m = min(m_base + idx / PIECES, M - 1);
-            xr[i] = *reinterpret_cast<const u32x4*>(X + static_cast<size_t>(m) * K + kbeg + c * KCH +
-                                                    (idx % PIECES) * 8);
+            const int r = m_base + tid / PIECES + i * XROWSTEP;
+            if constexpr (BUF) {
+                // the row lives in the lane offset, which the range check covers
+                xr[i] = bload<0>(xrs, r * rowb + (tid % PIECES) * 16 + kbeg * 2,
+                                 static_cast<uint32_t>(c) * KCH * 2);
+            } else {
+                const int m = min(r, p.M - 1);
+                xr[i] = *reinterpret_cast<const u32x4*>(p.X + static_cast<size_t>(m) * K + kbeg +
+                                                        c * KCH + (tid % PIECES) * 8);
+            }
         }
     };
     auto store_x = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < XLOADS; ++i) {
-            const int idx = tid + 256 * i;
-            const int r = idx / PIECES, pc = idx % PIECES;
-            xs[buf][r * PIECES + (pc ^ (r & (PIECES - 1)))] = xr[i];
+            const int r = tid / PIECES + i * XROWSTEP, pc = tid % PIECES;
+            const int off = BUF ? r * ROWB + pc * 16 : r * ROWB + ((pc ^ (r & (PIECES - 1))) * 16);
+            *reinterpret_cast<u32x4*>(xs + buf * XBUF + off) = xr[i];
         }
     };
 
@@ -128,19 +226,27 @@ void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict
 
     auto compute = [&](u32x4* wa, int buf) {
 #pragma unroll
-        for (int c2 = 0; c2 < LINES; ++c2) fix_lines(wa[2 * c2], wa[2 * c2 + 1], low8);
+        for (int c2 = 0; c2 < LINES; ++c2) {
+            fix_lines(wa[2 * c2], wa[2 * c2 + 1], low8);
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-            const int pc = 4 * kc + lg;
+            for (int kk = 0; kk < 2; ++kk) {
+                const int kc = 2 * c2 + kk;
+                const int pc = 4 * kc + lg;
+                u32x4 b[MB];
 #pragma unroll
-            for (int j = 0; j < MB; ++j) {
-                const int r = 16 * j + ln;
-                const u32x4 b = xs[buf][r * PIECES + (pc ^ (r & (PIECES - 1)))];
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wa[kc]),
-                                                                 __builtin_bit_cast(bf16x8, b),
-                                                                 acc[j], 0, 0, 0);
+                for (int j = 0; j < MB; ++j) {
+                    const int r = 16 * j + ln;
+                    const int off = BUF ? r * ROWB + pc * 16 : r * ROWB + ((pc ^ (r & (PIECES - 1))) * 16);
+                    b[j] = *reinterpret_cast<const u32x4*>(xs + buf * XBUF + off);
+                }
+#pragma unroll
+                for (int j = 0; j < MB; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, wa[kc]), __builtin_bit_cast(bf16x8, b[j]), acc[j],
+                        0, 0, 0);
             }
         }
+        (void)KC;
     };
 
     u32x4 wa0[2 * LINES], wa1[2 * LINES];
@@ -179,21 +285,94 @@ void gemm_bf16_stream(const uint16_t* __restrict__ X, const uint16_t* __restrict
         step(wa0, wa1, 0, c, Last{});
     }
 
-    // acc[j][r] = Y[m_base + 16j + ln][n0 + 4lg + r]
+    // acc[j][r] = output (token m_base + 16j + ln, wave row 4lg + r): weight
+    // row (lg < 2 ? rowA : rowB) + cw + r
+    const bool hi = lg >= 2;
+    const int cw = 4 * (lg & 1);
+    if (p.part != nullptr) {
+        const int n = (hi ? rowB : rowA) + cw;
 #pragma unroll
-    for (int j = 0; j < MB; ++j) {
-        const int m = m_base + 16 * j + ln;
-        if (m >= M) continue;
-        const int n = n0 + 4 * lg;
-        if (part == nullptr) {
+        for (int j = 0; j < MB; ++j) {
+            const int m = m_base + 16 * j + ln;
+            if (m >= p.M) continue;
+            *reinterpret_cast<f32x4*>(p.part + (static_cast<size_t>(blockIdx.y) * p.M + m) * p.N + n) = acc[j];
+        }
+        return;
+    }
+    if constexpr (EPI == kEpiPlain) {
+        const int n = rowA + 4 * lg;
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            const int m = m_base + 16 * j + ln;
+            if (m >= p.M) continue;
             f32x4 v = acc[j];
-            if (R != nullptr) v = add_residual(v, R + static_cast<size_t>(m) * N + n);
-            u32x2 o;
-            o[0] = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-            o[1] = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-            *reinterpret_cast<u32x2*>(Y + static_cast<size_t>(m) * N + n) = o;
-        } else {
-            *reinterpret_cast<f32x4*>(part + (static_cast<size_t>(blockIdx.y) * M + m) * N + n) = acc[j];
+            if (p.R != nullptr) v = add_residual(v, p.R + static_cast<size_t>(m) * p.N + n);
+            *reinterpret_cast<u32x2*>(p.Y + static_cast<size_t>(m) * p.N + n) = pack4_bf16(v);
+        }
+    } else if constexpr (EPI == kEpiSwiglu) {
+        const int I = p.N / 2;
+        const int col = rowA + cw;
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            f32x4 g, u;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float own = bf16_round_f32(acc[j][r]);
+                const float other = __shfl_xor(own, 32);
+                g[r] = hi ? other : own;
+                u[r] = hi ? own : other;
+            }
+            const int m = m_base + 16 * j + ln;
+            if (hi || m >= p.M) continue;
+            f32x4 a;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[r] = swiglu_bf16(g[r], u[r]);
+            *reinterpret_cast<u32x2*>(p.Y + static_cast<size_t>(m) * I + col) = pack4_bf16(a);
+        }
+    } else {
+        const int D = p.D;
+        const int head = rowA / D;                // wave-uniform
+        const int i0 = rowA - head * D + cw;      // rotation pair of r = 0
+        const bool rotate = head < p.hq + p.hkv;
+        const int e0 = i0 + (hi ? D / 2 : 0);     // element of r = 0 in the head
+        float ifr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ifr[r] = rotate ? p.inv_freq[i0 + r] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            f32x4 own, other;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                own[r] = bf16_round_f32(acc[j][r]);
+                other[r] = __shfl_xor(own[r], 32);
+            }
+            const int m = m_base + 16 * j + ln;
+            if (m >= p.M) continue;
+            const int pos = p.seq_lens[m] - 1;
+            if (pos < 0 || pos >= p.mbps * p.block_size) continue;   // no token / past the table
+            f32x4 out = own;
+            if (rotate) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float cs, sn;
+                    rope_cos_sin(pos, ifr[r], &cs, &sn);
+                    out[r] = hi ? rope_second(other[r], own[r], cs, sn)
+                                : rope_first(own[r], other[r], cs, sn);
+                }
+            }
+            uint16_t* dst;
+            if (head < p.hq) {
+                dst = p.q_out + (static_cast<size_t>(m) * p.hq + head) * D + e0;
+            } else {
+                const int lb = pos / p.block_size;
+                const uint64_t page =
+                    p.offsets_f16[p.block_tables[static_cast<size_t>(m) * p.mbps + lb]] * 2ull +
+                    static_cast<uint64_t>(pos - lb * p.block_size) * p.row_bytes;
+                uint8_t* region = head < p.hq + p.hkv ? p.k_base : p.v_base;
+                const int kvh = head < p.hq + p.hkv ? head - p.hq : head - p.hq - p.hkv;
+                dst = reinterpret_cast<uint16_t*>(region + page + static_cast<uint64_t>(kvh) * D * 2) + e0;
+            }
+            *reinterpret_cast<u32x2*>(dst) = pack4_bf16(out);
         }
     }
 }
@@ -207,10 +386,29 @@ __global__ __launch_bounds__(256) void gemm_split_reduce(const float* __restrict
     f32x4 s = *reinterpret_cast<const f32x4*>(part + i);
     for (int k = 1; k < splits; ++k) s += *reinterpret_cast<const f32x4*>(part + static_cast<size_t>(k) * MN + i);
     if (R != nullptr) s = add_residual(s, R + i);
-    u32x2 o;
-    o[0] = f32_to_bf16_bits(s[0]) | (f32_to_bf16_bits(s[1]) << 16);
-    o[1] = f32_to_bf16_bits(s[2]) | (f32_to_bf16_bits(s[3]) << 16);
-    *reinterpret_cast<u32x2*>(Y + i) = o;
+    *reinterpret_cast<u32x2*>(Y + i) = pack4_bf16(s);
+}
+
+// act[m][j..j+3] = swiglu of the split sums of gate (column j) and up
+// (column I + j); 4 outputs per thread.
+__global__ __launch_bounds__(256) void gemm_split_swiglu(const float* __restrict__ part,
+                                                         uint16_t* __restrict__ act, int M, int I,
+                                                         int splits) {
+    const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= M * I) return;
+    const int m = i / I, j = i - m * I;
+    const size_t MN = static_cast<size_t>(M) * 2 * I;
+    const float* g0 = part + static_cast<size_t>(m) * 2 * I + j;
+    f32x4 g = *reinterpret_cast<const f32x4*>(g0);
+    f32x4 u = *reinterpret_cast<const f32x4*>(g0 + I);
+    for (int k = 1; k < splits; ++k) {
+        g += *reinterpret_cast<const f32x4*>(g0 + k * MN);
+        u += *reinterpret_cast<const f32x4*>(g0 + k * MN + I);
+    }
+    f32x4 a;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a[r] = swiglu_bf16(bf16_round_f32(g[r]), bf16_round_f32(u[r]));
+    *reinterpret_cast<u32x2*>(act + i) = pack4_bf16(a);
 }
 
 int env_int(const char* name, int dflt) {
@@ -221,15 +419,15 @@ int env_int(const char* name, int dflt) {
 // K splits: the smallest divisor of K/kch giving at least `target` workgroups
 // (KCMM_GEMM_WGS, default 256: fewer, longer splits measured faster than
 // 512-1024 at the Llama-3-8B decode shapes) with each split at least two
-// chunks long.
+// chunks long; at most 16.
 int choose_splits(int N, int K, int kch, int mgroups) {
     const int chunks = K / kch;
     const int forced = env_int("KCMM_GEMM_SPLITS", 0);
-    if (forced >= 1 && chunks % forced == 0) return forced;
+    if (forced >= 1 && forced <= 16 && chunks % forced == 0) return forced;
     const int target = env_int("KCMM_GEMM_WGS", 256);
     const int tiles = (N / 64) * mgroups;
     int best = 1;
-    for (int s = 1; s <= chunks; ++s) {
+    for (int s = 1; s <= std::min(chunks, 16); ++s) {
         if (chunks % s) continue;
         if (chunks / s < 2 && s > 1) break;
         best = s;
@@ -238,39 +436,54 @@ int choose_splits(int N, int K, int kch, int mgroups) {
     return best;
 }
 
-template <int MB, int KCH>
-bool launch_gemm(const uint16_t* X, const uint16_t* W, uint16_t* Y, const uint16_t* R, int M,
-                 int N, int K, uint64_t stream, std::string* err) {
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int mgroups = (M + 16 * MB - 1) / (16 * MB);
-    const int splits = choose_splits(N, K, KCH, mgroups);
-    float* part = nullptr;
-    if (splits > 1) {
-        void* ws = nullptr;
-        if (!dev::stream_workspace(stream, 1, static_cast<size_t>(splits) * M * N * sizeof(float),
-                                   &ws, false, err))
-            return false;
-        part = static_cast<float*>(ws);
-    }
-    const dim3 grid(N / 64, splits, mgroups);
-    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH>), grid, dim3(256), 0, s, X, W, Y, part, R, M, N, K,
-                       K / splits);
-    KCMM_HIP_CHECK(hipGetLastError(), err);
-    if (splits > 1) {
-        const int MN = M * N;
-        hipLaunchKernelGGL(gemm_split_reduce, dim3((MN / 4 + 255) / 256), dim3(256), 0, s, part, Y,
-                           R, MN, splits);
-        KCMM_HIP_CHECK(hipGetLastError(), err);
-    }
-    return true;
+// Tile shape by M: token blocks per pass (the activation chunk, M x KCH
+// bf16, is 32 KiB).
+template <typename F>
+bool by_m(int M, F&& f) {
+    if (M <= 16) return f(std::integral_constant<int, 1>{}, std::integral_constant<int, 256>{});
+    if (M <= 32) return f(std::integral_constant<int, 2>{}, std::integral_constant<int, 256>{});
+    if (M <= 64) return f(std::integral_constant<int, 4>{}, std::integral_constant<int, 256>{});
+    if (M <= 128) return f(std::integral_constant<int, 8>{}, std::integral_constant<int, 128>{});
+    return f(std::integral_constant<int, 16>{}, std::integral_constant<int, 64>{});
 }
 
-}  // namespace
+int splits_for(int M, int N, int K) {
+    int s = 1;
+    by_m(M, [&](auto mb, auto kch) {
+        const int mgroups = (M + 16 * mb.value - 1) / (16 * mb.value);
+        s = choose_splits(N, K, kch.value, mgroups);
+        return true;
+    });
+    return s;
+}
 
-namespace dev {
+// Launch the streaming kernel with `splits` K splits; splits > 1 or
+// want_partials writes fp32 partials [splits][M][N] to the stream's workspace
+// (returned in *part) instead of running the epilogue.
+template <int EPI>
+bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, uint64_t stream,
+                   std::string* err) {
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    p.part = nullptr;
+    if (splits > 1 || want_partials) {
+        void* ws = nullptr;
+        if (!dev::stream_workspace(stream, 1, static_cast<size_t>(splits) * p.M * p.N * sizeof(float),
+                                   &ws, false, err))
+            return false;
+        p.part = static_cast<float*>(ws);
+    }
+    if (part) *part = p.part;
+    p.klen = p.K / splits;
+    return by_m(p.M, [&](auto mb, auto kch) {
+        constexpr int MB = decltype(mb)::value, KCH = decltype(kch)::value;
+        const dim3 grid(p.N / 64, splits, (p.M + 16 * MB - 1) / (16 * MB));
+        hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI>), grid, dim3(256), 0, s, p);
+        KCMM_HIP_CHECK(hipGetLastError(), err);
+        return true;
+    });
+}
 
-bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
-               uint64_t stream, std::string* err, uint64_t residual) {
+bool shape_ok(uint32_t m, uint32_t n, uint32_t k, std::string* err) {
     if (m == 0 || n % 64 != 0 || k % 256 != 0 || n == 0 || k == 0) {
         *err = "gemm_bf16 needs m > 0, n % 64 == 0 and k % 256 == 0";
         return false;
@@ -280,17 +493,101 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
         *err = "gemm_bf16 operand too large";
         return false;
     }
-    const auto* X = reinterpret_cast<const uint16_t*>(x);
-    const auto* W = reinterpret_cast<const uint16_t*>(w);
-    auto* Y = reinterpret_cast<uint16_t*>(y);
-    const auto* R = reinterpret_cast<const uint16_t*>(residual);
-    const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
-    // token blocks per pass: the activation chunk (M x KCH bf16) is 32 KiB
-    if (M <= 16) return launch_gemm<1, 256>(X, W, Y, R, M, N, K, stream, err);
-    if (M <= 32) return launch_gemm<2, 256>(X, W, Y, R, M, N, K, stream, err);
-    if (M <= 64) return launch_gemm<4, 256>(X, W, Y, R, M, N, K, stream, err);
-    if (M <= 128) return launch_gemm<8, 128>(X, W, Y, R, M, N, K, stream, err);
-    return launch_gemm<16, 64>(X, W, Y, R, M, N, K, stream, err);
+    return true;
+}
+
+GemmParams base_params(uint64_t x, uint64_t w, uint32_t m, uint32_t n, uint32_t k) {
+    GemmParams p{};
+    p.X = reinterpret_cast<const uint16_t*>(x);
+    p.W = reinterpret_cast<const uint16_t*>(w);
+    p.M = static_cast<int>(m);
+    p.N = static_cast<int>(n);
+    p.K = static_cast<int>(k);
+    return p;
+}
+
+}  // namespace
+
+namespace dev {
+
+bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
+               uint64_t stream, std::string* err, uint64_t residual) {
+    if (!shape_ok(m, n, k, err)) return false;
+    GemmParams p = base_params(x, w, m, n, k);
+    p.Y = reinterpret_cast<uint16_t*>(y);
+    p.R = reinterpret_cast<const uint16_t*>(residual);
+    const int splits = splits_for(p.M, p.N, p.K);
+    float* part = nullptr;
+    if (!launch_stream<kEpiPlain>(p, splits, false, &part, stream, err)) return false;
+    if (splits > 1) {
+        const int MN = p.M * p.N;
+        hipLaunchKernelGGL(gemm_split_reduce, dim3((MN / 4 + 255) / 256), dim3(256), 0,
+                           reinterpret_cast<hipStream_t>(stream), part, p.Y, p.R, MN, splits);
+        KCMM_HIP_CHECK(hipGetLastError(), err);
+    }
+    return true;
+}
+
+bool gemm_bf16_partials(uint64_t x, uint64_t w, uint32_t m, uint32_t n, uint32_t k,
+                        uint64_t stream, float** part, int* splits, std::string* err) {
+    if (!shape_ok(m, n, k, err)) return false;
+    GemmParams p = base_params(x, w, m, n, k);
+    *splits = splits_for(p.M, p.N, p.K);
+    return launch_stream<kEpiPlain>(p, *splits, true, part, stream, err);
+}
+
+bool gemm_bf16_swiglu(uint64_t x, uint64_t w_gate_up, uint64_t act, uint32_t m, uint32_t inter,
+                      uint32_t k, uint64_t stream, std::string* err) {
+    if (inter == 0 || inter % 32 != 0) {
+        *err = "gemm_bf16_swiglu needs intermediate % 32 == 0";
+        return false;
+    }
+    if (!shape_ok(m, 2 * inter, k, err)) return false;
+    GemmParams p = base_params(x, w_gate_up, m, 2 * inter, k);
+    p.Y = reinterpret_cast<uint16_t*>(act);
+    const int splits = splits_for(p.M, p.N, p.K);
+    float* part = nullptr;
+    if (!launch_stream<kEpiSwiglu>(p, splits, false, &part, stream, err)) return false;
+    if (splits > 1) {
+        const int n = p.M * static_cast<int>(inter);
+        hipLaunchKernelGGL(gemm_split_swiglu, dim3((n / 4 + 255) / 256), dim3(256), 0,
+                           reinterpret_cast<hipStream_t>(stream), part, p.Y, p.M,
+                           static_cast<int>(inter), splits);
+        KCMM_HIP_CHECK(hipGetLastError(), err);
+    }
+    return true;
+}
+
+bool gemm_bf16_rope_append(uint64_t x, uint64_t w_qkv, uint32_t m, uint32_t k,
+                           const RopeAppendArgs& a, std::string* err) {
+    const uint32_t D = a.head_dim;
+    const uint64_t n = static_cast<uint64_t>(a.num_q_heads + 2 * a.kv_heads) * D;
+    if (D == 0 || D % 16 != 0 || n % 64 != 0 || a.num_q_heads == 0 || a.kv_heads == 0 ||
+        m != a.batch) {
+        *err = "gemm_bf16_rope_append needs head_dim % 16 == 0, (Hq + 2 Hkv) * head_dim % 64 == 0 "
+               "and one token per sequence";
+        return false;
+    }
+    if (!shape_ok(m, static_cast<uint32_t>(n), k, err)) return false;
+    GemmParams p = base_params(x, w_qkv, m, static_cast<uint32_t>(n), k);
+    p.q_out = reinterpret_cast<uint16_t*>(a.q_out);
+    p.k_base = reinterpret_cast<uint8_t*>(a.k_base);
+    p.v_base = reinterpret_cast<uint8_t*>(a.v_base);
+    p.block_tables = reinterpret_cast<const int32_t*>(a.block_tables);
+    p.seq_lens = reinterpret_cast<const int32_t*>(a.seq_lens);
+    p.offsets_f16 = reinterpret_cast<const uint64_t*>(a.offsets_f16);
+    p.inv_freq = reinterpret_cast<const float*>(a.inv_freq);
+    p.hq = static_cast<int>(a.num_q_heads);
+    p.hkv = static_cast<int>(a.kv_heads);
+    p.D = static_cast<int>(D);
+    p.block_size = static_cast<int>(a.block_size);
+    p.mbps = static_cast<int>(a.mbps);
+    p.row_bytes = static_cast<int>(a.row_bytes);
+    const int splits = splits_for(p.M, p.N, p.K);
+    float* part = nullptr;
+    if (!launch_stream<kEpiRope>(p, splits, false, &part, a.stream, err)) return false;
+    if (splits > 1) return rope_append_from_partials(a, part, splits, err);
+    return true;
 }
 
 }  // namespace dev

@@ -15,16 +15,13 @@
 //    trip through HBM).  HF rotate_half pairing (i, i + D/2), angle =
 //    pos * inv_freq[i], inv_freq supplied by the caller so that any HF
 //    rope_type is served;
-//  * silu_mul: act = bf16(silu(gate) * up) over the fused [gate | up] row.
+//  * silu_mul: act = bf16(bf16(silu(gate)) * up) over the fused [gate | up]
+//    row (F.silu on a bf16 tensor rounds before the multiply).
 #include "../device_api.hpp"
 #include "common.hpp"
 
 namespace kcmm {
 namespace {
-
-__device__ __forceinline__ float bf16_round(float f) {
-    return bf16_bits_to_f32(f32_to_bf16_bits(f));
-}
 
 // 8 bf16 <-> 8 floats
 __device__ __forceinline__ void unpack8(const u32x4& v, float (&f)[8]) {
@@ -50,33 +47,68 @@ __device__ __forceinline__ float block_sum_256(float v, float* red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
-// One row per workgroup; H % 8 == 0.
-__global__ __launch_bounds__(256) void rmsnorm_rows(const uint16_t* __restrict__ x,
+// Sum of the `splits` fp32 partials at pp, pp + MN, ... in split order; up
+// to 8 splits' loads are in flight together.
+__device__ __forceinline__ f32x4 sum_partials(const float* pp, size_t MN, int splits) {
+    f32x4 s = f32x4{0, 0, 0, 0};
+    for (int k0 = 0; k0 < splits; k0 += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            v[k] = *reinterpret_cast<const f32x4*>(pp + static_cast<size_t>(min(k0 + k, splits - 1)) * MN);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k0 + k < splits) s += v[k];
+    }
+    return s;
+}
+
+// One row per workgroup; H % 8 == 0.  FROM_PARTIALS: the row is first
+// finished as the O projection's residual add -- x = bf16(x + bf16(sum of
+// the `splits` fp32 partials [s][rows][H])) -- and written back to x (the
+// hidden state), exactly what the GEMM's residual store would have written.
+template <bool FROM_PARTIALS>
+__global__ __launch_bounds__(256) void rmsnorm_rows(uint16_t* __restrict__ x,
                                                     const uint16_t* __restrict__ w,
-                                                    uint16_t* __restrict__ y, int H, float eps) {
+                                                    uint16_t* __restrict__ y, int H, float eps,
+                                                    const float* __restrict__ part, int splits) {
     __shared__ float red[4];
-    const uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * H;
+    uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * H;
     uint16_t* yr = y + static_cast<size_t>(blockIdx.x) * H;
     float ss = 0.0f;
     for (int i = threadIdx.x * 8; i < H; i += 256 * 8) {
         float f[8];
         unpack8(*reinterpret_cast<const u32x4*>(xr + i), f);
+        if constexpr (FROM_PARTIALS) {
+            const size_t MN = static_cast<size_t>(gridDim.x) * H;
+            const float* pp = part + static_cast<size_t>(blockIdx.x) * H + i;
+            const f32x4 s0 = sum_partials(pp, MN, splits);
+            const f32x4 s1 = sum_partials(pp + 4, MN, splits);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f[j] = bf16_round_f32(bf16_round_f32(s0[j]) + f[j]);
+                f[4 + j] = bf16_round_f32(bf16_round_f32(s1[j]) + f[4 + j]);
+            }
+            *reinterpret_cast<u32x4*>(xr + i) = pack8(f);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
     }
     const float r = 1.0f / sqrtf(block_sum_256(ss, red) / static_cast<float>(H) + eps);
     for (int i = threadIdx.x * 8; i < H; i += 256 * 8) {
         float f[8], g[8];
-        unpack8(*reinterpret_cast<const u32x4*>(xr + i), f);
+        unpack8(*reinterpret_cast<const u32x4*>(xr + i), f);   // (this thread's own writes)
         unpack8(*reinterpret_cast<const u32x4*>(w + i), g);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = g[j] * bf16_round(f[j] * r);
+        for (int j = 0; j < 8; ++j) f[j] = g[j] * bf16_round_f32(f[j] * r);
         *reinterpret_cast<u32x4*>(yr + i) = pack8(f);
     }
 }
 
 struct RopeAppendParams {
-    const uint16_t* qkv;      // [B][(Hq + 2 Hkv) D]
+    const uint16_t* qkv;      // [B][(Hq + 2 Hkv) D] (bf16 source)
+    const float* part;        // [splits][B][(Hq + 2 Hkv) D] (fp32 partials source)
+    int splits;
     uint16_t* q_out;          // [B][Hq][D]
     uint8_t* k_base;
     uint8_t* v_base;
@@ -87,9 +119,14 @@ struct RopeAppendParams {
     int num_q_heads, kv_heads, head_dim, block_size, mbps, row_bytes;
 };
 
-// One workgroup per sequence.  Thread t takes quad iq = t % (D/8) of the
-// D/2 rotation pairs (elements 4iq..4iq+3 and D/2 + 4iq..+3) of heads
-// t / (D/8), + 256/(D/8), ...; its four (cos, sin) pairs serve every head.
+// Workgroup (b, y) handles heads [y*hs, (y+1)*hs) of sequence b's qkv row,
+// hs = 256 / (D/8): thread t takes quad iq = t % (D/8) of the D/2 rotation
+// pairs (elements 4iq..4iq+3 and D/2 + 4iq..+3) of head y*hs + t / (D/8).
+// q and k heads are rotated (into q_out / the token's K page row), v heads
+// copied into the V page row.  FROM_PARTIALS: the qkv row is the split-order
+// sum of the QKV projection's fp32 partials, rounded to bf16 (what the
+// projection's own store writes).
+template <bool FROM_PARTIALS>
 __global__ __launch_bounds__(256) void rope_append_rows(RopeAppendParams p) {
     const int b = blockIdx.x;
     const int L = p.seq_lens[b];
@@ -97,25 +134,30 @@ __global__ __launch_bounds__(256) void rope_append_rows(RopeAppendParams p) {
     const int pos = L - 1;
     if (pos < 0 || pos >= p.mbps * p.block_size) return;   // no token / past the table
     const int quads = D / 8;
+    const int hs = 256 / quads;
     const int iq = threadIdx.x % quads;
-    const int h0 = threadIdx.x / quads;
-    const int hstep = 256 / quads;
-    float cs[4], sn[4];
+    const int hl = threadIdx.x / quads;
+    const int h = blockIdx.y * hs + hl;
+    const int heads = p.num_q_heads + 2 * p.kv_heads;
+    if (hl >= hs || h >= heads) return;                    // (threads past whole heads idle)
+    const int stride = heads * D;
+    const int e1 = h * D + 4 * iq, e2 = e1 + D / 2;
+    // elements e..e+3 of the row (as bf16 values)
+    float x1[4], x2[4];
+    if constexpr (FROM_PARTIALS) {
+        const size_t MN = static_cast<size_t>(gridDim.x) * stride;
+        const float* row = p.part + static_cast<size_t>(b) * stride;
+        const f32x4 s1 = sum_partials(row + e1, MN, p.splits);
+        const f32x4 s2 = sum_partials(row + e2, MN, p.splits);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float ang = static_cast<float>(pos) * p.inv_freq[4 * iq + j];
-        cs[j] = cosf(ang);
-        sn[j] = sinf(ang);
-    }
-    const int lb = pos / p.block_size;
-    const uint64_t page = p.offsets_f16[p.block_tables[static_cast<size_t>(b) * p.mbps + lb]] * 2ull +
-                          static_cast<uint64_t>(pos - lb * p.block_size) * p.row_bytes;
-    const int stride = (p.num_q_heads + 2 * p.kv_heads) * D;
-    const uint16_t* row = p.qkv + static_cast<size_t>(b) * stride;
-    auto rotate = [&](const uint16_t* src, uint16_t* dst) {
-        const u32x2 a = *reinterpret_cast<const u32x2*>(src + 4 * iq);
-        const u32x2 c = *reinterpret_cast<const u32x2*>(src + D / 2 + 4 * iq);
-        float x1[4], x2[4];
+        for (int j = 0; j < 4; ++j) {
+            x1[j] = bf16_round_f32(s1[j]);
+            x2[j] = bf16_round_f32(s2[j]);
+        }
+    } else {
+        const uint16_t* row = p.qkv + static_cast<size_t>(b) * stride;
+        const u32x2 a = *reinterpret_cast<const u32x2*>(row + e1);
+        const u32x2 c = *reinterpret_cast<const u32x2*>(row + e2);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             x1[2 * j] = __uint_as_float(a[j] << 16);
@@ -123,34 +165,46 @@ __global__ __launch_bounds__(256) void rope_append_rows(RopeAppendParams p) {
             x2[2 * j] = __uint_as_float(c[j] << 16);
             x2[2 * j + 1] = __uint_as_float(c[j] & 0xffff0000u);
         }
-        u32x2 o1, o2;
+    }
+    float y1[4], y2[4];
+    if (h < p.num_q_heads + p.kv_heads) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float y0 = x1[2 * j] * cs[2 * j] - x2[2 * j] * sn[2 * j];
-            const float y1 = x1[2 * j + 1] * cs[2 * j + 1] - x2[2 * j + 1] * sn[2 * j + 1];
-            const float z0 = x2[2 * j] * cs[2 * j] + x1[2 * j] * sn[2 * j];
-            const float z1 = x2[2 * j + 1] * cs[2 * j + 1] + x1[2 * j + 1] * sn[2 * j + 1];
-            o1[j] = f32_to_bf16_bits(y0) | (f32_to_bf16_bits(y1) << 16);
-            o2[j] = f32_to_bf16_bits(z0) | (f32_to_bf16_bits(z1) << 16);
+        for (int j = 0; j < 4; ++j) {
+            float cs, sn;
+            rope_cos_sin(pos, p.inv_freq[4 * iq + j], &cs, &sn);
+            y1[j] = rope_first(x1[j], x2[j], cs, sn);
+            y2[j] = rope_second(x1[j], x2[j], cs, sn);
         }
-        *reinterpret_cast<u32x2*>(dst + 4 * iq) = o1;
-        *reinterpret_cast<u32x2*>(dst + D / 2 + 4 * iq) = o2;
-    };
-    const int hq_end = h0 < hstep ? p.num_q_heads : 0;   // (threads past whole head groups idle)
-    const int hk_end = h0 < hstep ? p.kv_heads : 0;
-    for (int h = h0; h < hq_end; h += hstep)
-        rotate(row + h * D, p.q_out + (static_cast<size_t>(b) * p.num_q_heads + h) * D);
-    for (int h = h0; h < hk_end; h += hstep)
-        rotate(row + (p.num_q_heads + h) * D,
-               reinterpret_cast<uint16_t*>(p.k_base + page + static_cast<uint64_t>(h) * D * 2));
-    // v: plain copy of the kv_heads x D row (8 bytes per thread and step)
-    const uint16_t* vsrc = row + (p.num_q_heads + p.kv_heads) * D;
-    uint16_t* vdst = reinterpret_cast<uint16_t*>(p.v_base + page);
-    for (int e = threadIdx.x * 4; e < p.kv_heads * D; e += 256 * 4)
-        *reinterpret_cast<u32x2*>(vdst + e) = *reinterpret_cast<const u32x2*>(vsrc + e);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            y1[j] = x1[j];
+            y2[j] = x2[j];
+        }
+    }
+    uint16_t* dst;
+    if (h < p.num_q_heads) {
+        dst = p.q_out + (static_cast<size_t>(b) * p.num_q_heads + h) * D;
+    } else {
+        const int lb = pos / p.block_size;
+        const uint64_t page = p.offsets_f16[p.block_tables[static_cast<size_t>(b) * p.mbps + lb]] * 2ull +
+                              static_cast<uint64_t>(pos - lb * p.block_size) * p.row_bytes;
+        const bool is_k = h < p.num_q_heads + p.kv_heads;
+        const int kvh = is_k ? h - p.num_q_heads : h - p.num_q_heads - p.kv_heads;
+        dst = reinterpret_cast<uint16_t*>((is_k ? p.k_base : p.v_base) + page +
+                                          static_cast<uint64_t>(kvh) * D * 2);
+    }
+    u32x2 o1, o2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        o1[j] = f32_to_bf16_bits(y1[2 * j]) | (f32_to_bf16_bits(y1[2 * j + 1]) << 16);
+        o2[j] = f32_to_bf16_bits(y2[2 * j]) | (f32_to_bf16_bits(y2[2 * j + 1]) << 16);
+    }
+    *reinterpret_cast<u32x2*>(dst + 4 * iq) = o1;
+    *reinterpret_cast<u32x2*>(dst + D / 2 + 4 * iq) = o2;
 }
 
-// act[m][j] = bf16(silu(gu[m][j]) * gu[m][I + j]); 8 elements per thread.
+// act[m][j] = bf16(bf16(silu(gu[m][j])) * gu[m][I + j]); 8 elements per thread.
 __global__ __launch_bounds__(256) void silu_mul_rows(const uint16_t* __restrict__ gu,
                                                      uint16_t* __restrict__ act, int M, int I) {
     const size_t idx = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
@@ -161,7 +215,7 @@ __global__ __launch_bounds__(256) void silu_mul_rows(const uint16_t* __restrict_
     unpack8(*reinterpret_cast<const u32x4*>(row + j), g);
     unpack8(*reinterpret_cast<const u32x4*>(row + I + j), u);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = g[e] / (1.0f + __expf(-g[e])) * u[e];
+    for (int e = 0; e < 8; ++e) g[e] = swiglu_bf16(g[e], u[e]);
     *reinterpret_cast<u32x4*>(act + idx) = pack8(g);
 }
 
@@ -176,14 +230,32 @@ bool rmsnorm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t rows, uint32_t hi
         *err = "rmsnorm: hidden size must be a positive multiple of 8";
         return false;
     }
-    hipLaunchKernelGGL(rmsnorm_rows, dim3(rows), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
-                       reinterpret_cast<const uint16_t*>(x), reinterpret_cast<const uint16_t*>(w),
-                       reinterpret_cast<uint16_t*>(y), static_cast<int>(hidden), eps);
+    hipLaunchKernelGGL(rmsnorm_rows<false>, dim3(rows), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), reinterpret_cast<uint16_t*>(x),
+                       reinterpret_cast<const uint16_t*>(w), reinterpret_cast<uint16_t*>(y),
+                       static_cast<int>(hidden), eps, nullptr, 0);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     return true;
 }
 
-bool rope_append_bf16(const RopeAppendArgs& a, std::string* err) {
+bool residual_rmsnorm_from_partials(const float* part, int splits, uint64_t hidden, uint64_t w,
+                                    uint64_t y, uint32_t rows, uint32_t H, float eps,
+                                    uint64_t stream, std::string* err) {
+    if (rows == 0) return true;
+    if (H == 0 || H % 8 != 0 || splits < 1) {
+        *err = "residual_rmsnorm: hidden size must be a positive multiple of 8";
+        return false;
+    }
+    hipLaunchKernelGGL(rmsnorm_rows<true>, dim3(rows), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), reinterpret_cast<uint16_t*>(hidden),
+                       reinterpret_cast<const uint16_t*>(w), reinterpret_cast<uint16_t*>(y),
+                       static_cast<int>(H), eps, part, splits);
+    KCMM_HIP_CHECK(hipGetLastError(), err);
+    return true;
+}
+
+namespace {
+bool launch_rope(const RopeAppendArgs& a, const float* part, int splits, std::string* err) {
     if (a.batch == 0) return true;
     if (a.head_dim % 8 != 0 || a.head_dim > 2048) {
         *err = "rope_append: head_dim must be a multiple of 8 (<= 2048)";
@@ -191,6 +263,8 @@ bool rope_append_bf16(const RopeAppendArgs& a, std::string* err) {
     }
     RopeAppendParams p{};
     p.qkv = reinterpret_cast<const uint16_t*>(a.qkv);
+    p.part = part;
+    p.splits = splits;
     p.q_out = reinterpret_cast<uint16_t*>(a.q_out);
     p.k_base = reinterpret_cast<uint8_t*>(a.k_base);
     p.v_base = reinterpret_cast<uint8_t*>(a.v_base);
@@ -204,10 +278,26 @@ bool rope_append_bf16(const RopeAppendArgs& a, std::string* err) {
     p.block_size = static_cast<int>(a.block_size);
     p.mbps = static_cast<int>(a.mbps);
     p.row_bytes = static_cast<int>(a.row_bytes);
-    hipLaunchKernelGGL(rope_append_rows, dim3(a.batch), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(a.stream), p);
+    const uint32_t hs = 256 / (a.head_dim / 8);
+    const dim3 grid(a.batch, (a.num_q_heads + 2 * a.kv_heads + hs - 1) / hs);
+    if (part != nullptr)
+        hipLaunchKernelGGL(rope_append_rows<true>, grid, dim3(256), 0,
+                           reinterpret_cast<hipStream_t>(a.stream), p);
+    else
+        hipLaunchKernelGGL(rope_append_rows<false>, grid, dim3(256), 0,
+                           reinterpret_cast<hipStream_t>(a.stream), p);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     return true;
+}
+}  // namespace
+
+bool rope_append_bf16(const RopeAppendArgs& a, std::string* err) {
+    return launch_rope(a, nullptr, 1, err);
+}
+
+bool rope_append_from_partials(const RopeAppendArgs& a, const float* part, int splits,
+                               std::string* err) {
+    return launch_rope(a, part, splits, err);
 }
 
 bool silu_mul_bf16(uint64_t gate_up, uint64_t act, uint32_t rows, uint32_t inter,

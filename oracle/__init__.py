@@ -396,5 +396,6 @@ def decode_layer_step_f64(hidden_bits, w, k_region, v_region, block_tables, seq_
     h1 = rnd(x + rnd(att @ f("o").T))
     n2 = rmsnorm_f64(h1, f("mlp_norm"), eps, round_bf16)
     gu = rnd(n2 @ f("gate_up").T)
-    act = rnd(silu_mul_f64(gu[:, :intermediate], gu[:, intermediate:]))
+    g = gu[:, :intermediate]
+    act = rnd(rnd(g / (1.0 + np.exp(-g))) * gu[:, intermediate:])   # F.silu rounds, then * up
     return rnd(h1 + rnd(act @ f("down").T))

@@ -83,6 +83,25 @@ bool rope_append_bf16(const RopeAppendArgs&, std::string* err) { return no_devic
 bool silu_mul_bf16(uint64_t, uint64_t, uint32_t, uint32_t, uint64_t, std::string* err) {
     return no_device(err);
 }
+bool gemm_bf16_rope_append(uint64_t, uint64_t, uint32_t, uint32_t, const RopeAppendArgs&,
+                           std::string* err) {
+    return no_device(err);
+}
+bool gemm_bf16_swiglu(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t,
+                      std::string* err) {
+    return no_device(err);
+}
+bool gemm_bf16_partials(uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, float**, int*,
+                        std::string* err) {
+    return no_device(err);
+}
+bool rope_append_from_partials(const RopeAppendArgs&, const float*, int, std::string* err) {
+    return no_device(err);
+}
+bool residual_rmsnorm_from_partials(const float*, int, uint64_t, uint64_t, uint64_t, uint32_t,
+                                    uint32_t, float, uint64_t, std::string* err) {
+    return no_device(err);
+}
 
 }  // namespace dev
 }  // namespace kcmm

@@ -66,7 +66,8 @@ def test_silu_mul(gpu_lib, rows, inter):
     torch.cuda.synchronize()
     got = O.decode(O.BF16, bits_of(ad)).astype(np.float64)
     g = O.decode(O.BF16, gu).astype(np.float64)
-    ref = O.bf16_round(O.silu_mul_f64(g[:, :inter], g[:, inter:]))
+    gate = g[:, :inter]
+    ref = O.bf16_round(O.bf16_round(gate / (1.0 + np.exp(-gate))) * g[:, inter:])
     assert within_ulp(got, ref)
 
 
@@ -157,11 +158,13 @@ def _layer_weights(torch, rng, h, inter, hq, hkv, d):
     return w, dev, lw
 
 
-@pytest.mark.parametrize("hq,hkv,d,h,inter", [(8, 2, 64, 512, 768), (32, 8, 128, 4096, 1024)])
+@pytest.mark.parametrize("hq,hkv,d,h,inter", [(8, 2, 64, 512, 768), (32, 8, 128, 4096, 1024),
+                                               (32, 8, 72, 512, 768)])
 def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter):
     """One decoder layer through kcmm_decode_layer_step_on_stream vs the
     oracle's bf16 layer (RMSNorm, QKV, RoPE + append, paged attention,
-    O + residual, RMSNorm, gate/up, SiLU*up, down + residual)."""
+    O + residual, RMSNorm, gate/up, SiLU*up, down + residual).  head_dim 72
+    takes the unfused QKV path (projection, then the RoPE/append kernel)."""
     import torch
     lens = [1, 16, 17, 130]
     case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
@@ -236,3 +239,46 @@ def test_layer_step_rejects_bad_shapes(gpu_lib):
                                         max_blocks_per_seq=case.mbps, rms_eps=1e-5)
     finally:
         case.pool.destroy()
+
+
+@pytest.mark.parametrize("hq,hkv,d,h,inter", [(32, 8, 128, 4096, 1024), (8, 2, 64, 512, 768)])
+def test_decode_layers_matches_layer_steps(gpu_lib, hq, hkv, d, h, inter):
+    """Three layers in one kcmm_decode_layers_on_stream call give the bits of
+    three kcmm_decode_layer_step_on_stream calls: hidden state and every
+    byte of the three layers' K/V regions."""
+    import torch
+    lens = [1, 16, 17, 130]
+    nl = 3
+    res = []
+    for one_call in (False, True):
+        case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                                 block_size=16, ctx_lens=lens, dtype=KV_BF16, seed=h,
+                                 num_layers=nl)
+        try:
+            rng = np.random.default_rng(5)
+            ws = [_layer_weights(torch, rng, h, inter, hq, hkv, d) for _ in range(nl)]
+            hid = O.encode(O.BF16, np.random.default_rng(6).standard_normal((len(lens), h)))
+            hd = bf16_dev(torch, hid)
+            invd = torch.from_numpy(O.default_inv_freq(500000.0, d).astype(np.float32)).cuda()
+            dv = case.dev
+            kw = dict(hidden_ptr=hd.data_ptr(), block_tables_ptr=dv["bt"].data_ptr(),
+                      seq_lens_ptr=dv["sl"].data_ptr(), block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                      inv_freq_ptr=invd.data_ptr(), batch=len(lens), hidden_size=h,
+                      num_q_heads=hq, intermediate_size=inter, max_blocks_per_seq=case.mbps,
+                      rms_eps=1e-5)
+            if one_call:
+                case.pool.decode_layers(first_layer=0, weights=[w[2] for w in ws], **kw)
+            else:
+                for layer in range(nl):
+                    case.pool.decode_layer_step(layer_idx=layer, weights=ws[layer][2], **kw)
+            torch.cuda.synchronize()
+            mb = case.geometry["mapped_bytes"]
+            regions = [memcpy_dtoh(case.pool.va_k(l), mb) for l in range(nl)] + \
+                      [memcpy_dtoh(case.pool.va_v(l), mb) for l in range(nl)]
+            res.append((bits_of(hd), regions))
+        finally:
+            case.pool.destroy()
+    assert np.isfinite(O.decode(O.BF16, res[1][0])).all()
+    assert np.array_equal(res[0][0], res[1][0])
+    for a, b in zip(res[0][1], res[1][1]):
+        assert np.array_equal(a, b)
