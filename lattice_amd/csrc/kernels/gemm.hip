@@ -28,9 +28,6 @@
 #include "../device_api.hpp"
 #include "common.hpp"
 
-#ifndef KCMM_GEMM_BUFFER_LOADS
-#define KCMM_GEMM_BUFFER_LOADS 0
-#endif
 
 namespace kcmm {
 namespace {
@@ -63,16 +60,6 @@ __device__ __forceinline__ void fix_lines(u32x4& x, u32x4& y, bool low8) {
 
 __device__ __forceinline__ u32x4 load_stream(const uint8_t* a) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a));
-}
-
-// Buffer resources: the range check makes rows past M read as zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                             static_cast<int>(bytes), 0x00020000);
-}
-template <int POLICY>   // 2: streaming
-__device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POLICY));
 }
 
 __device__ __forceinline__ u32x2 pack4_bf16(f32x4 v) {
@@ -113,180 +100,13 @@ struct GemmParams {
     int hq, hkv, D, block_size, mbps, row_bytes;
 };
 
-// Weight-streaming GEMM.  Workgroup = 4 waves = 64 weight rows (16 per wave)
-// x up to 16*MB tokens x one K split of `klen`, walked in chunks of KCH:
-//  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
-//    whole-line streaming loads (8 rows x 128 B per instruction) and is put
-//    into MFMA A layout by fix_lines, one line at a time; chunk c+1 is in
-//    flight while chunk c is consumed, so every weight byte is read once and
-//    never touches LDS;
-//  * the activation chunk (M x KCH) is staged in LDS, double-buffered, laid
-//    out so that B-operand reads are conflict-free; one barrier per chunk;
-//  * activation rows past M are clamped or read as zero (their outputs are
-//    never stored).
-// (Measured alternatives that were not faster at the Llama-3-8B decode
-// shapes: a persistent grid over (row block, k chunk) tiles with a 6-deep
-// ring; direct-to-LDS activation loads with a 3-deep weight ring; 8-wave
-// workgroups at 2 or 4 waves per SIMD; summing the split partials inside
-// this kernel by the last workgroup of each tile, whose coherent stores and
-// arrival count put several memory round trips on every tile's tail.)
-template <int MB, int KCH, int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void gemm_bf16_stream(GemmParams p) {
-    constexpr int NT = 256;
-    constexpr int LINES = KCH / 64;          // 128-byte lines per weight row per chunk
-    constexpr int KC = KCH / 32;             // MFMA k-steps per chunk
-    constexpr int PIECES = KCH / 8;          // 16-byte pieces per activation row
-    constexpr int MROWS = 16 * MB;
-    constexpr int XLOADS = MROWS * PIECES / NT;
-    constexpr int XROWSTEP = NT / PIECES;    // activation rows per load round
-    static_assert(XLOADS * NT == MROWS * PIECES, "activation chunk must split over the threads");
-    constexpr bool BUF = KCMM_GEMM_BUFFER_LOADS != 0;
-    // LDS row: padded by 16 bytes (buffer form) or XOR-swizzled pieces
-    constexpr int ROWB = BUF ? (PIECES + 1) * 16 : PIECES * 16;
-    constexpr int XBUF = MROWS * ROWB;
-    __shared__ __attribute__((aligned(16))) uint8_t xs[2 * XBUF];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ln = lane & 15, lg = lane >> 4;
-    const bool low8 = ln < 8;
-    const int K = p.K;
-    const int m_base = blockIdx.z * MROWS;
-    const int kbeg = blockIdx.y * p.klen;
-    const int nchunks = p.klen / KCH;
-    const uint32_t rowb = static_cast<uint32_t>(K) * 2;
-
-    // weight rows of this wave: rowA + 0..7 (MFMA rows 0..7), rowB + 0..7 (8..15)
-    const int gw = blockIdx.x * 4 + wave;
-    int rowA, rowB;
-    if constexpr (EPI == kEpiRope) {
-        const int wph = p.D / 16;            // waves per head: 8 rotation pairs each
-        const int head = gw / wph;
-        rowA = head * p.D + (gw - head * wph) * 8;
-        rowB = rowA + p.D / 2;
-    } else if constexpr (EPI == kEpiSwiglu) {
-        rowA = gw * 8;
-        rowB = p.N / 2 + gw * 8;
-    } else {
-        rowA = gw * 16;
-        rowB = rowA + 8;
-    }
-
-    const uint32_t piece = ((ln >> 3) * 4 + lg) * 16;
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.W, static_cast<uint32_t>(p.N) * rowb);
-    const uint32_t wv0 = (rowA + (ln & 7)) * rowb + piece;
-    const uint32_t wv1 = (rowB + (ln & 7)) * rowb + piece;
-    const uint8_t* wp0 = reinterpret_cast<const uint8_t*>(p.W) + wv0 + static_cast<size_t>(kbeg) * 2;
-    const uint8_t* wp1 = reinterpret_cast<const uint8_t*>(p.W) + wv1 + static_cast<size_t>(kbeg) * 2;
-    auto load_w = [&](u32x4* dst, int c) {
-#pragma unroll
-        for (int c2 = 0; c2 < LINES; ++c2) {
-            if constexpr (BUF) {
-                const uint32_t so = static_cast<uint32_t>(kbeg + c * KCH) * 2 + c2 * 128;
-                dst[2 * c2] = bload<2>(wr, wv0, so);
-                dst[2 * c2 + 1] = bload<2>(wr, wv1, so);
-            } else {
-                const size_t o = static_cast<size_t>(c) * KCH * 2 + c2 * 128;
-                dst[2 * c2] = load_stream(wp0 + o);
-                dst[2 * c2 + 1] = load_stream(wp1 + o);
-            }
-        }
-    };
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.X, static_cast<uint32_t>(p.M) * rowb);
-    u32x4 xr[XLOADS];
-    auto load_x = [&](int c) {
-#pragma unroll
-        for (int i = 0; i < XLOADS; ++i) {
-            const int r = m_base + tid / PIECES + i * XROWSTEP;
-            if constexpr (BUF) {
-                // the row lives in the lane offset, which the range check covers
-                xr[i] = bload<0>(xrs, r * rowb + (tid % PIECES) * 16 + kbeg * 2,
-                                 static_cast<uint32_t>(c) * KCH * 2);
-            } else {
-                const int m = min(r, p.M - 1);
-                xr[i] = *reinterpret_cast<const u32x4*>(p.X + static_cast<size_t>(m) * K + kbeg +
-                                                        c * KCH + (tid % PIECES) * 8);
-            }
-        }
-    };
-    auto store_x = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < XLOADS; ++i) {
-            const int r = tid / PIECES + i * XROWSTEP, pc = tid % PIECES;
-            const int off = BUF ? r * ROWB + pc * 16 : r * ROWB + ((pc ^ (r & (PIECES - 1))) * 16);
-            *reinterpret_cast<u32x4*>(xs + buf * XBUF + off) = xr[i];
-        }
-    };
-
-    f32x4 acc[MB];
-#pragma unroll
-    for (int j = 0; j < MB; ++j) acc[j] = f32x4{0, 0, 0, 0};
-
-    auto compute = [&](u32x4* wa, int buf) {
-#pragma unroll
-        for (int c2 = 0; c2 < LINES; ++c2) {
-            fix_lines(wa[2 * c2], wa[2 * c2 + 1], low8);
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int kc = 2 * c2 + kk;
-                const int pc = 4 * kc + lg;
-                u32x4 b[MB];
-#pragma unroll
-                for (int j = 0; j < MB; ++j) {
-                    const int r = 16 * j + ln;
-                    const int off = BUF ? r * ROWB + pc * 16 : r * ROWB + ((pc ^ (r & (PIECES - 1))) * 16);
-                    b[j] = *reinterpret_cast<const u32x4*>(xs + buf * XBUF + off);
-                }
-#pragma unroll
-                for (int j = 0; j < MB; ++j)
-                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8, wa[kc]), __builtin_bit_cast(bf16x8, b[j]), acc[j],
-                        0, 0, 0);
-            }
-        }
-        (void)KC;
-    };
-
-    u32x4 wa0[2 * LINES], wa1[2 * LINES];
-    load_x(0);
-    load_w(wa0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    store_x(0);
-    __syncthreads();
-    // one chunk: loads of chunk c+1 (when MORE) are issued before chunk c is consumed
-    auto step = [&](u32x4* now, u32x4* later, int buf, int c, auto more_tag) {
-        constexpr bool MORE = decltype(more_tag)::value;
-        if constexpr (MORE) {
-            load_x(c + 1);
-            load_w(later, c + 1);
-        }
-        // keep the compiler from sinking these loads below the chunk's math
-        __builtin_amdgcn_sched_barrier(0);
-        compute(now, buf);
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (MORE) {
-            store_x(buf ^ 1);
-            __syncthreads();
-        }
-    };
-    using More = std::integral_constant<bool, true>;
-    using Last = std::integral_constant<bool, false>;
-    int c = 0;
-    for (; c + 2 < nchunks; c += 2) {
-        step(wa0, wa1, 0, c, More{});
-        step(wa1, wa0, 1, c + 1, More{});
-    }
-    if (c + 1 < nchunks) {
-        step(wa0, wa1, 0, c, More{});
-        step(wa1, wa0, 1, c + 1, Last{});
-    } else {
-        step(wa0, wa1, 0, c, Last{});
-    }
-
-    // acc[j][r] = output (token m_base + 16j + ln, wave row 4lg + r): weight
-    // row (lg < 2 ? rowA : rowB) + cw + r
+// The store of one wave's 16 weight rows x 16*MB tokens: acc[j][r] = output
+// (token m_base + 16j + ln, wave row 4lg + r), wave rows 0..7 = weight rows
+// rowA + 0..7 and 8..15 = rowB + 0..7.  With p.part set: fp32 partials of
+// split blockIdx.y, else the EPI epilogue.
+template <int MB, int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x4 (&acc)[MB], int rowA,
+                                              int rowB, int m_base, int ln, int lg) {
     const bool hi = lg >= 2;
     const int cw = 4 * (lg & 1);
     if (p.part != nullptr) {
@@ -375,6 +195,167 @@ void gemm_bf16_stream(GemmParams p) {
             *reinterpret_cast<u32x2*>(dst) = pack4_bf16(out);
         }
     }
+}
+
+// Weight-streaming GEMM.  Workgroup = 4 waves = 64 weight rows (16 per wave)
+// x up to 16*MB tokens x one K split of `klen`, walked in chunks of KCH:
+//  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
+//    whole-line streaming loads (8 rows x 128 B per instruction) and is put
+//    into MFMA A layout by fix_lines, one line at a time; chunk c+1 is in
+//    flight while chunk c is consumed, so every weight byte is read once and
+//    never touches LDS;
+//  * the activation chunk (M x KCH) is staged in LDS, double-buffered, 16-byte
+//    pieces XOR-swizzled by row so that B-operand reads are conflict-free;
+//    one barrier per chunk;
+//  * activation rows past M are clamped (their outputs are never stored).
+// (Measured alternatives that were not faster at the Llama-3-8B decode
+// shapes: a persistent grid over (row block, k chunk) tiles with a 6-deep
+// ring; direct-to-LDS activation loads with a 3-deep weight ring; a 3-deep
+// register weight ring (two chunks always in flight); buffer loads with
+// padded LDS rows; 8-wave workgroups at 2 or 4 waves per SIMD; waves that
+// each take a quarter of every chunk's k range over all 64 rows (no LDS
+// staging or per-chunk barrier, but a row's lines are then read by four
+// drifting waves: 20% slower); summing the split partials inside this kernel
+// by the last workgroup of each tile, whose coherent stores and arrival count
+// put several memory round trips on every tile's tail.)
+template <int MB, int KCH, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_bf16_stream(GemmParams p) {
+    constexpr int NT = 256;
+    constexpr int LINES = KCH / 64;          // 128-byte lines per weight row per chunk
+    constexpr int KC = KCH / 32;             // MFMA k-steps per chunk
+    constexpr int PIECES = KCH / 8;          // 16-byte pieces per activation row
+    constexpr int MROWS = 16 * MB;
+    constexpr int XLOADS = MROWS * PIECES / NT;
+    constexpr int XROWSTEP = NT / PIECES;    // activation rows per load round
+    static_assert(XLOADS * NT == MROWS * PIECES, "activation chunk must split over the threads");
+    constexpr int ROWB = PIECES * 16;         // LDS row; 16-byte pieces XOR-swizzled by row
+    constexpr int XBUF = MROWS * ROWB;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2 * XBUF];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ln = lane & 15, lg = lane >> 4;
+    const bool low8 = ln < 8;
+    const int K = p.K;
+    const int m_base = blockIdx.z * MROWS;
+    const int kbeg = blockIdx.y * p.klen;
+    const int nchunks = p.klen / KCH;
+    const uint32_t rowb = static_cast<uint32_t>(K) * 2;
+
+    // weight rows of this wave: rowA + 0..7 (MFMA rows 0..7), rowB + 0..7 (8..15)
+    const int gw = blockIdx.x * 4 + wave;
+    int rowA, rowB;
+    if constexpr (EPI == kEpiRope) {
+        const int wph = p.D / 16;            // waves per head: 8 rotation pairs each
+        const int head = gw / wph;
+        rowA = head * p.D + (gw - head * wph) * 8;
+        rowB = rowA + p.D / 2;
+    } else if constexpr (EPI == kEpiSwiglu) {
+        rowA = gw * 8;
+        rowB = p.N / 2 + gw * 8;
+    } else {
+        rowA = gw * 16;
+        rowB = rowA + 8;
+    }
+
+    const uint32_t piece = ((ln >> 3) * 4 + lg) * 16;
+    const uint8_t* wp0 = reinterpret_cast<const uint8_t*>(p.W) + (rowA + (ln & 7)) * static_cast<size_t>(rowb) +
+                         piece + static_cast<size_t>(kbeg) * 2;
+    const uint8_t* wp1 = reinterpret_cast<const uint8_t*>(p.W) + (rowB + (ln & 7)) * static_cast<size_t>(rowb) +
+                         piece + static_cast<size_t>(kbeg) * 2;
+    auto load_w = [&](u32x4* dst, int c) {
+#pragma unroll
+        for (int c2 = 0; c2 < LINES; ++c2) {
+            const size_t o = static_cast<size_t>(c) * KCH * 2 + c2 * 128;
+            dst[2 * c2] = load_stream(wp0 + o);
+            dst[2 * c2 + 1] = load_stream(wp1 + o);
+        }
+    };
+    u32x4 xr[XLOADS];
+    auto load_x = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < XLOADS; ++i) {
+            const int m = min(m_base + tid / PIECES + i * XROWSTEP, p.M - 1);
+            xr[i] = *reinterpret_cast<const u32x4*>(p.X + static_cast<size_t>(m) * K + kbeg + c * KCH +
+                                                    (tid % PIECES) * 8);
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XLOADS; ++i) {
+            const int r = tid / PIECES + i * XROWSTEP, pc = tid % PIECES;
+            *reinterpret_cast<u32x4*>(xs + buf * XBUF + r * ROWB + ((pc ^ (r & (PIECES - 1))) * 16)) = xr[i];
+        }
+    };
+
+    f32x4 acc[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) acc[j] = f32x4{0, 0, 0, 0};
+
+    auto compute = [&](u32x4* wa, int buf) {
+#pragma unroll
+        for (int c2 = 0; c2 < LINES; ++c2) {
+            fix_lines(wa[2 * c2], wa[2 * c2 + 1], low8);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int kc = 2 * c2 + kk;
+                const int pc = 4 * kc + lg;
+                u32x4 b[MB];
+#pragma unroll
+                for (int j = 0; j < MB; ++j) {
+                    const int r = 16 * j + ln;
+                    b[j] = *reinterpret_cast<const u32x4*>(xs + buf * XBUF + r * ROWB +
+                                                           ((pc ^ (r & (PIECES - 1))) * 16));
+                }
+#pragma unroll
+                for (int j = 0; j < MB; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, wa[kc]), __builtin_bit_cast(bf16x8, b[j]), acc[j],
+                        0, 0, 0);
+            }
+        }
+        (void)KC;
+    };
+
+    u32x4 wa0[2 * LINES], wa1[2 * LINES];
+    load_x(0);
+    load_w(wa0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    store_x(0);
+    __syncthreads();
+    // one chunk: loads of chunk c+1 (when MORE) are issued before chunk c is consumed
+    auto step = [&](u32x4* now, u32x4* later, int buf, int c, auto more_tag) {
+        constexpr bool MORE = decltype(more_tag)::value;
+        if constexpr (MORE) {
+            load_x(c + 1);
+            load_w(later, c + 1);
+        }
+        // keep the compiler from sinking these loads below the chunk's math
+        __builtin_amdgcn_sched_barrier(0);
+        compute(now, buf);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MORE) {
+            store_x(buf ^ 1);
+            __syncthreads();
+        }
+    };
+    using More = std::integral_constant<bool, true>;
+    using Last = std::integral_constant<bool, false>;
+    int c = 0;
+    for (; c + 2 < nchunks; c += 2) {
+        step(wa0, wa1, 0, c, More{});
+        step(wa1, wa0, 1, c + 1, More{});
+    }
+    if (c + 1 < nchunks) {
+        step(wa0, wa1, 0, c, More{});
+        step(wa1, wa0, 1, c + 1, Last{});
+    } else {
+        step(wa0, wa1, 0, c, Last{});
+    }
+
+    gemm_epilogue<MB, EPI>(p, acc, rowA, rowB, m_base, ln, lg);
 }
 
 // Y = bf16(sum over splits of the fp32 partials) (+ R); 4 outputs per thread.
