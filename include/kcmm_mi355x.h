@@ -148,7 +148,7 @@ int kcmm_gemm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
                              uint64_t stream_ptr);
 
 /** Y = R + X * W^T: the O / down projections with the residual add of ref
- *  llama_transformer.rs:358,377 (add.cu) in the GEMM's store.  The product
+ *  llama_transformer.rs:358-360,377-379 (add.cu) in the GEMM's store.  The product
  *  is rounded to bf16 before the add, as a bf16 model computes it; R may be
  *  the same buffer as Y.  Same shape rules as kcmm_gemm_bf16_on_stream. */
 int kcmm_gemm_bf16_add_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t residual_ptr,
@@ -163,7 +163,7 @@ int kcmm_gemm_bf16_add_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t residu
  * device addresses aligned to 16 bytes. */
 
 /** The O projection with its residual add and the post-attention RMSNorm
- *  (ref llama_transformer.rs:355-364: o GEMM, add.cu, rms_norm.cu):
+ *  (ref llama_transformer.rs:356-362: o GEMM, add.cu, rms_norm.cu):
  *  hidden = bf16(hidden + bf16(x * w^T)) in place ([m][n]), then normed =
  *  rmsnorm(hidden) with weight norm_w.  Bit-identical to
  *  kcmm_gemm_bf16_add_on_stream followed by kcmm_rmsnorm_bf16_on_stream; the
@@ -188,7 +188,7 @@ int kcmm_silu_mul_bf16_on_stream(uint64_t gate_up_ptr, uint64_t act_ptr, uint32_
                                  uint32_t intermediate, uint64_t stream_ptr);
 
 /** The gate/up projection with SwiGLU in its store (ref
- *  llama_transformer.rs:365-375: gate and up GEMMs, silu_mul.cu): act[m][j]
+ *  llama_transformer.rs:370-375: gate and up GEMMs, silu_mul.cu): act[m][j]
  *  = bf16(bf16(silu(G)) * U) with G, U the bf16-rounded projections
  *  x * w[j]^T and x * w[intermediate + j]^T; w_gate_up = [gate rows; up
  *  rows], [2 intermediate][k].  Bit-identical to kcmm_gemm_bf16_on_stream
@@ -216,7 +216,7 @@ int kcmm_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, uint6
                                     uint64_t stream_ptr);
 
 /** The QKV projection of a decode step with RoPE and the KV append in its
- *  store (ref llama_transformer.rs:300-340: q/k/v GEMMs, rope.cu, the cache
+ *  store (ref llama_transformer.rs:315-333: q/k/v GEMMs, rope.cu, the cache
  *  write): x_ptr [batch][hidden] times w_qkv_ptr [(Hq + 2 Hkv) head_dim]
  *  [hidden] (q rows, k rows, v rows), each product rounded to bf16 and then
  *  treated exactly as kcmm_rope_append_bf16_on_stream treats a qkv row, so
