@@ -53,6 +53,7 @@ MODEL_LAYERS = 32
 HIDDEN, INTER = 4096, 14336
 KV_BF16_CODE = 1
 ROPE_THETA, RMS_EPS = 500000.0, 1e-5      # Llama-3-8B config.json
+BEAM_WIDTH = 4                             # configs[4]
 GEMMS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
 
 
@@ -307,6 +308,25 @@ def main():
     names = ["norm1", "qkv", "rope_append", "attn", "o", "norm2", "gate_up", "silu", "down"]
     if args.attn_only:
         names = ["append", "attn"]
+    beam = {"children": [], "copies": 0}
+    if args.config == "cfg5":
+        # beam search, width 4: every step each of the B sequences is forked
+        # into 3 more beams whose last partial page is made private (one
+        # host call, one page-copy kernel) before the step's append/attention
+        parents = list(range(B))
+
+        def beam_fork(_):
+            children, ncopy = case.pool.fork_beams(parents, BEAM_WIDTH, stream_ptr=sp)
+            beam["children"].extend(children)
+            beam["copies"] = ncopy
+
+        calls["beam_fork"] = beam_fork
+        names = ["beam_fork", "append", "attn"]
+
+    def release_beams():
+        for c in beam["children"]:
+            case.pool.unregister_sequence(c)
+        beam["children"] = []
 
     if args.calib_copy:
         src = torch.empty(128 << 20, dtype=torch.int16, device=dev)
@@ -319,6 +339,7 @@ def main():
     for i in range(args.warmup):
         for n in names:
             calls[n](i % args.layers)
+        release_beams()
     torch.cuda.synchronize()
     log(f"warmup done ({args.warmup} steps)")
 
@@ -332,6 +353,7 @@ def main():
         for j, n in enumerate(names):
             calls[n](layer)
             ev[i][j + 1].record(stream)
+        release_beams()                              # pruned beams (between steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
     per = {n: np.mean([ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(args.steps)])
@@ -358,6 +380,26 @@ def main():
             extra[label] = float(np.mean([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]))
         log(f"layer step (one call) ms={extra['layer_step']:.4f}, append ms={extra['append']:.4f}, "
             f"32-layer decode step ms={extra['decode_step']:.4f}")
+        # the projections at M = 256 tokens (configs[3]'s second size), same weights
+        m256 = {}
+        x256 = {k: torch.randn((256, k), generator=g, device=dev).to(torch.bfloat16)
+                for k in (HIDDEN, INTER)}
+        y256 = torch.empty((256, 2 * INTER), dtype=torch.bfloat16, device=dev)
+        for name, n, k in GEMMS:
+            fn = lambda l, n=n, k=k, name=name: lib.gemm_bf16(
+                x256[k].data_ptr(), W(l, name), y256.data_ptr(), 256, n, k, sp)
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+            for i in range(min(args.warmup, args.steps)):
+                fn(i)
+            torch.cuda.synchronize()
+            for i in range(args.steps):
+                evs[i].record(stream)
+                fn(i)
+            evs[-1].record(stream)
+            torch.cuda.synchronize()
+            m256[name] = float(np.mean([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]))
+        del x256, y256
+        log("M=256 GEMM ms: " + ", ".join(f"{k}={v:.4f}" for k, v in m256.items()))
         assert torch.isfinite(hidden.float()).all(), "layer step produced non-finite hidden state"
 
     attn_s = per["attn"] / 1e3
@@ -378,7 +420,8 @@ def main():
         "config": {"workload": ("llama3-8b-shape decode layer-step: RMSNorm, QKV GEMM, RoPE + KV "
                                 "append, paged attention, O GEMM + residual, RMSNorm, gate_up "
                                 "GEMM, SiLU*up, down GEMM + residual") if args.config == "cfg2" else
-                               "cfg5: fp8-e4m3 paged decode attention + KV append, long-tail ctx",
+                               "cfg5: beam-width-4 CoW fork of the last partial page + KV append "
+                               "+ fp8-e4m3 paged decode attention, long-tail ctx",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "block_size": BS,
                    "ctx": f"U[{CTX_LO},{CTX_HI}]+1" if args.config == "cfg2" else
                           "80% U[1024,8192] + 20% U[16384,32768], +1",
@@ -390,12 +433,22 @@ def main():
         "kv_bytes_per_layer_step": kv_bytes,
         "roofline": {"bound": "hbm", "achieved": round(kv_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kv_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(),
+                     # counter-measured HBM bytes exist for the Cfg2 call only
+                     "traffic": measured_traffic() if args.config == "cfg2" else None,
                      "kernel": "paged decode attention call (attn_decode_stream + attn_decode_merge)",
                      "algorithmic_bytes": kv_bytes},
         "append_us": round((per["append"] if args.attn_only else extra["append"]) * 1e3, 2),
         "wall_s_timed": round(wall, 3),
     }
+    if args.config == "cfg5":
+        g = case.geometry
+        result["beam_fork_us"] = round(per["beam_fork"] * 1e3, 2)
+        result["beam_fork"] = {"beam_width": BEAM_WIDTH, "parents": B,
+                               "cow_pages_per_step": beam["copies"],
+                               "cow_copy_bytes_per_step": beam["copies"] * 2 * args.layers *
+                               g["block_bytes"],
+                               "note": "host fork/CoW bookkeeping + one page-copy kernel, "
+                                       "HIP events around the call"}
     if not args.attn_only:
         t_step_s = extra["decode_step"] / 1e3
         result["decode_tokens_per_s"] = round(B / t_step_s, 1)
@@ -403,18 +456,23 @@ def main():
         result["t_layer_us"] = round(t_step_s / MODEL_LAYERS * 1e6, 2)
         result["t_layer_single_call_us"] = round(extra["layer_step"] * 1e3, 2)
         result["t_layer_components_us"] = {n: round(per[n] * 1e3, 2) for n in names}
-        gem = {}
-        for name, n, k in GEMMS:
-            s = per[name] / 1e3
-            flops = 2.0 * B * n * k
-            # W, X and Y; O and down also read the residual they add
-            byts = 2.0 * (n * k + B * k + B * n * (2 if name in ("o", "down") else 1))
-            ceiling = min(BF16_PEAK_TFLOPS * 1e12, HBM_PEAK_GBS * 1e9 * flops / byts)
-            gem[name] = {"us": round(per[name] * 1e3, 2), "tflops": round(flops / s / 1e12, 1),
-                         "gbs": round(byts / s / 1e9, 1),
-                         "frac_of_min_roofline": round(flops / s / ceiling, 4),
-                         "frac_of_mfma_peak": round(flops / s / (BF16_PEAK_TFLOPS * 1e12), 4)}
-        result["gemm_m64"] = gem
+        def gemm_report(times_ms, M, residual):
+            gem = {}
+            for name, n, k in GEMMS:
+                s = times_ms[name] / 1e3
+                flops = 2.0 * M * n * k
+                # W, X and Y; with a residual store O and down also read it
+                res = 2 if residual and name in ("o", "down") else 1
+                byts = 2.0 * (n * k + M * k + M * n * res)
+                ceiling = min(BF16_PEAK_TFLOPS * 1e12, HBM_PEAK_GBS * 1e9 * flops / byts)
+                gem[name] = {"us": round(times_ms[name] * 1e3, 2),
+                             "tflops": round(flops / s / 1e12, 1),
+                             "gbs": round(byts / s / 1e9, 1),
+                             "frac_of_min_roofline": round(flops / s / ceiling, 4),
+                             "frac_of_mfma_peak": round(flops / s / (BF16_PEAK_TFLOPS * 1e12), 4)}
+            return gem
+        result["gemm_m64"] = gemm_report(per, B, True)
+        result["gemm_m256"] = gemm_report(m256, 256, False)
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))
         log(f"cpu baseline on {threads} threads ...")

@@ -129,6 +129,21 @@ int kcmm_cow_block_for_append(kcmm_pool_t *pool, uint32_t seq_idx,
 int kcmm_copy_blocks_on_stream(kcmm_pool_t *pool, const uint32_t *src_dst,
                                uint32_t num_pairs, uint64_t stream_ptr);
 
+/** Beam-search fork of one decode step in one call (the vLLM block manager's
+ *  fork + copy-on-write + copy_blocks, patch_vllm.py:1083-1101; ref
+ *  sharing.rs:24-65 leaves it a placeholder).  Each parents[i] gets
+ *  beam_width - 1 children (written to children_out, parent-major) that
+ *  share its pages; each child's page for its next token (logical block
+ *  seq_len / block_size, when already allocated) is made private as
+ *  kcmm_cow_block_for_append does, in the same order as the separate calls
+ *  (fork child, CoW child, next child), and all the page copies (every
+ *  layer's K and V) are enqueued on stream_ptr in one kernel.  The parent
+ *  keeps the original page, private again once its children have copied.
+ *  Returns the number of pages copied, or -1. */
+int kcmm_fork_beams_on_stream(kcmm_pool_t *pool, const uint32_t *parents, uint32_t n_parents,
+                              uint32_t beam_width, uint32_t *children_out,
+                              uint64_t stream_ptr);
+
 /** Device-side variant (vLLM copy_blocks contract): `pairs_ptr` is a device
  *  int64 [num_pairs][2] array of block ids, translated through the device
  *  f16-unit offset table.  Enqueue only; no host state is read. */

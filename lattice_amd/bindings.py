@@ -155,6 +155,8 @@ SIGNATURES = {
     "kcmm_fork_sequence": ([_P, _U32, _P], C.c_int),
     "kcmm_get_block_refcount": ([_P, _U32], _U32),
     "kcmm_cow_block_for_append": ([_P, _U32, _U32, _P, _P], C.c_int),
+    "kcmm_fork_beams_on_stream": ([_P, C.POINTER(C.c_uint32), _U32, _U32, C.POINTER(C.c_uint32),
+                                   _U64], C.c_int),
     "kcmm_copy_blocks_on_stream": ([_P, _P, _U32, _U64], C.c_int),
     "kcmm_copy_blocks_device_on_stream": ([_P, _U64, _U64, _U32, _U64], C.c_int),
     "kcmm_gemm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
@@ -489,6 +491,16 @@ class KcmmPool:
         out = C.c_uint32(0)
         self._check(self.lib.kcmm_fork_sequence(self.handle, src, C.byref(out)), "kcmm_fork_sequence")
         return out.value
+
+    def fork_beams(self, parents, beam_width: int, stream_ptr: int = 0):
+        """Children (parent-major) and the number of pages copied."""
+        n = len(parents)
+        par = (C.c_uint32 * max(1, n))(*parents)
+        out = (C.c_uint32 * max(1, n * max(0, beam_width - 1)))()
+        rc = self.lib.kcmm_fork_beams_on_stream(self.handle, par, n, beam_width, out, stream_ptr)
+        if rc < 0:
+            raise KcmmError(f"kcmm_fork_beams_on_stream: {self.last_error()}")
+        return list(out[:n * max(0, beam_width - 1)]), rc
 
     def share_prefix(self, src: int, dst: int, n: int) -> list[int]:
         out = (C.c_uint32 * max(1, n))()

@@ -820,6 +820,32 @@ int kcmm_copy_blocks_on_stream(kcmm_pool_t* pool, const uint32_t* pairs, uint32_
     return 0;
 }
 
+int kcmm_fork_beams_on_stream(kcmm_pool_t* pool, const uint32_t* parents, uint32_t n_parents,
+                              uint32_t beam_width, uint32_t* children_out, uint64_t stream) {
+    if (pool == nullptr || ((parents == nullptr || children_out == nullptr) && n_parents > 0)) {
+        if (pool) pool->set_error("kcmm_fork_beams_on_stream: null arguments");
+        return -1;
+    }
+    std::vector<uint32_t> pairs;
+    std::string err;
+    if (!pool->core->fork_beams(parents, n_parents, beam_width, children_out, &pairs, &err)) {
+        pool->set_error(err);
+        return -1;
+    }
+    const uint32_t n = static_cast<uint32_t>(pairs.size() / 2);
+    if (n == 0) return 0;
+    std::vector<uint64_t> offs;
+    if (!pool->core->resolve_pairs(pairs.data(), n, &offs, &err) ||
+        !kcmm::dev::set_device(pool->device, &err) ||
+        !kcmm::dev::copy_pages(region_bases(pool), offs.data(), n,
+                               static_cast<uint32_t>(pool->core->geo().block_bytes), stream,
+                               &err)) {
+        pool->set_error("kcmm_fork_beams_on_stream: " + err);
+        return -1;
+    }
+    return static_cast<int>(n);
+}
+
 int kcmm_copy_blocks_device_on_stream(kcmm_pool_t* pool, uint64_t pairs_ptr, uint64_t offs_ptr,
                                       uint32_t n, uint64_t stream) {
     if (pool == nullptr || pairs_ptr == 0 || offs_ptr == 0) {

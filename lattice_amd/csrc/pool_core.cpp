@@ -309,6 +309,37 @@ bool PoolCore::share_prefix(uint32_t src, uint32_t dst, uint32_t n, uint32_t* ou
     return true;
 }
 
+bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
+                          uint32_t* children, std::vector<uint32_t>* pairs, std::string* err) {
+    if (width == 0) {
+        *err = "kcmm_fork_beams: beam width must be at least 1";
+        return false;
+    }
+    const uint32_t bs = static_cast<uint32_t>(geo_.block_size);
+    for (uint32_t i = 0; i < n; ++i) {
+        for (uint32_t c = 0; c + 1 < width; ++c) {
+            uint32_t child = 0;
+            if (!fork_sequence(parents[i], &child, err)) return false;
+            children[static_cast<size_t>(i) * (width - 1) + c] = child;
+            uint32_t logical = 0, table_len = 0;
+            {
+                std::lock_guard<std::mutex> lk(mu_);
+                logical = seqs_[child].seq_len / bs;
+                table_len = static_cast<uint32_t>(seqs_[child].table.size());
+            }
+            if (logical >= table_len) continue;   // the next token opens a new page
+            uint32_t src = 0, dst = 0;
+            const int rc = cow_block_for_append(child, logical, &src, &dst, err);
+            if (rc < 0) return false;
+            if (rc == 1) {
+                pairs->push_back(src);
+                pairs->push_back(dst);
+            }
+        }
+    }
+    return true;
+}
+
 int PoolCore::cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src,
                                    uint32_t* dst, std::string* err) {
     std::lock_guard<std::mutex> lk(mu_);

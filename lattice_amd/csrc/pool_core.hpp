@@ -142,6 +142,14 @@ public:
     bool share_prefix(uint32_t src, uint32_t dst, uint32_t n, uint32_t* out, std::string* err);
     int cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src, uint32_t* dst,
                              std::string* err);
+    // Beam fork of a decode step: for each parent, width - 1 children, each
+    // forked and then made private at the page of its next token (logical
+    // block seq_len / block_size, when allocated).  Appends the (src, dst)
+    // page copies to *pairs and the children (parent-major) to children.
+    // On error the operations already done stay done (as with the separate
+    // calls).
+    bool fork_beams(const uint32_t* parents, uint32_t n, uint32_t width, uint32_t* children,
+                    std::vector<uint32_t>* pairs, std::string* err);
     // Byte offsets of the pages of (src, dst) pairs; false if an id is not in use.
     bool resolve_pairs(const uint32_t* pairs, size_t n, std::vector<uint64_t>* out,
                        std::string* err);

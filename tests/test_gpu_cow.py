@@ -113,3 +113,59 @@ def test_shared_block_write_is_refused(gpu_lib):
         pool.synchronize()
     finally:
         pool.destroy()
+
+
+@pytest.mark.parametrize("dtype,width", [(KV_BF16, 4), (KV_FP8, 4), (KV_BF16, 1), (KV_BF16, 2)])
+def test_fork_beams_matches_separate_calls(gpu_lib, dtype, width):
+    """kcmm_fork_beams_on_stream against the oracle pool doing fork + CoW per
+    child in the same order: child ids, every table and refcount, the number
+    of copies, and every byte of all 2*L regions after the one copy kernel.
+    Sequences whose next token opens a new page need no copy."""
+    import torch
+    rng = np.random.default_rng(7 + dtype + width)
+    L, hk, d, bs, B = 2, 8, 128, 16, 6
+    pool = gpu_lib.create_pool(make_config(num_layers=L, kv_heads=hk, head_dim=d,
+                                           max_batch=B * width, max_seq_len=256), dtype)
+    opool = O.OraclePool(bs, L, hk, d, B * width, 256, dtype)
+    try:
+        seqs, lens = [], {}
+        for b in range(B):
+            n = int(rng.integers(1, 6))
+            ids = pool.alloc_blocks(n)
+            assert ids == opool.alloc(n)
+            s = pool.register_sequence(ids)
+            assert s == opool.register(ids)
+            # every other sequence ends exactly on a page boundary
+            ln = n * bs if b % 2 else n * bs - int(rng.integers(1, bs))
+            pool.update_seq_len(s, ln)
+            opool.update_seq_len(s, ln)
+            seqs.append(s)
+            lens[s] = ln
+        regs = fill_random(pool, rng)
+        stream = torch.cuda.current_stream()
+        children, ncopy = pool.fork_beams(seqs, width, stream_ptr=stream.cuda_stream)
+        stream.synchronize()
+        ochildren, opairs = [], []
+        for s in seqs:
+            for _ in range(width - 1):
+                c = opool.fork(s)
+                ochildren.append(c)
+                logical = lens[s] // bs          # the child's next token
+                if logical < len(opool.block_table(c)):
+                    rc, pair = opool.cow(c, logical)
+                    if rc == 1:
+                        opairs.append(tuple(pair))
+        assert children == ochildren
+        assert ncopy == len(opairs) == (width - 1) * (B // 2 + B % 2)
+        for s in seqs + children:
+            assert pool.block_table(s) == opool.block_table(s)
+            for blk in pool.block_table(s):
+                assert pool.refcount(blk) == opool.refcount(blk)
+        flat = [r for pair in regs for r in pair]
+        O.copy_pages(flat, [(opool.block_offset(a), opool.block_offset(b)) for a, b in opairs],
+                     pool.stats()["block_bytes"])
+        got = read_all(pool)
+        for l in range(L):
+            assert np.array_equal(got[l][0], regs[l][0]) and np.array_equal(got[l][1], regs[l][1])
+    finally:
+        pool.destroy()
