@@ -215,7 +215,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x4 (
 // padded LDS rows; 8-wave workgroups at 2 or 4 waves per SIMD; waves that
 // each take a quarter of every chunk's k range over all 64 rows (no LDS
 // staging or per-chunk barrier, but a row's lines are then read by four
-// drifting waves: 20% slower); summing the split partials inside this kernel
+// drifting waves: 20% slower); for M > 128, waves of 32 rows x 128 tokens in
+// 4- or 8-wave workgroups (halves the activation reads per MFMA, but two waves
+// then stream each weight line: 20-40% slower); summing the split partials inside this kernel
 // by the last workgroup of each tile, whose coherent stores and arrival count
 // put several memory round trips on every tile's tail.)
 template <int MB, int KCH, int EPI>
