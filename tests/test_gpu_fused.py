@@ -54,15 +54,16 @@ def test_swiglu_gemm_matches_unfused(gpu_lib, m, inter, k):
     assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
 
 
-@pytest.mark.parametrize("hq,hkv,d,h", [(32, 8, 128, 4096), (8, 2, 64, 256), (12, 4, 80, 512),
-                                         (32, 8, 128, 256)])
-def test_qkv_rope_append_matches_unfused(gpu_lib, hq, hkv, d, h):
+@pytest.mark.parametrize("hq,hkv,d,h,nseq", [(32, 8, 128, 4096, 6), (8, 2, 64, 256, 6),
+                                              (12, 4, 80, 512, 6), (32, 8, 128, 256, 6),
+                                              (8, 2, 128, 1024, 160)])
+def test_qkv_rope_append_matches_unfused(gpu_lib, hq, hkv, d, h, nseq):
     """q_out and every byte of both regions identical between the fused QKV
     projection and projection -> RoPE/append; ragged lengths, a sequence
     with no token and one whose position lies past its table (both
     skipped: their q_out rows keep the NaN fill)."""
     import torch
-    lens = [1, 16, 17, 300, 0, 48]
+    lens = ([1, 16, 17, 300, 0, 48] * (nseq // 6 + 1))[:nseq]
     B = len(lens)
     n = (hq + 2 * hkv) * d
     if n % 64:
@@ -97,8 +98,10 @@ def test_qkv_rope_append_matches_unfused(gpu_lib, hq, hkv, d, h):
             case.pool.destroy()
     (q0, k0, v0), (q1, k1, v1) = outs
     assert np.array_equal(q0, q1)
-    assert np.isnan(O.decode(O.BF16, q1[[1, 4]])).all()
-    assert not np.isnan(O.decode(O.BF16, q1[[0, 2, 3, 5]])).any()
+    skipped = [b for b, L in enumerate(lens) if b == 1 or L == 0]
+    live = [b for b in range(B) if b not in skipped]
+    assert np.isnan(O.decode(O.BF16, q1[skipped])).all()
+    assert not np.isnan(O.decode(O.BF16, q1[live])).any()
     assert np.array_equal(k0, k1)
     assert np.array_equal(v0, v1)
 
