@@ -16,13 +16,14 @@ call.  After the timed steps the same layer is timed through the single
 entry point kcmm_decode_layer_step_on_stream, the standalone slot append
 (kcmm_append_kv_device_slots) on its own, and a whole decode step -- all 32
 layers, each over its own KV -- through one kcmm_decode_layers_on_stream
-call.
+call, followed by the final RMSNorm and the lm_head GEMM (vocab 128256) to
+bf16 logits.
 
 Printed JSON: `value` is decode-attention KV GB/s (algorithmic K+V bytes of
 one layer-step / attention call time, the call's average launch duration over
 consecutive calls on the cycled KV sets); decode tokens/s = 64 / t_step with
-t_step the 32-layer call (embedding, the final norm, lm_head and sampling
-are outside this path and excluded).
+t_step the 32-layer call plus the final norm and lm_head (embedding and
+sampling are outside this path and excluded).
 
 `roofline` prices the attention call (streaming kernel + log-sum-exp merge,
 timed by HIP events on the launch stream) against MI355X's 8 TB/s; its
@@ -51,7 +52,7 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, vendor figure
 B, HQ, HKV, D, BS = 64, 32, 8, 128, 16
 CTX_LO, CTX_HI = 512, 4096
 MODEL_LAYERS = 32
-HIDDEN, INTER = 4096, 14336
+HIDDEN, INTER, VOCAB = 4096, 14336, 128256
 KV_BF16_CODE = 1
 ROPE_THETA, RMS_EPS = 500000.0, 1e-5      # Llama-3-8B config.json
 BEAM_WIDTH = 4                             # configs[4]
@@ -241,6 +242,11 @@ def main():
                                    ("attn_norm", "qkv", "o", "mlp_norm", "gate_up", "down")})
                for w in weights]
     inv_freq = torch.from_numpy(rope_inv_freq(ROPE_THETA, D)).to(dev)
+    # final norm + lm_head (1.05 GB) for the whole-step timing
+    if not args.attn_only:
+        final_norm = (1.0 + 0.1 * torch.randn(HIDDEN, generator=g, device=dev)).to(torch.bfloat16)
+        lm_head = (torch.randn((VOCAB, HIDDEN), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        logits = torch.empty((B, VOCAB), dtype=torch.bfloat16, device=dev)
     hidden = torch.randn((B, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
     normed = torch.empty((B, HIDDEN), dtype=torch.bfloat16, device=dev)
     qkv_out = torch.empty((B, (HQ + 2 * HKV) * D), dtype=torch.bfloat16, device=dev)
@@ -280,7 +286,8 @@ def main():
                                     max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
 
     def decode_step(_):
-        """All 32 layers of one decode step in one call (weight sets alternate)."""
+        """One decode step: all 32 layers in one call (weight sets alternate),
+        then the final norm and lm_head to bf16 logits."""
         case.pool.decode_layers(first_layer=0, weights=[layer_w[i % nw] for i in range(MODEL_LAYERS)],
                                 hidden_ptr=hidden.data_ptr(), block_tables_ptr=dv["bt"].data_ptr(),
                                 seq_lens_ptr=dv["sl"].data_ptr(),
@@ -288,6 +295,8 @@ def main():
                                 inv_freq_ptr=inv_freq.data_ptr(), batch=B, hidden_size=HIDDEN,
                                 num_q_heads=HQ, intermediate_size=INTER,
                                 max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
+        lib.decode_logits_bf16(hidden.data_ptr(), final_norm.data_ptr(), lm_head.data_ptr(),
+                               logits.data_ptr(), B, HIDDEN, VOCAB, RMS_EPS, sp)
 
     W = lambda layer, name: weights[layer % nw][name].data_ptr()
     calls = {
@@ -367,7 +376,12 @@ def main():
         # the same layer through the single entry point (what a serving loop
         # calls 32 times per decode step), then the standalone slot append
         full_steps = max(4, args.steps // 8)
+        def logits_step(_):
+            lib.decode_logits_bf16(hidden.data_ptr(), final_norm.data_ptr(), lm_head.data_ptr(),
+                                   logits.data_ptr(), B, HIDDEN, VOCAB, RMS_EPS, sp)
+
         for label, fn, steps in (("layer_step", layer_step, args.steps), ("append", append, args.steps),
+                                 ("logits", logits_step, args.steps),
                                  ("decode_step", decode_step, full_steps)):
             evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
             for i in range(min(args.warmup, steps)):
@@ -471,7 +485,8 @@ def main():
         t_step_s = extra["decode_step"] / 1e3
         result["decode_tokens_per_s"] = round(B / t_step_s, 1)
         result["t_decode_step_us"] = round(t_step_s * 1e6, 1)
-        result["t_layer_us"] = round(t_step_s / MODEL_LAYERS * 1e6, 2)
+        result["t_layer_us"] = round((t_step_s - extra["logits"] / 1e3) / MODEL_LAYERS * 1e6, 2)
+        result["t_logits_us"] = round(extra["logits"] * 1e3, 2)
         result["t_layer_single_call_us"] = round(extra["layer_step"] * 1e3, 2)
         result["t_layer_components_us"] = {n: round(per[n] * 1e3, 2) for n in names}
         def gemm_report(times_ms, M, residual):

@@ -245,6 +245,16 @@ int kcmm_qkv_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, u
                                         uint32_t num_q_heads, uint32_t max_blocks_per_seq,
                                         uint64_t stream_ptr);
 
+/** The end of a decode step (ref llama_transformer.rs:382-390: final norm,
+ *  lm_head GEMM): logits[b] = lm_head * rmsnorm(hidden[b]) with weight
+ *  norm_w, bf16 [batch][vocab_size] on the device (the reference copies fp32
+ *  logits to the host; the caller converts or samples where it needs them).
+ *  hidden_size % 256 == 0, vocab_size % 64 == 0.  Enqueue only. */
+int kcmm_decode_logits_bf16_on_stream(uint64_t hidden_ptr, uint64_t norm_w_ptr,
+                                      uint64_t lm_head_ptr, uint64_t logits_ptr, uint32_t batch,
+                                      uint32_t hidden_size, uint32_t vocab_size, float rms_eps,
+                                      uint64_t stream_ptr);
+
 /** Device addresses of one layer's weights (bf16, row-major [out][in]). */
 typedef struct kcmm_layer_weights {
     uint64_t attn_norm; /**< [hidden] */

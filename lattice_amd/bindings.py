@@ -164,6 +164,8 @@ SIGNATURES = {
     "kcmm_rmsnorm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, C.c_float, _U64], C.c_int),
     "kcmm_silu_mul_bf16_on_stream": ([_U64, _U64, _U32, _U32, _U64], C.c_int),
     "kcmm_gemm_bf16_swiglu_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
+    "kcmm_decode_logits_bf16_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, C.c_float,
+                                           _U64], C.c_int),
     "kcmm_gemm_bf16_add_rmsnorm_on_stream": ([_U64, _U64, _U64, _U64, _U64, _U32, _U32, _U32,
                                               C.c_float, _U64], C.c_int),
     "kcmm_qkv_rope_append_bf16_on_stream": ([_P, _U32, _U64, _U64, _U64, _U64, _U64, _U64, _U64,
@@ -233,6 +235,14 @@ class KcmmLibrary:
         if self.lib.kcmm_silu_mul_bf16_on_stream(gate_up_ptr, act_ptr, rows, intermediate,
                                                  stream_ptr) != 0:
             raise KcmmError("kcmm_silu_mul_bf16_on_stream failed")
+
+    def decode_logits_bf16(self, hidden_ptr, norm_w_ptr, lm_head_ptr, logits_ptr, batch,
+                           hidden_size, vocab_size, eps, stream_ptr=0) -> None:
+        """logits = lm_head(rmsnorm(hidden)), bf16 on the device."""
+        if self.lib.kcmm_decode_logits_bf16_on_stream(hidden_ptr, norm_w_ptr, lm_head_ptr,
+                                                      logits_ptr, batch, hidden_size, vocab_size,
+                                                      C.c_float(eps), stream_ptr) != 0:
+            raise KcmmError("kcmm_decode_logits_bf16_on_stream failed")
 
     def gemm_bf16_add_rmsnorm(self, x_ptr, w_ptr, hidden_ptr, norm_w_ptr, normed_ptr, m, n, k,
                               eps, stream_ptr=0) -> None:

@@ -21,7 +21,7 @@ bool set_device(int device, std::string* err);
 
 // Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
 // attention partials, 1: GEMM split partials, 2: decode attention segment
-// table, 3: decode layer-step activations).
+// table, 3: decode layer-step activations, 4: the final norm's output).
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);

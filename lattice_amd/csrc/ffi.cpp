@@ -1212,6 +1212,27 @@ int kcmm_decode_layers_on_stream(kcmm_pool_t* pool, uint32_t first_layer, uint32
                              rms_eps, stream);
 }
 
+int kcmm_decode_logits_bf16_on_stream(uint64_t hidden, uint64_t norm_w, uint64_t lm_head,
+                                      uint64_t logits, uint32_t batch, uint32_t hidden_size,
+                                      uint32_t vocab_size, float rms_eps, uint64_t stream) {
+    if (hidden == 0 || norm_w == 0 || lm_head == 0 || logits == 0 || batch == 0 ||
+        hidden_size == 0 || hidden_size % 256 != 0 || vocab_size == 0 || vocab_size % 64 != 0 ||
+        !(rms_eps >= 0.0f))
+        return -1;
+    std::string err;
+    void* ws = nullptr;
+    if (!kcmm::dev::stream_workspace(stream, 4, static_cast<size_t>(batch) * hidden_size * 2, &ws,
+                                     false, &err) ||
+        !kcmm::dev::rmsnorm_bf16(hidden, norm_w, reinterpret_cast<uint64_t>(ws), batch,
+                                 hidden_size, rms_eps, stream, &err) ||
+        !kcmm::dev::gemm_bf16(reinterpret_cast<uint64_t>(ws), lm_head, logits, batch, vocab_size,
+                              hidden_size, stream, &err)) {
+        std::fprintf(stderr, "kcmm_decode_logits_bf16_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
 // ---- utilities ---------------------------------------------------------------------------------
 
 int kcmm_below_low_watermark(kcmm_pool_t* pool, float threshold) {

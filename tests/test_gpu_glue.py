@@ -282,3 +282,25 @@ def test_decode_layers_matches_layer_steps(gpu_lib, hq, hkv, d, h, inter):
     assert np.array_equal(res[0][0], res[1][0])
     for a, b in zip(res[0][1], res[1][1]):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("b,h,vocab", [(5, 512, 1024), (64, 4096, 2048)])
+def test_decode_logits(gpu_lib, b, h, vocab):
+    """Final RMSNorm + lm_head vs the oracle's bf16 norm and fp64 product
+    (bf16 tolerance on the logits)."""
+    import torch
+    rng = np.random.default_rng(h + vocab)
+    x = O.encode(O.BF16, rng.standard_normal((b, h)) * 4)
+    nw = O.encode(O.BF16, 1.0 + 0.1 * rng.standard_normal(h))
+    w = O.encode(O.BF16, rng.standard_normal((vocab, h)) * 0.02)
+    xd, nwd, wd = bf16_dev(torch, x), bf16_dev(torch, nw), bf16_dev(torch, w)
+    lg = torch.full((b, vocab), float("nan"), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.decode_logits_bf16(xd.data_ptr(), nwd.data_ptr(), wd.data_ptr(), lg.data_ptr(), b, h,
+                               vocab, 1e-5, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    normed = O.rmsnorm_f64(O.decode(O.BF16, x), O.decode(O.BF16, nw), 1e-5)
+    ref = O.bf16_round(O.gemm_bf16_f64(O.encode(O.BF16, normed), w))
+    got = O.decode(O.BF16, bits_of(lg)).astype(np.float64)
+    assert rel_err(got, ref) <= 1e-2
+    # hidden is not modified
+    assert np.array_equal(bits_of(xd), x)
