@@ -38,13 +38,19 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
     return v;
 }
 
-__device__ __forceinline__ float block_sum_256(float v, float* red) {
+// Sum over the NT threads of the workgroup, waves added in order (the same
+// order for every row and kernel variant).
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) red[wave] = v;
     __syncthreads();
-    return red[0] + red[1] + red[2] + red[3];
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) s += red[w];
+    return s;
 }
 
 // Sum of the `splits` fp32 partials at pp, pp + MN, ... in split order; up
@@ -67,16 +73,16 @@ __device__ __forceinline__ f32x4 sum_partials(const float* pp, size_t MN, int sp
 // finished as the O projection's residual add -- x = bf16(x + bf16(sum of
 // the `splits` fp32 partials [s][rows][H])) -- and written back to x (the
 // hidden state), exactly what the GEMM's residual store would have written.
-template <bool FROM_PARTIALS>
-__global__ __launch_bounds__(256) void rmsnorm_rows(uint16_t* __restrict__ x,
-                                                    const uint16_t* __restrict__ w,
-                                                    uint16_t* __restrict__ y, int H, float eps,
-                                                    const float* __restrict__ part, int splits) {
-    __shared__ float red[4];
+template <bool FROM_PARTIALS, int NT>
+__global__ __launch_bounds__(NT) void rmsnorm_rows(uint16_t* __restrict__ x,
+                                                   const uint16_t* __restrict__ w,
+                                                   uint16_t* __restrict__ y, int H, float eps,
+                                                   const float* __restrict__ part, int splits) {
+    __shared__ float red[NT / 64];
     uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * H;
     uint16_t* yr = y + static_cast<size_t>(blockIdx.x) * H;
     float ss = 0.0f;
-    for (int i = threadIdx.x * 8; i < H; i += 256 * 8) {
+    for (int i = threadIdx.x * 8; i < H; i += NT * 8) {
         float f[8];
         unpack8(*reinterpret_cast<const u32x4*>(xr + i), f);
         if constexpr (FROM_PARTIALS) {
@@ -94,8 +100,8 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(uint16_t* __restrict__ x,
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
     }
-    const float r = 1.0f / sqrtf(block_sum_256(ss, red) / static_cast<float>(H) + eps);
-    for (int i = threadIdx.x * 8; i < H; i += 256 * 8) {
+    const float r = 1.0f / sqrtf(block_sum<NT>(ss, red) / static_cast<float>(H) + eps);
+    for (int i = threadIdx.x * 8; i < H; i += NT * 8) {
         float f[8], g[8];
         unpack8(*reinterpret_cast<const u32x4*>(xr + i), f);   // (this thread's own writes)
         unpack8(*reinterpret_cast<const u32x4*>(w + i), g);
@@ -219,6 +225,25 @@ __global__ __launch_bounds__(256) void silu_mul_rows(const uint16_t* __restrict_
     *reinterpret_cast<u32x4*>(act + idx) = pack8(g);
 }
 
+// Workgroup size by row length: one 8-element piece per thread when H <=
+// 8192 (every load of a row in flight at once); the same choice for both
+// variants, so they reduce in the same order.
+template <bool FROM_PARTIALS>
+void launch_rmsnorm(uint16_t* x, const uint16_t* w, uint16_t* y, uint32_t rows, uint32_t H,
+                    float eps, const float* part, int splits, uint64_t stream) {
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int h = static_cast<int>(H);
+    if (H > 4096)
+        hipLaunchKernelGGL((rmsnorm_rows<FROM_PARTIALS, 1024>), dim3(rows), dim3(1024), 0, s, x, w, y,
+                           h, eps, part, splits);
+    else if (H > 2048)
+        hipLaunchKernelGGL((rmsnorm_rows<FROM_PARTIALS, 512>), dim3(rows), dim3(512), 0, s, x, w, y,
+                           h, eps, part, splits);
+    else
+        hipLaunchKernelGGL((rmsnorm_rows<FROM_PARTIALS, 256>), dim3(rows), dim3(256), 0, s, x, w, y,
+                           h, eps, part, splits);
+}
+
 }  // namespace
 
 namespace dev {
@@ -230,10 +255,8 @@ bool rmsnorm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t rows, uint32_t hi
         *err = "rmsnorm: hidden size must be a positive multiple of 8";
         return false;
     }
-    hipLaunchKernelGGL(rmsnorm_rows<false>, dim3(rows), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), reinterpret_cast<uint16_t*>(x),
-                       reinterpret_cast<const uint16_t*>(w), reinterpret_cast<uint16_t*>(y),
-                       static_cast<int>(hidden), eps, nullptr, 0);
+    launch_rmsnorm<false>(reinterpret_cast<uint16_t*>(x), reinterpret_cast<const uint16_t*>(w),
+                          reinterpret_cast<uint16_t*>(y), rows, hidden, eps, nullptr, 0, stream);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     return true;
 }
@@ -246,10 +269,8 @@ bool residual_rmsnorm_from_partials(const float* part, int splits, uint64_t hidd
         *err = "residual_rmsnorm: hidden size must be a positive multiple of 8";
         return false;
     }
-    hipLaunchKernelGGL(rmsnorm_rows<true>, dim3(rows), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), reinterpret_cast<uint16_t*>(hidden),
-                       reinterpret_cast<const uint16_t*>(w), reinterpret_cast<uint16_t*>(y),
-                       static_cast<int>(H), eps, part, splits);
+    launch_rmsnorm<true>(reinterpret_cast<uint16_t*>(hidden), reinterpret_cast<const uint16_t*>(w),
+                         reinterpret_cast<uint16_t*>(y), rows, H, eps, part, splits, stream);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     return true;
 }
