@@ -211,7 +211,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x4 (
 // (Measured alternatives that were not faster at the Llama-3-8B decode
 // shapes: a persistent grid over (row block, k chunk) tiles with a 6-deep
 // ring; direct-to-LDS activation loads with a 3-deep weight ring; a 3-deep
-// register weight ring (two chunks always in flight); buffer loads with
+// register weight ring (two chunks always in flight; also fully unrolled, so
+// that no wait lands inside a chunk's math: still 4% slower -- more weight
+// requests in flight lower the DRAM efficiency); buffer loads with
 // padded LDS rows; 8-wave workgroups at 2 or 4 waves per SIMD; waves that
 // each take a quarter of every chunk's k range over all 64 rows (no LDS
 // staging or per-chunk barrier, but a row's lines are then read by four
