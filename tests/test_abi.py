@@ -145,3 +145,58 @@ def test_null_and_argument_checks(hostcheck_lib):
         assert L.kcmm_get_last_error(pool.handle, small, 5) == 4 and len(small.value) == 4
     finally:
         pool.destroy()
+
+
+def test_decode_layer_entry_points_validate_before_device_work(hostcheck_lib):
+    """The decode-layer, fused-GEMM and beam-fork entry points reject bad
+    arguments (and say why) before any device work, on the host-check build."""
+    from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, make_config
+    L = hostcheck_lib.lib
+    # pool-free entry points: shape rules
+    assert L.kcmm_gemm_bf16_swiglu_on_stream(1, 1, 1, 4, 100, 256, 0) == -1      # inter % 32
+    assert L.kcmm_gemm_bf16_add_rmsnorm_on_stream(1, 1, 1, 1, 1, 4, 100, 256,
+                                                  C.c_float(1e-5), 0) == -1     # n % 8
+    assert L.kcmm_decode_logits_bf16_on_stream(1, 1, 1, 1, 4, 4096, 1000, C.c_float(1e-5),
+                                               0) == -1                          # vocab % 64
+    assert L.kcmm_rmsnorm_bf16_on_stream(1, 1, 1, 4, 100, C.c_float(-1.0), 0) == -1
+    cfg = make_config(num_layers=2, kv_heads=2, head_dim=64, max_batch=4, max_seq_len=64)
+    w = KcmmLayerWeights(attn_norm=1, qkv=1, o=1, mlp_norm=1, gate_up=1, down=1)
+    f16 = hostcheck_lib.create_pool(cfg)
+    bf = hostcheck_lib.create_pool(cfg, KV_BF16)
+    try:
+        kw = dict(hidden_ptr=1, block_tables_ptr=1, seq_lens_ptr=1, block_offsets_f16_ptr=1,
+                  inv_freq_ptr=1, batch=2, hidden_size=512, num_q_heads=8, intermediate_size=768,
+                  max_blocks_per_seq=4, rms_eps=1e-5)
+        with pytest.raises(Exception):
+            f16.decode_layer_step(layer_idx=0, weights=w, **kw)
+        assert "bf16" in f16.last_error()
+        with pytest.raises(Exception):
+            bf.decode_layer_step(layer_idx=0, weights=KcmmLayerWeights(), **kw)
+        assert "null" in bf.last_error()
+        with pytest.raises(Exception):
+            bf.decode_layer_step(layer_idx=0, weights=w, **{**kw, "hidden_size": 500})
+        assert "multiples of 256" in bf.last_error()
+        with pytest.raises(Exception):
+            bf.decode_layer_step(layer_idx=0, weights=w, **{**kw, "num_q_heads": 7})
+        with pytest.raises(Exception):
+            bf.decode_layers(first_layer=1, weights=[w, w], **kw)            # layers 1..2 of 2
+        assert "layer" in bf.last_error()
+        with pytest.raises(Exception):
+            bf.decode_layers(first_layer=0, weights=[], **kw)
+        # beam fork: bad width and an unknown parent are errors; a parent whose
+        # next token opens a new page forks with no copy (so no device work)
+        ids = bf.alloc_blocks(2)
+        s = bf.register_sequence(ids)
+        bf.update_seq_len(s, 32)
+        with pytest.raises(Exception):
+            bf.fork_beams([s], 0)
+        with pytest.raises(Exception):
+            bf.fork_beams([12345], 4)
+        children, copies = bf.fork_beams([s], 4)
+        assert copies == 0 and len(children) == 3
+        for c in children:
+            assert bf.block_table(c) == ids
+        assert [bf.refcount(i) for i in ids] == [4, 4]
+    finally:
+        f16.destroy()
+        bf.destroy()
