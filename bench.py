@@ -396,25 +396,37 @@ def main():
         log(f"layer step (one call) ms={extra['layer_step']:.4f}, append ms={extra['append']:.4f}, "
             f"32-layer decode step ms={extra['decode_step']:.4f}")
         # the projections at M = 256 tokens (configs[3]'s second size), same weights
-        m256 = {}
+        # (kcmm_gemm_bf16 hands M > 128 to hipBLASLt; KCMM_GEMM_LT=0 keeps the
+        # weight-stream kernel, timed beside it)
+        m256, m256_stream = {}, {}
         x256 = {k: torch.randn((256, k), generator=g, device=dev).to(torch.bfloat16)
                 for k in (HIDDEN, INTER)}
         y256 = torch.empty((256, 2 * INTER), dtype=torch.bfloat16, device=dev)
-        for name, n, k in GEMMS:
-            fn = lambda l, n=n, k=k, name=name: lib.gemm_bf16(
-                x256[k].data_ptr(), W(l, name), y256.data_ptr(), 256, n, k, sp)
-            evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-            for i in range(min(args.warmup, args.steps)):
-                fn(i)
-            torch.cuda.synchronize()
-            for i in range(args.steps):
-                evs[i].record(stream)
-                fn(i)
-            evs[-1].record(stream)
-            torch.cuda.synchronize()
-            m256[name] = float(np.mean([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]))
+        lt_env = os.environ.get("KCMM_GEMM_LT")
+        for backend, out in (("1", m256), ("0", m256_stream)):
+            os.environ["KCMM_GEMM_LT"] = backend
+            for name, n, k in GEMMS:
+                fn = lambda l, n=n, k=k, name=name: lib.gemm_bf16(
+                    x256[k].data_ptr(), W(l, name), y256.data_ptr(), 256, n, k, sp)
+                evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+                for i in range(min(args.warmup, args.steps)):
+                    fn(i)
+                torch.cuda.synchronize()
+                for i in range(args.steps):
+                    evs[i].record(stream)
+                    fn(i)
+                evs[-1].record(stream)
+                torch.cuda.synchronize()
+                out[name] = float(np.mean([evs[i].elapsed_time(evs[i + 1])
+                                           for i in range(args.steps)]))
+        if lt_env is None:
+            os.environ.pop("KCMM_GEMM_LT", None)
+        else:
+            os.environ["KCMM_GEMM_LT"] = lt_env
         del x256, y256
-        log("M=256 GEMM ms: " + ", ".join(f"{k}={v:.4f}" for k, v in m256.items()))
+        log("M=256 GEMM ms (hipBLASLt): " + ", ".join(f"{k}={v:.4f}" for k, v in m256.items()))
+        log("M=256 GEMM ms (weight-stream kernel): " +
+            ", ".join(f"{k}={v:.4f}" for k, v in m256_stream.items()))
         assert torch.isfinite(hidden.float()).all(), "layer step produced non-finite hidden state"
 
     # attention calls back to back over the cycled KV sets (the order a decode
@@ -506,6 +518,8 @@ def main():
             return gem
         result["gemm_m64"] = gemm_report(per, B, True)
         result["gemm_m256"] = gemm_report(m256, 256, False)
+        result["gemm_m256"]["backend"] = "hipBLASLt"
+        result["gemm_m256_stream_kernel"] = gemm_report(m256_stream, 256, False)
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))
         log(f"cpu baseline on {threads} threads ...")

@@ -157,7 +157,10 @@ int kcmm_copy_blocks_device_on_stream(kcmm_pool_t *pool, uint64_t pairs_ptr,
  *  ref llama_transformer.rs:115-120), bf16 inputs and output, fp32
  *  accumulation on MFMA.  Replaces the cuBLAS call of ref runtime.rs:17-41
  *  (whose column-major arguments equal this product only at m == 1).
- *  Enqueue only; requires k % 256 == 0 and n % 64 == 0. */
+ *  m <= 128 runs the weight-stream MFMA kernel; m > 128 runs hipBLASLt
+ *  (same product, fp32 accumulation, not the same bits) unless the
+ *  environment sets KCMM_GEMM_LT=0.  Enqueue only; requires k % 256 == 0
+ *  and n % 64 == 0. */
 int kcmm_gemm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
                              uint32_t m, uint32_t n, uint32_t k,
                              uint64_t stream_ptr);
@@ -207,6 +210,7 @@ int kcmm_silu_mul_bf16_on_stream(uint64_t gate_up_ptr, uint64_t act_ptr, uint32_
  *  = bf16(bf16(silu(G)) * U) with G, U the bf16-rounded projections
  *  x * w[j]^T and x * w[intermediate + j]^T; w_gate_up = [gate rows; up
  *  rows], [2 intermediate][k].  Bit-identical to kcmm_gemm_bf16_on_stream
+ *  (on the weight-stream kernel: m <= 128 or KCMM_GEMM_LT=0)
  *  followed by kcmm_silu_mul_bf16_on_stream, without the [m][2 intermediate]
  *  intermediate.  intermediate % 32 == 0, k % 256 == 0. */
 int kcmm_gemm_bf16_swiglu_on_stream(uint64_t x_ptr, uint64_t w_gate_up_ptr, uint64_t act_ptr,
@@ -235,7 +239,9 @@ int kcmm_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, uint6
  *  write): x_ptr [batch][hidden] times w_qkv_ptr [(Hq + 2 Hkv) head_dim]
  *  [hidden] (q rows, k rows, v rows), each product rounded to bf16 and then
  *  treated exactly as kcmm_rope_append_bf16_on_stream treats a qkv row, so
- *  the pair gives identical bits without the qkv intermediate.  head_dim %
+ *  the pair gives identical bits without the qkv intermediate (with the
+ *  pair's GEMM on the weight-stream kernel: batch <= 128 or
+ *  KCMM_GEMM_LT=0).  head_dim %
  *  16 == 0, hidden % 256 == 0, (Hq + 2 Hkv) head_dim % 64 == 0. */
 int kcmm_qkv_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, uint64_t x_ptr,
                                         uint64_t w_qkv_ptr, uint64_t q_out_ptr,

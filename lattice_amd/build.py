@@ -28,6 +28,7 @@ HOSTCHECK_LIB = HOSTCHECK_DIR / "libkcmm_hostcheck.so"
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 CXX = os.environ.get("CXX", "g++")
 
 # -packed-fp32-ops: no v_pk_*_f32 in generated code.
@@ -41,7 +42,7 @@ CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-Wno-unused-para
 HOST_SOURCES = ["pool_core.cpp", "ffi.cpp"]
 HIP_SOURCES = ["kernels/backing.hip", "kernels/attn_decode.hip", "kernels/attn_prefill.hip",
                "kernels/kv_write.hip",
-               "kernels/page_copy.hip", "kernels/gemm.hip", "kernels/glue.hip"]
+               "kernels/page_copy.hip", "kernels/gemm.hip", "kernels/gemm_lt.hip", "kernels/glue.hip"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -75,7 +76,8 @@ def build_kcmm(jobs: int = 8) -> Path:
         list(ex.map(_run, cmds))
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-          *map(str, objs), "-Wl,--no-undefined"])
+          *map(str, objs), f"-L{ROCM}/lib", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib",
+          "-Wl,--no-undefined"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -21,7 +21,8 @@ bool set_device(int device, std::string* err);
 
 // Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
 // attention partials, 1: GEMM split partials, 2: decode attention segment
-// table, 3: decode layer-step activations, 4: the final norm's output).
+// table, 3: decode layer-step activations, 4: the final norm's output,
+// 5: hipBLASLt workspace).
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);
@@ -93,6 +94,11 @@ bool copy_pages_device(const std::vector<uint64_t>& region_bases, uint64_t pairs
 // residual the product is rounded to bf16 before the add, as a bf16 model does.
 bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
                uint64_t stream, std::string* err, uint64_t residual = 0);
+
+// The same product through hipBLASLt (kernels/gemm_lt.hip); *used is false
+// (and the call succeeds) when the library offers no algorithm for the shape.
+bool lt_gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
+                  uint64_t stream, bool* used, std::string* err);
 
 // Decode-step glue (kernels/glue.hip), bf16.
 bool rmsnorm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t rows, uint32_t hidden, float eps,

@@ -498,6 +498,13 @@ namespace dev {
 bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
                uint64_t stream, std::string* err, uint64_t residual) {
     if (!shape_ok(m, n, k, err)) return false;
+    // many tokens, plain store: hipBLASLt's MFMA tiling (KCMM_GEMM_LT=0 keeps
+    // the weight-stream kernel)
+    if (m > 128 && residual == 0 && env_int("KCMM_GEMM_LT", 1) != 0) {
+        bool used = false;
+        if (!lt_gemm_bf16(x, w, y, m, n, k, stream, &used, err)) return false;
+        if (used) return true;
+    }
     GemmParams p = base_params(x, w, m, n, k);
     p.Y = reinterpret_cast<uint16_t*>(y);
     p.R = reinterpret_cast<const uint16_t*>(residual);

@@ -91,6 +91,11 @@ bool gemm_bf16_swiglu(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t
                       std::string* err) {
     return no_device(err);
 }
+bool lt_gemm_bf16(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, bool* used,
+                  std::string* err) {
+    *used = false;
+    return no_device(err);
+}
 bool gemm_bf16_partials(uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, float**, int*,
                         std::string* err) {
     return no_device(err);

@@ -5,7 +5,8 @@ replace (same GEMM arithmetic, then the same element arithmetic):
   kcmm_gemm_bf16_swiglu        == kcmm_gemm_bf16 -> kcmm_silu_mul_bf16
   kcmm_qkv_rope_append_bf16    == kcmm_gemm_bf16 -> kcmm_rope_append_bf16
   kcmm_gemm_bf16_add_rmsnorm   == kcmm_gemm_bf16_add -> kcmm_rmsnorm_bf16
-The unfused kernels are themselves checked against the oracle
+(the unfused GEMM on the weight-stream kernel: KCMM_GEMM_LT=0).  The
+unfused kernels are themselves checked against the oracle
 (tests/test_gpu_glue.py, tests/test_gpu_gemm.py).  Shapes cover both the
 single-pass GEMM (epilogue in its store) and the split-K path whose fp32
 partials are summed, in split order, by the finishing kernel."""
@@ -32,8 +33,9 @@ def _randn_bf16(torch, shape, std, seed):
 
 @pytest.mark.parametrize("m,inter,k", [(5, 256, 512), (64, 1024, 4096), (64, 14336, 4096),
                                        (100, 512, 1024), (256, 768, 2048)])
-def test_swiglu_gemm_matches_unfused(gpu_lib, m, inter, k):
+def test_swiglu_gemm_matches_unfused(gpu_lib, monkeypatch, m, inter, k):
     import torch
+    monkeypatch.setenv("KCMM_GEMM_LT", "0")   # the unfused GEMM on the same kernel
     x = _randn_bf16(torch, (m, k), 1.0, 1)
     w = _randn_bf16(torch, (2 * inter, k), 0.05, 2)
     gu = torch.empty((m, 2 * inter), dtype=torch.bfloat16, device="cuda")
@@ -57,12 +59,13 @@ def test_swiglu_gemm_matches_unfused(gpu_lib, m, inter, k):
 @pytest.mark.parametrize("hq,hkv,d,h,nseq", [(32, 8, 128, 4096, 6), (8, 2, 64, 256, 6),
                                               (12, 4, 80, 512, 6), (32, 8, 128, 256, 6),
                                               (8, 2, 128, 1024, 160)])
-def test_qkv_rope_append_matches_unfused(gpu_lib, hq, hkv, d, h, nseq):
+def test_qkv_rope_append_matches_unfused(gpu_lib, monkeypatch, hq, hkv, d, h, nseq):
     """q_out and every byte of both regions identical between the fused QKV
     projection and projection -> RoPE/append; ragged lengths, a sequence
     with no token and one whose position lies past its table (both
     skipped: their q_out rows keep the NaN fill)."""
     import torch
+    monkeypatch.setenv("KCMM_GEMM_LT", "0")   # the unfused GEMM on the same kernel
     lens = ([1, 16, 17, 300, 0, 48] * (nseq // 6 + 1))[:nseq]
     B = len(lens)
     n = (hq + 2 * hkv) * d

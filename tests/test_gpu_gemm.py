@@ -13,6 +13,15 @@ def rel_err(got, ref):
     return float(np.abs(got - ref).max() / np.abs(ref).max())
 
 
+@pytest.fixture(params=["lt", "stream"])
+def backend(request, monkeypatch):
+    """kcmm_gemm_bf16 hands plain products with M > 128 to hipBLASLt;
+    KCMM_GEMM_LT=0 keeps them on the weight-stream kernel.  Both are
+    checked."""
+    monkeypatch.setenv("KCMM_GEMM_LT", "1" if request.param == "lt" else "0")
+    return request.param
+
+
 def run(gpu_lib, x, w):
     import torch
     m, k = x.shape
@@ -26,8 +35,10 @@ def run(gpu_lib, x, w):
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 256), (17, 192, 512), (64, 256, 1024),
                                    (100, 128, 768), (256, 320, 2048)])
-def test_vs_oracle(gpu_lib, m, n, k):
+def test_vs_oracle(gpu_lib, backend, m, n, k):
     import torch
+    if backend == "lt" and m <= 128:
+        pytest.skip("M <= 128 always runs the weight-stream kernel")
     rng = np.random.default_rng(m + n + k)
     xb = O.encode(O.BF16, rng.standard_normal((m, k)))
     wb = O.encode(O.BF16, rng.standard_normal((n, k)) * 0.02)
@@ -36,14 +47,16 @@ def test_vs_oracle(gpu_lib, m, n, k):
     y = run(gpu_lib, x, w)
     got = O.decode(O.BF16, y.cpu().view(torch.int16).numpy().view(np.uint16))
     err = rel_err(got, O.gemm_bf16_f64(xb, wb))
-    print(f"gemm {m}x{n}x{k} err={err:.3e}", flush=True)
+    print(f"gemm {backend} {m}x{n}x{k} err={err:.3e}", flush=True)
     assert err <= 1e-2
 
 
 @pytest.mark.parametrize("m", [64, 256])
 @pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)])
-def test_llama3_8b_projections(gpu_lib, m, n, k):
+def test_llama3_8b_projections(gpu_lib, backend, m, n, k):
     import torch
+    if backend == "lt" and m <= 128:
+        pytest.skip("M <= 128 always runs the weight-stream kernel")
     g = torch.Generator(device="cuda")
     g.manual_seed(m * 7 + n + k)
     x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
@@ -51,7 +64,7 @@ def test_llama3_8b_projections(gpu_lib, m, n, k):
     y = run(gpu_lib, x, w).float()
     ref = x.float() @ w.float().t()
     err = float((y - ref).abs().max() / ref.abs().max())
-    print(f"gemm {m}x{n}x{k} err={err:.3e}", flush=True)
+    print(f"gemm {backend} {m}x{n}x{k} err={err:.3e}", flush=True)
     assert err <= 1e-2
 
 
@@ -64,6 +77,7 @@ def test_split_k_choices(gpu_lib, monkeypatch, target, m, n, k):
     partials and their reduction are exact up to fp32 rounding."""
     import torch
     monkeypatch.setenv("KCMM_GEMM_WGS", target)
+    monkeypatch.setenv("KCMM_GEMM_LT", "0")
     g = torch.Generator(device="cuda")
     g.manual_seed(m * 31 + n + k + len(target))
     x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
@@ -73,3 +87,21 @@ def test_split_k_choices(gpu_lib, monkeypatch, target, m, n, k):
     err = float((y - ref).abs().max() / ref.abs().max())
     print(f"gemm target={target} {m}x{n}x{k} err={err:.3e}", flush=True)
     assert err <= 1e-2
+
+
+def test_lt_repeatable_and_odd_shape(gpu_lib, monkeypatch):
+    """The hipBLASLt path: a cached plan reused for a second, different
+    input gives the oracle's product both times; a shape with M not a
+    multiple of any tile (M = 129) is covered too."""
+    import torch
+    monkeypatch.setenv("KCMM_GEMM_LT", "1")
+    for seed, (m, n, k) in enumerate([(129, 192, 512), (129, 192, 512), (300, 1024, 256)]):
+        rng = np.random.default_rng(100 + seed)
+        xb = O.encode(O.BF16, rng.standard_normal((m, k)))
+        wb = O.encode(O.BF16, rng.standard_normal((n, k)) * 0.02)
+        x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+        w = torch.from_numpy(wb.view(np.int16)).view(torch.bfloat16).cuda()
+        got = O.decode(O.BF16, run(gpu_lib, x, w).cpu().view(torch.int16).numpy().view(np.uint16))
+        err = rel_err(got, O.gemm_bf16_f64(xb, wb))
+        print(f"gemm lt {m}x{n}x{k} err={err:.3e}", flush=True)
+        assert err <= 1e-2
