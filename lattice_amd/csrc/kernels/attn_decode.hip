@@ -8,9 +8,14 @@
 // region.  L <= 0 writes zeros.  Accumulation is fp32.
 //
 // MI355X design (the reference uses one scalar thread per (b, h)):
-//  * the work is the list of 32-token tiles of every (sequence b, kv head g),
-//    b-major; every wave (one per workgroup) streams an equal contiguous
-//    slice of that list, so a ragged batch leaves no tail of idle CUs;
+//  * the work is the list of 32-token tiles of every (sequence b, block of
+//    HW kv heads), b-major; every workgroup of HW waves (wave w = kv head
+//    hb*HW + w of the block) streams an equal contiguous slice of that list,
+//    so a ragged batch leaves no tail of idle CUs, and the waves of a
+//    workgroup read the same tokens' rows of neighbouring heads together:
+//    with HW = Hkv a workgroup reads whole token rows (all heads, 2 KiB
+//    contiguous at the Llama-3-8B shape) instead of one head's 256-byte
+//    pieces at a 2 KiB stride, which streams ~7% faster from HBM;
 //  * one tile read serves all G = Hq/Hkv query heads of its kv head (GQA
 //    reuse: each K/V byte is read from HBM once);
 //  * every load instruction covers eight tokens x 128 contiguous bytes (whole
@@ -48,10 +53,11 @@ struct AttnParams {
     const uint64_t* offsets_f16;
     float* part_acc;        // [waves][2][G][D]  (slot 0: head of slice, 1: tail)
     float* part_ml;         // [waves][2][G][2]  (max in log2 units, denominator)
-    int2* seg_info;         // [B][Hkv]: (first wave, waves) of each (b, g); waves <= 1: no merge
+    int2* seg_info;         // [B][Hkv]: (first slice, slices) of each (b, g); slices <= 1: no merge
     int batch, num_q_heads, kv_heads, group, block_size, mbps;
     int row_bytes, data_bytes;
-    int total_waves;        // grid of the streaming kernel (one wave per workgroup)
+    int hw;                 // waves per workgroup = kv heads per head block (divides Hkv)
+    int total_waves;        // slices = workgroups of the streaming kernel
     int min_tiles;          // smallest slice a wave takes
     float scale_log2;       // scale * log2(e)
 };
@@ -91,8 +97,7 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
 __device__ __forceinline__ int clamp_len(int L, int cap) { return L < 0 ? 0 : (L > cap ? cap : L); }
 __device__ __forceinline__ int tiles_of(int L) { return (L + 31) >> 5; }
 
-// Slice length of one wave for `total` tiles; the attention and the merge
-// kernel must agree on it.
+// Slice length of one workgroup for `total` tiles.
 __device__ __forceinline__ int wave_slice(int total, const AttnParams& p) {
     const int per = (total + p.total_waves - 1) / p.total_waves;
     return per > p.min_tiles ? per : p.min_tiles;
@@ -325,15 +330,18 @@ __device__ __forceinline__ int dim_offset(int db, int lg) {
     }
 }
 
-// Streaming decode attention: one wave per workgroup, each on the slice
-// [gw*per, gw*per + per) of the b-major tile list, with P tiles in flight.
+// Streaming decode attention: workgroup s of HW waves takes the slice
+// [s*per, s*per + per) of the b-major (sequence, head block, tile) list, wave
+// w the kv head hb*HW + w of each entry, with P tiles in flight per wave.
+// The waves share nothing (no LDS, no barrier): the workgroup only places
+// the waves that read one token row's heads on one CU at one time.
 // Read-only tables come as separate restrict arguments so that wave-uniform
 // reads of them compile to scalar loads, which do not wait behind the vector
 // loads in flight.  Past the end of its slice a wave keeps issuing loads, of
 // `idle` (a small workspace region that stays in L2), so that every step has
 // the same loads outstanding and the waits stay exact.
 template <int DT, int D, int BS, int P>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P == 2 ? 2 : 1)))
+__global__ __launch_bounds__(P == 2 ? 512 : 256) __attribute__((amdgpu_waves_per_eu(P == 2 ? 2 : 1)))
 void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
                         const int32_t* __restrict__ sl, const uint64_t* __restrict__ offs,
                         const uint8_t* __restrict__ kreg, const uint8_t* __restrict__ vreg,
@@ -346,20 +354,23 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     constexpr int TK = 2 * LINES;              // loaded fragments per half
     constexpr int DB = D / 16;
     static_assert(!F8 || D == 128, "fp8 pages take the streaming path at head_dim 128");
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int ln = lane & 15;
     const int lg = lane >> 4;
     const int bs = BS > 0 ? BS : p.block_size;
     const int cap = p.mbps * bs;
     const int Hkv = p.kv_heads;
+    const int HW = p.hw;
+    const int NHB = Hkv / HW;
     const int G = p.group;
 
-    // ---- this wave's slice of the tile list ----
+    // ---- this workgroup's slice of the tile list ----
     // lane i of chunk c describes sequence c + i: clamped length, tiles
     auto chunk_vals = [&](int c, int& Lc, int& v) {
         const int bb = c + lane;
         Lc = bb < p.batch ? clamp_len(sl[bb], cap) : 0;
-        v = Hkv * tiles_of(Lc);
+        v = NHB * tiles_of(Lc);
     };
     auto inclusive_scan = [&](int v) {
 #pragma unroll
@@ -385,11 +396,12 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     for (int bb = blockIdx.x; bb < p.batch; bb += gridDim.x) {
         if (clamp_len(sl[bb], cap) > 0) continue;
         uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + static_cast<size_t>(bb) * p.num_q_heads * D;
-        for (int e = lane; e < p.num_q_heads * D; e += 64) o[e] = 0;
-        if (lane < Hkv) p.seg_info[bb * Hkv + lane] = int2{0, 0};
+        for (int e = threadIdx.x; e < p.num_q_heads * D; e += HW * 64) o[e] = 0;
+        for (int e = threadIdx.x; e < Hkv; e += HW * 64) p.seg_info[bb * Hkv + e] = int2{0, 0};
     }
 
     const int slice = static_cast<int>(blockIdx.x);
+    const int gw = slice * HW + wave;   // this wave's partial-result rows
     const int t0 = slice * per;
     if (t0 >= total) return;
     const int n = min(per, total - t0);
@@ -422,7 +434,8 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
         }
     }
 
-    // Cursor over the tile list: (sequence, kv head, tile, length, tiles).
+    // Cursor over the tile list: (sequence, kv head, tile, length, tiles);
+    // g = hb*HW + wave advances by HW from one head block to the next.
     struct Cur {
         int b, g, t, L, nt;
         float ks[F8 ? 4 : 1], vs[F8 ? 4 : 1];   // fp8: page scales of the 8-token groups
@@ -433,14 +446,15 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     ic.nt = tiles_of(ic.L);
     {
         const int rem = t0 - __builtin_amdgcn_readfirstlane(start);
-        ic.g = rem / ic.nt;
-        ic.t = rem - ic.g * ic.nt;
+        const int hb = rem / ic.nt;
+        ic.g = hb * HW + wave;
+        ic.t = rem - hb * ic.nt;
     }
     auto advance = [&](Cur& c) {
         if (++c.t < c.nt) return;
         c.t = 0;
-        if (++c.g < Hkv) return;
-        c.g = 0;
+        if ((c.g += HW) < Hkv) return;
+        c.g = wave;
         ++c.b;
         c.L = clamp_len(sl[c.b], cap);
         c.nt = tiles_of(c.L);
@@ -514,10 +528,10 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
         const float l = wave_sum_across_groups(l_run);
         const bool complete = began_here && c.t == c.nt - 1;
         if (began_here && lane == 0) {
-            // the wave where (b, g) begins tells the merge where its parts are
+            // the slice where (b, g) begins tells the merge where its parts are
             const int first = t0 + i - c.t;
-            const int waves = complete ? 1 : (first + c.nt - 1) / per - slice + 1;
-            p.seg_info[c.b * Hkv + c.g] = int2{slice, waves};
+            const int slices = complete ? 1 : (first + c.nt - 1) / per - slice + 1;
+            p.seg_info[c.b * Hkv + c.g] = int2{slice, slices};
         }
         if (ln < G) {
             if (complete) {
@@ -532,7 +546,7 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
                     *reinterpret_cast<u32x2*>(o + dim_offset<F8>(db, lg)) = w;
                 }
             } else {
-                const size_t unit = static_cast<size_t>(slice) * 2 + (began_here ? 1 : 0);
+                const size_t unit = static_cast<size_t>(gw) * 2 + (began_here ? 1 : 0);
                 float* pa = p.part_acc + (unit * G + ln) * D;
 #pragma unroll
                 for (int db = 0; db < DB; ++db)
@@ -637,9 +651,10 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
     }
 }
 
-// Log-sum-exp merge, one wave per (b, kv head) that spans several waves of
-// the streaming kernel: its partials sit in slot 1 of its first wave wa and
-// in slot 0 of waves wa+1 .. wa+np-1.  Two dependent memory steps: the
+// Log-sum-exp merge, one wave per (b, kv head g) that spans several slices
+// of the streaming kernel: its partials sit in slot 1 of the wave for g of
+// its first slice wa and in slot 0 of that wave of slices wa+1 .. wa+np-1
+// (wave rows (wa + k) * HW + g % HW).  Two dependent memory steps: the
 // segment record, then the (max, denominator) pairs of up to 64 parts (one
 // part per lane) together with the accumulators of the first QP parts; the
 // weights reach every lane through v_readlane.  NO = outputs per lane
@@ -658,7 +673,10 @@ __global__ __launch_bounds__(64) void attn_decode_merge(AttnParams p,
     const int b = blockIdx.x / p.kv_heads;
     const int g = blockIdx.x - b * p.kv_heads;
     const int n_out = G * D / 64;      // lane holds outputs lane + 64e, e < n_out
-    auto unit = [&](int k) { return static_cast<size_t>(wa + k) * 2 + (k == 0 ? 1 : 0); };
+    const int gofs = g % p.hw;
+    auto unit = [&](int k) {
+        return (static_cast<size_t>(wa + k) * p.hw + gofs) * 2 + (k == 0 ? 1 : 0);
+    };
     auto load_parts = [&](float (&v)[QP][NO], int k0) {
 #pragma unroll
         for (int q = 0; q < QP; ++q) {
@@ -833,15 +851,15 @@ int env_int(const char* name, int dflt, int lo, int hi) {
 }
 
 // Tunables, read on every call (getenv is cheap next to a launch):
-// KCMM_ATTN_WAVES waves of the streaming kernel (default by page type), KCMM_ATTN_MIN_TILES the
-// smallest slice a wave takes, KCMM_ATTN_DEPTH tiles in flight (2 or 3).
-// fp8 tiles carry half the bytes of 16-bit ones and use fewer registers
-// (3 waves per SIMD fit), so they need more waves to keep as many bytes in
-// flight (measured at the Llama-3-8B shape: 1024 waves best for 16-bit
-// pages, 3072 for fp8).
+// KCMM_ATTN_WAVES waves of the streaming kernel (default by page type),
+// KCMM_ATTN_HW waves per workgroup (kv heads read together; the largest
+// divisor of Hkv not above it is used), KCMM_ATTN_MIN_TILES the smallest
+// slice a workgroup takes, KCMM_ATTN_DEPTH tiles in flight (2 or 3; 3 keeps
+// at most 4 waves per workgroup).
 int stream_waves(int dtype) {
-    return env_int("KCMM_ATTN_WAVES", dtype == kDtFP8 ? 3072 : 1024, 1, 1 << 20);
+    return env_int("KCMM_ATTN_WAVES", dtype == kDtFP8 ? 2048 : 1024, 1, 1 << 20);
 }
+int stream_hw(int dtype) { return env_int("KCMM_ATTN_HW", dtype == kDtFP8 ? 8 : 4, 1, 8); }
 int stream_min_tiles() { return env_int("KCMM_ATTN_MIN_TILES", 8, 1, 1 << 16); }
 int stream_depth() { return env_int("KCMM_ATTN_DEPTH", 2, 2, 3); }
 
@@ -855,10 +873,16 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
         return false;
     }
     if (p.batch == 0) return true;
+    const int depth = stream_depth();
+    int hw = std::min(stream_hw(DT), depth == 3 ? 4 : 8);
+    while (p.kv_heads % hw) --hw;
+    p.hw = hw;
     p.min_tiles = stream_min_tiles();
-    const long long want = (tmax + p.min_tiles - 1) / p.min_tiles;
-    p.total_waves = static_cast<int>(std::max(1LL, std::min<long long>(stream_waves(DT), want)));
-    const size_t units = static_cast<size_t>(p.total_waves) * 2 * p.group;
+    const long long lists = tmax / p.kv_heads * (p.kv_heads / hw);   // entries of the slice list
+    const long long want = (lists + p.min_tiles - 1) / p.min_tiles;
+    p.total_waves = static_cast<int>(
+        std::max(1LL, std::min<long long>(std::max(1, stream_waves(DT) / hw), want)));
+    const size_t units = static_cast<size_t>(p.total_waves) * hw * 2 * p.group;
     // idle-load region first: it must cover one tile's lane addresses
     const size_t idle_bytes = (static_cast<size_t>(8) * p.row_bytes + 1023) & ~static_cast<size_t>(255);
     void* ws = nullptr;
@@ -874,12 +898,14 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
                                false, err))
         return false;
     p.seg_info = static_cast<int2*>(info);
-    if (stream_depth() == 3)
-        hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 3>), dim3(p.total_waves), dim3(64), 0, s,
-                           p, p.block_tables, p.seq_lens, p.offsets_f16, p.k_base, p.v_base, idle);
+    if (depth == 3)
+        hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 3>), dim3(p.total_waves), dim3(64 * hw),
+                           0, s, p, p.block_tables, p.seq_lens, p.offsets_f16, p.k_base, p.v_base,
+                           idle);
     else
-        hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 2>), dim3(p.total_waves), dim3(64), 0, s,
-                           p, p.block_tables, p.seq_lens, p.offsets_f16, p.k_base, p.v_base, idle);
+        hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 2>), dim3(p.total_waves), dim3(64 * hw),
+                           0, s, p, p.block_tables, p.seq_lens, p.offsets_f16, p.k_base, p.v_base,
+                           idle);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     launch_merge<DT == kDtFP8 ? kDtBF16 : DT, D>(p, s);
     KCMM_HIP_CHECK(hipGetLastError(), err);

@@ -84,6 +84,7 @@ def test_ragged_lengths_and_chunk_edges(gpu_lib, dtype):
     (8, 1, 256, 16),
     (32, 8, 128, 32),    # block size not 16: runtime divide path
     (12, 4, 64, 8),
+    (24, 6, 128, 16),    # 6 kv heads: workgroups of 3 waves (largest divisor <= 4)
 ])
 def test_mfma_path_shapes(gpu_lib, hq, hkv, d, bs):
     rng = np.random.default_rng(hq * d + bs)
@@ -175,16 +176,23 @@ def test_entry_point_variants_agree(gpu_lib):
         case.pool.destroy()
 
 
-@pytest.fixture(params=["default", "depth3", "many_waves"])
+@pytest.fixture(params=["default", "depth3", "many_waves", "one_head_per_wg", "all_heads_per_wg"])
 def stream_tuning(request, monkeypatch):
-    """Streaming-kernel settings: the default, three tiles in flight, and a
-    tiny slice per wave (every (b, kv head) split over many waves, so the
-    log-sum-exp merge runs everywhere)."""
+    """Streaming-kernel settings: the default, three tiles in flight, a tiny
+    slice per workgroup (every (b, kv head) split over many slices, so the
+    log-sum-exp merge runs everywhere), and workgroups of one wave (one kv
+    head) or of eight waves (all kv heads of a token row)."""
     if request.param == "depth3":
         monkeypatch.setenv("KCMM_ATTN_DEPTH", "3")
     elif request.param == "many_waves":
         monkeypatch.setenv("KCMM_ATTN_WAVES", "4096")
         monkeypatch.setenv("KCMM_ATTN_MIN_TILES", "1")
+    elif request.param == "one_head_per_wg":
+        monkeypatch.setenv("KCMM_ATTN_HW", "1")
+    elif request.param == "all_heads_per_wg":
+        monkeypatch.setenv("KCMM_ATTN_HW", "8")
+        monkeypatch.setenv("KCMM_ATTN_WAVES", "2048")
+        monkeypatch.setenv("KCMM_ATTN_MIN_TILES", "2")
     return request.param
 
 
