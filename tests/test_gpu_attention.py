@@ -84,13 +84,29 @@ def test_ragged_lengths_and_chunk_edges(gpu_lib, dtype):
     (8, 1, 256, 16),
     (32, 8, 128, 32),    # block size not 16: runtime divide path
     (12, 4, 64, 8),
-    (24, 6, 128, 16),    # 6 kv heads: workgroups of 3 waves (largest divisor <= 4)
+    (24, 6, 128, 16),    # 6 kv heads
 ])
 def test_mfma_path_shapes(gpu_lib, hq, hkv, d, bs):
     rng = np.random.default_rng(hq * d + bs)
     ctx = rng.integers(1, 700, size=5)
     case = build_decode_case(gpu_lib, batch=5, num_q_heads=hq, kv_heads=hkv, head_dim=d,
                              block_size=bs, ctx_lens=ctx, dtype=KV_BF16, seed=3)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+@pytest.mark.parametrize("hw,hq,hkv", [("4", 24, 6), ("8", 24, 12), ("8", 10, 5)])
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_FP8])
+def test_head_block_not_dividing(gpu_lib, monkeypatch, hw, hq, hkv, dtype):
+    """Workgroups take the largest divisor of Hkv not above KCMM_ATTN_HW
+    (6 kv heads at 4 -> 3, 12 at 8 -> 6, 5 at 8 -> 5)."""
+    monkeypatch.setenv("KCMM_ATTN_HW", hw)
+    rng = np.random.default_rng(hq + hkv)
+    ctx = rng.integers(1, 900, size=7)
+    case = build_decode_case(gpu_lib, batch=7, num_q_heads=hq, kv_heads=hkv, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=dtype, seed=12)
     try:
         check(case)
     finally:
@@ -176,19 +192,20 @@ def test_entry_point_variants_agree(gpu_lib):
         case.pool.destroy()
 
 
-@pytest.fixture(params=["default", "depth3", "many_waves", "one_head_per_wg", "all_heads_per_wg"])
+@pytest.fixture(params=["default", "depth3", "many_waves", "four_heads_per_wg", "all_heads_per_wg"])
 def stream_tuning(request, monkeypatch):
     """Streaming-kernel settings: the default, three tiles in flight, a tiny
     slice per workgroup (every (b, kv head) split over many slices, so the
-    log-sum-exp merge runs everywhere), and workgroups of one wave (one kv
-    head) or of eight waves (all kv heads of a token row)."""
+    log-sum-exp merge runs everywhere), and workgroups of four waves (four
+    kv heads) or of eight waves (all kv heads of a token row); the default
+    is one wave per workgroup for 16-bit pages, eight for fp8."""
     if request.param == "depth3":
         monkeypatch.setenv("KCMM_ATTN_DEPTH", "3")
     elif request.param == "many_waves":
         monkeypatch.setenv("KCMM_ATTN_WAVES", "4096")
         monkeypatch.setenv("KCMM_ATTN_MIN_TILES", "1")
-    elif request.param == "one_head_per_wg":
-        monkeypatch.setenv("KCMM_ATTN_HW", "1")
+    elif request.param == "four_heads_per_wg":
+        monkeypatch.setenv("KCMM_ATTN_HW", "4")
     elif request.param == "all_heads_per_wg":
         monkeypatch.setenv("KCMM_ATTN_HW", "8")
         monkeypatch.setenv("KCMM_ATTN_WAVES", "2048")
