@@ -520,6 +520,7 @@ def main():
         result["gemm_m256"] = gemm_report(m256, 256, False)
         result["gemm_m256"]["backend"] = "hipBLASLt"
         result["gemm_m256_stream_kernel"] = gemm_report(m256_stream, 256, False)
+        result["tiering"] = tiering_report(lib, args)
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))
         log(f"cpu baseline on {threads} threads ...")
@@ -528,6 +529,44 @@ def main():
         result["cpu_baseline"] = None
     case.pool.destroy()
     print(json.dumps(result), flush=True)
+
+
+def tiering_report(lib, args) -> dict:
+    """HBM <-> host swap of whole blocks at the model shape: 32 layers of
+    bf16 K and V pages (Hkv 8, D 128, 16 tokens: 32 KiB each, 2 MiB per block
+    over all layers); kcmm_evict_blocks / kcmm_restore_evicted_blocks of 64
+    blocks (the reference's default batch) timed on the host clock (both are
+    synchronous), best of a few reps."""
+    from lattice_amd.bindings import KV_BF16, make_config
+    cfg = make_config(num_layers=MODEL_LAYERS, kv_heads=8, head_dim=128, max_batch=4,
+                      max_seq_len=4096, tiering=True, max_blocks=512)
+    pool = lib.create_pool(cfg, KV_BF16)
+    try:
+        n = 64
+        blocks = pool.alloc_blocks(n)
+        per_block = 2 * MODEL_LAYERS * pool.stats()["block_bytes"]
+        ev, rs = [], []
+        for rep in range(4):
+            t0 = time.perf_counter()
+            got = pool.evict_blocks(n)
+            t1 = time.perf_counter()
+            pool.restore_blocks(blocks)
+            t2 = time.perf_counter()
+            assert got == n
+            ev.append(t1 - t0)
+            rs.append(t2 - t1)
+        gb = n * per_block / 1e9
+        out = {"blocks_per_call": n, "bytes_per_call": n * per_block,
+               "evict_ms": round(min(ev) * 1e3, 2), "restore_ms": round(min(rs) * 1e3, 2),
+               "evict_gbs": round(gb / min(ev), 2), "restore_gbs": round(gb / min(rs), 2),
+               "note": "host clock around the synchronous C calls; one gather/scatter launch per "
+                       "64 blocks + one 2 MiB copy per block to/from page-locked swap memory; "
+                       "host link PCIe Gen5 x16 (64 GB/s per direction)"}
+        log(f"tiering: evict {out['evict_gbs']} GB/s, restore {out['restore_gbs']} GB/s "
+            f"({n} blocks x {per_block >> 20} MiB)")
+        return out
+    finally:
+        pool.destroy()
 
 
 if __name__ == "__main__":

@@ -69,10 +69,14 @@ class KcmmPoolStats(C.Structure):
 
 
 def make_config(*, num_layers, kv_heads, head_dim, max_batch, max_seq_len, block_size=16,
-                max_blocks=0, device_ordinal=0) -> KcmmConfig:
+                max_blocks=0, device_ordinal=0, tiering=False, eviction_policy=0,
+                max_batch_blocks=0) -> KcmmConfig:
     cfg = KcmmConfig()
     cfg.block_size = block_size
     cfg.max_blocks = max_blocks
+    cfg.tiering = 1 if tiering else 0
+    cfg.eviction_policy = eviction_policy
+    cfg.max_batch_blocks = max_batch_blocks
     cfg.num_layers = num_layers
     cfg.kv_heads = kv_heads
     cfg.head_dim = head_dim
@@ -288,6 +292,53 @@ class KcmmPool:
     def _check(self, rc: int, op: str) -> None:
         if rc != 0:
             raise KcmmError(f"{op} failed: {self.last_error()}")
+
+    # -- tiering (ref ffi.rs:1900-2008, 2195-2272) --
+    LOCATIONS = {0: "gpu", 1: "cpu", 2: "nvme", 3: "evicting", 4: "restoring"}
+
+    def tiering_enabled(self) -> bool:
+        return bool(self.lib.kcmm_is_tiering_enabled(self.handle))
+
+    def evict_blocks(self, count: int) -> int:
+        return self.lib.kcmm_evict_blocks(self.handle, count)
+
+    def restore_block(self, blk: int) -> int:
+        va = self.lib.kcmm_restore_evicted_block(self.handle, blk)
+        if va == 0:
+            raise KcmmError(f"kcmm_restore_evicted_block failed: {self.last_error()}")
+        return va
+
+    def restore_blocks(self, blocks) -> None:
+        blocks = list(blocks)
+        self._check(self.lib.kcmm_restore_evicted_blocks(self.handle, _arr(C.c_uint32, blocks),
+                                                         len(blocks)),
+                    "kcmm_restore_evicted_blocks")
+
+    def block_location(self, blk: int):
+        v = C.c_int(0)
+        if self.lib.kcmm_get_block_location(self.handle, blk, C.byref(v)) != 0:
+            return None
+        return self.LOCATIONS[v.value]
+
+    def is_gpu_resident(self, blk: int) -> bool:
+        return bool(self.lib.kcmm_is_gpu_resident(self.handle, blk))
+
+    def set_eviction_policy(self, name: str) -> None:
+        self._check(self.lib.kcmm_set_eviction_policy(self.handle, name.encode()),
+                    "kcmm_set_eviction_policy")
+
+    def eviction_policy(self) -> str:
+        buf = C.create_string_buffer(64)
+        self.lib.kcmm_get_eviction_policy(self.handle, buf, 64)
+        return buf.value.decode()
+
+    def hint(self, seq: int, hint: int) -> None:
+        self._check(self.lib.kcmm_hint(self.handle, seq, hint), "kcmm_hint")
+
+    def protect(self, seq: int, blocks, level: int) -> None:
+        blocks = list(blocks)
+        self._check(self.lib.kcmm_protect(self.handle, seq, _arr(C.c_uint32, blocks), len(blocks),
+                                          level), "kcmm_protect")
 
     # -- allocation / sequences --
     def alloc_blocks(self, n: int) -> list[int]:

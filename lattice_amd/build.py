@@ -3,7 +3,7 @@
     python -m lattice_amd.build            # build everything
     python -m lattice_amd.build --jobs 8
 
-libkcmm.so: the C++ host runtime (pool_core.cpp, ffi.cpp; g++) plus the HIP
+libkcmm.so: the C++ host runtime (pool_core.cpp, tiering.cpp, ffi.cpp; g++) plus the HIP
 kernels (kernels/*.hip; hipcc --offload-arch=gfx950), linked with hipcc.
 libkcmm_hostcheck.so: the same host runtime over a host-memory page backing
 (tests/hostcheck), so CPU tests exercise the product's bookkeeping code.
@@ -39,10 +39,11 @@ HIP_FLAGS = [
 ]
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 
-HOST_SOURCES = ["pool_core.cpp", "ffi.cpp"]
+HOST_SOURCES = ["pool_core.cpp", "tiering.cpp", "ffi.cpp"]
 HIP_SOURCES = ["kernels/backing.hip", "kernels/attn_decode.hip", "kernels/attn_prefill.hip",
                "kernels/kv_write.hip",
-               "kernels/page_copy.hip", "kernels/gemm.hip", "kernels/gemm_lt.hip", "kernels/glue.hip"]
+               "kernels/page_copy.hip", "kernels/gemm.hip", "kernels/gemm_lt.hip", "kernels/glue.hip",
+               "kernels/tier_copy.hip"]
 
 
 def _run(cmd: list[str]) -> None:

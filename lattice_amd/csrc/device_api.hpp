@@ -22,7 +22,7 @@ bool set_device(int device, std::string* err);
 // Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
 // attention partials, 1: GEMM split partials, 2: decode attention segment
 // table, 3: decode layer-step activations, 4: the final norm's output,
-// 5: hipBLASLt workspace).
+// 5: hipBLASLt workspace, 6: tiering staging on the null stream).
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);
@@ -89,6 +89,19 @@ bool copy_pages(const std::vector<uint64_t>& region_bases, const uint64_t* pair_
 bool copy_pages_device(const std::vector<uint64_t>& region_bases, uint64_t pairs_ptr,
                        uint64_t offsets_f16, size_t num_pairs, uint32_t block_bytes,
                        uint64_t stream, std::string* err);
+
+// Tiering moves (kernels/tier_copy.hip): n whole blocks between the pool's
+// regions (page byte offset pages[b] in every region) and host swap memory
+// (host[b]: the block's slot, regions in order, block_bytes each).  On the
+// null stream; returns when the copies have finished.
+bool tier_evict_copy(const std::vector<uint64_t>& region_bases, const uint64_t* pages,
+                     uint8_t* const* host, size_t n, uint32_t block_bytes, std::string* err);
+bool tier_restore_copy(const std::vector<uint64_t>& region_bases, const uint64_t* pages,
+                       uint8_t* const* host, size_t n, uint32_t block_bytes, std::string* err);
+// Page-locked host memory for the swap buffer (hipHostMalloc), freed only by
+// host_pinned_free.
+bool host_pinned_alloc(size_t bytes, void** out, std::string* err);
+void host_pinned_free(void* p);
 
 // Y = X W^T (+ R when residual != 0; R may be Y), bf16, fp32 accumulate.  With a
 // residual the product is rounded to bf16 before the add, as a bf16 model does.

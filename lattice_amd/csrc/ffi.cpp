@@ -5,6 +5,8 @@
 #include <execinfo.h>
 #include <unistd.h>
 
+#include <algorithm>
+#include <cctype>
 #include <cmath>
 #include <csignal>
 #include <cstdio>
@@ -25,10 +27,33 @@ struct kcmm_pool_t {
     int device = 0;
     std::mutex err_mu;
     std::string last_error;
+    // Host swap buffer of the tiering engine: page-locked chunks of
+    // kSwapChunkBlocks slots, allocated when a slot in them is first used
+    // and kept until the pool is destroyed.  Slots are whole blocks at
+    // multiples of the slot size, so none straddles two chunks.
+    static constexpr size_t kSwapChunkBlocks = 64;
+    std::vector<uint8_t*> swap_chunks;
+    size_t swap_slot_bytes = 0;
+    std::mutex tier_mu;   // one evict / restore data move at a time
 
     void set_error(const std::string& s) {
         std::lock_guard<std::mutex> lk(err_mu);
         last_error = s;
+    }
+    // host address of the swap slot at byte offset off (chunk allocated on demand)
+    uint8_t* swap_slot(uint64_t off, std::string* err) {
+        const size_t chunk_bytes = kSwapChunkBlocks * swap_slot_bytes;
+        const size_t c = static_cast<size_t>(off / chunk_bytes);
+        if (c >= swap_chunks.size()) swap_chunks.resize(c + 1, nullptr);
+        if (swap_chunks[c] == nullptr) {
+            void* p = nullptr;
+            if (!kcmm::dev::host_pinned_alloc(chunk_bytes, &p, err)) return nullptr;
+            swap_chunks[c] = static_cast<uint8_t*>(p);
+        }
+        return swap_chunks[c] + (off - c * chunk_bytes);
+    }
+    ~kcmm_pool_t() {
+        for (uint8_t* c : swap_chunks) kcmm::dev::host_pinned_free(c);
     }
 };
 
@@ -244,6 +269,14 @@ kcmm_pool_t* kcmm_pool_create_typed(const kcmm_config_t* cfg, int32_t kv_dtype) 
     auto* p = new kcmm_pool_t;
     p->core.reset(new kcmm::PoolCore(g, std::move(backing)));
     p->device = device;
+    if (cfg->tiering != 0) {
+        // ref ffi.rs:480-497 defaults, tiering.rs:723-770 swap sizing (max_blocks
+        // blocks of every layer's K and V)
+        const size_t max_blocks = cfg->max_blocks ? cfg->max_blocks : 16384;
+        const size_t max_batch = cfg->max_batch_blocks ? cfg->max_batch_blocks : 64;
+        p->core->enable_tiering(cfg->eviction_policy, max_blocks, max_batch);
+        p->swap_slot_bytes = p->core->block_swap_bytes();
+    }
     return p;
 }
 
@@ -403,13 +436,14 @@ int kcmm_get_all_block_valid(kcmm_pool_t* pool, uint8_t* out, uint32_t max_block
 }
 
 int kcmm_get_block_location(kcmm_pool_t* pool, uint32_t blk, kcmm_block_location_t* loc) {
+    // ref ffi.rs:951-972
     if (pool == nullptr || loc == nullptr) return -1;
-    uint64_t v;
-    if (!pool->core->block_va_offset(blk, &v)) {
+    const int l = pool->core->block_location(blk);
+    if (l < 0) {
         pool->set_error(fmtu("kcmm_get_block_location: block_idx %llu not found", blk));
         return -1;
     }
-    *loc = KCMM_LOC_GPU_RESIDENT;
+    *loc = static_cast<kcmm_block_location_t>(l);
     return 0;
 }
 
@@ -624,26 +658,121 @@ int kcmm_paged_attn_prefill_on_stream(kcmm_pool_t* pool, uint32_t layer_idx, uin
 
 int kcmm_precompile_paged_attn_decode_f16(kcmm_pool_t* pool) { return pool ? 0 : -1; }
 
-// ---- tiering: not built (every block stays resident in HBM) ----------------------
+// ---- tiering: HBM <-> host swap (ref tiering.rs, pool.rs:824-1002) ----------------
 
-uint32_t kcmm_evict_blocks(kcmm_pool_t*, uint32_t) { return 0; }
+namespace {
 
-uint64_t kcmm_restore_evicted_block(kcmm_pool_t* pool, uint32_t blk) {
-    if (pool == nullptr) return 0;
-    uint64_t v = 0;
-    if (!pool->core->block_va_offset(blk, &v)) {
-        pool->set_error(fmtu("kcmm_restore_evicted_block: block_idx %llu not found", blk));
+// every layer's K and V region base, in region order (K0, V0, K1, V1, ...)
+std::vector<uint64_t> region_bases(kcmm_pool_t* pool) {
+    std::vector<uint64_t> r;
+    for (size_t l = 0; l < pool->core->geo().num_layers; ++l) {
+        r.push_back(pool->core->va_k(l));
+        r.push_back(pool->core->va_v(l));
+    }
+    return r;
+}
+
+// Restores the blocks of ids (begin, copy, end); false with *err on failure.
+bool restore_blocks(kcmm_pool_t* pool, const uint32_t* ids, size_t n, std::string* err) {
+    std::lock_guard<std::mutex> lk(pool->tier_mu);
+    std::vector<kcmm::TierMove> moves;
+    bool partial = false;
+    if (!pool->core->begin_restore(ids, n, &moves, &partial, err)) return false;
+    std::string why = *err;
+    if (!moves.empty()) {
+        std::vector<uint64_t> pages;
+        std::vector<uint8_t*> host;
+        std::string cerr;
+        bool ok = true;
+        for (const auto& m : moves) {
+            pages.push_back(m.va_offset);
+            host.push_back(pool->swap_slot(m.cpu_offset, &cerr));
+            ok = ok && host.back() != nullptr;
+        }
+        ok = ok && kcmm::dev::set_device(pool->device, &cerr) &&
+             kcmm::dev::tier_restore_copy(region_bases(pool), pages.data(), host.data(),
+                                          moves.size(),
+                                          static_cast<uint32_t>(pool->core->geo().block_bytes),
+                                          &cerr);
+        pool->core->end_restore(moves, ok);
+        if (!ok) {
+            *err = "restore copy failed: " + cerr;
+            return false;
+        }
+    }
+    if (partial) {
+        *err = why;
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+uint32_t kcmm_evict_blocks(kcmm_pool_t* pool, uint32_t count) {
+    // ref ffi.rs:1900-1945: every in-use GPU-resident block is a candidate
+    if (pool == nullptr || count == 0 || !pool->core->tiering_enabled()) return 0;
+    std::lock_guard<std::mutex> lk(pool->tier_mu);
+    const std::vector<kcmm::TierMove> moves = pool->core->begin_evict(count);
+    if (moves.empty()) return 0;
+    std::vector<uint64_t> pages;
+    std::vector<uint8_t*> host;
+    std::string err;
+    bool ok = true;
+    for (const auto& m : moves) {
+        pages.push_back(m.va_offset);
+        host.push_back(pool->swap_slot(m.cpu_offset, &err));
+        ok = ok && host.back() != nullptr;
+    }
+    ok = ok && kcmm::dev::set_device(pool->device, &err) &&
+         kcmm::dev::tier_evict_copy(region_bases(pool), pages.data(), host.data(), moves.size(),
+                                    static_cast<uint32_t>(pool->core->geo().block_bytes), &err);
+    pool->core->end_evict(moves, ok);
+    if (!ok) {
+        pool->set_error("kcmm_evict_blocks: " + err);
         return 0;
     }
+    return static_cast<uint32_t>(moves.size());
+}
+
+uint64_t kcmm_restore_evicted_block(kcmm_pool_t* pool, uint32_t blk) {
+    // ref ffi.rs:1954-1972, pool.rs:833-884: the block's (new) page offset, 0 on error
+    if (pool == nullptr) return 0;
+    if (!pool->core->tiering_enabled()) {
+        pool->set_error("kcmm_restore_evicted_block: tiering is disabled; cannot restore "
+                        "evicted block");
+        return 0;
+    }
+    std::string err;
+    if (!restore_blocks(pool, &blk, 1, &err)) {
+        pool->set_error("kcmm_restore_evicted_block: " + err);
+        return 0;
+    }
+    uint64_t v = 0;
+    pool->core->block_va_offset(blk, &v);
     return v;
 }
 
-int kcmm_restore_evicted_blocks(kcmm_pool_t*, const uint32_t*, uint32_t) { return 0; }
+int kcmm_restore_evicted_blocks(kcmm_pool_t* pool, const uint32_t* ids, uint32_t count) {
+    // ref ffi.rs:1984-2003
+    if (pool == nullptr || ids == nullptr || count == 0) return 0;
+    std::string err;
+    if (!pool->core->tiering_enabled()) {
+        pool->set_error("kcmm_restore_evicted_blocks: tiering is disabled; cannot restore "
+                        "evicted blocks");
+        return -1;
+    }
+    if (!restore_blocks(pool, ids, count, &err)) {
+        pool->set_error("kcmm_restore_evicted_blocks: " + err);
+        return -1;
+    }
+    return 0;
+}
 
 int kcmm_is_gpu_resident(kcmm_pool_t* pool, uint32_t blk) {
+    // ref ffi.rs:2010-2022
     if (pool == nullptr) return 0;
-    uint64_t v;
-    return pool->core->block_va_offset(blk, &v) ? 1 : 0;
+    return pool->core->block_location(blk) == kcmm::kLocGpu ? 1 : 0;
 }
 
 // ---- metrics ---------------------------------------------------------------------
@@ -677,7 +806,7 @@ int kcmm_get_pool_stats(kcmm_pool_t* pool, kcmm_pool_stats_t* out) {
     out->block_size = s.block_size;
     out->max_blocks_per_seq = s.max_blocks_per_seq;
     out->block_bytes = s.block_bytes;
-    out->tiering_enabled = 0;
+    out->tiering_enabled = pool->core->tiering_enabled() ? 1 : 0;
     out->sharing_enabled = 1;
     out->physical_idle_ratio = s.physical_idle_ratio;
     return 0;
@@ -699,14 +828,33 @@ uint32_t kcmm_active_sequences(kcmm_pool_t* pool) {
 // ---- policy / hints -------------------------------------------------------------------
 
 int kcmm_set_eviction_policy(kcmm_pool_t* pool, const char* policy) {
+    // ref ffi.rs:2200-2231, tiering.rs:851-875 (names are case-insensitive)
     if (pool == nullptr || policy == nullptr) return -1;
-    pool->set_error("kcmm_set_eviction_policy: tiering is disabled");
-    return -1;
+    if (!pool->core->tiering_enabled()) {
+        pool->set_error("kcmm_set_eviction_policy: tiering is disabled");
+        return -1;
+    }
+    std::string name(policy);
+    std::transform(name.begin(), name.end(), name.begin(),
+                   [](unsigned char c) { return static_cast<char>(std::tolower(c)); });
+    if (!pool->core->set_eviction_policy(name)) {
+        pool->set_error("kcmm_set_eviction_policy: unknown eviction policy '" + name +
+                        "' (expected lru, lfu, fifo, arc, or sink_window)");
+        return -1;
+    }
+    return 0;
 }
 
-uint32_t kcmm_get_eviction_policy(kcmm_pool_t*, char*, uint32_t) { return 0; }
+uint32_t kcmm_get_eviction_policy(kcmm_pool_t* pool, char* out, uint32_t max_len) {
+    // ref ffi.rs:2243-2259
+    if (pool == nullptr || out == nullptr || max_len == 0) return 0;
+    if (!pool->core->tiering_enabled()) return 0;
+    return static_cast<uint32_t>(write_c_str(out, max_len, pool->core->eviction_policy_name()));
+}
 
-int kcmm_is_tiering_enabled(kcmm_pool_t*) { return 0; }
+int kcmm_is_tiering_enabled(kcmm_pool_t* pool) {
+    return pool != nullptr && pool->core->tiering_enabled() ? 1 : 0;
+}
 
 int kcmm_hint(kcmm_pool_t* pool, uint32_t seq, kcmm_hint_t hint) {
     // ref ffi.rs:2296-2379 with tiering off: touch/cool and priority class.
@@ -719,7 +867,14 @@ int kcmm_hint(kcmm_pool_t* pool, uint32_t seq, kcmm_hint_t hint) {
         case KCMM_HINT_MULTI_TURN:
         case KCMM_HINT_SYSTEM_PROMPT:
         case KCMM_HINT_ATTENTION_SINK:
-        case KCMM_HINT_HEAVY_HITTER: pool->core->touch(seq); break;
+        case KCMM_HINT_HEAVY_HITTER: {
+            pool->core->touch(seq);
+            // ref ffi.rs:2326-2336: and an access of every block of the table
+            std::vector<uint32_t> table;
+            if (pool->core->tiering_enabled() && pool->core->get_block_table(seq, &table))
+                for (uint32_t b : table) pool->core->policy_access(b);
+            break;
+        }
         case KCMM_HINT_HIGH_PRIORITY:
             pool->core->touch(seq);
             pool->core->set_priority(seq, 3);
@@ -739,9 +894,18 @@ int kcmm_hint(kcmm_pool_t* pool, uint32_t seq, kcmm_hint_t hint) {
 }
 
 int kcmm_protect(kcmm_pool_t* pool, uint32_t, const uint32_t* ids, uint32_t n,
-                 kcmm_protection_t) {
-    // ref ffi.rs:2388-2442: with tiering off only the argument check remains.
+                 kcmm_protection_t level) {
+    // ref ffi.rs:2388-2442: with tiering, never-evict / preferred refresh the
+    // blocks' access, evict-preferred leaves them; an unknown block is an error
     if (pool == nullptr || ids == nullptr || n == 0) return -1;
+    if (!pool->core->tiering_enabled()) return 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (pool->core->block_location(ids[i]) < 0) {
+            pool->set_error(fmtu("kcmm_protect: block_idx %llu not found", ids[i]));
+            return -1;
+        }
+        if (level != KCMM_EVICT_PREFERRED) pool->core->policy_access(ids[i]);
+    }
     return 0;
 }
 
@@ -787,15 +951,6 @@ int kcmm_cow_block_for_append(kcmm_pool_t* pool, uint32_t seq, uint32_t logical,
     return rc;
 }
 
-static std::vector<uint64_t> region_bases(kcmm_pool_t* pool) {
-    std::vector<uint64_t> r;
-    const size_t L = pool->core->geo().num_layers;
-    for (size_t l = 0; l < L; ++l) {
-        r.push_back(pool->core->va_k(l));
-        r.push_back(pool->core->va_v(l));
-    }
-    return r;
-}
 
 int kcmm_copy_blocks_on_stream(kcmm_pool_t* pool, const uint32_t* pairs, uint32_t n,
                                uint64_t stream) {

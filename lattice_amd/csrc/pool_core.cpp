@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <map>
 
 namespace kcmm {
 
@@ -99,6 +100,7 @@ bool PoolCore::alloc_one_locked(uint32_t* id_out, std::string* err) {
     bi.block_index = h.second;
     bi.refcount = 1;
     bi.in_use = true;
+    bi.location = kLocGpu;
     uint32_t id;
     if (!free_ids_.empty()) {
         id = free_ids_.back();
@@ -110,6 +112,7 @@ bool PoolCore::alloc_one_locked(uint32_t* id_out, std::string* err) {
     }
     ++epoch_;
     *id_out = id;
+    if (policy_) policy_->on_allocate(h);   // ref pool.rs:446-449
     return true;
 }
 
@@ -148,9 +151,17 @@ void PoolCore::release_locked(const uint32_t* ids, size_t n) {
             --bi.refcount;
             continue;
         }
+        // ref pool.rs:491-545: a swapped-out block gives back its swap slot,
+        // one in transit is left alone
+        if (bi.location == kLocEvicting || bi.location == kLocRestoring) continue;
         bi.in_use = false;
         bi.refcount = 0;
-        free_handles_.emplace_back(bi.superblock_idx, bi.block_index);
+        if (bi.location == kLocCpu) {
+            if (slots_) slots_->free(bi.cpu_offset, block_swap_bytes_);
+        } else {
+            free_handles_.emplace_back(bi.superblock_idx, bi.block_index);
+        }
+        bi.location = kLocGpu;
         recycled.push_back(id);
     }
     if (!recycled.empty()) {
@@ -358,6 +369,11 @@ int PoolCore::cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src
         return -1;
     }
     if (blocks_[old_id].refcount <= 1) return 0;
+    if (blocks_[old_id].location != kLocGpu) {
+        *err = fmt("kcmm_cow_block_for_append: block %llu is not resident in HBM "
+                   "(restore it first)", old_id);
+        return -1;
+    }
     uint32_t new_id;
     if (!alloc_one_locked(&new_id, err)) return -1;
     seqs_[seq].table[logical] = new_id;
@@ -375,6 +391,10 @@ bool PoolCore::resolve_pairs(const uint32_t* pairs, size_t n, std::vector<uint64
         const uint32_t id = pairs[i];
         if (id >= blocks_.size() || !blocks_[id].in_use) {
             *err = fmt("kcmm_copy_blocks: block %llu not in use", id);
+            return false;
+        }
+        if (blocks_[id].location != kLocGpu) {
+            *err = fmt("kcmm_copy_blocks: block %llu is not resident in HBM", id);
             return false;
         }
         (*out)[i] = blocks_[id].va_offset;
@@ -411,6 +431,11 @@ bool PoolCore::resolve_positions(const uint32_t* seqs, const uint32_t* pos, uint
                        id, blocks_[id].refcount);
             return false;
         }
+        if (blocks_[id].location != kLocGpu) {
+            *err = fmt("kcmm_append_kv_step: block_idx %llu is not resident in HBM "
+                       "(restore it first)", id);
+            return false;
+        }
         out->push_back(RowDst{b, blocks_[id].va_offset, static_cast<uint32_t>(off)});
     }
     return true;
@@ -436,9 +461,203 @@ bool PoolCore::resolve_slots(const int64_t* slots, uint32_t batch, std::vector<R
                        blocks_[id].refcount);
             return false;
         }
+        if (blocks_[id].location != kLocGpu) {
+            *err = fmt("kcmm_append_kv_slots: block_idx %llu is not resident in HBM "
+                       "(restore it first)", id);
+            return false;
+        }
         out->push_back(RowDst{b, blocks_[id].va_offset, off});
     }
     return true;
+}
+
+// ---- tiering ------------------------------------------------------------------
+
+void PoolCore::enable_tiering(int policy, size_t max_blocks, size_t max_batch_blocks) {
+    std::lock_guard<std::mutex> lk(mu_);
+    block_swap_bytes_ = static_cast<uint64_t>(geo_.num_layers) * 2 * geo_.block_bytes;
+    swap_bytes_ = static_cast<uint64_t>(max_blocks) * block_swap_bytes_;
+    max_batch_ = max_batch_blocks;
+    const PolicyKind k = policy == 1 ? PolicyKind::kLfu
+                         : policy == 2 ? PolicyKind::kFifo
+                                       : PolicyKind::kLru;
+    policy_.reset(new EvictionPolicy(k, max_blocks));
+    slots_.reset(new SwapSlots(swap_bytes_));
+}
+
+bool PoolCore::tiering_enabled() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return policy_ != nullptr;
+}
+
+// ref tiering.rs:851-875: a fresh policy, arc sized from the swap buffer
+bool PoolCore::set_eviction_policy(const std::string& name) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (!policy_) return false;
+    PolicyKind k;
+    size_t cap = 1;
+    if (name == "lru") k = PolicyKind::kLru;
+    else if (name == "lfu") k = PolicyKind::kLfu;
+    else if (name == "fifo") k = PolicyKind::kFifo;
+    else if (name == "sink_window") k = PolicyKind::kSinkWindow;
+    else if (name == "arc") {
+        k = PolicyKind::kArc;
+        cap = static_cast<size_t>(swap_bytes_ / std::max<size_t>(max_batch_, 1));
+    } else {
+        return false;
+    }
+    policy_.reset(new EvictionPolicy(k, cap));
+    return true;
+}
+
+std::string PoolCore::eviction_policy_name() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return policy_ ? policy_->name() : "";
+}
+
+int PoolCore::block_location(uint32_t block) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (block >= blocks_.size() || !blocks_[block].in_use) return -1;
+    return blocks_[block].location;
+}
+
+bool PoolCore::policy_access(uint32_t block) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (block >= blocks_.size() || !blocks_[block].in_use) return false;
+    if (policy_) policy_->on_access({blocks_[block].superblock_idx, blocks_[block].block_index});
+    return true;
+}
+
+std::vector<TierMove> PoolCore::begin_evict(uint32_t count) {
+    std::lock_guard<std::mutex> lk(mu_);
+    std::vector<TierMove> moves;
+    if (!policy_ || count == 0) return moves;
+    std::vector<PageHandle> cands;
+    std::map<PageHandle, uint32_t> owner;
+    for (uint32_t i = 0; i < blocks_.size(); ++i) {
+        const BlockInfo& b = blocks_[i];
+        if (!b.in_use || b.location != kLocGpu) continue;
+        const PageHandle h{b.superblock_idx, b.block_index};
+        cands.push_back(h);
+        owner.emplace(h, i);
+    }
+    for (const PageHandle& h : policy_->select_victims(cands, count)) {
+        const uint32_t id = owner.at(h);
+        uint64_t off;
+        if (!slots_->allocate(block_swap_bytes_, &off)) continue;   // swap full: skipped
+        BlockInfo& b = blocks_[id];
+        b.location = kLocEvicting;
+        b.cpu_offset = off;
+        moves.push_back(TierMove{id, b.va_offset, off});
+    }
+    if (!moves.empty()) ++epoch_;
+    return moves;
+}
+
+void PoolCore::end_evict(const std::vector<TierMove>& moves, bool copied) {
+    std::lock_guard<std::mutex> lk(mu_);
+    for (const TierMove& m : moves) {
+        BlockInfo& b = blocks_[m.block];
+        if (copied) {
+            // ref tiering.rs:995-1010, 1172-1176: the page handle returns to
+            // the free list, the policy forgets it
+            free_handles_.emplace_back(b.superblock_idx, b.block_index);
+            b.location = kLocCpu;
+            policy_->on_evict({b.superblock_idx, b.block_index});
+        } else {
+            slots_->free(m.cpu_offset, block_swap_bytes_);
+            b.location = kLocGpu;
+            b.cpu_offset = 0;
+        }
+    }
+    if (!moves.empty()) ++epoch_;
+}
+
+bool PoolCore::begin_restore(const uint32_t* ids, size_t n, std::vector<TierMove>* moves,
+                             bool* partial, std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    moves->clear();
+    *partial = false;
+    if (!policy_) {
+        *err = "tiering is disabled; cannot restore evicted blocks";
+        return false;
+    }
+    // ref pool.rs:905-931: every id checked before anything changes
+    for (size_t i = 0; i < n; ++i) {
+        if (ids[i] >= blocks_.size()) {
+            *err = fmt("block_idx %llu out of bounds", ids[i]);
+            return false;
+        }
+        const BlockInfo& b = blocks_[ids[i]];
+        if (!b.in_use) {
+            *err = fmt("block_idx %llu is not in use", ids[i]);
+            return false;
+        }
+        if (b.location == kLocEvicting || b.location == kLocRestoring) {
+            *err = fmt(b.location == kLocEvicting
+                           ? "block %llu is in transit (Evicting); cannot restore"
+                           : "block %llu is in transit (Restoring); cannot restore",
+                       ids[i]);
+            return false;
+        }
+    }
+    std::vector<uint32_t> todo;
+    for (size_t i = 0; i < n; ++i)
+        if (blocks_[ids[i]].location == kLocCpu &&
+            std::find(todo.begin(), todo.end(), ids[i]) == todo.end())
+            todo.push_back(ids[i]);
+    // ref tiering.rs:1711-1745: fewer than 8 one at a time (the first
+    // failure ends the call), 8 or more as a batch (failures skipped)
+    const bool one_by_one = todo.size() < 8;
+    size_t failed = 0;
+    std::string alloc_err;
+    for (uint32_t id : todo) {
+        if (!ensure_capacity_locked(&alloc_err)) {
+            ++failed;
+            if (one_by_one) break;
+            continue;
+        }
+        const auto h = free_handles_.back();
+        free_handles_.pop_back();
+        BlockInfo& b = blocks_[id];
+        b.superblock_idx = h.first;
+        b.block_index = h.second;
+        b.va_offset = static_cast<uint64_t>(h.first) * kSuperblockBytes +
+                      static_cast<uint64_t>(h.second) * geo_.block_bytes;
+        b.location = kLocRestoring;
+        moves->push_back(TierMove{id, b.va_offset, b.cpu_offset});
+    }
+    if (!moves->empty()) ++epoch_;
+    if (failed > 0) {
+        *partial = true;
+        if (one_by_one)
+            *err = alloc_err;
+        else if (moves->empty())
+            *err = fmt("batched restore could not allocate GPU physical blocks for any of %llu "
+                       "requested blocks", todo.size());
+        else
+            *err = fmt("batched restore only restored %llu of %llu requested blocks",
+                       moves->size(), todo.size());
+    }
+    return true;
+}
+
+void PoolCore::end_restore(const std::vector<TierMove>& moves, bool copied) {
+    std::lock_guard<std::mutex> lk(mu_);
+    for (const TierMove& m : moves) {
+        BlockInfo& b = blocks_[m.block];
+        if (copied) {
+            // ref tiering.rs:1860-1885
+            b.location = kLocGpu;
+            slots_->free(m.cpu_offset, block_swap_bytes_);
+            b.cpu_offset = 0;
+            policy_->on_access({b.superblock_idx, b.block_index});
+        } else {
+            free_handles_.emplace_back(b.superblock_idx, b.block_index);
+            b.location = kLocCpu;
+        }
+    }
+    if (!moves.empty()) ++epoch_;
 }
 
 uint32_t PoolCore::blocks_in_use_locked() const {

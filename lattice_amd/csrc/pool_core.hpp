@@ -29,6 +29,8 @@
 #include <string>
 #include <vector>
 
+#include "tiering.hpp"
+
 namespace kcmm {
 
 constexpr size_t kSuperblockBytes = 2u * 1024u * 1024u;
@@ -71,12 +73,26 @@ struct PoolGeometry {
     bool compute(std::string* err);
 };
 
+// Where a block's data is (kcmm.h kcmm_block_location_t, ref pool.rs:30-45).
+enum BlockLoc : int { kLocGpu = 0, kLocCpu = 1, kLocEvicting = 3, kLocRestoring = 4 };
+
 struct BlockInfo {
     uint64_t va_offset = 0;
     uint32_t superblock_idx = 0;
     uint32_t block_index = 0;
     uint32_t refcount = 0;
     bool in_use = false;
+    int location = kLocGpu;
+    uint64_t cpu_offset = 0;   // swap offset while kLocCpu / kLocEvicting
+};
+
+// One block moving between HBM and the host swap buffer: its page offset in
+// every region (the old one when evicting, the new one when restoring) and
+// its swap offset.
+struct TierMove {
+    uint32_t block;
+    uint64_t va_offset;
+    uint64_t cpu_offset;
 };
 
 struct SequenceState {
@@ -161,6 +177,36 @@ public:
     bool resolve_slots(const int64_t* slots, uint32_t batch, std::vector<RowDst>* out,
                        std::string* err);
 
+    // ---- tiering (ref tiering.rs, pool.rs:824-1002, ffi.rs:1900-2008) ----
+    // Policy 0 lru, 1 lfu, 2 fifo (anything else lru, ref ffi.rs:425-432);
+    // the swap buffer holds max_blocks blocks of every layer's K and V.
+    void enable_tiering(int policy, size_t max_blocks, size_t max_batch_blocks);
+    bool tiering_enabled();
+    bool set_eviction_policy(const std::string& name);   // lru lfu fifo arc sink_window
+    std::string eviction_policy_name();
+    uint64_t swap_bytes() const { return swap_bytes_; }
+    uint64_t block_swap_bytes() const { return block_swap_bytes_; }
+    size_t max_batch_blocks() const { return max_batch_; }
+    int block_location(uint32_t block);   // -1 when not in use
+    // The hint / protect path: on_access of the block's handle; false when
+    // the block is not in use.
+    bool policy_access(uint32_t block);
+    // Eviction in two steps around the data copy: victims chosen by the
+    // policy among GPU-resident blocks (in id order), each given a swap slot
+    // and marked evicting; then, once copied, the page handle goes back to
+    // the free list and the block is swapped out (copied == false rolls back).
+    std::vector<TierMove> begin_evict(uint32_t count);
+    void end_evict(const std::vector<TierMove>& moves, bool copied);
+    // Restore in two steps: ids validated (out of bounds, not in use or in
+    // transit: error, nothing done), swapped-out ids (each once) given a new
+    // page by the allocation rule and marked restoring; fewer than 8 stop at
+    // the first allocation failure, 8 or more skip it (*partial set, *err
+    // says why).  Then, once copied, each block is GPU-resident, its swap
+    // slot free and the policy told of an access.
+    bool begin_restore(const uint32_t* ids, size_t n, std::vector<TierMove>* moves,
+                       bool* partial, std::string* err);
+    void end_restore(const std::vector<TierMove>& moves, bool copied);
+
     Stats stats();
     Metrics metrics();
     bool below_low_watermark(float threshold);
@@ -189,6 +235,11 @@ private:
     std::vector<uint32_t> free_ids_;
     std::vector<SequenceState> seqs_;
     uint64_t epoch_ = 0;
+    // tiering (null policy: disabled)
+    std::unique_ptr<EvictionPolicy> policy_;
+    std::unique_ptr<SwapSlots> slots_;
+    uint64_t swap_bytes_ = 0, block_swap_bytes_ = 0;
+    size_t max_batch_ = 0;
 };
 
 }  // namespace kcmm

@@ -136,14 +136,15 @@ def build_decode_case(lib: KcmmLibrary, *, batch: int, num_q_heads: int, kv_head
                       head_dim: int, block_size: int, ctx_lens, dtype: int = KV_BF16,
                       num_layers: int = 1, seed: int = 0, host_mirror: bool = True,
                       extra_seq_len: int = 0, device: str = "cuda",
-                      shuffle: bool = True) -> DecodeCase:
+                      shuffle: bool = True, tiering: bool = False) -> DecodeCase:
     """Allocate pages for `ctx_lens` tokens per sequence (+ `extra_seq_len`
     page headroom), shuffle them over the pool, fill them and upload q."""
     rng = np.random.default_rng(seed)
     ctx = np.asarray(ctx_lens, dtype=np.int64)
     max_len = int(max(1, ctx.max() + extra_seq_len))
     cfg = make_config(num_layers=num_layers, kv_heads=kv_heads, head_dim=head_dim,
-                      max_batch=batch, max_seq_len=max_len, block_size=block_size)
+                      max_batch=batch, max_seq_len=max_len, block_size=block_size,
+                      tiering=tiering)
     pool = lib.create_pool(cfg, dtype)
     pages = [max(1, -(-int(L + extra_seq_len) // block_size)) for L in ctx]
     ids = []

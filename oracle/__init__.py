@@ -68,6 +68,24 @@ def _bind(l: C.CDLL) -> None:
         "opool_stats": ([P, P], None),
         "opool_metrics": ([P, P], None),
         "opool_below_low_watermark": ([P, F], C.c_int),
+        "opool_enable_tiering": ([P, C.c_int, C.c_size_t, C.c_size_t], C.c_int),
+        "opool_set_policy": ([P, C.c_char_p], C.c_int),
+        "opool_policy_name": ([P], C.c_char_p),
+        "opool_location": ([P, U32], C.c_int),
+        "opool_cpu_offset": ([P, U32], C.c_uint64),
+        "opool_access": ([P, U32], C.c_int),
+        "opool_evict": ([P, U32, P], U32),
+        "opool_restore_one": ([P, U32, P], C.c_int),
+        "opool_restore": ([P, P, U32], C.c_int),
+        "otier_new": ([C.c_int, C.c_size_t, C.c_uint64, C.c_uint64], P),
+        "otier_free": ([P], None),
+        "otier_event": ([P, C.c_int, U32, U32], None),
+        "otier_select": ([P, P, C.c_size_t, C.c_size_t, P], C.c_size_t),
+        "otier_slot_alloc": ([P, C.c_uint64, P], C.c_int),
+        "otier_slot_free": ([P, C.c_uint64, C.c_uint64], None),
+        "otier_ranges": ([P, P, C.c_size_t], C.c_size_t),
+        "otier_arc_list": ([P, C.c_int, P, C.c_size_t], C.c_size_t),
+        "otier_arc_p": ([P], C.c_size_t),
         "oracle_kv_write_rows": ([C.c_int, P, P, P, P, P, P, P, U32, U32, U32, U32, U32], C.c_int),
         "oracle_kv_write_device_slots": ([C.c_int, P, P, P, P, P, U32, P, P, U32, U32, U32, U32,
                                           U32, U32, P], C.c_int),
@@ -203,6 +221,89 @@ class OraclePool:
 
     def below_low_watermark(self, t) -> bool:
         return bool(lib().opool_below_low_watermark(self._h, t))
+
+    # tiering (ref tiering.rs, pool.rs:824-1002, ffi.rs:1900-2008)
+    def enable_tiering(self, policy=0, max_blocks=0, max_batch_blocks=0):
+        return lib().opool_enable_tiering(self._h, policy, max_blocks, max_batch_blocks) == 0
+
+    def set_policy(self, name: str) -> bool:
+        return lib().opool_set_policy(self._h, name.encode()) == 0
+
+    def policy_name(self) -> str:
+        return lib().opool_policy_name(self._h).decode()
+
+    def location(self, blk) -> int | None:
+        v = lib().opool_location(self._h, blk)
+        return None if v < 0 else v
+
+    def cpu_offset(self, blk):
+        v = lib().opool_cpu_offset(self._h, blk)
+        return None if v == 2**64 - 1 else v
+
+    def access(self, blk) -> bool:
+        return lib().opool_access(self._h, blk) == 0
+
+    def evict(self, count) -> list[int]:
+        out = np.zeros(max(self.stats()["total_blocks"], 1), dtype=np.uint32)
+        n = lib().opool_evict(self._h, count, _p(out))
+        return out[:n].tolist()
+
+    def restore_one(self, blk):
+        v = C.c_uint64(0)
+        return None if lib().opool_restore_one(self._h, blk, C.byref(v)) else v.value
+
+    def restore(self, ids) -> bool:
+        a = np.asarray(ids, dtype=np.uint32)
+        return lib().opool_restore(self._h, _p(a) if a.size else None, a.size) == 0
+
+
+class OracleTier:
+    """One eviction policy + swap-slot allocator (ref tiering.rs:25-643),
+    with handles as (superblock, index) tuples."""
+    POLICIES = {"lru": 0, "lfu": 1, "fifo": 2, "arc": 3, "sink_window": 4}
+
+    def __init__(self, policy="lru", arc_capacity=1, swap_size=0, per_block=0):
+        self._h = lib().otier_new(self.POLICIES[policy], arc_capacity, swap_size, per_block)
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().otier_free(self._h)
+            self._h = None
+
+    def on_allocate(self, h):
+        lib().otier_event(self._h, 0, h[0], h[1])
+
+    def on_access(self, h):
+        lib().otier_event(self._h, 1, h[0], h[1])
+
+    def on_evict(self, h):
+        lib().otier_event(self._h, 2, h[0], h[1])
+
+    def select_victims(self, cands, count):
+        a = np.asarray(cands, dtype=np.uint32).reshape(-1)
+        out = np.zeros(max(a.size, 2), dtype=np.uint32)
+        n = lib().otier_select(self._h, _p(a) if a.size else None, a.size // 2, count, _p(out))
+        return [tuple(int(v) for v in out[2 * i:2 * i + 2]) for i in range(n)]
+
+    def allocate(self, size):
+        v = C.c_uint64(0)
+        return None if lib().otier_slot_alloc(self._h, size, C.byref(v)) else v.value
+
+    def free(self, off, size):
+        lib().otier_slot_free(self._h, off, size)
+
+    def free_ranges(self):
+        out = np.zeros(2 * 4096, dtype=np.uint64)
+        n = lib().otier_ranges(self._h, _p(out), 4096)
+        return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(n)]
+
+    def arc_list(self, which):
+        out = np.zeros(2 * 4096, dtype=np.uint32)
+        n = lib().otier_arc_list(self._h, {"t1": 0, "t2": 1, "b1": 2, "b2": 3}[which], _p(out), 4096)
+        return [tuple(int(v) for v in out[2 * i:2 * i + 2]) for i in range(n)]
+
+    def arc_p(self):
+        return lib().otier_arc_p(self._h)
 
 
 # ---- KV write / page copy ------------------------------------------------------

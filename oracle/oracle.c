@@ -140,7 +140,11 @@ typedef struct {
     uint32_t sb, idx;
     uint32_t refcount;
     int in_use;
+    int loc;            /* 0 GPU, 1 CPU swap, 3 evicting, 4 restoring (kcmm.h:63-68) */
+    uint64_t cpu_off;   /* swap offset while loc == 1 */
 } OBlock;
+
+typedef struct OTier OTier;
 
 typedef struct {
     uint32_t *table;
@@ -160,7 +164,12 @@ struct OPool {
     size_t nfree_ids, cap_free_ids;
     OSeq *seqs;
     size_t nseqs, cap_seqs;
+    OTier *tier;             /* NULL: tiering disabled */
 };
+
+static void tier_on_allocate(OTier *t, Handle h);
+static void tier_free_slot(OTier *t, uint64_t off);
+static void tier_delete(OTier *t);
 
 static void *grow(void *p, size_t *cap, size_t need, size_t elem) {
     if (need <= *cap) return p;
@@ -199,6 +208,7 @@ void opool_delete(OPool *p) {
     for (size_t l = 0; l < 2 * p->num_layers; ++l) free(p->pools[l].free);
     for (size_t s = 0; s < p->nseqs; ++s) free(p->seqs[s].table);
     free(p->pools); free(p->blocks); free(p->free_ids); free(p->seqs);
+    if (p->tier) tier_delete(p->tier);
     free(p);
 }
 
@@ -231,6 +241,7 @@ static int alloc_one(OPool *p, uint32_t *id_out) {
     OBlock b;
     b.va = (uint64_t)h.sb * SB_BYTES + (uint64_t)h.idx * p->block_bytes;
     b.sb = h.sb; b.idx = h.idx; b.refcount = 1; b.in_use = 1;
+    b.loc = 0; b.cpu_off = 0;
     uint32_t id;
     if (p->nfree_ids > 0) {
         id = p->free_ids[--p->nfree_ids];
@@ -241,6 +252,7 @@ static int alloc_one(OPool *p, uint32_t *id_out) {
         p->blocks[id] = b;
     }
     *id_out = id;
+    if (p->tier) tier_on_allocate(p->tier, h);   /* ref pool.rs:446-449 */
     return 0;
 }
 
@@ -287,7 +299,12 @@ void opool_release(OPool *p, const uint32_t *ids, uint32_t n) {
         if (b->refcount > 1) { b->refcount--; continue; }
         b->in_use = 0;
         b->refcount = 0;
-        push_handle(p, b->sb, b->idx);
+        /* ref pool.rs:491-545: a swapped-out block gives back its swap slot */
+        if (b->loc == 1) {
+            if (p->tier) tier_free_slot(p->tier, b->cpu_off);
+        } else {
+            push_handle(p, b->sb, b->idx);
+        }
         p->free_ids = (uint32_t *)grow(p->free_ids, &p->cap_free_ids, p->nfree_ids + 1,
                                        sizeof(uint32_t));
         p->free_ids[p->nfree_ids++] = id;
@@ -409,6 +426,7 @@ int opool_cow(OPool *p, uint32_t seq, uint32_t logical, uint32_t *src, uint32_t 
     uint32_t old = p->seqs[seq].table[logical];
     if (old >= p->nblocks || !p->blocks[old].in_use) return -1;
     if (p->blocks[old].refcount <= 1) return 0;
+    if (p->blocks[old].loc != 0) return -1;   /* page data must be in HBM to copy */
     uint32_t nid;
     if (alloc_one(p, &nid)) return -1;
     p->seqs[seq].table[logical] = nid;
@@ -480,6 +498,474 @@ int opool_below_low_watermark(OPool *p, float threshold) {
     if (!total) return 0;
     return (float)p->pools[0].nfree / (float)total < threshold;
 }
+
+/* ======================================================================
+ * Tiering: HBM <-> host swap of whole blocks (all layers' K and V).
+ * Restates ref tiering.rs: the eviction policies (:25-545), the swap-slot
+ * allocator (:547-643), evict (:937-1406) and restore (:1476-1935), and the
+ * pool side (pool.rs:412-454 on_allocate, :478-549 free, :824-936 restore,
+ * :983-1002 physical release; ffi.rs:1900-2008 the C entry points).
+ * Time stamps are a logical clock (one tick per policy event) instead of
+ * Instant::now(): the same order, without ties.
+ * Deviation: a victim handle maps to the GPU-resident block that owns it
+ * (ref find_block_idx, pool.rs:769-779, takes the first in-use block with
+ * that handle, which can be a swapped-out block whose stale handle was
+ * reissued).
+ * ====================================================================== */
+
+enum { POL_LRU = 0, POL_LFU = 1, POL_FIFO = 2, POL_ARC = 3, POL_SINK = 4 };
+
+typedef struct { Handle h; uint64_t v; } PolEntry;
+typedef struct { Handle *a; size_t n, cap; } HList;
+typedef struct { uint64_t start, end; } ORange;
+
+struct OTier {
+    int policy;
+    uint64_t clock;
+    PolEntry *map; size_t nmap, cap_map;      /* lru/fifo/sink: time; lfu: count */
+    HList t1, t2, b1, b2;                     /* arc (index 0 = MRU end) */
+    size_t arc_p, arc_cap;
+    ORange *fr; size_t nfr, cap_fr;           /* free swap ranges, sorted by start */
+    uint64_t swap_size, per_block;
+    size_t max_batch;
+};
+
+static int heq(Handle a, Handle b) { return a.sb == b.sb && a.idx == b.idx; }
+
+static PolEntry *map_find(OTier *t, Handle h) {
+    for (size_t i = 0; i < t->nmap; ++i) if (heq(t->map[i].h, h)) return &t->map[i];
+    return NULL;
+}
+static void map_set(OTier *t, Handle h, uint64_t v) {
+    PolEntry *e = map_find(t, h);
+    if (e) { e->v = v; return; }
+    t->map = (PolEntry *)grow(t->map, &t->cap_map, t->nmap + 1, sizeof(PolEntry));
+    t->map[t->nmap].h = h;
+    t->map[t->nmap].v = v;
+    t->nmap++;
+}
+static void map_remove(OTier *t, Handle h) {
+    for (size_t i = 0; i < t->nmap; ++i)
+        if (heq(t->map[i].h, h)) { t->map[i] = t->map[--t->nmap]; return; }
+}
+
+static long hl_find(HList *l, Handle h) {
+    for (size_t i = 0; i < l->n; ++i) if (heq(l->a[i], h)) return (long)i;
+    return -1;
+}
+static void hl_insert(HList *l, size_t at, Handle h) {
+    l->a = (Handle *)grow(l->a, &l->cap, l->n + 1, sizeof(Handle));
+    memmove(l->a + at + 1, l->a + at, (l->n - at) * sizeof(Handle));
+    l->a[at] = h;
+    l->n++;
+}
+static void hl_remove_at(HList *l, size_t at) {
+    memmove(l->a + at, l->a + at + 1, (l->n - at - 1) * sizeof(Handle));
+    l->n--;
+}
+static void hl_push_bounded(HList *l, Handle h, size_t cap) {
+    hl_insert(l, l->n, h);
+    while (l->n > cap) hl_remove_at(l, 0);
+}
+
+/* ARC replace(): ref tiering.rs:269-296 */
+static void arc_replace(OTier *t) {
+    if (t->t1.n > 0 && (t->t1.n > t->arc_p || t->t2.n == 0)) {
+        Handle v = t->t1.a[t->t1.n - 1];
+        t->t1.n--;
+        hl_push_bounded(&t->b1, v, t->arc_cap);
+    } else if (t->t2.n > 0) {
+        Handle v = t->t2.a[t->t2.n - 1];
+        t->t2.n--;
+        hl_push_bounded(&t->b2, v, t->arc_cap);
+    }
+}
+
+/* on_allocate: ref tiering.rs:75-77 (lru), :128-130 (lfu), :184-186 (fifo),
+ * :299-337 (arc), :492-494 (sink_window) */
+static void tier_on_allocate(OTier *t, Handle h) {
+    switch (t->policy) {
+    case POL_LFU: map_set(t, h, 1); break;
+    case POL_ARC: {
+        long i1 = hl_find(&t->b1, h);
+        if (i1 >= 0) hl_remove_at(&t->b1, (size_t)i1);
+        long i2 = hl_find(&t->b2, h);
+        if (i2 >= 0) hl_remove_at(&t->b2, (size_t)i2);
+        if (i1 >= 0) {
+            size_t nb2 = t->b2.n ? t->b2.n : 1, nb1 = t->b1.n ? t->b1.n : 1;
+            size_t d = nb2 / nb1; if (d < 1) d = 1;
+            t->arc_p = t->arc_p + d < t->arc_cap ? t->arc_p + d : t->arc_cap;
+            hl_insert(&t->t2, 0, h);
+        } else if (i2 >= 0) {
+            size_t nb1 = t->b1.n ? t->b1.n : 1, nb2 = t->b2.n ? t->b2.n : 1;
+            size_t d = nb1 / nb2; if (d < 1) d = 1;
+            t->arc_p = t->arc_p > d ? t->arc_p - d : 0;
+            hl_insert(&t->t2, 0, h);
+        } else {
+            hl_insert(&t->t1, 0, h);
+        }
+        while (t->t1.n + t->t2.n > t->arc_cap) arc_replace(t);
+        break;
+    }
+    default: map_set(t, h, ++t->clock); break;
+    }
+}
+
+/* on_access: ref tiering.rs:94-96, :147-150, :203-206 (fifo: none),
+ * :376-393 (arc), :526-528 */
+static void tier_on_access(OTier *t, Handle h) {
+    switch (t->policy) {
+    case POL_FIFO: break;
+    case POL_LFU: {
+        PolEntry *e = map_find(t, h);
+        if (e) e->v++; else map_set(t, h, 1);
+        break;
+    }
+    case POL_ARC: {
+        long i = hl_find(&t->t1, h);
+        if (i >= 0) { hl_remove_at(&t->t1, (size_t)i); hl_insert(&t->t2, 0, h); break; }
+        i = hl_find(&t->t2, h);
+        if (i >= 0) { hl_remove_at(&t->t2, (size_t)i); hl_insert(&t->t2, 0, h); }
+        break;
+    }
+    default: map_set(t, h, ++t->clock); break;
+    }
+}
+
+/* on_evict: ref tiering.rs:98-100, :152-154, :208-210, :395-424, :530-533 */
+static void tier_on_evict(OTier *t, Handle h) {
+    if (t->policy != POL_ARC) { map_remove(t, h); return; }
+    long i = hl_find(&t->t1, h);
+    if (i >= 0) {
+        hl_remove_at(&t->t1, (size_t)i);
+        if (hl_find(&t->b1, h) < 0) hl_push_bounded(&t->b1, h, t->arc_cap);
+        return;
+    }
+    i = hl_find(&t->t2, h);
+    if (i >= 0) {
+        hl_remove_at(&t->t2, (size_t)i);
+        if (hl_find(&t->b2, h) < 0) hl_push_bounded(&t->b2, h, t->arc_cap);
+    }
+}
+
+/* select_victims: candidates in order, keyed, stable sort ascending,
+ * truncated (ref tiering.rs:79-92, :132-145, :188-201, :339-374, :497-524).
+ * Untracked candidates are dropped except under ARC (score |T1|+|T2|+1). */
+static size_t tier_select(OTier *t, const Handle *cand, size_t n, size_t count, Handle *out) {
+    if (n == 0 || count == 0) return 0;
+    PolEntry *k = (PolEntry *)malloc(n * sizeof(PolEntry));
+    size_t m = 0;
+    for (size_t i = 0; i < n; ++i) {
+        if (t->policy == POL_ARC) {
+            long p1 = -1, p2 = -1;
+            for (size_t j = t->t1.n; j-- > 0;) if (heq(t->t1.a[j], cand[i])) { p1 = (long)(t->t1.n - 1 - j); break; }
+            if (p1 < 0)
+                for (size_t j = t->t2.n; j-- > 0;) if (heq(t->t2.a[j], cand[i])) { p2 = (long)(t->t2.n - 1 - j); break; }
+            k[m].h = cand[i];
+            k[m].v = p1 >= 0 ? (uint64_t)p1 : p2 >= 0 ? t->t1.n + (uint64_t)p2 : t->t1.n + t->t2.n + 1;
+            m++;
+        } else {
+            PolEntry *e = map_find(t, cand[i]);
+            if (!e) continue;
+            k[m].h = cand[i];
+            k[m].v = e->v;
+            m++;
+        }
+    }
+    /* stable insertion sort by key */
+    for (size_t i = 1; i < m; ++i) {
+        PolEntry x = k[i];
+        size_t j = i;
+        while (j > 0 && k[j - 1].v > x.v) { k[j] = k[j - 1]; --j; }
+        k[j] = x;
+    }
+    size_t r = m < count ? m : count;
+    for (size_t i = 0; i < r; ++i) out[i] = k[i].h;
+    free(k);
+    return r;
+}
+
+/* swap-slot allocator: best fit, shrink from the left; free merges
+ * (ref tiering.rs:578-643) */
+static int tier_alloc_slot(OTier *t, uint64_t size, uint64_t *off) {
+    if (size == 0 || t->nfr == 0) return -1;
+    size_t best = (size_t)-1;
+    uint64_t best_len = UINT64_MAX;
+    for (size_t i = 0; i < t->nfr; ++i) {
+        uint64_t len = t->fr[i].end - t->fr[i].start;
+        if (len >= size && len < best_len) { best_len = len; best = i; }
+    }
+    if (best == (size_t)-1) return -1;
+    *off = t->fr[best].start;
+    if (best_len == size) {
+        memmove(t->fr + best, t->fr + best + 1, (t->nfr - best - 1) * sizeof(ORange));
+        t->nfr--;
+    } else {
+        t->fr[best].start += size;
+    }
+    return 0;
+}
+static void tier_free_range(OTier *t, uint64_t off, uint64_t size) {
+    if (size == 0) return;
+    uint64_t end = off + size;
+    size_t at = 0;
+    while (at < t->nfr && !(t->fr[at].start > off)) ++at;
+    int mp = at > 0 && t->fr[at - 1].end == off;
+    int mn = at < t->nfr && t->fr[at].start == end;
+    if (mp && mn) {
+        t->fr[at - 1].end = t->fr[at].end;
+        memmove(t->fr + at, t->fr + at + 1, (t->nfr - at - 1) * sizeof(ORange));
+        t->nfr--;
+    } else if (mp) {
+        t->fr[at - 1].end = end;
+    } else if (mn) {
+        t->fr[at].start = off;
+    } else {
+        t->fr = (ORange *)grow(t->fr, &t->cap_fr, t->nfr + 1, sizeof(ORange));
+        memmove(t->fr + at + 1, t->fr + at, (t->nfr - at) * sizeof(ORange));
+        t->fr[at].start = off;
+        t->fr[at].end = end;
+        t->nfr++;
+    }
+}
+static void tier_free_slot(OTier *t, uint64_t off) { tier_free_range(t, off, t->per_block); }
+
+static void tier_reset_policy(OTier *t, int policy, size_t arc_cap) {
+    t->policy = policy;
+    t->nmap = 0;
+    t->t1.n = t->t2.n = t->b1.n = t->b2.n = 0;
+    t->arc_p = 0;
+    t->arc_cap = arc_cap ? arc_cap : 1;
+}
+
+static void tier_delete(OTier *t) {
+    free(t->map); free(t->t1.a); free(t->t2.a); free(t->b1.a); free(t->b2.a); free(t->fr);
+    free(t);
+}
+
+/* ref ffi.rs:480-497 (defaults), tiering.rs:723-826 (sizing, policy) */
+int opool_enable_tiering(OPool *p, int policy, size_t max_blocks, size_t max_batch_blocks) {
+    if (p->tier) return -1;
+    OTier *t = (OTier *)calloc(1, sizeof(OTier));
+    if (!max_blocks) max_blocks = 16384;
+    if (!max_batch_blocks) max_batch_blocks = 64;
+    t->per_block = (uint64_t)p->num_layers * 2 * p->block_bytes;
+    t->swap_size = (uint64_t)max_blocks * t->per_block;
+    t->max_batch = max_batch_blocks;
+    /* ffi.rs:425-432: only 0/1/2 name a policy, anything else is LRU */
+    tier_reset_policy(t, policy == 1 ? POL_LFU : policy == 2 ? POL_FIFO : POL_LRU, max_blocks);
+    if (t->swap_size) {
+        t->fr = (ORange *)malloc(sizeof(ORange));
+        t->fr[0].start = 0;
+        t->fr[0].end = t->swap_size;
+        t->nfr = 1;
+        t->cap_fr = 1;
+    }
+    p->tier = t;
+    return 0;
+}
+
+/* ref tiering.rs:851-875: a fresh policy (no history); arc sized from the
+ * swap buffer, sink_window (1, 4) */
+int opool_set_policy(OPool *p, const char *name) {
+    if (!p->tier) return -1;
+    OTier *t = p->tier;
+    if (!strcmp(name, "lru")) tier_reset_policy(t, POL_LRU, 0);
+    else if (!strcmp(name, "lfu")) tier_reset_policy(t, POL_LFU, 0);
+    else if (!strcmp(name, "fifo")) tier_reset_policy(t, POL_FIFO, 0);
+    else if (!strcmp(name, "arc")) {
+        size_t cap = (size_t)(t->swap_size / (t->max_batch ? t->max_batch : 1));
+        tier_reset_policy(t, POL_ARC, cap ? cap : 1);
+    } else if (!strcmp(name, "sink_window")) tier_reset_policy(t, POL_SINK, 0);
+    else return -1;
+    return 0;
+}
+
+const char *opool_policy_name(OPool *p) {
+    static const char *names[] = {"lru", "lfu", "fifo", "arc", "sink_window"};
+    return p->tier ? names[p->tier->policy] : "";
+}
+
+int opool_location(OPool *p, uint32_t blk) {
+    if (blk >= p->nblocks || !p->blocks[blk].in_use) return -1;
+    return p->blocks[blk].loc;
+}
+
+uint64_t opool_cpu_offset(OPool *p, uint32_t blk) {
+    if (blk >= p->nblocks || !p->blocks[blk].in_use || p->blocks[blk].loc != 1) return UINT64_MAX;
+    return p->blocks[blk].cpu_off;
+}
+
+/* the hint / protect path: on_access of an in-use block's handle
+ * (ref ffi.rs:2326-2336, 2404-2421) */
+int opool_access(OPool *p, uint32_t blk) {
+    if (!p->tier) return 0;
+    if (blk >= p->nblocks || !p->blocks[blk].in_use) return -1;
+    Handle h = {p->blocks[blk].sb, p->blocks[blk].idx};
+    tier_on_access(p->tier, h);
+    return 0;
+}
+
+/* kcmm_evict_blocks (ref ffi.rs:1900-1945, tiering.rs:1064-1111 and the
+ * unbatched / batched paths :1113-1406, which agree on the state they leave):
+ * candidates = handles of in-use GPU-resident blocks in id order; victims by
+ * the policy; per victim a swap slot (skipped when none is left); then each
+ * victim's handle returns to the free list, the block becomes CPU-resident
+ * and the policy forgets the handle.  Returns the number evicted; out gets
+ * their block ids in victim order. */
+uint32_t opool_evict(OPool *p, uint32_t count, uint32_t *out) {
+    OTier *t = p->tier;
+    if (!t || count == 0) return 0;
+    Handle *cand = (Handle *)malloc((p->nblocks + 1) * sizeof(Handle));
+    size_t nc = 0;
+    for (size_t i = 0; i < p->nblocks; ++i)
+        if (p->blocks[i].in_use && p->blocks[i].loc == 0) {
+            cand[nc].sb = p->blocks[i].sb;
+            cand[nc].idx = p->blocks[i].idx;
+            nc++;
+        }
+    Handle *vic = (Handle *)malloc((nc + 1) * sizeof(Handle));
+    size_t nv = tier_select(t, cand, nc, count, vic);
+    uint32_t done = 0;
+    for (size_t v = 0; v < nv; ++v) {
+        uint32_t id = UINT32_MAX;
+        for (size_t i = 0; i < p->nblocks; ++i)
+            if (p->blocks[i].in_use && p->blocks[i].loc == 0 && p->blocks[i].sb == vic[v].sb &&
+                p->blocks[i].idx == vic[v].idx) { id = (uint32_t)i; break; }
+        if (id == UINT32_MAX) continue;
+        uint64_t off;
+        if (tier_alloc_slot(t, t->per_block, &off)) continue;
+        p->blocks[id].loc = 3;
+        p->blocks[id].cpu_off = off;
+        out[done++] = id;
+    }
+    for (uint32_t j = 0; j < done; ++j) {
+        OBlock *b = &p->blocks[out[j]];
+        Handle h = {b->sb, b->idx};
+        push_handle(p, b->sb, b->idx);
+        b->loc = 1;
+        tier_on_evict(t, h);
+    }
+    free(cand);
+    free(vic);
+    return done;
+}
+
+/* restore of one block (ref tiering.rs:1801-1935): new handle by the
+ * allocation rule (growth included), block re-pointed, swap slot freed,
+ * on_access(new handle). */
+static int restore_one(OPool *p, uint32_t id) {
+    OTier *t = p->tier;
+    OBlock *b = &p->blocks[id];
+    if (ensure_capacity(p)) return -1;
+    Handle h = {0, 0};
+    for (size_t l = 0; l < 2 * p->num_layers; ++l) {
+        LayerPool *lp = &p->pools[l];
+        Handle x = lp->free[--lp->nfree];
+        if (l == 0) h = x;
+    }
+    b = &p->blocks[id];
+    b->sb = h.sb;
+    b->idx = h.idx;
+    b->va = (uint64_t)h.sb * SB_BYTES + (uint64_t)h.idx * p->block_bytes;
+    tier_free_slot(t, b->cpu_off);
+    b->loc = 0;
+    b->cpu_off = 0;
+    tier_on_access(t, h);
+    return 0;
+}
+
+/* kcmm_restore_evicted_block (ref pool.rs:833-884): 0 and an error when
+ * tiering is off, the block is not in use or in transit; a GPU-resident
+ * block returns its offset. */
+int opool_restore_one(OPool *p, uint32_t blk, uint64_t *va) {
+    if (!p->tier || blk >= p->nblocks || !p->blocks[blk].in_use) return -1;
+    OBlock *b = &p->blocks[blk];
+    if (b->loc == 0) { *va = b->va; return 0; }
+    if (b->loc != 1) return -1;
+    if (restore_one(p, blk)) return -1;
+    *va = p->blocks[blk].va;
+    return 0;
+}
+
+/* kcmm_restore_evicted_blocks (ref pool.rs:895-936, tiering.rs:1711-1745):
+ * every id validated first (out of bounds / not in use / in transit: error,
+ * nothing done); GPU-resident ids skipped; a repeated id restores once.
+ * Fewer than 8 blocks: one at a time, stopping at the first failure; 8 or
+ * more: a failed block stays swapped out and the call reports an error. */
+int opool_restore(OPool *p, const uint32_t *ids, uint32_t n) {
+    if (!p->tier) return -1;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (ids[i] >= p->nblocks || !p->blocks[ids[i]].in_use) return -1;
+        int l = p->blocks[ids[i]].loc;
+        if (l == 3 || l == 4) return -1;
+    }
+    uint32_t *todo = (uint32_t *)malloc((n + 1) * sizeof(uint32_t));
+    uint32_t m = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (p->blocks[ids[i]].loc != 1) continue;
+        int dup = 0;
+        for (uint32_t j = 0; j < m; ++j) dup |= todo[j] == ids[i];
+        if (!dup) todo[m++] = ids[i];
+    }
+    int rc = 0;
+    for (uint32_t i = 0; i < m; ++i) {
+        if (restore_one(p, todo[i])) {
+            rc = -1;
+            if (m < 8) break;
+        }
+    }
+    free(todo);
+    return rc;
+}
+
+/* Standalone policy / swap-slot objects, for pinning them to the
+ * reference's own unit tests (ref tiering.rs:2106-2740, 3796-4030). */
+OTier *otier_new(int policy, size_t arc_cap, uint64_t swap_size, uint64_t per_block) {
+    OTier *t = (OTier *)calloc(1, sizeof(OTier));
+    tier_reset_policy(t, policy, arc_cap);
+    t->per_block = per_block;
+    t->swap_size = swap_size;
+    if (swap_size) {
+        t->fr = (ORange *)malloc(sizeof(ORange));
+        t->fr[0].start = 0;
+        t->fr[0].end = swap_size;
+        t->nfr = 1;
+        t->cap_fr = 1;
+    }
+    return t;
+}
+void otier_free(OTier *t) { tier_delete(t); }
+void otier_event(OTier *t, int kind, uint32_t sb, uint32_t idx) {
+    Handle h = {sb, idx};
+    if (kind == 0) tier_on_allocate(t, h);
+    else if (kind == 1) tier_on_access(t, h);
+    else tier_on_evict(t, h);
+}
+size_t otier_select(OTier *t, const uint32_t *hs, size_t n, size_t count, uint32_t *out) {
+    Handle *c = (Handle *)malloc((n + 1) * sizeof(Handle));
+    Handle *o = (Handle *)malloc((n + 1) * sizeof(Handle));
+    for (size_t i = 0; i < n; ++i) { c[i].sb = hs[2 * i]; c[i].idx = hs[2 * i + 1]; }
+    size_t r = tier_select(t, c, n, count, o);
+    for (size_t i = 0; i < r; ++i) { out[2 * i] = o[i].sb; out[2 * i + 1] = o[i].idx; }
+    free(c);
+    free(o);
+    return r;
+}
+int otier_slot_alloc(OTier *t, uint64_t size, uint64_t *off) { return tier_alloc_slot(t, size, off); }
+void otier_slot_free(OTier *t, uint64_t off, uint64_t size) { tier_free_range(t, off, size); }
+size_t otier_ranges(OTier *t, uint64_t *out, size_t max) {
+    size_t n = t->nfr < max ? t->nfr : max;
+    for (size_t i = 0; i < n; ++i) { out[2 * i] = t->fr[i].start; out[2 * i + 1] = t->fr[i].end; }
+    return n;
+}
+size_t otier_arc_list(OTier *t, int which, uint32_t *out, size_t max) {
+    HList *l = which == 0 ? &t->t1 : which == 1 ? &t->t2 : which == 2 ? &t->b1 : &t->b2;
+    size_t n = l->n < max ? l->n : max;
+    for (size_t i = 0; i < n; ++i) { out[2 * i] = l->a[i].sb; out[2 * i + 1] = l->a[i].idx; }
+    return n;
+}
+size_t otier_arc_p(OTier *t) { return t->arc_p; }
 
 /* ======================================================================
  * KV write

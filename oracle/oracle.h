@@ -63,6 +63,30 @@ void opool_stats(OPool *p, uint64_t *stats);
 void opool_metrics(OPool *p, float *m);
 int opool_below_low_watermark(OPool *p, float threshold);
 
+/* ---- tiering: HBM <-> host swap (ref tiering.rs, pool.rs:824-1002, ffi.rs:1900-2008) ---- */
+/* policy: 0 lru, 1 lfu, 2 fifo (anything else lru); 0 max_* = reference defaults */
+int opool_enable_tiering(OPool *p, int policy, size_t max_blocks, size_t max_batch_blocks);
+int opool_set_policy(OPool *p, const char *name);   /* lru lfu fifo arc sink_window */
+const char *opool_policy_name(OPool *p);
+int opool_location(OPool *p, uint32_t blk);          /* -1 not in use, else 0/1/3/4 */
+uint64_t opool_cpu_offset(OPool *p, uint32_t blk);   /* UINT64_MAX unless swapped out */
+int opool_access(OPool *p, uint32_t blk);            /* hint/protect on_access */
+uint32_t opool_evict(OPool *p, uint32_t count, uint32_t *out_blocks);
+int opool_restore_one(OPool *p, uint32_t blk, uint64_t *va);
+int opool_restore(OPool *p, const uint32_t *ids, uint32_t n);
+/* standalone policy (0 lru, 1 lfu, 2 fifo, 3 arc, 4 sink_window) and swap-slot
+ * allocator; handles are (superblock, index) pairs */
+typedef struct OTier OTier;
+OTier *otier_new(int policy, size_t arc_cap, uint64_t swap_size, uint64_t per_block);
+void otier_free(OTier *t);
+void otier_event(OTier *t, int kind, uint32_t sb, uint32_t idx);  /* 0 alloc 1 access 2 evict */
+size_t otier_select(OTier *t, const uint32_t *hs, size_t n, size_t count, uint32_t *out);
+int otier_slot_alloc(OTier *t, uint64_t size, uint64_t *off);
+void otier_slot_free(OTier *t, uint64_t off, uint64_t size);
+size_t otier_ranges(OTier *t, uint64_t *out, size_t max);
+size_t otier_arc_list(OTier *t, int which, uint32_t *out, size_t max);  /* 0 t1 1 t2 2 b1 3 b2 */
+size_t otier_arc_p(OTier *t);
+
 /* ---- KV write (ref pool.rs:1036-1098, ffi.rs:1088-1551, kcmm_vllm_kv_write.cu) ---- */
 /* rows: destination page byte offset, slot in page, source row. */
 int oracle_kv_write_rows(int dtype, uint8_t *k_region, uint8_t *v_region,

@@ -5,8 +5,10 @@
 // the exact bookkeeping code that ships (block ids, page offsets, sequences,
 // reference counts, error paths).  Regions get distinct fake base addresses
 // and superblock mapping is only recorded; every data-path entry point fails
-// with "no device", so nothing here can stand in for the HIP kernels.
+// with "no device" (the tiering moves, which carry no bytes here, aside), so
+// nothing here can stand in for the HIP kernels.
 #include <cstdint>
+#include <cstdlib>
 #include <memory>
 #include <string>
 #include <vector>
@@ -96,6 +98,27 @@ bool lt_gemm_bf16(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, ui
     *used = false;
     return no_device(err);
 }
+// The host-check backing has no page memory (fake region addresses), so the
+// tiering moves carry no bytes here: they succeed, and the CPU tier checks
+// the bookkeeping around them (victims, swap slots, locations, new pages).
+// The bytes are checked on the GPU (tests/test_gpu_tiering.py).
+bool tier_evict_copy(const std::vector<uint64_t>&, const uint64_t*, uint8_t* const*, size_t,
+                     uint32_t, std::string*) {
+    return true;
+}
+bool tier_restore_copy(const std::vector<uint64_t>&, const uint64_t*, uint8_t* const*, size_t,
+                       uint32_t, std::string*) {
+    return true;
+}
+bool host_pinned_alloc(size_t bytes, void** out, std::string* err) {
+    *out = std::malloc(bytes);
+    if (*out == nullptr) {
+        *err = "host allocation failed";
+        return false;
+    }
+    return true;
+}
+void host_pinned_free(void* p) { std::free(p); }
 bool gemm_bf16_partials(uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, float**, int*,
                         std::string* err) {
     return no_device(err);

@@ -13,9 +13,12 @@ STAT_KEYS = ["blocks_in_use", "total_blocks", "total_physical_blocks", "free_phy
 
 class OracleAdapter:
     def __init__(self, *, block_size, num_layers, kv_heads, head_dim, max_batch, max_seq_len,
-                 dtype=O.F16, rollback=True):
+                 dtype=O.F16, rollback=True, tiering=False, policy=0, max_blocks=0,
+                 max_batch_blocks=0):
         self.p = O.OraclePool(block_size, num_layers, kv_heads, head_dim, max_batch, max_seq_len,
                               dtype, rollback)
+        if tiering:
+            self.p.enable_tiering(policy, max_blocks, max_batch_blocks)
 
     def alloc(self, n):
         return self.p.alloc(n)
@@ -73,12 +76,49 @@ class OracleAdapter:
     def below(self, t):
         return self.p.below_low_watermark(t)
 
+    # tiering
+    def evict(self, count):
+        return len(self.p.evict(count))
+
+    def restore_one(self, b):
+        return self.p.restore_one(b)
+
+    def restore(self, ids):
+        return self.p.restore(ids)
+
+    def location(self, b):
+        return self.p.location(b)
+
+    def set_policy(self, name):
+        return self.p.set_policy(name.lower())
+
+    def policy_name(self):
+        return self.p.policy_name()
+
+    def protect(self, blocks, level):
+        for b in blocks:
+            if self.p.location(b) is None:
+                return False
+            if level != 2:
+                self.p.access(b)
+        return True
+
+    def hint_protect(self, s):
+        t = self.p.block_table(s)
+        if t is None:
+            return False
+        for b in t:
+            self.p.access(b)
+        return True
+
 
 class ProductAdapter:
     def __init__(self, lib: KcmmLibrary, *, block_size, num_layers, kv_heads, head_dim, max_batch,
-                 max_seq_len, dtype=0):
+                 max_seq_len, dtype=0, tiering=False, policy=0, max_blocks=0, max_batch_blocks=0):
         cfg = make_config(num_layers=num_layers, kv_heads=kv_heads, head_dim=head_dim,
-                          max_batch=max_batch, max_seq_len=max_seq_len, block_size=block_size)
+                          max_batch=max_batch, max_seq_len=max_seq_len, block_size=block_size,
+                          tiering=tiering, eviction_policy=policy, max_blocks=max_blocks,
+                          max_batch_blocks=max_batch_blocks)
         self.pool = lib.create_pool(cfg, dtype)
 
     def close(self):
@@ -167,3 +207,48 @@ class ProductAdapter:
 
     def below(self, t):
         return bool(self.pool.lib.kcmm_below_low_watermark(self.pool.handle, t))
+
+    # tiering
+    def evict(self, count):
+        return self.pool.evict_blocks(count)
+
+    def restore_one(self, b):
+        try:
+            return self.pool.restore_block(b)
+        except KcmmError:
+            return None
+
+    def restore(self, ids):
+        try:
+            self.pool.restore_blocks(ids)
+            return True
+        except KcmmError:
+            return False
+
+    def location(self, b):
+        return {None: None, "gpu": 0, "cpu": 1, "evicting": 3, "restoring": 4}[
+            self.pool.block_location(b)]
+
+    def set_policy(self, name):
+        try:
+            self.pool.set_eviction_policy(name)
+            return True
+        except KcmmError:
+            return False
+
+    def policy_name(self):
+        return self.pool.eviction_policy()
+
+    def protect(self, blocks, level):
+        try:
+            self.pool.protect(0, blocks, level)
+            return True
+        except KcmmError:
+            return False
+
+    def hint_protect(self, s):
+        try:
+            self.pool.hint(s, 1)   # KCMM_HINT_MULTI_TURN
+            return True
+        except KcmmError:
+            return False
