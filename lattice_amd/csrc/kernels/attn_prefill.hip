@@ -121,7 +121,7 @@ struct Shape {
 };
 
 // Workgroups over (query-token block, kv head), kv head fastest: blockIdx.x
-// = block * Hkv + g.  Workgroups are dealt to the 8 XCDs round-robin, so with
+// = item * Hkv + g, items in longest-first order (see below).  Workgroups are dealt to the 8 XCDs round-robin, so with
 // 8 kv heads every XCD serves one head and its L2 holds that head's pages
 // (shared prefixes included) for all sequences.
 template <int DT, int D, int G, int NW, int NCB, int KT>
@@ -150,27 +150,44 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     const int item = static_cast<int>(blockIdx.x) / p.kv_heads;
 
     // ---- sequence and token block of this workgroup ----
+    // Items are dealt longest first: rank r = 0 is every sequence's last
+    // token block (the most keys under the causal mask), r = 1 the block
+    // before it, and so on; within a rank, sequences in order.  For chunks of
+    // equal length this is longest-processing-time order, so the workgroups
+    // that start last are the short ones and the rounds end together.
     int b = -1, blk = 0;
     {
-        int base = 0;
-        for (int c = 0; c < p.batch; c += 64) {
-            const int bb = c + lane;
+        auto blocks_of = [&](int bb) {   // token blocks of sequence bb (0 past the batch)
             const int n = bb < p.batch ? qsl[bb + 1] - qsl[bb] : 0;
-            const int v = n > 0 ? (n + TWG - 1) / TWG : 0;
-            int incl = v;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(incl, o);
-                if (lane >= o) incl += y;
+            return n > 0 ? (n + TWG - 1) / TWG : 0;
+        };
+        const int v0 = blocks_of(lane);   // the first 64 sequences stay in registers
+        int base = 0;                      // items of the ranks before r
+        for (int r = 0; b < 0; ++r) {
+            int cnt = 0;
+            for (int c = 0; c < p.batch; c += 64) {
+                const int v = c == 0 ? v0 : blocks_of(c + lane);
+                cnt += __popcll(__ballot(v > r));
             }
-            const unsigned long long hit = __ballot(base + incl > item);
-            if (hit) {
-                const int j = __ffsll(static_cast<long long>(hit)) - 1;
-                b = c + j;
-                blk = item - (base + __shfl(incl - v, j));
+            if (cnt == 0) break;          // no item of this rank: a spare workgroup
+            if (item < base + cnt) {
+                int j = item - base;       // the j-th sequence (in order) with more than r blocks
+                for (int c = 0; c < p.batch; c += 64) {
+                    const int v = c == 0 ? v0 : blocks_of(c + lane);
+                    unsigned long long m = __ballot(v > r);
+                    const int n = __popcll(m);
+                    if (j < n) {
+                        for (int k = 0; k < j; ++k) m &= m - 1;
+                        const int bit = __ffsll(static_cast<long long>(m)) - 1;
+                        b = c + bit;
+                        blk = __shfl(v, bit) - 1 - r;
+                        break;
+                    }
+                    j -= n;
+                }
                 break;
             }
-            base += __shfl(incl, 63);
+            base += cnt;
         }
     }
     b = __builtin_amdgcn_readfirstlane(b);

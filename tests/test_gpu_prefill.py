@@ -168,3 +168,23 @@ def test_shared_prefix_chunked_prefill(gpu_lib):
         assert np.isfinite(got).all() and err <= TOL[KV_BF16]
     finally:
         case.pool.destroy()
+
+
+def test_many_sequences_ragged_chunks(gpu_lib):
+    """70 sequences (two 64-lane chunks in the workgroup -> (sequence,
+    token block) lookup, which deals blocks longest first across
+    sequences), chunk lengths 0..200 so sequences own 0..4 token blocks."""
+    rng = np.random.default_rng(71)
+    lens = rng.integers(0, 201, size=70)
+    lens[[0, 63, 64, 69]] = [200, 0, 130, 1]
+    ctx = lens + rng.integers(0, 120, size=70)
+    ctx = np.maximum(ctx, 1)
+    case = build_decode_case(gpu_lib, batch=70, num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=72)
+    try:
+        got, ref = run_prefill(case, lens, 32, 73)
+        err = rel_err(got, ref)
+        print(f"70 sequences, {int(lens.sum())} queries, err={err:.3e}", flush=True)
+        assert np.isfinite(got).all() and err <= TOL[KV_BF16]
+    finally:
+        case.pool.destroy()
