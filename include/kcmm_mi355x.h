@@ -218,7 +218,9 @@ int kcmm_gemm_bf16_swiglu_on_stream(uint64_t x_ptr, uint64_t w_gate_up_ptr, uint
                                     uint64_t stream_ptr);
 
 /** RoPE fused with the KV append for the decode token of every sequence of a
- *  bf16 pool: row b of qkv_ptr holds [q heads | k heads | v heads] x
+ *  bf16 or fp8 pool (bf16 activations; on an fp8 pool the rotated k and the
+ *  v rows go through the fp8 page writer of kcmm_append_kv_device_slots,
+ *  scales included): row b of qkv_ptr holds [q heads | k heads | v heads] x
  *  head_dim; the token's position is seq_lens[b] - 1 (seq_lens include it).
  *  q is rotated into q_out_ptr ([batch][num_q_heads][head_dim], the layout
  *  the attention reads); k is rotated and written, with v, into the token's
@@ -272,7 +274,7 @@ typedef struct kcmm_layer_weights {
 } kcmm_layer_weights_t;
 
 /** One decoder layer of a decode step, in place on hidden_ptr
- *  ([batch][hidden] bf16), for layer `layer_idx` of a bf16 pool (ref
+ *  ([batch][hidden] bf16), for layer `layer_idx` of a bf16 or fp8 pool (ref
  *  LlamaTransformer::forward_step_paged, llama_transformer.rs:262-391, per
  *  layer): h += o(attn(rope(qkv(rmsnorm(h))))), with this token's k / v
  *  appended to the pages; h += down(silu(gate) * up(rmsnorm(h))).  kv

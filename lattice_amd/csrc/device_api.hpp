@@ -22,7 +22,8 @@ bool set_device(int device, std::string* err);
 // Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
 // attention partials, 1: GEMM split partials, 2: decode attention segment
 // table, 3: decode layer-step activations, 4: the final norm's output,
-// 5: hipBLASLt workspace, 6: tiering staging on the null stream).
+// 5: hipBLASLt workspace, 6: tiering staging on the null stream, 7: fp8
+// RoPE/append staging).
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);
@@ -124,6 +125,9 @@ struct RopeAppendArgs {
     uint64_t inv_freq;        // fp32 [D/2]
     uint32_t batch, num_q_heads, kv_heads, head_dim, block_size, mbps, row_bytes;
     uint64_t stream;
+    int32_t dtype = 1;        // page type: 1 bf16 (rows stored in the pages), 2 fp8
+                              // (rows staged, then the fp8 page writer: workspace slot 7)
+    uint32_t data_bytes = 0;  // fp8: page bytes before the scale footer
 };
 bool rope_append_bf16(const RopeAppendArgs& a, std::string* err);
 bool silu_mul_bf16(uint64_t gate_up, uint64_t act, uint32_t rows, uint32_t inter,

@@ -1107,8 +1107,8 @@ bool step_shapes_ok(kcmm_pool_t* pool, const char* fn, uint32_t layer_idx, uint3
                     uint32_t hq, uint32_t mbps) {
     if (!layer_ok(pool, layer_idx, fn)) return false;
     const kcmm::PoolGeometry& g = pool->core->geo();
-    if (g.dtype != kcmm::kBF16) {
-        pool->set_error(std::string(fn) + ": needs a bf16 pool");
+    if (g.dtype != kcmm::kBF16 && g.dtype != kcmm::kFP8) {
+        pool->set_error(std::string(fn) + ": needs a bf16 or fp8 pool (bf16 activations)");
         return false;
     }
     if (batch == 0 || hq == 0 || mbps == 0 || hq % g.kv_heads != 0 || hq > 0xFFFF ||
@@ -1147,6 +1147,8 @@ kcmm::dev::RopeAppendArgs rope_args(kcmm_pool_t* pool, uint32_t layer_idx, uint6
     a.mbps = mbps;
     a.row_bytes = static_cast<uint32_t>(g.row_bytes);
     a.stream = stream;
+    a.dtype = g.dtype;
+    a.data_bytes = static_cast<uint32_t>(g.data_bytes);
     return a;
 }
 

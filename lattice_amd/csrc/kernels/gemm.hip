@@ -561,6 +561,15 @@ bool gemm_bf16_rope_append(uint64_t x, uint64_t w_qkv, uint32_t m, uint32_t k,
         return false;
     }
     if (!shape_ok(m, static_cast<uint32_t>(n), k, err)) return false;
+    if (a.dtype == kDtFP8) {
+        // fp8 pages take their rows through the fp8 page writer: the
+        // projection leaves fp32 partials, the RoPE kernel sums them
+        float* part = nullptr;
+        int splits = 1;
+        return gemm_bf16_partials(x, w_qkv, m, static_cast<uint32_t>(n), k, a.stream, &part,
+                                  &splits, err) &&
+               rope_append_from_partials(a, part, splits, err);
+    }
     GemmParams p = base_params(x, w_qkv, m, static_cast<uint32_t>(n), k);
     p.q_out = reinterpret_cast<uint16_t*>(a.q_out);
     p.k_base = reinterpret_cast<uint8_t*>(a.k_base);

@@ -123,6 +123,12 @@ struct RopeAppendParams {
     const uint64_t* offsets_f16;
     const float* inv_freq;    // [D/2]
     int num_q_heads, kv_heads, head_dim, block_size, mbps, row_bytes;
+    // fp8 pages: k / v rows go to bf16 staging [B][Hkv D] and each
+    // sequence's slot id (page * block_size + offset, -1 when skipped) to
+    // slots, for the fp8 page writer (null: rows go straight into the pages)
+    uint16_t* k_stage;
+    uint16_t* v_stage;
+    int64_t* slots;
 };
 
 // Workgroup (b, y) handles heads [y*hs, (y+1)*hs) of sequence b's qkv row,
@@ -138,7 +144,14 @@ __global__ __launch_bounds__(256) void rope_append_rows(RopeAppendParams p) {
     const int L = p.seq_lens[b];
     const int D = p.head_dim;
     const int pos = L - 1;
-    if (pos < 0 || pos >= p.mbps * p.block_size) return;   // no token / past the table
+    const bool has_row = pos >= 0 && pos < p.mbps * p.block_size;   // no token / past the table
+    if (p.slots != nullptr && blockIdx.y == 0 && threadIdx.x == 0)
+        p.slots[b] = has_row ? static_cast<int64_t>(p.block_tables[static_cast<size_t>(b) * p.mbps +
+                                                                   pos / p.block_size]) *
+                                       p.block_size +
+                                   pos % p.block_size
+                             : -1;
+    if (!has_row) return;
     const int quads = D / 8;
     const int hs = 256 / quads;
     const int iq = threadIdx.x % quads;
@@ -191,6 +204,10 @@ __global__ __launch_bounds__(256) void rope_append_rows(RopeAppendParams p) {
     uint16_t* dst;
     if (h < p.num_q_heads) {
         dst = p.q_out + (static_cast<size_t>(b) * p.num_q_heads + h) * D;
+    } else if (p.k_stage != nullptr) {
+        const bool is_k = h < p.num_q_heads + p.kv_heads;
+        const int kvh = is_k ? h - p.num_q_heads : h - p.num_q_heads - p.kv_heads;
+        dst = (is_k ? p.k_stage : p.v_stage) + (static_cast<size_t>(b) * p.kv_heads + kvh) * D;
     } else {
         const int lb = pos / p.block_size;
         const uint64_t page = p.offsets_f16[p.block_tables[static_cast<size_t>(b) * p.mbps + lb]] * 2ull +
@@ -299,6 +316,21 @@ bool launch_rope(const RopeAppendArgs& a, const float* part, int splits, std::st
     p.block_size = static_cast<int>(a.block_size);
     p.mbps = static_cast<int>(a.mbps);
     p.row_bytes = static_cast<int>(a.row_bytes);
+    const bool fp8 = a.dtype == kDtFP8;
+    uint64_t stage = 0;
+    const size_t rows_bytes = static_cast<size_t>(a.batch) * a.kv_heads * a.head_dim * 2;
+    if (fp8) {
+        // fp8 pages: rotated k and v rows are staged in bf16, then written by
+        // the fp8 page writer (per-page scales), which reads the slot ids
+        void* ws = nullptr;
+        if (!stream_workspace(a.stream, 7, 2 * rows_bytes + a.batch * sizeof(int64_t), &ws, false,
+                              err))
+            return false;
+        stage = reinterpret_cast<uint64_t>(ws);
+        p.k_stage = reinterpret_cast<uint16_t*>(stage);
+        p.v_stage = reinterpret_cast<uint16_t*>(stage + rows_bytes);
+        p.slots = reinterpret_cast<int64_t*>(stage + 2 * rows_bytes);
+    }
     const uint32_t hs = 256 / (a.head_dim / 8);
     const dim3 grid(a.batch, (a.num_q_heads + 2 * a.kv_heads + hs - 1) / hs);
     if (part != nullptr)
@@ -308,6 +340,27 @@ bool launch_rope(const RopeAppendArgs& a, const float* part, int splits, std::st
         hipLaunchKernelGGL(rope_append_rows<false>, grid, dim3(256), 0,
                            reinterpret_cast<hipStream_t>(a.stream), p);
     KCMM_HIP_CHECK(hipGetLastError(), err);
+    if (fp8) {
+        KvDeviceSlotsArgs w{};
+        w.dtype = kDtFP8;
+        w.k_base = a.k_base;
+        w.v_base = a.v_base;
+        w.k_src = stage;
+        w.v_src = stage + rows_bytes;
+        w.slot_mapping = stage + 2 * rows_bytes;
+        w.offsets_f16 = a.offsets_f16;
+        w.valid_blocks = 0;   // slots come from the block table
+        w.status = 0;
+        w.offsets_len = 0xFFFFFFFFu;
+        w.batch = a.batch;
+        w.block_size = a.block_size;
+        w.kv_heads = a.kv_heads;
+        w.head_dim = a.head_dim;
+        w.row_bytes = a.row_bytes;
+        w.data_bytes = a.data_bytes;
+        w.stream = a.stream;
+        if (!kv_write_device_slots(w, err)) return false;
+    }
     return true;
 }
 }  // namespace

@@ -441,10 +441,25 @@ def silu_mul_f64(gate, up):
     return g / (1.0 + np.exp(-g)) * np.asarray(up, dtype=np.float64)
 
 
+def fp8_page_rows(region, page_byte, slots, kv_heads, head_dim, row_bytes, data_bytes):
+    """Dequantized rows [len(slots)][Hkv][D] of an fp8 page: e4m3 codes times
+    the page's per-kv-head scale (footer at data_bytes)."""
+    sc = region[page_byte + data_bytes:page_byte + data_bytes + 4 * kv_heads].view(np.float32)
+    out = np.empty((len(slots), kv_heads, head_dim), dtype=np.float64)
+    for i, s in enumerate(slots):
+        a = page_byte + s * row_bytes
+        codes = region[a:a + kv_heads * head_dim].reshape(kv_heads, head_dim)
+        out[i] = decode(FP8, codes).astype(np.float64) * sc[:, None]
+    return out
+
+
 def decode_layer_step_f64(hidden_bits, w, k_region, v_region, block_tables, seq_lens,
                           offsets_f16, inv_freq, num_q_heads, kv_heads, head_dim,
-                          intermediate, block_size, row_bytes, eps, round_bf16=True):
-    """One decoder layer of a decode step for a bf16 pool.
+                          intermediate, block_size, row_bytes, eps, round_bf16=True,
+                          dtype=BF16, data_bytes=0):
+    """One decoder layer of a decode step for a bf16 pool (dtype FP8: an
+    fp8-e4m3 pool, the new k / v rows written by kv_write_rows and every row
+    read back dequantized).
 
     hidden_bits [B][H] uint16 (bf16); w: dict of bf16-bit arrays attn_norm [H],
     qkv [(Hq+2Hkv)D][H], o [H][Hq D], mlp_norm [H], gate_up [2I][H], down [H][I].
@@ -476,7 +491,19 @@ def decode_layer_step_f64(hidden_bits, w, k_region, v_region, block_tables, seq_
         if p < 0 or p >= bt.shape[1] * block_size:
             continue
         rows_k, rows_v = [], []
-        for t in range(p + 1):
+        if dtype == FP8:
+            pb = int(offsets_f16[bt[b, p // block_size]]) * 2
+            kv_write_rows(FP8, k_region, v_region,
+                          encode(BF16, k_r[b].ravel()).reshape(1, -1),
+                          encode(BF16, v[b].ravel()).reshape(1, -1), [pb], [p % block_size],
+                          [0], hkv, d, row_bytes, data_bytes)
+            for t in range(p + 1):
+                pg = int(offsets_f16[bt[b, t // block_size]]) * 2
+                rows_k.append(fp8_page_rows(k_region, pg, [t % block_size], hkv, d, row_bytes,
+                                            data_bytes)[0])
+                rows_v.append(fp8_page_rows(v_region, pg, [t % block_size], hkv, d, row_bytes,
+                                            data_bytes)[0])
+        for t in range(p + 1 if dtype != FP8 else 0):
             base = int(offsets_f16[bt[b, t // block_size]]) * 2 + (t % block_size) * row_bytes
             if t == p:
                 k_region[base:base + hkv * d * 2] = encode(BF16, k_r[b].ravel()).view(np.uint8)

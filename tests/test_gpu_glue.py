@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, memcpy_dtoh
+from lattice_amd.bindings import KV_BF16, KV_FP8, KcmmLayerWeights, memcpy_dtoh
 from lattice_amd.workload import build_decode_case
 
 pytestmark = pytest.mark.gpu
@@ -147,6 +147,60 @@ def test_rope_append(gpu_lib, hq, hkv, d):
         case.pool.destroy()
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 2, 64)])
+def test_rope_append_fp8_pool(gpu_lib, hq, hkv, d):
+    """On an fp8 pool the rotated k and the v rows go through the fp8 page
+    writer: q_out has the bits of the bf16 pool's run, and the fp8 regions
+    are byte-identical to the oracle's fp8 writer applied to the rows the
+    bf16 pool stored (scales, rescaled earlier rows and all)."""
+    import torch
+    lens = [1, 16, 17, 300, 0, 33]
+    rng = np.random.default_rng(8)
+    qkv = O.encode(O.BF16, rng.standard_normal((len(lens), (hq + 2 * hkv) * d)) * 3.0)
+    inv = O.default_inv_freq(500000.0, d)
+    out = {}
+    for dtype in (KV_BF16, KV_FP8):
+        case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv,
+                                 head_dim=d, block_size=16, ctx_lens=lens, dtype=dtype, seed=d)
+        try:
+            qo = torch.full((len(lens), hq, d), float("nan"), dtype=torch.bfloat16, device="cuda")
+            invd = torch.from_numpy(inv.astype(np.float32)).cuda()
+            qkvd = bf16_dev(torch, qkv)
+            dv = case.dev
+            k0, v0 = _region(case, "k"), _region(case, "v")
+            case.pool.rope_append(layer_idx=0, qkv_ptr=qkvd.data_ptr(), q_out_ptr=qo.data_ptr(),
+                                  block_tables_ptr=dv["bt"].data_ptr(),
+                                  seq_lens_ptr=dv["sl"].data_ptr(),
+                                  block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                  inv_freq_ptr=invd.data_ptr(), batch=len(lens), num_q_heads=hq,
+                                  max_blocks_per_seq=case.mbps,
+                                  stream_ptr=torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            out[dtype] = dict(q=bits_of(qo), k0=k0, v0=v0, k=_region(case, "k"),
+                              v=_region(case, "v"), g=case.geometry, bt=case.block_tables,
+                              offs=case.offsets_f16)
+        finally:
+            case.pool.destroy()
+    bf, f8 = out[KV_BF16], out[KV_FP8]
+    assert np.array_equal(bf["q"][[0, 1, 2, 3, 5]], f8["q"][[0, 1, 2, 3, 5]])
+    g = f8["g"]
+    kref, vref = f8["k0"].copy(), f8["v0"].copy()
+    for b, L in enumerate(lens):
+        if L <= 0:
+            continue
+        pos = L - 1
+        seg = lambda c: slice(int(c["offs"][c["bt"][b, pos // 16]]) * 2 + (pos % 16) * c["g"]["row_bytes"],
+                              int(c["offs"][c["bt"][b, pos // 16]]) * 2 + (pos % 16) * c["g"]["row_bytes"]
+                              + hkv * d * 2)
+        krow = bf["k"][seg(bf)].view(np.uint16).reshape(1, -1)
+        vrow = bf["v"][seg(bf)].view(np.uint16).reshape(1, -1)
+        pg = int(f8["offs"][f8["bt"][b, pos // 16]]) * 2
+        O.kv_write_rows(O.FP8, kref, vref, krow, vrow, [pg], [pos % 16], [0], hkv, d,
+                        g["row_bytes"], g["data_bytes"])
+    assert np.array_equal(f8["k"], kref)
+    assert np.array_equal(f8["v"], vref)
+
+
 def _layer_weights(torch, rng, h, inter, hq, hkv, d):
     enc = lambda shape, std: O.encode(O.BF16, rng.standard_normal(shape) * std)
     w = {"attn_norm": O.encode(O.BF16, 1.0 + 0.1 * rng.standard_normal(h)),
@@ -158,17 +212,22 @@ def _layer_weights(torch, rng, h, inter, hq, hkv, d):
     return w, dev, lw
 
 
-@pytest.mark.parametrize("hq,hkv,d,h,inter", [(8, 2, 64, 512, 768), (32, 8, 128, 4096, 1024),
-                                               (32, 8, 72, 512, 768)])
-def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter):
+@pytest.mark.parametrize("hq,hkv,d,h,inter,dtype", [
+    (8, 2, 64, 512, 768, KV_BF16), (32, 8, 128, 4096, 1024, KV_BF16), (32, 8, 72, 512, 768, KV_BF16),
+    (32, 8, 128, 4096, 1024, KV_FP8), (8, 2, 64, 512, 768, KV_FP8)])
+def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter, dtype):
     """One decoder layer through kcmm_decode_layer_step_on_stream vs the
-    oracle's bf16 layer (RMSNorm, QKV, RoPE + append, paged attention,
+    oracle's layer (RMSNorm, QKV, RoPE + append, paged attention,
     O + residual, RMSNorm, gate/up, SiLU*up, down + residual).  head_dim 72
-    takes the unfused QKV path (projection, then the RoPE/append kernel)."""
+    takes the unfused QKV path (projection, then the RoPE/append kernel).
+    fp8 pools: the new rows go through the fp8 page writer (bf16 activations,
+    fp8 K/V); tolerances are the fp8 attention's (3e-2 on the layer output,
+    8e-2 on its update)."""
     import torch
     lens = [1, 16, 17, 130]
+    fp8 = dtype == KV_FP8
     case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
-                             block_size=16, ctx_lens=lens, dtype=KV_BF16, seed=h)
+                             block_size=16, ctx_lens=lens, dtype=dtype, seed=h)
     try:
         g = case.geometry
         rng = np.random.default_rng(11)
@@ -191,19 +250,31 @@ def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter):
         got = O.decode(O.BF16, bits_of(hd)).astype(np.float64)
         ref = O.decode_layer_step_f64(hid, w, kreg, vreg, case.block_tables, case.seq_lens,
                                       case.offsets_f16, inv, hq, hkv, d, inter, 16,
-                                      g["row_bytes"], 1e-5)
+                                      g["row_bytes"], 1e-5, dtype=dtype,
+                                      data_bytes=g["data_bytes"])
         x = O.decode(O.BF16, hid).astype(np.float64)
         err = rel_err(got, ref)
         upd = rel_err(got - x, ref - x)
-        print(f"layer step hq={hq} d={d} h={h}: err {err:.2e}, update err {upd:.2e}", flush=True)
-        assert np.isfinite(got).all() and err <= 1e-2 and upd <= 5e-2
-        # the new token's K / V rows hold what the oracle wrote (within bf16)
+        print(f"layer step hq={hq} d={d} h={h} dtype={dtype}: err {err:.2e}, update err {upd:.2e}",
+              flush=True)
+        assert np.isfinite(got).all() and err <= (3e-2 if fp8 else 1e-2)
+        assert upd <= (8e-2 if fp8 else 5e-2)
+        # the new token's K / V rows hold what the oracle wrote (within bf16 /
+        # one fp8 step)
         k1, v1 = _region(case, "k"), _region(case, "v")
         for b, L in enumerate(lens):
             pos = L - 1
-            base = int(case.offsets_f16[case.block_tables[b, pos // 16]]) * 2 + (pos % 16) * g["row_bytes"]
-            seg = slice(base, base + hkv * d * 2)
+            pg = int(case.offsets_f16[case.block_tables[b, pos // 16]]) * 2
             for got_r, ref_r in ((k1, kreg), (v1, vreg)):
+                if fp8:
+                    a = O.fp8_page_rows(got_r, pg, [pos % 16], hkv, d, g["row_bytes"],
+                                        g["data_bytes"])
+                    r = O.fp8_page_rows(ref_r, pg, [pos % 16], hkv, d, g["row_bytes"],
+                                        g["data_bytes"])
+                    assert rel_err(a, r) <= 1.3e-1, b
+                    continue
+                base = pg + (pos % 16) * g["row_bytes"]
+                seg = slice(base, base + hkv * d * 2)
                 a = O.decode(O.BF16, got_r[seg].view(np.uint16)).astype(np.float64)
                 r = O.decode(O.BF16, ref_r[seg].view(np.uint16)).astype(np.float64)
                 assert rel_err(a, r) <= 2e-2, b
@@ -241,8 +312,10 @@ def test_layer_step_rejects_bad_shapes(gpu_lib):
         case.pool.destroy()
 
 
-@pytest.mark.parametrize("hq,hkv,d,h,inter", [(32, 8, 128, 4096, 1024), (8, 2, 64, 512, 768)])
-def test_decode_layers_matches_layer_steps(gpu_lib, hq, hkv, d, h, inter):
+@pytest.mark.parametrize("hq,hkv,d,h,inter,dtype", [(32, 8, 128, 4096, 1024, KV_BF16),
+                                                     (8, 2, 64, 512, 768, KV_BF16),
+                                                     (32, 8, 128, 4096, 1024, KV_FP8)])
+def test_decode_layers_matches_layer_steps(gpu_lib, hq, hkv, d, h, inter, dtype):
     """Three layers in one kcmm_decode_layers_on_stream call give the bits of
     three kcmm_decode_layer_step_on_stream calls: hidden state and every
     byte of the three layers' K/V regions."""
@@ -252,7 +325,7 @@ def test_decode_layers_matches_layer_steps(gpu_lib, hq, hkv, d, h, inter):
     res = []
     for one_call in (False, True):
         case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
-                                 block_size=16, ctx_lens=lens, dtype=KV_BF16, seed=h,
+                                 block_size=16, ctx_lens=lens, dtype=dtype, seed=h,
                                  num_layers=nl)
         try:
             rng = np.random.default_rng(5)
