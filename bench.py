@@ -485,14 +485,52 @@ def main():
         "wall_s_timed": round(wall, 3),
     }
     if args.config == "cfg5":
-        g = case.geometry
+        geo5 = case.geometry
         result["beam_fork_us"] = round(per["beam_fork"] * 1e3, 2)
         result["beam_fork"] = {"beam_width": BEAM_WIDTH, "parents": B,
                                "cow_pages_per_step": beam["copies"],
                                "cow_copy_bytes_per_step": beam["copies"] * 2 * args.layers *
-                               g["block_bytes"],
+                               geo5["block_bytes"],
                                "note": "host fork/CoW bookkeeping + one page-copy kernel, "
                                        "HIP events around the call"}
+        # the decoder layer on the fp8 pool: kcmm_decode_layers_on_stream over
+        # the pool's layers (bf16 activations and weights, fp8 KV with the
+        # fp8 append), one weight set
+        w = {name: (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+             for name, n, k in GEMMS}
+        for name in ("attn_norm", "mlp_norm"):
+            w[name] = (1.0 + 0.1 * torch.randn(HIDDEN, generator=g, device=dev)).to(torch.bfloat16)
+        lw = KcmmLayerWeights(**{k: w[k].data_ptr() for k in
+                                 ("attn_norm", "qkv", "o", "mlp_norm", "gate_up", "down")})
+        hid5 = torch.randn((B, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
+
+        def fp8_layers():
+            case.pool.decode_layers(first_layer=0, weights=[lw] * args.layers,
+                                    hidden_ptr=hid5.data_ptr(), block_tables_ptr=dv["bt"].data_ptr(),
+                                    seq_lens_ptr=dv["sl"].data_ptr(),
+                                    block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                    inv_freq_ptr=inv_freq.data_ptr(), batch=B, hidden_size=HIDDEN,
+                                    num_q_heads=HQ, intermediate_size=INTER,
+                                    max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
+        fp8_layers()
+        torch.cuda.synchronize()
+        reps = max(2, min(args.steps, 8))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fp8_layers()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t_l = e0.elapsed_time(e1) / reps / args.layers
+        assert torch.isfinite(hid5.float()).all(), "fp8 layer step produced non-finite hidden state"
+        result["fp8_layer_step"] = {
+            "t_layer_us": round(t_l * 1e3, 2), "layers_per_call": args.layers, "batch": B,
+            "kv_bytes_per_layer": kv_bytes,
+            "note": "kcmm_decode_layers_on_stream on the fp8 pool: RMSNorm, QKV (partials) + "
+                    "RoPE + fp8 append, fp8 attention, O + residual + RMSNorm, gate/up + SwiGLU, "
+                    "down + residual; HIP events around the calls"}
+        log(f"fp8 layer step: {t_l * 1e3:.1f} us per layer ({args.layers} layers per call)")
+        del w, hid5
     if not args.attn_only:
         t_step_s = extra["decode_step"] / 1e3
         result["decode_tokens_per_s"] = round(B / t_step_s, 1)
