@@ -6,11 +6,19 @@
 // Y^T[N][M] = op(W) X^T with W stored as a K x N column-major matrix
 // (transposed by the op) and X as a K x M one: m = N, n = M, k = K.
 // bf16 operands and result, fp32 compute.
+//
+// The first call of a shape times the library's top candidates (up to
+// kLtCandidates, 2 + 5 runs each on the caller's stream, HIP events) and
+// keeps the fastest for the process; that call synchronizes the stream.
+// KCMM_GEMM_LT_TUNE=0 takes the heuristic's first choice instead.
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <vector>
 
 #include "../device_api.hpp"
 #include "common.hpp"
@@ -19,13 +27,16 @@ namespace kcmm {
 namespace {
 
 constexpr size_t kLtWorkspace = 32u << 20;   // bytes offered to the heuristic
+constexpr int kLtCandidates = 8;
 
 struct LtPlan {
     bool ok = false;
+    bool tuned = false;
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
     size_t workspace = 0;
+    std::vector<hipblasLtMatmulHeuristicResult_t> cands;
 };
 
 struct LtState {
@@ -33,6 +44,11 @@ struct LtState {
     std::map<int, hipblasLtHandle_t> handles;                              // per device
     std::map<std::tuple<int, uint32_t, uint32_t, uint32_t>, LtPlan> plans;
 };
+
+int env_int_lt(const char* name, int dflt) {
+    const char* e = std::getenv(name);
+    return e ? std::atoi(e) : dflt;
+}
 
 LtState& state() {
     static LtState* s = new LtState();   // kept for the process lifetime
@@ -57,14 +73,16 @@ bool make_plan(hipblasLtHandle_t h, uint32_t m, uint32_t n, uint32_t k, LtPlan* 
     const uint64_t ws = kLtWorkspace;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
                                           sizeof(ws));
-    hipblasLtMatmulHeuristicResult_t res{};
+    hipblasLtMatmulHeuristicResult_t res[kLtCandidates] = {};
     int returned = 0;
     const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(h, p->desc, p->a, p->b, p->c, p->c,
-                                                               pref, 1, &res, &returned);
+                                                               pref, kLtCandidates, res, &returned);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS || returned < 1) return false;
-    p->algo = res.algo;
-    p->workspace = res.workspaceSize;
+    p->algo = res[0].algo;
+    p->workspace = res[0].workspaceSize;
+    for (int i = 0; i < returned; ++i)
+        if (res[i].state == HIPBLAS_STATUS_SUCCESS) p->cands.push_back(res[i]);
     return true;
 }
 
@@ -100,15 +118,58 @@ bool lt_gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, ui
         plan = it->second;
     }
     if (!plan.ok) return true;
+    const float alpha = 1.0f, beta = 0.0f;
+    hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    auto run = [&](const hipblasLtMatmulAlgo_t& algo, void* ws, size_t wsz) {
+        return hipblasLtMatmul(h, plan.desc, &alpha, reinterpret_cast<const void*>(w), plan.a,
+                               reinterpret_cast<const void*>(x), plan.b, &beta,
+                               reinterpret_cast<const void*>(y), plan.c, reinterpret_cast<void*>(y),
+                               plan.c, &algo, ws, wsz, hs);
+    };
+    if (!plan.tuned && plan.cands.size() > 1 && env_int_lt("KCMM_GEMM_LT_TUNE", 1) != 0) {
+        // time the candidates once for this shape and keep the fastest
+        size_t wmax = 0;
+        for (const auto& c : plan.cands) wmax = std::max(wmax, c.workspaceSize);
+        void* tws = nullptr;
+        if (wmax > 0 && !stream_workspace(stream, 5, wmax, &tws, false, err)) return false;
+        hipEvent_t e0, e1;
+        KCMM_HIP_CHECK(hipEventCreate(&e0), err);
+        KCMM_HIP_CHECK(hipEventCreate(&e1), err);
+        float best = 0.0f;
+        size_t pick = 0;
+        for (size_t i = 0; i < plan.cands.size(); ++i) {
+            const auto& c = plan.cands[i];
+            bool ok = run(c.algo, tws, c.workspaceSize) == HIPBLAS_STATUS_SUCCESS &&
+                      run(c.algo, tws, c.workspaceSize) == HIPBLAS_STATUS_SUCCESS;
+            if (!ok) continue;
+            (void)hipEventRecord(e0, hs);
+            for (int r = 0; r < 5 && ok; ++r)
+                ok = run(c.algo, tws, c.workspaceSize) == HIPBLAS_STATUS_SUCCESS;
+            (void)hipEventRecord(e1, hs);
+            if (!ok || hipEventSynchronize(e1) != hipSuccess) continue;
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
+            if (best == 0.0f || ms < best) {
+                best = ms;
+                pick = i;
+            }
+        }
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        (void)hipGetLastError();
+        plan.algo = plan.cands[pick].algo;
+        plan.workspace = plan.cands[pick].workspaceSize;
+        plan.tuned = true;
+        std::lock_guard<std::mutex> lk(s.mu);
+        LtPlan& stored = s.plans[std::make_tuple(device, m, n, k)];
+        stored.algo = plan.algo;
+        stored.workspace = plan.workspace;
+        stored.tuned = true;
+    }
     void* ws = nullptr;
     if (plan.workspace > 0 && !stream_workspace(stream, 5, plan.workspace, &ws, false, err))
         return false;
-    const float alpha = 1.0f, beta = 0.0f;
-    const hipblasStatus_t st = hipblasLtMatmul(
-        h, plan.desc, &alpha, reinterpret_cast<const void*>(w), plan.a,
-        reinterpret_cast<const void*>(x), plan.b, &beta, reinterpret_cast<const void*>(y), plan.c,
-        reinterpret_cast<void*>(y), plan.c, &plan.algo, ws, plan.workspace,
-        reinterpret_cast<hipStream_t>(stream));
+    const hipblasStatus_t st = run(plan.algo, ws, plan.workspace);
     if (st != HIPBLAS_STATUS_SUCCESS) {
         *err = "hipblasLtMatmul failed (status " + std::to_string(static_cast<int>(st)) + ")";
         return false;
