@@ -183,7 +183,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
-                          "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+                          "(the path would shard by sequence or kv head; no multi-GPU run is made)"}))
         sys.exit(2)
     if args.config == "cfg3":
         return bench_prefill(args)

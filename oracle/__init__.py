@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY: the checker used by tests/, by
 __graft_entry__.smoke() and by bench.py's cpu_baseline leg.  Nothing in the
 lattice_amd package imports this module, and no product code path may fall
-back to it.  See oracle.h for what each function restates and DESIGN.md for
-how each one is pinned.
+back to it.  oracle.h says which reference lines each function restates;
+tests/test_oracle_*.py pin each one to the reference's own expectations.
 """
 from __future__ import annotations
 
