@@ -357,10 +357,11 @@ def test_decode_layers_matches_layer_steps(gpu_lib, hq, hkv, d, h, inter, dtype)
         assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("b,h,vocab", [(5, 512, 1024), (64, 4096, 2048)])
+@pytest.mark.parametrize("b,h,vocab", [(5, 512, 1024), (64, 4096, 2048), (8, 256, 128256)])
 def test_decode_logits(gpu_lib, b, h, vocab):
     """Final RMSNorm + lm_head vs the oracle's bf16 norm and fp64 product
-    (bf16 tolerance on the logits)."""
+    (bf16 tolerance on the logits); the last case has Llama-3's vocabulary
+    width."""
     import torch
     rng = np.random.default_rng(h + vocab)
     x = O.encode(O.BF16, rng.standard_normal((b, h)) * 4)
