@@ -146,7 +146,9 @@ int kcmm_fork_beams_on_stream(kcmm_pool_t *pool, const uint32_t *parents, uint32
 
 /** Device-side variant (vLLM copy_blocks contract): `pairs_ptr` is a device
  *  int64 [num_pairs][2] array of block ids, translated through the device
- *  f16-unit offset table.  Enqueue only; no host state is read. */
+ *  f16-unit offset table (which must cover every id the pool has issued).
+ *  A pair with an id outside [0, ids issued at enqueue time) is skipped.
+ *  Enqueue only; apart from that id count no host state is read. */
 int kcmm_copy_blocks_device_on_stream(kcmm_pool_t *pool, uint64_t pairs_ptr,
                                       uint64_t block_offsets_f16_ptr,
                                       uint32_t num_pairs, uint64_t stream_ptr);

@@ -87,9 +87,10 @@ bool kv_write_device_slots(const KvDeviceSlotsArgs& a, std::string* err);
 // Page copies: every (src, dst) byte-offset pair is copied in every region.
 bool copy_pages(const std::vector<uint64_t>& region_bases, const uint64_t* pair_offsets,
                 size_t num_pairs, uint32_t block_bytes, uint64_t stream, std::string* err);
+// Pairs of block ids read on the device; ids outside [0, n_ids) are skipped.
 bool copy_pages_device(const std::vector<uint64_t>& region_bases, uint64_t pairs_ptr,
-                       uint64_t offsets_f16, size_t num_pairs, uint32_t block_bytes,
-                       uint64_t stream, std::string* err);
+                       uint64_t offsets_f16, size_t num_pairs, uint32_t n_ids,
+                       uint32_t block_bytes, uint64_t stream, std::string* err);
 
 // Tiering moves (kernels/tier_copy.hip): n whole blocks between the pool's
 // regions (page byte offset pages[b] in every region) and host swap memory

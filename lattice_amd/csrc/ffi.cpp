@@ -1011,6 +1011,7 @@ int kcmm_copy_blocks_device_on_stream(kcmm_pool_t* pool, uint64_t pairs_ptr, uin
     std::string err;
     if (!kcmm::dev::set_device(pool->device, &err) ||
         !kcmm::dev::copy_pages_device(region_bases(pool), pairs_ptr, offs_ptr, n,
+                                      pool->core->total_blocks(),
                                       static_cast<uint32_t>(pool->core->geo().block_bytes),
                                       stream, &err)) {
         pool->set_error("kcmm_copy_blocks_device_on_stream: " + err);

@@ -33,13 +33,17 @@ __global__ __launch_bounds__(256) void copy_pages_host(CopyBatch cb, uint32_t bl
               block_bytes);
 }
 
+// A pair naming an id outside [0, n_ids) is skipped: the offset table is
+// never read past the pool's ids, and no page outside the pool is written.
 __global__ __launch_bounds__(256) void copy_pages_dev(CopyBatch cb, const int64_t* pairs,
                                                       const uint64_t* offsets_f16,
-                                                      uint32_t block_bytes) {
+                                                      uint32_t block_bytes, int64_t n_ids) {
     const uint32_t pr = blockIdx.x / cb.n_regions;
     const uint32_t rg = blockIdx.x - pr * cb.n_regions;
-    const uint64_t src = offsets_f16[pairs[2 * pr]] * 2ull;
-    const uint64_t dst = offsets_f16[pairs[2 * pr + 1]] * 2ull;
+    const int64_t a = pairs[2 * pr], b = pairs[2 * pr + 1];
+    if (a < 0 || b < 0 || a >= n_ids || b >= n_ids) return;
+    const uint64_t src = offsets_f16[a] * 2ull;
+    const uint64_t dst = offsets_f16[b] * 2ull;
     copy_page(reinterpret_cast<uint8_t*>(cb.region[rg]), src, dst, block_bytes);
 }
 
@@ -70,8 +74,8 @@ bool copy_pages(const std::vector<uint64_t>& regions, const uint64_t* pair_offse
 }
 
 bool copy_pages_device(const std::vector<uint64_t>& regions, uint64_t pairs_ptr,
-                       uint64_t offsets_f16, size_t num_pairs, uint32_t block_bytes,
-                       uint64_t stream, std::string* err) {
+                       uint64_t offsets_f16, size_t num_pairs, uint32_t n_ids,
+                       uint32_t block_bytes, uint64_t stream, std::string* err) {
     if (block_bytes % 16 != 0) {
         *err = "page size must be a multiple of 16 bytes";
         return false;
@@ -88,7 +92,8 @@ bool copy_pages_device(const std::vector<uint64_t>& regions, uint64_t pairs_ptr,
             return false;
         }
         hipLaunchKernelGGL(copy_pages_dev, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, cb,
-                           pairs, reinterpret_cast<const uint64_t*>(offsets_f16), block_bytes);
+                           pairs, reinterpret_cast<const uint64_t*>(offsets_f16), block_bytes,
+                           static_cast<int64_t>(n_ids));
         KCMM_HIP_CHECK(hipGetLastError(), err);
     }
     return true;

@@ -70,7 +70,7 @@ bool copy_pages(const std::vector<uint64_t>&, const uint64_t*, size_t, uint32_t,
     return no_device(err);
 }
 bool copy_pages_device(const std::vector<uint64_t>&, uint64_t, uint64_t, size_t, uint32_t,
-                       uint64_t, std::string* err) {
+                       uint32_t, uint64_t, std::string* err) {
     return no_device(err);
 }
 bool gemm_bf16(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t,

@@ -84,9 +84,12 @@ def test_beam_fork_cow_copy_bit_exact(gpu_lib, dtype):
             opool.cow(f, 0)
             if pair:
                 more.append(pair)
-        offs_t = torch.tensor(pool.all_block_offsets_f16(), dtype=torch.int64, device="cuda")
-        pairs_t = torch.tensor(more, dtype=torch.int64, device="cuda")
-        pool.copy_blocks_device(pairs_t.data_ptr(), offs_t.data_ptr(), len(more),
+        offs_host = pool.all_block_offsets_f16()
+        offs_t = torch.tensor(offs_host, dtype=torch.int64, device="cuda")
+        # pairs naming ids the pool never issued are skipped by the kernel
+        bad = [(10**9, more[0][1]), (-1, more[0][1]), (more[0][0], len(offs_host))]
+        pairs_t = torch.tensor(bad[:2] + more + bad[2:], dtype=torch.int64, device="cuda")
+        pool.copy_blocks_device(pairs_t.data_ptr(), offs_t.data_ptr(), len(more) + len(bad),
                                 stream_ptr=stream.cuda_stream)
         stream.synchronize()
         O.copy_pages(flat, [(opool.block_offset(a), opool.block_offset(b)) for a, b in more],
