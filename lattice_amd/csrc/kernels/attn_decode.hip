@@ -52,8 +52,10 @@ struct AttnParams {
     const int32_t* block_tables;
     const int32_t* seq_lens;
     const uint64_t* offsets_f16;
-    float* part_acc;        // [waves][2][G][D]  (slot 0: head of slice, 1: tail)
-    float* part_ml;         // [waves][2][G][2]  (max in log2 units, denominator)
+    float* part_acc;        // [units][G][D]: [waves][2] (slot 0: head of slice, 1: tail),
+                            // then [B][Hkv][kSegPieces] from seg_unit0
+    float* part_ml;         // [units][G][2]  (max in log2 units, denominator)
+    size_t seg_unit0;       // first segment-indexed unit
     int2* seg_info;         // [B][Hkv]: (first slice, slices) of each (b, g); slices <= 1: no merge
     int batch, num_q_heads, kv_heads, group, block_size, mbps;
     int row_bytes, data_bytes;
@@ -62,6 +64,11 @@ struct AttnParams {
     int min_tiles;          // smallest slice a wave takes
     float scale_log2;       // scale * log2(e)
 };
+
+// Pieces 0 .. kSegPieces-1 of a split (b, g) are stored at units indexed by
+// (b, g), so the merge can load them before it has read the segment record;
+// later pieces stay at the unit of their slice's wave.
+constexpr int kSegPieces = 4;
 
 __device__ __forceinline__ float wave_max_across_groups(float x) {
     // lanes j, j+16, j+32, j+48 hold the same column; combine them.
@@ -547,7 +554,11 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
                     *reinterpret_cast<u32x2*>(o + dim_offset<F8>(db, lg)) = w;
                 }
             } else {
-                const size_t unit = static_cast<size_t>(gw) * 2 + (began_here ? 1 : 0);
+                const int piece = slice - (t0 + i - c.t) / per;   // 0 when began_here
+                const size_t unit =
+                    piece < kSegPieces
+                        ? p.seg_unit0 + static_cast<size_t>(c.b * Hkv + c.g) * kSegPieces + piece
+                        : static_cast<size_t>(gw) * 2;
                 float* pa = p.part_acc + (unit * G + ln) * D;
 #pragma unroll
                 for (int db = 0; db < DB; ++db)
@@ -653,30 +664,52 @@ void attn_decode_stream(AttnParams p, const int32_t* __restrict__ bt,
 }
 
 // Log-sum-exp merge, one wave per (b, kv head g) that spans several slices
-// of the streaming kernel: its partials sit in slot 1 of the wave for g of
-// its first slice wa and in slot 0 of that wave of slices wa+1 .. wa+np-1
-// (wave rows (wa + k) * HW + g % HW).  Two dependent memory steps: the
-// segment record, then the (max, denominator) pairs of up to 64 parts (one
-// part per lane) together with the accumulators of the first QP parts; the
-// weights reach every lane through v_readlane.  NO = outputs per lane
-// rounded up to a power of two; every load is issued unconditionally
-// (clamped index) so that none waits behind a branch.
+// of the streaming kernel: part k of the np parts from slice wa on sits at
+// the (b, g) unit k for k < kSegPieces and in slot 0 of the wave for g of
+// slice wa+k after that (wave rows (wa + k) * HW + g % HW).  The
+// (max, denominator) pairs of parts 0..kSegPieces-1 (one part per lane) and
+// the accumulators of the first QP parts are loaded together with the
+// segment record, so a (b, g) of at most kSegPieces parts takes one memory
+// step; parts past kSegPieces wait for the record.  The weights reach every
+// lane through v_readlane.  NO = outputs per lane rounded up to a power of
+// two; loads past np read stale units whose values are masked out.
 template <int DT, int D, int NO>
 __global__ __launch_bounds__(64) void attn_decode_merge(AttnParams p,
                                                         const int2* __restrict__ info) {
     constexpr int NJ = NO * 64 / D > 0 ? NO * 64 / D : 1;   // heads covered (power of two)
     constexpr int QP = NO >= 16 ? 2 : 32 / NO > 4 ? 4 : 32 / NO;   // parts per round
-    const int2 si = info[blockIdx.x];
-    const int wa = si.x, np = si.y;
-    if (np <= 1) return;
+    static_assert(QP <= kSegPieces, "the first round's accumulators are segment-indexed");
     const int lane = threadIdx.x;
     const int G = p.group;
     const int b = blockIdx.x / p.kv_heads;
     const int g = blockIdx.x - b * p.kv_heads;
     const int n_out = G * D / 64;      // lane holds outputs lane + 64e, e < n_out
+    const size_t seg0 = p.seg_unit0 + static_cast<size_t>(blockIdx.x) * kSegPieces;
+
+    // first round, before the record: (max, denominator) of part min(lane, 3)
+    // and the accumulators of parts 0 .. QP-1
+    float m[NJ], l[NJ], v[QP][NO];
+    {
+        const size_t u0 = seg0 + min(lane, kSegPieces - 1);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const size_t u = (u0 * G + min(j, G - 1)) * 2;
+            m[j] = p.part_ml[u];
+            l[j] = p.part_ml[u + 1];
+        }
+#pragma unroll
+        for (int q = 0; q < QP; ++q) {
+            const float* pa = p.part_acc + (seg0 + q) * G * D + lane;
+#pragma unroll
+            for (int e = 0; e < NO; ++e) v[q][e] = pa[min(e, n_out - 1) * 64];
+        }
+    }
+    const int2 si = info[blockIdx.x];
+    const int wa = si.x, np = si.y;
+    if (np <= 1) return;
     const int gofs = g % p.hw;
-    auto unit = [&](int k) {
-        return (static_cast<size_t>(wa + k) * p.hw + gofs) * 2 + (k == 0 ? 1 : 0);
+    auto unit = [&](int k) -> size_t {
+        return k < kSegPieces ? seg0 + k : (static_cast<size_t>(wa + k) * p.hw + gofs) * 2;
     };
     auto load_parts = [&](float (&v)[QP][NO], int k0) {
 #pragma unroll
@@ -698,14 +731,16 @@ __global__ __launch_bounds__(64) void attn_decode_merge(AttnParams p,
     for (int k0 = 0; k0 < np; k0 += 64) {
         const bool live = k0 + lane < np;
         const int k = min(k0 + lane, np - 1);
-        float m[NJ], l[NJ], v[QP][NO];
+        // lanes whose part is not among the ones loaded above
+        if (k0 > 0 || (np > kSegPieces && lane >= kSegPieces)) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const size_t u = (unit(k) * G + min(j, G - 1)) * 2;
-            m[j] = p.part_ml[u];
-            l[j] = p.part_ml[u + 1];
+            for (int j = 0; j < NJ; ++j) {
+                const size_t u = (unit(k) * G + min(j, G - 1)) * 2;
+                m[j] = p.part_ml[u];
+                l[j] = p.part_ml[u + 1];
+            }
         }
-        load_parts(v, k0);   // in flight with the (max, denominator) loads
+        if (k0 > 0) load_parts(v, k0);   // in flight with the (max, denominator) loads
         float w[NJ];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
@@ -886,7 +921,10 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
     const long long want = (lists + p.min_tiles - 1) / p.min_tiles;
     p.total_waves = static_cast<int>(
         std::max(1LL, std::min<long long>(std::max(1, stream_waves(DT) / hw), want)));
-    const size_t units = static_cast<size_t>(p.total_waves) * hw * 2 * p.group;
+    // slice-indexed units, then kSegPieces per (b, g); G rows of each
+    p.seg_unit0 = static_cast<size_t>(p.total_waves) * hw * 2;
+    const size_t units =
+        (p.seg_unit0 + static_cast<size_t>(p.batch) * p.kv_heads * kSegPieces) * p.group;
     // idle-load region first: it must cover one tile's lane addresses
     const size_t idle_bytes = (static_cast<size_t>(8) * p.row_bytes + 1023) & ~static_cast<size_t>(255);
     void* ws = nullptr;
