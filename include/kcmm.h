@@ -33,7 +33,8 @@ extern "C" {
 /** Opaque pool handle (ref kcmm.h:36). */
 typedef struct kcmm_pool_t kcmm_pool_t;
 
-/** Eviction hints (ref kcmm.h:43-52).  Accepted; tiering is not built here. */
+/** Eviction hints (ref kcmm.h:43-52).  With tiering on, protect-class hints
+ *  record an access of the sequence's blocks (ref ffi.rs:2296-2379). */
 typedef enum {
     KCMM_HINT_MULTI_TURN     = 1,
     KCMM_HINT_NEAR_END       = 2,
@@ -52,8 +53,9 @@ typedef enum {
     KCMM_EVICT_PREFERRED     = 2,
 } kcmm_protection_t;
 
-/** Where a block's bytes live (ref kcmm.h:62-68).  This build keeps every
- *  block resident in HBM, so queries only ever report GPU_RESIDENT. */
+/** Where a block's bytes live (ref kcmm.h:62-68).  With tiering on, blocks
+ *  move between HBM and page-locked host memory (CPU_RESIDENT); this build
+ *  has no NVMe tier, so NVME_RESIDENT is never reported. */
 typedef enum {
     KCMM_LOC_GPU_RESIDENT  = 0,
     KCMM_LOC_CPU_RESIDENT  = 1,
@@ -72,8 +74,8 @@ typedef enum {
 typedef struct {
     size_t block_size;                /* tokens per block; default 16 */
     size_t max_blocks;                /* default 16384 (informational, as in the reference) */
-    char cpu_cache_path[256];         /* swap path; unused (no tiering) */
-    int32_t tiering;                  /* requested tiering; this build never enables it */
+    char cpu_cache_path[256];         /* unused: the swap space is page-locked host memory */
+    int32_t tiering;                  /* non-zero: evict / restore between HBM and host */
     int32_t eviction_policy;          /* 0 lru, 1 lfu, 2 fifo */
     size_t prefetch_window;           /* default 4 */
     size_t max_batch_blocks;          /* default 64 */
@@ -268,13 +270,18 @@ int kcmm_paged_attn_decode_f16_on_current_context_stream(
 /** ref kcmm.h:559, ffi.rs:182-205.  Idempotent; validates the pool. */
 int kcmm_precompile_paged_attn_decode_f16(kcmm_pool_t *pool);
 
-/* ---- tiering (ref kcmm.h:577-613): not built; link-compatible stubs ----- */
+/* ---- tiering (ref kcmm.h:577-613): HBM <-> page-locked host memory ------ */
 
-/** ref kcmm.h:577, ffi.rs:1900-1945.  Returns 0 (tiering disabled). */
+/** ref kcmm.h:577, ffi.rs:1900-1945.  Moves up to `count` policy-chosen
+ *  blocks to host swap slots; returns how many moved (0 with tiering off).
+ *  Synchronous. */
 uint32_t kcmm_evict_blocks(kcmm_pool_t *pool, uint32_t count);
-/** ref kcmm.h:590, ffi.rs:1954-1972.  Resident block: its VA offset; else 0. */
+/** ref kcmm.h:590, ffi.rs:1954-1972.  Brings a swapped-out block back to a
+ *  new page; returns its VA offset (a resident block: its offset; 0 on
+ *  error).  Synchronous. */
 uint64_t kcmm_restore_evicted_block(kcmm_pool_t *pool, uint32_t block_idx);
-/** ref kcmm.h:603, ffi.rs:1984-2002.  All blocks are resident: returns 0. */
+/** ref kcmm.h:603, ffi.rs:1984-2002.  Restores every swapped-out block of the
+ *  list (each once); 0 on success, -1 if any failed.  Synchronous. */
 int kcmm_restore_evicted_blocks(kcmm_pool_t *pool, const uint32_t *block_indices,
                                 uint32_t count);
 /** ref kcmm.h:613, ffi.rs:2011-2025. */
@@ -303,11 +310,12 @@ uint32_t kcmm_active_sequences(kcmm_pool_t *pool);
 int kcmm_get_all_block_valid(kcmm_pool_t *pool, uint8_t *out_valid,
                              uint32_t max_blocks, uint32_t *out_count);
 
-/* ---- policy / hints (tiering-dependent; reference behaviour with tiering off) */
+/* ---- policy / hints (tiering-dependent) --------------------------------- */
 
-/** ref kcmm.h:664, ffi.rs:2200-2234.  -1: tiering is disabled. */
+/** ref kcmm.h:664, ffi.rs:2200-2234.  lru, lfu, fifo, arc or sink_window;
+ *  -1 when tiering is disabled or the name is unknown. */
 int kcmm_set_eviction_policy(kcmm_pool_t *pool, const char *policy);
-/** ref kcmm.h:674, ffi.rs:2243-2259.  0: tiering is disabled. */
+/** ref kcmm.h:674, ffi.rs:2243-2259.  Name length; 0 when tiering is disabled. */
 uint32_t kcmm_get_eviction_policy(kcmm_pool_t *pool, char *out_policy, uint32_t max_len);
 /** ref kcmm.h:683, ffi.rs:2268. */
 int kcmm_is_tiering_enabled(kcmm_pool_t *pool);

@@ -22,6 +22,7 @@ typedef enum {
     KCMM_KV_F16 = 0,       /* IEEE half (the reference's only type) */
     KCMM_KV_BF16 = 1,      /* bfloat16 */
     KCMM_KV_FP8_E4M3 = 2,  /* OCP e4m3fn + one fp32 scale per (page, kv head) */
+    KCMM_KV_F32 = 3,       /* IEEE single */
 } kcmm_kv_dtype_t;
 
 /**
@@ -37,10 +38,13 @@ kcmm_pool_t *kcmm_pool_create_typed(const kcmm_config_t *config, int32_t kv_dtyp
 /** Pool element type (kcmm_kv_dtype_t), or -1 for NULL. */
 int32_t kcmm_get_kv_dtype(kcmm_pool_t *pool);
 
-/** 1 = one hipMalloc per region holding the full capacity (default),
- *  0 = HIP VMM 2 MiB superblocks mapped on demand (the reference design, ref
- *  cuda_vmm.rs; selected with KCMM_BACKING=vmm), -1 for NULL.  Block ids and
- *  offsets are identical for both. */
+/** 1 = one hipMalloc per region holding the full capacity (the only backing
+ *  this build creates), -1 for NULL.  Value 0 is reserved for HIP VMM 2 MiB
+ *  superblocks mapped on demand (the reference design, ref cuda_vmm.rs);
+ *  KCMM_BACKING=vmm makes kcmm_pool_create* fail, because that backing is
+ *  disabled (unexplained hipMemSetAccess failures after repeated pool
+ *  create/destroy in one process).  Block ids and offsets do not depend on
+ *  the backing. */
 int32_t kcmm_get_backing_kind(kcmm_pool_t *pool);
 
 /** Why the last kcmm_pool_create* on this thread returned NULL (the reference
@@ -77,6 +81,27 @@ int kcmm_paged_attn_decode_fp8_on_stream(
     uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
     uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
 
+/** fp32 pool: fp32 q/out, same tensor contract as
+ *  kcmm_paged_attn_decode_f16 (ref kcmm.h:505).  Synchronizes before
+ *  returning. */
+int kcmm_paged_attn_decode_f32(kcmm_pool_t *pool, uint32_t layer_idx,
+                               uint64_t query_ptr, uint64_t out_ptr,
+                               uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+                               uint64_t block_offsets_f16_ptr,
+                               uint32_t batch, uint32_t num_q_heads,
+                               uint32_t kv_heads, uint32_t head_dim,
+                               uint32_t block_size, uint32_t max_blocks_per_seq,
+                               float scale);
+
+/** As kcmm_paged_attn_decode_f16_on_stream (ref kcmm.h:525) for fp32 pools.
+ *  Enqueue only. */
+int kcmm_paged_attn_decode_f32_on_stream(
+    kcmm_pool_t *pool, uint32_t layer_idx, uint64_t query_ptr, uint64_t out_ptr,
+    uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+    uint64_t block_offsets_f16_ptr, uint32_t batch, uint32_t num_q_heads,
+    uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
+    uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
+
 /* ---- chunked prefill attention ----------------------------------------- */
 
 /**
@@ -89,6 +114,7 @@ int kcmm_paged_attn_decode_fp8_on_stream(
  * position seq_lens[b] - len_b + i and attends to keys 0..position.  q/out
  * are f16 for f16 pools and bf16 otherwise; seq_lens and query_start_loc are
  * device int32 arrays; rows without a valid position are written as zeros.
+ * fp32 pools take fp32 q/out.
  * Enqueue only.
  */
 int kcmm_paged_attn_prefill_on_stream(

@@ -21,7 +21,7 @@ except Exception:  # pragma: no cover - torch is optional for the host-check tie
 PKG = Path(__file__).resolve().parent
 DEFAULT_LIB = PKG / "libkcmm.so"
 
-KV_F16, KV_BF16, KV_FP8 = 0, 1, 2
+KV_F16, KV_BF16, KV_FP8, KV_F32 = 0, 1, 2, 3
 
 
 class KcmmError(RuntimeError):
@@ -134,6 +134,8 @@ SIGNATURES = {
     "kcmm_paged_attn_decode_bf16": (_ATTN, C.c_int),
     "kcmm_paged_attn_decode_bf16_on_stream": (_ATTN + [_U64], C.c_int),
     "kcmm_paged_attn_decode_fp8_on_stream": (_ATTN + [_U64], C.c_int),
+    "kcmm_paged_attn_decode_f32": (_ATTN, C.c_int),
+    "kcmm_paged_attn_decode_f32_on_stream": (_ATTN + [_U64], C.c_int),
     "kcmm_paged_attn_prefill_on_stream": ([_P, _U32, _U64, _U64, _U64, _U64, _U64, _U64, _U32,
                                            _U32, _U32, _U32, _U32, _U32, _U32, C.c_float, _U64],
                                           C.c_int),
@@ -472,7 +474,7 @@ class KcmmPool:
                           block_offsets_f16_ptr, batch, num_q_heads, kv_heads, head_dim,
                           block_size, max_blocks_per_seq, scale, stream_ptr=None,
                           variant="auto") -> None:
-        """Dispatch to the entry point matching the pool dtype (f16/bf16/fp8)."""
+        """Dispatch to the entry point matching the pool dtype (f16/bf16/fp8/fp32)."""
         dt = self.kv_dtype()
         args = (self.handle, layer_idx, query_ptr, out_ptr, block_tables_ptr, seq_lens_ptr,
                 block_offsets_f16_ptr, batch, num_q_heads, kv_heads, head_dim, block_size,
@@ -489,6 +491,11 @@ class KcmmPool:
                 rc = self.lib.kcmm_paged_attn_decode_bf16(*args)
             else:
                 rc = self.lib.kcmm_paged_attn_decode_bf16_on_stream(*args, stream_ptr)
+        elif dt == KV_F32:
+            if stream_ptr is None:
+                rc = self.lib.kcmm_paged_attn_decode_f32(*args)
+            else:
+                rc = self.lib.kcmm_paged_attn_decode_f32_on_stream(*args, stream_ptr)
         else:
             rc = self.lib.kcmm_paged_attn_decode_fp8_on_stream(*args, stream_ptr or 0)
         self._check(rc, "paged_attn_decode")
@@ -497,7 +504,8 @@ class KcmmPool:
                            seq_lens_ptr, query_start_loc_ptr, block_offsets_f16_ptr, batch,
                            total_query_tokens, num_q_heads, kv_heads, head_dim, block_size,
                            max_blocks_per_seq, scale, stream_ptr=0) -> None:
-        """Causal chunked prefill (q/out f16 for f16 pools, bf16 otherwise)."""
+        """Causal chunked prefill (q/out f16 for f16 pools, fp32 for fp32 pools, bf16
+        otherwise)."""
         rc = self.lib.kcmm_paged_attn_prefill_on_stream(
             self.handle, layer_idx, query_ptr, out_ptr, block_tables_ptr, seq_lens_ptr,
             query_start_loc_ptr, block_offsets_f16_ptr, batch, total_query_tokens, num_q_heads,

@@ -23,7 +23,8 @@ bool set_device(int device, std::string* err);
 // attention partials, 1: GEMM split partials, 2: decode attention segment
 // table, 3: decode layer-step activations, 4: the final norm's output,
 // 5: hipBLASLt workspace, 6: tiering staging on the null stream, 7: fp8
-// RoPE/append staging).
+// RoPE/append staging, 8: fp8 page-writer row table).  `zero_fill` buffers
+// start zeroed by a fill kernel, and their users leave them zeroed.
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);
@@ -129,6 +130,8 @@ struct RopeAppendArgs {
     int32_t dtype = 1;        // page type: 1 bf16 (rows stored in the pages), 2 fp8
                               // (rows staged, then the fp8 page writer: workspace slot 7)
     uint32_t data_bytes = 0;  // fp8: page bytes before the scale footer
+    uint32_t n_ids = 0;       // fp8: block ids the pool has issued (rows naming
+                              // a larger id are skipped)
 };
 bool rope_append_bf16(const RopeAppendArgs& a, std::string* err);
 bool silu_mul_bf16(uint64_t gate_up, uint64_t act, uint32_t rows, uint32_t inter,

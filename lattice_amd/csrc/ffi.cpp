@@ -2,13 +2,9 @@
 // error channel and return conventions follow the reference's Rust FFI
 // (ref src/kcmm/ffi.rs); bookkeeping is PoolCore, device work goes through
 // device_api.hpp.  This file has no HIP dependency.
-#include <execinfo.h>
-#include <unistd.h>
-
 #include <algorithm>
 #include <cctype>
 #include <cmath>
-#include <csignal>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -60,28 +56,6 @@ struct kcmm_pool_t {
 namespace {
 
 thread_local std::string g_create_error;
-
-// KCMM_CRASH_TRACE=1: print a native backtrace on SIGSEGV/SIGBUS before the
-// default action, to locate host-side crashes inside the library.
-void crash_trace_handler(int sig) {
-    void* frames[64];
-    const int n = backtrace(frames, 64);
-    const char msg[] = "\n[kcmm] fatal signal; native backtrace:\n";
-    (void)!write(2, msg, sizeof(msg) - 1);
-    backtrace_symbols_fd(frames, n, 2);
-    signal(sig, SIG_DFL);
-    raise(sig);
-}
-
-struct CrashTraceInstaller {
-    CrashTraceInstaller() {
-        const char* e = std::getenv("KCMM_CRASH_TRACE");
-        if (e != nullptr && e[0] == '1') {
-            signal(SIGSEGV, crash_trace_handler);
-            signal(SIGBUS, crash_trace_handler);
-        }
-    }
-} g_crash_trace_installer;
 
 size_t write_c_str(char* buf, size_t max_len, const std::string& s) {
     // ref ffi.rs:412-422: copy at most max_len-1 bytes and terminate.
@@ -585,6 +559,16 @@ int kcmm_paged_attn_decode_bf16(KCMM_ATTN_ARGS) {
 
 int kcmm_paged_attn_decode_bf16_on_stream(KCMM_ATTN_ARGS, uint64_t stream) {
     return attn_impl(pool, kcmm::kBF16, "kcmm_paged_attn_decode_bf16", KCMM_ATTN_PASS, stream,
+                     false, true);
+}
+
+int kcmm_paged_attn_decode_f32(KCMM_ATTN_ARGS) {
+    return attn_impl(pool, kcmm::kF32, "kcmm_paged_attn_decode_f32", KCMM_ATTN_PASS, 0, true,
+                     true);
+}
+
+int kcmm_paged_attn_decode_f32_on_stream(KCMM_ATTN_ARGS, uint64_t stream) {
+    return attn_impl(pool, kcmm::kF32, "kcmm_paged_attn_decode_f32", KCMM_ATTN_PASS, stream,
                      false, true);
 }
 
@@ -1150,6 +1134,7 @@ kcmm::dev::RopeAppendArgs rope_args(kcmm_pool_t* pool, uint32_t layer_idx, uint6
     a.stream = stream;
     a.dtype = g.dtype;
     a.data_bytes = static_cast<uint32_t>(g.data_bytes);
+    a.n_ids = pool->core->total_blocks();
     return a;
 }
 

@@ -811,24 +811,22 @@ __global__ __launch_bounds__(64) void attn_decode_generic(AttnParams p, int head
     const int kvh = h * p.kv_heads / p.num_q_heads;  // ref kcmm_vllm_paged_attn.cu:40
     const int lane = threadIdx.x;
     const int L = min(p.seq_lens[b], p.mbps * p.block_size);
-    // q/out are 16-bit (f16 for f16 pools, bf16 otherwise).
-    constexpr int QDT = DT == kDtFP8 ? kDtBF16 : DT;
-    const uint16_t* qrow =
-        reinterpret_cast<const uint16_t*>(p.q) + (static_cast<size_t>(b) * p.num_q_heads + h) * head_dim;
-    uint16_t* orow = reinterpret_cast<uint16_t*>(p.out) +
-                     (static_cast<size_t>(b) * p.num_q_heads + h) * head_dim;
+    // q/out: f16 for f16 pools, fp32 for fp32 pools, bf16 otherwise
+    const size_t io_off = (static_cast<size_t>(b) * p.num_q_heads + h) * head_dim * io_bytes<DT>();
+    const uint8_t* qrow = p.q + io_off;
+    uint8_t* orow = p.out + io_off;
     if (L <= 0) {
-        for (int d = lane; d < head_dim; d += 64) orow[d] = 0;
+        for (int d = lane; d < head_dim; d += 64) io_store<DT>(orow, d, 0.0f);
         return;
     }
     float qv[4], acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int d = lane + 64 * i;
-        qv[i] = d < head_dim ? elem_to_f32<QDT>(qrow[d]) : 0.0f;
+        qv[i] = d < head_dim ? io_load<DT>(qrow, d) : 0.0f;
         acc[i] = 0.0f;
     }
-    const int esize = DT == kDtFP8 ? 1 : 2;
+    const int esize = kv_elem_bytes<DT>();
     float m = -INFINITY, s = 0.0f;
     for (int pos = 0; pos < L; ++pos) {
         const int lb = pos / p.block_size;
@@ -852,6 +850,9 @@ __global__ __launch_bounds__(64) void attn_decode_generic(AttnParams p, int head
                 if constexpr (DT == kDtFP8) {
                     kx = fp8e4m3_to_f32(p.k_base[roff + d]) * ks;
                     vx = fp8e4m3_to_f32(p.v_base[roff + d]) * vs;
+                } else if constexpr (DT == kDtF32) {
+                    kx = reinterpret_cast<const float*>(p.k_base + roff)[d];
+                    vx = reinterpret_cast<const float*>(p.v_base + roff)[d];
                 } else {
                     kx = elem_to_f32<DT>(reinterpret_cast<const uint16_t*>(p.k_base + roff)[d]);
                     vx = elem_to_f32<DT>(reinterpret_cast<const uint16_t*>(p.v_base + roff)[d]);
@@ -864,8 +865,8 @@ __global__ __launch_bounds__(64) void attn_decode_generic(AttnParams p, int head
         for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
         dot *= scale;
         const float m_new = fmaxf(m, dot);
-        const float e = __expf(dot - m_new);
-        const float corr = __expf(m - m_new);
+        const float e = kexp<DT>(dot - m_new);
+        const float corr = kexp<DT>(m - m_new);
         s = s * corr + e;
         m = m_new;
 #pragma unroll
@@ -875,7 +876,7 @@ __global__ __launch_bounds__(64) void attn_decode_generic(AttnParams p, int head
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int d = lane + 64 * i;
-        if (d < head_dim) orow[d] = static_cast<uint16_t>(f32_to_elem<QDT>(acc[i] * inv));
+        if (d < head_dim) io_store<DT>(orow, d, acc[i] * inv);
     }
 }
 
@@ -927,18 +928,16 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
         (p.seg_unit0 + static_cast<size_t>(p.batch) * p.kv_heads * kSegPieces) * p.group;
     // idle-load region first: it must cover one tile's lane addresses
     const size_t idle_bytes = (static_cast<size_t>(8) * p.row_bytes + 1023) & ~static_cast<size_t>(255);
+    const size_t part_bytes = idle_bytes + ((units * (D + 2) * sizeof(float) + 255) & ~size_t(255));
+    const size_t info_bytes = static_cast<size_t>(p.batch) * p.kv_heads * sizeof(int2);
     void* ws = nullptr;
-    if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 0,
-                               idle_bytes + units * (D + 2) * sizeof(float), &ws, false, err))
+    void* info = nullptr;
+    if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 0, part_bytes, &ws, false, err) ||
+        !dev::stream_workspace(reinterpret_cast<uint64_t>(s), 2, info_bytes, &info, false, err))
         return false;
     const uint8_t* idle = static_cast<const uint8_t*>(ws);
     p.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + idle_bytes);
     p.part_acc = p.part_ml + units * 2;
-    void* info = nullptr;
-    if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 2,
-                               static_cast<size_t>(p.batch) * p.kv_heads * sizeof(int2), &info,
-                               false, err))
-        return false;
     p.seg_info = static_cast<int2*>(info);
     if (depth == 3)
         hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 3>), dim3(p.total_waves), dim3(64 * hw),
@@ -1008,6 +1007,10 @@ bool attn_decode(const AttnDecodeArgs& a, std::string* err) {
             break;
         case kDtBF16:
             hipLaunchKernelGGL(attn_decode_generic<kDtBF16>, grid, dim3(64), 0, s, p,
+                               static_cast<int>(a.head_dim), a.scale);
+            break;
+        case kDtF32:
+            hipLaunchKernelGGL(attn_decode_generic<kDtF32>, grid, dim3(64), 0, s, p,
                                static_cast<int>(a.head_dim), a.scale);
             break;
         default:

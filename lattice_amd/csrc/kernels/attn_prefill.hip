@@ -456,7 +456,6 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
                                                            const int32_t* __restrict__ sl,
                                                            const int32_t* __restrict__ qsl,
                                                            const uint64_t* __restrict__ offs) {
-    constexpr int QDT = DT == kDtFP8 ? kDtBF16 : DT;
     const int lane = threadIdx.x;
     const int rowi = blockIdx.x / p.num_q_heads;
     const int h = blockIdx.x - rowi * p.num_q_heads;
@@ -467,20 +466,22 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
     const int L = min(sl[b], p.mbps * p.block_size);
     const int pos = L - len + (rowi - qsl[b]);
     const int kvh = h * p.kv_heads / p.num_q_heads;
-    uint16_t* orow = reinterpret_cast<uint16_t*>(p.out) + (static_cast<size_t>(rowi) * p.num_q_heads + h) * D;
+    // q/out: f16 for f16 pools, fp32 for fp32 pools, bf16 otherwise
+    const size_t io_off = (static_cast<size_t>(rowi) * p.num_q_heads + h) * D * io_bytes<DT>();
+    uint8_t* orow = reinterpret_cast<uint8_t*>(p.out) + io_off;
     if (pos < 0) {
-        for (int d = lane; d < D; d += 64) orow[d] = 0;
+        for (int d = lane; d < D; d += 64) io_store<DT>(orow, d, 0.0f);
         return;
     }
-    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(p.q) + (static_cast<size_t>(rowi) * p.num_q_heads + h) * D;
+    const uint8_t* qrow = reinterpret_cast<const uint8_t*>(p.q) + io_off;
     float qv[4], acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int d = lane + 64 * i;
-        qv[i] = d < D ? elem_to_f32<QDT>(qrow[d]) : 0.0f;
+        qv[i] = d < D ? io_load<DT>(qrow, d) : 0.0f;
         acc[i] = 0.0f;
     }
-    const int esize = DT == kDtFP8 ? 1 : 2;
+    const int esize = kv_elem_bytes<DT>();
     float m = -INFINITY, s = 0.0f;
     for (int key = 0; key <= pos; ++key) {
         const int lb = key / p.block_size;
@@ -502,6 +503,9 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
                 if constexpr (DT == kDtFP8) {
                     kx = fp8e4m3_to_f32(kreg[roff + d]) * ks;
                     vx = fp8e4m3_to_f32(vreg[roff + d]) * vs;
+                } else if constexpr (DT == kDtF32) {
+                    kx = reinterpret_cast<const float*>(kreg + roff)[d];
+                    vx = reinterpret_cast<const float*>(vreg + roff)[d];
                 } else {
                     kx = elem_to_f32<DT>(reinterpret_cast<const uint16_t*>(kreg + roff)[d]);
                     vx = elem_to_f32<DT>(reinterpret_cast<const uint16_t*>(vreg + roff)[d]);
@@ -514,8 +518,8 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
         for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
         dot *= p.scale;
         const float m_new = fmaxf(m, dot);
-        const float e = __expf(dot - m_new);
-        const float corr = __expf(m - m_new);
+        const float e = kexp<DT>(dot - m_new);
+        const float corr = kexp<DT>(m - m_new);
         s = s * corr + e;
         m = m_new;
 #pragma unroll
@@ -525,7 +529,7 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int d = lane + 64 * i;
-        if (d < D) orow[d] = static_cast<uint16_t>(f32_to_elem<QDT>(acc[i] * inv));
+        if (d < D) io_store<DT>(orow, d, acc[i] * inv);
     }
 }
 
@@ -594,7 +598,8 @@ bool attn_prefill(const AttnPrefillArgs& a, std::string* err) {
     const bool mfma_dim = a.head_dim == 64 || a.head_dim == 128;
     const bool pow2_bs = (1u << p.bs_shift) == a.block_size;
     // (the MFMA kernel takes column maxima of the raw scores: scale > 0)
-    if (a.dtype != kDtFP8 && mfma_group && mfma_dim && pow2_bs && a.scale > 0.0f &&
+    if ((a.dtype == kDtF16 || a.dtype == kDtBF16) && mfma_group && mfma_dim && pow2_bs &&
+        a.scale > 0.0f &&
         std::getenv("KCMM_ATTN_GENERIC") == nullptr) {
         if (a.dtype == kDtF16)
             return a.head_dim == 64 ? launch_group<kDtF16, 64>(a, p, s, err)
@@ -616,6 +621,10 @@ bool attn_prefill(const AttnPrefillArgs& a, std::string* err) {
             break;
         case kDtBF16:
             hipLaunchKernelGGL(attn_prefill_generic<kDtBF16>, grid, dim3(64), 0, s, p, kb, vb, btp,
+                               slp, qp, op);
+            break;
+        case kDtF32:
+            hipLaunchKernelGGL(attn_prefill_generic<kDtF32>, grid, dim3(64), 0, s, p, kb, vb, btp,
                                slp, qp, op);
             break;
         default:

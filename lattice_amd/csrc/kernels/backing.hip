@@ -11,6 +11,7 @@
 //    grows.  Opt-in: with the HIP runtime PyTorch-ROCm 7.0 ships, a process
 //    that created and destroyed a dozen VMM pools saw hipMemSetAccess fail
 //    with "invalid argument" and a crash inside pool teardown.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -130,19 +131,23 @@ private:
 
 }  // namespace
 
+__global__ void zero_words(u32x4* p, size_t n) {
+    for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256)
+        p[i] = u32x4{0, 0, 0, 0};
+}
+
 namespace dev {
 
 std::unique_ptr<PageBacking> make_backing(int device, std::string* err) {
     const char* env = std::getenv("KCMM_BACKING");
     if (env != nullptr && std::strcmp(env, "vmm") == 0) {
-        int vmm = 0;
-        if (hipDeviceGetAttribute(&vmm, hipDeviceAttributeVirtualMemoryManagementSupported,
-                                  device) != hipSuccess || !vmm) {
-            (void)hipGetLastError();
-            *err = "KCMM_BACKING=vmm but the device reports no HIP VMM support";
-            return nullptr;
-        }
-        return std::unique_ptr<PageBacking>(new HipVmmBacking(device));
+        // Switched off: in one process that created and destroyed about a
+        // dozen VMM pools, hipMemSetAccess began to fail ("invalid argument")
+        // and pool teardown crashed; the cause is not known.
+        *err = "KCMM_BACKING=vmm: the HIP VMM page backing is disabled in this build "
+               "(unexplained hipMemSetAccess failures after repeated pool create/destroy); "
+               "unset KCMM_BACKING for the flat backing";
+        return nullptr;
     }
     return std::unique_ptr<PageBacking>(new HipFlatBacking());
 }
@@ -175,12 +180,17 @@ bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool 
             w.ptr = nullptr;
             w.bytes = 0;
         }
-        const size_t want = bytes + bytes / 4;
+        const size_t want = (bytes + bytes / 4 + 255) & ~static_cast<size_t>(255);
         KCMM_HIP_CHECK(hipMalloc(&w.ptr, want), err);
         w.bytes = want;
-        if (zero_fill)
-            KCMM_HIP_CHECK(hipMemsetAsync(w.ptr, 0, want, reinterpret_cast<hipStream_t>(stream)),
-                           err);
+        if (zero_fill) {
+            // a kernel, not hipMemsetAsync: callers may be capturing a graph
+            const size_t words = want / 16;
+            hipLaunchKernelGGL(zero_words, dim3(static_cast<unsigned>(std::min<size_t>((words + 255) / 256, 4096))),
+                               dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                               static_cast<u32x4*>(w.ptr), words);
+            KCMM_HIP_CHECK(hipGetLastError(), err);
+        }
     }
     *out = w.ptr;
     return true;

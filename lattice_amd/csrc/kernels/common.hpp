@@ -19,6 +19,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 constexpr int kDtF16 = 0;
 constexpr int kDtBF16 = 1;
 constexpr int kDtFP8 = 2;
+constexpr int kDtF32 = 3;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
     return __uint_as_float(h << 16);
@@ -65,6 +66,33 @@ __device__ __forceinline__ float fp8e4m3_to_f32(uint32_t b) {
         return __uint_as_float(s) + (s ? -1.0f : 1.0f) * static_cast<float>(m) * 0.001953125f;
     }
     return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// q / out rows of the attention kernels: f16 for f16 pools, fp32 for fp32
+// pools, bf16 otherwise (bf16 and fp8 pools).  Element i of a row at `row`.
+template <int DT>
+__device__ __forceinline__ float io_load(const uint8_t* row, int i) {
+    if constexpr (DT == kDtF32) return reinterpret_cast<const float*>(row)[i];
+    else if constexpr (DT == kDtF16) return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(row)[i]);
+    else return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(row)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void io_store(uint8_t* row, int i, float v) {
+    if constexpr (DT == kDtF32) reinterpret_cast<float*>(row)[i] = v;
+    else if constexpr (DT == kDtF16) reinterpret_cast<uint16_t*>(row)[i] = static_cast<uint16_t>(f32_to_f16_bits(v));
+    else reinterpret_cast<uint16_t*>(row)[i] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+}
+template <int DT>
+constexpr int io_bytes() { return DT == kDtF32 ? 4 : 2; }
+// Bytes of one K/V element in a page of type DT.
+template <int DT>
+constexpr int kv_elem_bytes() { return DT == kDtFP8 ? 1 : (DT == kDtF32 ? 4 : 2); }
+// exp for the any-shape kernels: correctly rounded-ish expf for fp32 pools
+// (their tolerance is 1e-5), the hardware exp2 path otherwise.
+template <int DT>
+__device__ __forceinline__ float kexp(float x) {
+    if constexpr (DT == kDtF32) return expf(x);
+    else return __expf(x);
 }
 
 __device__ __forceinline__ float bf16_round_f32(float f) {

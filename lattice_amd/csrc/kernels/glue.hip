@@ -351,7 +351,7 @@ bool launch_rope(const RopeAppendArgs& a, const float* part, int splits, std::st
         w.offsets_f16 = a.offsets_f16;
         w.valid_blocks = 0;   // slots come from the block table
         w.status = 0;
-        w.offsets_len = 0xFFFFFFFFu;
+        w.offsets_len = a.n_ids;
         w.batch = a.batch;
         w.block_size = a.block_size;
         w.kv_heads = a.kv_heads;

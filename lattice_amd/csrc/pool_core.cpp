@@ -30,6 +30,7 @@ bool PoolGeometry::compute(std::string* err) {
         case kF16:
         case kBF16: elem_bytes = 2; break;
         case kFP8: elem_bytes = 1; break;
+        case kF32: elem_bytes = 4; break;
         default: *err = "pool geometry: unknown kv dtype"; return false;
     }
     row_bytes = kv_heads * head_dim * elem_bytes;
@@ -327,25 +328,77 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
         return false;
     }
     const uint32_t bs = static_cast<uint32_t>(geo_.block_size);
+    const uint32_t forks = width - 1;
+    std::lock_guard<std::mutex> lk(mu_);
+    // Everything that can fail is checked before any state changes: the
+    // parents, the page each child makes private, and the capacity for them.
+    // Every child needs its own copy of that page: after the forks it is
+    // shared by the parent and all the children still to be made private.
+    size_t needed = 0;
     for (uint32_t i = 0; i < n; ++i) {
-        for (uint32_t c = 0; c + 1 < width; ++c) {
-            uint32_t child = 0;
-            if (!fork_sequence(parents[i], &child, err)) return false;
-            children[static_cast<size_t>(i) * (width - 1) + c] = child;
-            uint32_t logical = 0, table_len = 0;
-            {
-                std::lock_guard<std::mutex> lk(mu_);
-                logical = seqs_[child].seq_len / bs;
-                table_len = static_cast<uint32_t>(seqs_[child].table.size());
+        if (parents[i] >= seqs_.size()) {
+            *err = fmt("kcmm_fork_beams: parent seq_idx %llu out of bounds", parents[i]);
+            return false;
+        }
+        const SequenceState& ps = seqs_[parents[i]];
+        const uint32_t logical = ps.seq_len / bs;
+        if (forks == 0 || logical >= ps.table.size()) continue;   // the next token opens a new page
+        const uint32_t id = ps.table[logical];
+        if (id >= blocks_.size() || !blocks_[id].in_use) {
+            *err = fmt("kcmm_fork_beams: block %llu of parent %llu not in use", id, parents[i]);
+            return false;
+        }
+        if (blocks_[id].location != kLocGpu) {
+            *err = fmt("kcmm_fork_beams: block %llu is not resident in HBM (restore it first)", id);
+            return false;
+        }
+        needed += forks;
+    }
+    const size_t grow = geo_.max_physical_blocks - superblock_count_ * geo_.blocks_per_superblock;
+    if (needed > free_handles_.size() + grow) {
+        *err = fmt("kcmm_fork_beams: %llu new pages needed, %llu free within the pool's capacity",
+                   needed, free_handles_.size() + grow);
+        return false;
+    }
+    const size_t seqs0 = seqs_.size(), pairs0 = pairs->size();
+    seqs_.reserve(seqs0 + static_cast<size_t>(n) * forks);
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t p = parents[i];
+        // the forks' references, all at once (ref fork: same ids, refcount + 1)
+        for (uint32_t id : seqs_[p].table)
+            if (id < blocks_.size() && blocks_[id].in_use) blocks_[id].refcount += forks;
+        const uint32_t logical = seqs_[p].seq_len / bs;
+        for (uint32_t c = 0; c < forks; ++c) {
+            SequenceState s;
+            s.table = seqs_[p].table;
+            s.seq_len = seqs_[p].seq_len;
+            seqs_.push_back(std::move(s));
+            const uint32_t child = static_cast<uint32_t>(seqs_.size() - 1);
+            children[static_cast<size_t>(i) * forks + c] = child;
+            if (logical >= seqs_[child].table.size()) continue;
+            const uint32_t old_id = seqs_[child].table[logical];
+            uint32_t new_id = 0;
+            if (!alloc_one_locked(&new_id, err)) {
+                // Only a page backing that fails to map memory gets here.
+                // Undo the call: new pages back in reverse order (the free
+                // list is LIFO), references and children removed.
+                for (size_t q = pairs->size(); q > pairs0; q -= 2) {
+                    const uint32_t nid = (*pairs)[q - 1];
+                    blocks_[nid].refcount = 1;
+                    release_locked(&nid, 1);
+                    ++blocks_[(*pairs)[q - 2]].refcount;
+                }
+                pairs->resize(pairs0);
+                for (uint32_t j = 0; j <= i; ++j)
+                    for (uint32_t id : seqs_[parents[j]].table)
+                        if (id < blocks_.size() && blocks_[id].in_use) blocks_[id].refcount -= forks;
+                seqs_.resize(seqs0);
+                return false;
             }
-            if (logical >= table_len) continue;   // the next token opens a new page
-            uint32_t src = 0, dst = 0;
-            const int rc = cow_block_for_append(child, logical, &src, &dst, err);
-            if (rc < 0) return false;
-            if (rc == 1) {
-                pairs->push_back(src);
-                pairs->push_back(dst);
-            }
+            seqs_[child].table[logical] = new_id;
+            --blocks_[old_id].refcount;
+            pairs->push_back(old_id);
+            pairs->push_back(new_id);
         }
     }
     return true;

@@ -35,7 +35,7 @@ namespace kcmm {
 
 constexpr size_t kSuperblockBytes = 2u * 1024u * 1024u;
 
-enum KvDtype : int32_t { kF16 = 0, kBF16 = 1, kFP8 = 2 };
+enum KvDtype : int32_t { kF16 = 0, kBF16 = 1, kFP8 = 2, kF32 = 3 };
 
 // Maps 2 MiB superblocks into 2*num_layers device VA regions (layer l: K at
 // region 2l, V at region 2l+1).  Implemented over HIP VMM / hipMalloc in the
@@ -162,8 +162,8 @@ public:
     // forked and then made private at the page of its next token (logical
     // block seq_len / block_size, when allocated).  Appends the (src, dst)
     // page copies to *pairs and the children (parent-major) to children.
-    // On error the operations already done stay done (as with the separate
-    // calls).
+    // All or nothing: parents, pages and capacity are checked before any
+    // state changes, so a failed call leaves the pool as it was.
     bool fork_beams(const uint32_t* parents, uint32_t n, uint32_t width, uint32_t* children,
                     std::vector<uint32_t>* pairs, std::string* err);
     // Byte offsets of the pages of (src, dst) pairs; false if an id is not in use.

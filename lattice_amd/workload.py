@@ -14,7 +14,8 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from .bindings import KV_BF16, KV_F16, KV_FP8, KcmmLibrary, KcmmPool, make_config, memcpy_htod
+from .bindings import (KV_BF16, KV_F16, KV_F32, KV_FP8, KcmmLibrary, KcmmPool, make_config,
+                       memcpy_htod)
 
 SB = 2 * 1024 * 1024
 
@@ -34,7 +35,24 @@ def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
 
 
 def encode16(dtype: int, x: np.ndarray) -> np.ndarray:
+    """Element bits of a 16-bit pool type (or the fp32 values of an fp32 pool)."""
+    if dtype == KV_F32:
+        return np.ascontiguousarray(x, dtype=np.float32)
     return f32_to_f16_bits(x) if dtype == KV_F16 else f32_to_bf16_bits(x)
+
+
+def elem_bytes(dtype: int) -> int:
+    """Bytes of one K/V element of a pool type."""
+    return {KV_FP8: 1, KV_F32: 4}.get(dtype, 2)
+
+
+def io_dtype(dtype: int) -> int:
+    """Element type of q/out rows: f16 for f16 pools, fp32 for fp32 pools, bf16 otherwise."""
+    return dtype if dtype in (KV_F16, KV_F32) else KV_BF16
+
+
+def torch_io_dtype(dtype: int):
+    return {KV_F16: torch.float16, KV_F32: torch.float32}.get(dtype, torch.bfloat16)
 
 
 def encode_fp8_page(blk: np.ndarray):
@@ -73,7 +91,7 @@ class DecodeCase:
     @property
     def geometry(self) -> dict:
         st = self.pool.stats()
-        elem = 1 if self.dtype == KV_FP8 else 2
+        elem = elem_bytes(self.dtype)
         row_bytes = self.kv_heads * self.head_dim * elem
         return dict(block_bytes=st["block_bytes"], row_bytes=row_bytes,
                     data_bytes=row_bytes * self.block_size,
@@ -81,7 +99,7 @@ class DecodeCase:
 
     def kv_bytes(self) -> int:
         """Algorithmic K+V bytes one decode attention step reads (one layer)."""
-        elem = 1 if self.dtype == KV_FP8 else 2
+        elem = elem_bytes(self.dtype)
         return int(self.seq_lens.astype(np.int64).sum()) * 2 * self.kv_heads * self.head_dim * elem
 
     def run_attention(self, layer: int = 0, stream_ptr: int | None = None, scale=None) -> None:
@@ -96,6 +114,9 @@ class DecodeCase:
             stream_ptr=stream_ptr)
 
     def out_bits(self) -> np.ndarray:
+        """Output element bits (fp32 values for an fp32 pool)."""
+        if self.dtype == KV_F32:
+            return self.dev["out"].cpu().numpy()
         return self.dev["out"].cpu().view(torch.int16).numpy().view(np.uint16)
 
 
@@ -163,7 +184,7 @@ def build_decode_case(lib: KcmmLibrary, *, batch: int, num_q_heads: int, kv_head
         s = pool.register_sequence(bt[b, :n].tolist())
         pool.update_seq_len(s, int(ctx[b]))
     offs = np.asarray(pool.all_block_offsets_f16(), dtype=np.uint64)
-    qdt = KV_F16 if dtype == KV_F16 else KV_BF16   # fp8 pools take bf16 queries
+    qdt = io_dtype(dtype)   # fp8 pools take bf16 queries
     q = encode16(qdt, rng.standard_normal((batch, num_q_heads, head_dim)).astype(np.float32))
     case = DecodeCase(lib=lib, pool=pool, dtype=dtype, batch=batch, num_q_heads=num_q_heads,
                       kv_heads=kv_heads, head_dim=head_dim, block_size=block_size,
@@ -173,9 +194,10 @@ def build_decode_case(lib: KcmmLibrary, *, batch: int, num_q_heads: int, kv_head
         _fill_pages_host(case, rng, ctx)
     else:
         fill_regions_on_device(case, seed)
-    tdt = torch.float16 if dtype == KV_F16 else torch.bfloat16
+    tdt = torch_io_dtype(dtype)
+    qt = torch.from_numpy(q.copy()) if dtype == KV_F32 else torch.from_numpy(q.view(np.int16)).view(tdt)
     case.dev = {
-        "q": torch.from_numpy(q.view(np.int16)).view(tdt).to(device),
+        "q": qt.to(device),
         "out": torch.zeros((batch, num_q_heads, head_dim), dtype=tdt, device=device),
         "bt": torch.from_numpy(bt).to(device),
         "sl": torch.from_numpy(case.seq_lens.copy()).to(device),
@@ -207,15 +229,16 @@ def fill_regions_on_device(case: DecodeCase, seed: int) -> None:
         _fill_fp8_on_device(case, gen)
         torch.cuda.synchronize()
         return
-    n = g["mapped_bytes"] // 2
-    tdt = torch.float16 if case.dtype == KV_F16 else torch.bfloat16
+    es = elem_bytes(case.dtype)
+    n = g["mapped_bytes"] // es
+    tdt = torch_io_dtype(case.dtype)
     for layer in range(case.num_layers):
         for base in (case.pool.va_k(layer), case.pool.va_v(layer)):
             chunk = 64 << 20
             for off in range(0, n, chunk):
                 m = min(chunk, n - off)
                 t = torch.randn(m, generator=gen, device="cuda", dtype=torch.float32).to(tdt)
-                _region_copy(base + 2 * off, t, 2 * m)
+                _region_copy(base + es * off, t, es * m)
     torch.cuda.synchronize()
 
 
@@ -328,8 +351,8 @@ def build_prefix_shared_case(lib: KcmmLibrary, *, batch: int, prefix_tokens: int
     offs = np.asarray(pool.all_block_offsets_f16(), dtype=np.uint64)
     sl = np.full(batch, total, dtype=np.int32)
     qsl = (np.arange(batch + 1) * chunk).astype(np.int32)
-    qdt = KV_F16 if dtype == KV_F16 else KV_BF16
-    q = encode16(qdt, rng.standard_normal((batch * chunk, num_q_heads, head_dim)).astype(np.float32))
+    q = encode16(io_dtype(dtype),
+                 rng.standard_normal((batch * chunk, num_q_heads, head_dim)).astype(np.float32))
     case = PrefillCase(pool=pool, dtype=dtype, num_q_heads=num_q_heads, kv_heads=kv_heads,
                        head_dim=head_dim, block_size=block_size, block_tables=bt, seq_lens=sl,
                        qsl=qsl, offsets_f16=offs, q_bits=q)
@@ -338,9 +361,10 @@ def build_prefix_shared_case(lib: KcmmLibrary, *, batch: int, prefix_tokens: int
                       num_layers=num_layers, seq_lens=sl, block_tables=bt, offsets_f16=offs,
                       q_bits=q)
     fill_regions_on_device(shim, seed + 1)
-    tdt = torch.float16 if dtype == KV_F16 else torch.bfloat16
+    tdt = torch_io_dtype(dtype)
+    qt = torch.from_numpy(q.copy()) if dtype == KV_F32 else torch.from_numpy(q.view(np.int16)).view(tdt)
     case.dev = {
-        "q": torch.from_numpy(q.view(np.int16)).view(tdt).to(device),
+        "q": qt.to(device),
         "out": torch.zeros((batch * chunk, num_q_heads, head_dim), dtype=tdt, device=device),
         "bt": torch.from_numpy(bt).to(device),
         "sl": torch.from_numpy(sl.copy()).to(device),

@@ -308,10 +308,24 @@ class OracleTier:
 
 # ---- KV write / page copy ------------------------------------------------------
 
+def _check_page_end(regions, page_end: int, what: str) -> None:
+    """The C oracle trusts its offsets: refuse writes past a host region."""
+    if any(r.nbytes < page_end for r in regions):
+        raise ValueError(f"{what}: a write ends at byte {page_end}, past a region of "
+                         f"{min(r.nbytes for r in regions)} bytes")
+
+
+def _page_bytes(dtype, kv_heads, data_bytes):
+    return data_bytes + (4 * kv_heads if dtype == FP8 else 0)
+
+
 def kv_write_rows(dtype, k_region, v_region, k_src, v_src, page_offsets, slots, src_rows,
                   kv_heads, head_dim, row_bytes, data_bytes):
     po = np.ascontiguousarray(page_offsets, dtype=np.uint64)
     sl = np.ascontiguousarray(slots, dtype=np.uint32)
+    if po.size:
+        _check_page_end((k_region, v_region),
+                        int(po.max()) + _page_bytes(dtype, kv_heads, data_bytes), "kv_write_rows")
     sr = np.ascontiguousarray(src_rows, dtype=np.uint32)
     lib().oracle_kv_write_rows(dtype, _p(k_region), _p(v_region), _p(k_src), _p(v_src), _p(po),
                                _p(sl), _p(sr), po.size, kv_heads, head_dim, row_bytes, data_bytes)
@@ -321,6 +335,12 @@ def kv_write_device_slots(dtype, k_region, v_region, k_src, v_src, slots, offset
                           block_size, kv_heads, head_dim, row_bytes, data_bytes) -> int:
     s = np.ascontiguousarray(slots, dtype=np.int64)
     o = np.ascontiguousarray(offsets_f16, dtype=np.uint64)
+    ids = s[s >= 0] // block_size
+    ids = ids[ids < o.size]
+    if ids.size:
+        _check_page_end((k_region, v_region),
+                        int(o[ids].max()) * 2 + _page_bytes(dtype, kv_heads, data_bytes),
+                        "kv_write_device_slots")
     v = None if valid is None else np.ascontiguousarray(valid, dtype=np.uint8)
     status = np.zeros(1, dtype=np.int32)
     lib().oracle_kv_write_device_slots(dtype, _p(k_region), _p(v_region), _p(k_src), _p(v_src),
@@ -332,6 +352,11 @@ def kv_write_device_slots(dtype, k_region, v_region, k_src, v_src, slots, offset
 def copy_pages(regions: list[np.ndarray], pairs, block_bytes: int) -> None:
     ptrs = (C.c_void_p * len(regions))(*[r.ctypes.data for r in regions])
     pr = np.ascontiguousarray(pairs, dtype=np.uint64).reshape(-1)
+    if pr.size:
+        end = int(pr.max()) + block_bytes
+        if any(r.nbytes < end for r in regions):
+            raise ValueError(f"copy_pages: a page ends at byte {end}, past a region of "
+                             f"{min(r.nbytes for r in regions)} bytes")
     lib().oracle_copy_pages(C.cast(ptrs, C.c_void_p), len(regions), _p(pr), pr.size // 2,
                             block_bytes)
 

@@ -200,3 +200,44 @@ def test_decode_layer_entry_points_validate_before_device_work(hostcheck_lib):
     finally:
         f16.destroy()
         bf.destroy()
+
+
+def test_fork_beams_all_or_nothing(hostcheck_lib):
+    """kcmm_fork_beams_on_stream checks parents, pages and capacity before it
+    changes anything: a call that would run out of pages partway through (or
+    names an unknown parent after valid ones) fails and leaves tables,
+    refcounts, sequences and the free lists exactly as they were."""
+    from lattice_amd.bindings import KV_BF16, make_config
+    # 64 blocks of capacity at this geometry: bs 16, max_batch 2 x 512 tokens
+    cfg = make_config(num_layers=2, kv_heads=2, head_dim=64, max_batch=2, max_seq_len=512)
+    pool = hostcheck_lib.create_pool(cfg, KV_BF16)
+    try:
+        cap = pool.stats()["blocks_per_superblock"]
+        parents = []
+        for _ in range(4):
+            ids = pool.alloc_blocks(3)
+            s = pool.register_sequence(ids)
+            pool.update_seq_len(s, 40)          # next token in logical block 2 (allocated)
+            parents.append(s)
+        def snapshot():
+            st = pool.stats()
+            return (st, [pool.block_table(s) for s in parents],
+                    [pool.refcount(i) for i in range(pool.total_blocks())])
+        before = snapshot()
+        free = before[0]["free_physical_blocks"]
+        width = 2 + free // len(parents)        # needs more new pages than are free
+        assert len(parents) * (width - 1) > free and cap >= 12
+        with pytest.raises(Exception):
+            pool.fork_beams(parents, width)
+        assert "new pages needed" in pool.last_error()
+        assert snapshot() == before
+        with pytest.raises(Exception):
+            pool.fork_beams(parents + [10 ** 6], 2)
+        assert "out of bounds" in pool.last_error()
+        assert snapshot() == before
+        # the pool still works: a fork with no page copy (no device work) goes through
+        pool.update_seq_len(parents[0], 48)
+        children, copies = pool.fork_beams(parents[:1], 3)
+        assert copies == 0 and [pool.block_table(c) for c in children] == [before[1][0]] * 2
+    finally:
+        pool.destroy()

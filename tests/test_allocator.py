@@ -10,6 +10,7 @@ import random
 import numpy as np
 import pytest
 
+import oracle as O
 from tests.poolapi import OracleAdapter, ProductAdapter
 
 SB = 2 * 1024 * 1024
@@ -314,3 +315,25 @@ def test_differential_oracle_vs_product(hostcheck_lib, oracle_lib, seed, shape):
             assert a.below(t) == b.below(t)
     finally:
         b.close()
+
+
+def test_fp32_pool_geometry_matches_oracle(hostcheck_lib):
+    """fp32 pages: 4-byte elements, so a page at
+    Hkv = 8, D = 64, bs = 16 is 32 KiB (64 per 2 MiB superblock); ids and
+    offsets of the product pool equal the oracle pool's."""
+    from lattice_amd.bindings import KV_F32, make_config
+    cfg = make_config(num_layers=1, kv_heads=8, head_dim=64, max_batch=4, max_seq_len=1024)
+    pool = hostcheck_lib.create_pool(cfg, KV_F32)
+    opool = O.OraclePool(16, 1, 8, 64, 4, 1024, O.F32)
+    try:
+        assert pool.kv_dtype() == KV_F32
+        ids = pool.alloc_blocks(256)
+        assert ids == opool.alloc(256) == list(range(256))
+        st = pool.stats()
+        assert st["block_bytes"] == 32768 and st["blocks_per_superblock"] == 64
+        assert st["superblock_count"] == 4
+        assert np.array_equal(pool.all_block_offsets_f16(), opool.offsets_f16()[:256])
+        with pytest.raises(Exception):
+            pool.alloc_blocks(1)                 # capacity: 4 x 1024 / 16 = 256 pages
+    finally:
+        pool.destroy()

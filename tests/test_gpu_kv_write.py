@@ -180,3 +180,134 @@ def test_host_variants_validate_before_writing(gpu_lib):
         assert not kr.any() and not vr.any()
     finally:
         pool.destroy()
+
+
+def _prefill_rows(rng, tables, bs, tokens, order):
+    """Slot ids of `tokens` tokens per sequence, in one of several call orders:
+    'seq' (each sequence's tokens in order, prefill style), 'interleaved'
+    (token-major: the rows of one page are not adjacent), 'shuffled' (random
+    order, some slots repeated and padding rows mixed in)."""
+    per_seq = [[tables[b][t // bs] * bs + t % bs for t in range(tokens)]
+               for b in range(len(tables))]
+    if order == "seq":
+        return [s for row in per_seq for s in row]
+    if order == "interleaved":
+        return [per_seq[b][t] for t in range(tokens) for b in range(len(tables))]
+    flat = [s for row in per_seq for s in row]
+    flat += [flat[i] for i in rng.choice(len(flat), size=len(flat) // 8, replace=False)]
+    flat += [-1] * 5
+    return [flat[i] for i in rng.permutation(len(flat))]
+
+
+@pytest.mark.parametrize("order", ["seq", "interleaved", "shuffled"])
+@pytest.mark.parametrize("path", ["device", "host"])
+def test_fp8_multi_token_pages_vs_oracle(gpu_lib, order, path):
+    """fp8 pages written by calls that put many tokens of a sequence (two and
+    a half pages' worth) into the same pages: every row of a page must be
+    applied in call order (each one may raise the page scale and re-encode
+    the rows before it), bit-exact with the oracle's sequential writer."""
+    import torch
+    rng = np.random.default_rng(77 + len(order) + (path == "host"))
+    B, hk, d, bs, L = 5, 8, 128, 16, 1
+    tokens = 2 * bs + bs // 2
+    pool = gpu_lib.create_pool(make_config(num_layers=L, kv_heads=hk, head_dim=d, max_batch=B,
+                                           max_seq_len=64), KV_FP8)
+    try:
+        n_pages = 3
+        ids = pool.alloc_blocks(B * n_pages)
+        perm = rng.permutation(ids)
+        tables = [perm[i * n_pages:(i + 1) * n_pages].tolist() for i in range(B)]
+        for t in tables:
+            pool.register_sequence(t)
+        zero_regions(pool)
+        nb = pool.stats()["superblock_count"] * SB
+        ok, ov = np.zeros(nb, np.uint8), np.zeros(nb, np.uint8)
+        offs = pool.all_block_offsets_f16()
+        offs_t = torch.tensor(offs, dtype=torch.int64, device="cuda")
+        g_row, data_bytes = hk * d, hk * d * bs
+        stream = torch.cuda.current_stream()
+        for call in range(2):   # the second call rewrites the same pages from slot 0
+            slots = _prefill_rows(rng, tables, bs, tokens, order)
+            n = len(slots)
+            mag = np.where(rng.random(n) < 0.2, 8.0, 1.0)[None, :, None]
+            x = (rng.standard_normal((2, n, hk * d)) * mag).astype(np.float32)
+            bits = O.encode(O.BF16, x)
+            k = torch.from_numpy(bits[0].view(np.int16)).view(torch.bfloat16).cuda()
+            v = torch.from_numpy(bits[1].view(np.int16)).view(torch.bfloat16).cuda()
+            if path == "device":
+                sl = torch.tensor(slots, dtype=torch.int64, device="cuda")
+                st = torch.zeros(1, dtype=torch.int32, device="cuda")
+                pool.append_kv_device_slots_on_stream(
+                    layer_idx=0, slot_mapping_ptr=sl.data_ptr(),
+                    block_offsets_f16_ptr=offs_t.data_ptr(), valid_blocks_ptr=0,
+                    block_offsets_f16_len=len(offs), batch=n, k_src_ptr=k.data_ptr(),
+                    v_src_ptr=v.data_ptr(), status_ptr=st.data_ptr(),
+                    stream_ptr=stream.cuda_stream)
+            else:
+                pool.append_kv_slots(0, slots, k.data_ptr(), v.data_ptr(),
+                                     stream_ptr=stream.cuda_stream)
+            stream.synchronize()
+            if path == "device":
+                assert int(st.item()) == 0
+            O.kv_write_device_slots(KV_FP8, ok, ov, bits[0], bits[1], slots,
+                                    np.asarray(offs, np.uint64), None, bs, hk, d, g_row,
+                                    data_bytes)
+            gk, gv = region_bytes(pool)
+            assert np.array_equal(gk, ok), f"K after call {call}"
+            assert np.array_equal(gv, ov), f"V after call {call}"
+    finally:
+        pool.destroy()
+
+
+def test_fp8_device_slots_status_and_repeat_calls(gpu_lib):
+    """The fp8 device-slot writer keeps its per-block row table zero between
+    calls: an inactive block (status 2) and an id past the table (status 1,
+    first error wins) are skipped, and later calls with other pages and batch
+    sizes stay bit-exact with the oracle."""
+    import torch
+    rng = np.random.default_rng(5)
+    hk, d, bs = 2, 128, 16
+    pool = gpu_lib.create_pool(make_config(num_layers=1, kv_heads=hk, head_dim=d, max_batch=4,
+                                           max_seq_len=128), KV_FP8)
+    try:
+        ids = pool.alloc_blocks(12)
+        zero_regions(pool)
+        nb = pool.stats()["superblock_count"] * SB
+        ok, ov = np.zeros(nb, np.uint8), np.zeros(nb, np.uint8)
+        offs = pool.all_block_offsets_f16()
+        valid = np.ones(len(offs), np.uint8)
+        valid[ids[3]] = 0
+        offs_t = torch.tensor(offs, dtype=torch.int64, device="cuda")
+        valid_t = torch.from_numpy(valid).cuda()
+        stream = torch.cuda.current_stream()
+        # "first error wins" is the first to arrive on the device (ref
+        # kcmm_vllm_kv_write.cu: atomicCAS), so a call mixing both kinds may
+        # report either; the oracle reports the first in row order
+        calls = [(40, [ids[3] * bs + 2, ids[3] * bs + 9], {2}),
+                 (7, [len(offs) * bs, len(offs) * bs + 40], {1}),
+                 (33, [len(offs) * bs + 3, ids[3] * bs], {1, 2}), (90, [], {0})]
+        for call, (n, bad, want) in enumerate(calls):
+            good = [i for i in ids if i != ids[3]]
+            slots = [int(rng.choice(good)) * bs + int(rng.integers(bs)) for _ in range(n)]
+            for j, s in enumerate(bad):
+                slots.insert(3 + 5 * j, s)
+            x = rng.standard_normal((2, len(slots), hk * d)).astype(np.float32) * 3
+            bits = O.encode(O.BF16, x)
+            k = torch.from_numpy(bits[0].view(np.int16)).view(torch.bfloat16).cuda()
+            v = torch.from_numpy(bits[1].view(np.int16)).view(torch.bfloat16).cuda()
+            sl = torch.tensor(slots, dtype=torch.int64, device="cuda")
+            st = torch.zeros(1, dtype=torch.int32, device="cuda")
+            pool.append_kv_device_slots_on_stream(
+                layer_idx=0, slot_mapping_ptr=sl.data_ptr(),
+                block_offsets_f16_ptr=offs_t.data_ptr(), valid_blocks_ptr=valid_t.data_ptr(),
+                block_offsets_f16_len=len(offs), batch=len(slots), k_src_ptr=k.data_ptr(),
+                v_src_ptr=v.data_ptr(), status_ptr=st.data_ptr(), stream_ptr=stream.cuda_stream)
+            stream.synchronize()
+            ost = O.kv_write_device_slots(KV_FP8, ok, ov, bits[0], bits[1], slots,
+                                          np.asarray(offs, np.uint64), valid, bs, hk, d, hk * d,
+                                          hk * d * bs)
+            assert int(st.item()) in want and ost in want
+            gk, gv = region_bytes(pool)
+            assert np.array_equal(gk, ok) and np.array_equal(gv, ov), f"call {call}"
+    finally:
+        pool.destroy()

@@ -10,7 +10,8 @@ import pytest
 
 import oracle as O
 from lattice_amd.bindings import KV_BF16, KV_F16, KV_FP8, memcpy_dtoh
-from lattice_amd.workload import build_decode_case, build_prefix_shared_case, encode16
+from lattice_amd.workload import (build_decode_case, build_prefix_shared_case, encode16,
+                                  io_dtype, torch_io_dtype)
 
 pytestmark = pytest.mark.gpu
 
@@ -27,11 +28,12 @@ def run_prefill(case, lens, hq, seed, scale=None):
     g = case.geometry
     d = case.head_dim
     qsl = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
-    qdt = KV_F16 if case.dtype == KV_F16 else KV_BF16
+    qdt = io_dtype(case.dtype)
     rng = np.random.default_rng(seed)
     q = encode16(qdt, rng.standard_normal((int(qsl[-1]), hq, d)).astype(np.float32))
-    tdt = torch.float16 if qdt == KV_F16 else torch.bfloat16
-    qt = torch.from_numpy(q.view(np.int16)).view(tdt).cuda()
+    tdt = torch_io_dtype(case.dtype)
+    qt = (torch.from_numpy(q.copy()) if qdt == O.F32 else
+          torch.from_numpy(q.view(np.int16)).view(tdt)).cuda()
     out = torch.full((int(qsl[-1]), hq, d), float("nan"), dtype=tdt, device="cuda")
     qslt = torch.from_numpy(qsl).cuda()
     scale = 1 / math.sqrt(d) if scale is None else scale
@@ -45,8 +47,11 @@ def run_prefill(case, lens, hq, seed, scale=None):
         max_blocks_per_seq=case.mbps, scale=scale,
         stream_ptr=torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    got = O.decode(O.F16 if qdt == KV_F16 else O.BF16,
-                   out.cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+    if qdt == O.F32:
+        got = out.cpu().numpy().astype(np.float64)
+    else:
+        got = O.decode(O.F16 if qdt == KV_F16 else O.BF16,
+                       out.cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
     ref = O.attn_prefill_f64(case.dtype, q, case.k_mirror[0], case.v_mirror[0],
                              case.block_tables, case.seq_lens, qsl, case.offsets_f16, hq,
                              case.kv_heads, d, case.block_size, g["row_bytes"],

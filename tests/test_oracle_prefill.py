@@ -41,14 +41,14 @@ def dense_causal(qd, lay, qsl, hq, hkv, scale):
     return out
 
 
-@pytest.mark.parametrize("dtype", [O.BF16, O.F16, O.FP8])
+@pytest.mark.parametrize("dtype", [O.BF16, O.F16, O.FP8, O.F32])
 @pytest.mark.parametrize("hq,hkv,d,bs", [(8, 2, 64, 16), (32, 8, 128, 16), (4, 4, 32, 8)])
 def test_matches_dense_causal_softmax(oracle_lib, dtype, hq, hkv, d, bs):
     ctx = [40, 17, 70, 1]
     lens = [13, 17, 32, 1]           # a chunk may be the whole sequence
     lay, qsl = chunk_setup(ctx, lens, hkv, d, bs, dtype, seed=hq + d + dtype)
     rng = np.random.default_rng(11)
-    qdt = O.F16 if dtype == O.F16 else O.BF16
+    qdt = dtype if dtype in (O.F16, O.F32) else O.BF16
     q = O.encode(qdt, rng.standard_normal((qsl[-1], hq, d)).astype(np.float32))
     scale = 1 / np.sqrt(d)
     got = run(lay, qsl, q, hq, hkv, d, bs, dtype, scale)
