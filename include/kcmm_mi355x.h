@@ -81,6 +81,24 @@ int kcmm_paged_attn_decode_fp8_on_stream(
     uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
     uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
 
+/**
+ * kcmm_paged_attn_decode_bf16_on_stream without any device allocation: the
+ * kernels' scratch (partial results, segment table) is a static 24 MiB device
+ * array in the library instead of a per-stream workspace.  No counterpart in
+ * the reference: for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  A batch
+ * whose scratch would exceed 24 MiB is refused (-1, error text names the
+ * sizes); at the Llama-3-8B decode shape (32/8 heads, head_dim 128) that is
+ * about 300 sequences.  Every call on a GPU shares that GPU's array: calls
+ * that overlap on one GPU (other streams, other threads) race.  Enqueue only.
+ */
+int kcmm_paged_attn_decode_bf16_noalloc_on_stream(
+    kcmm_pool_t *pool, uint32_t layer_idx, uint64_t query_ptr, uint64_t out_ptr,
+    uint64_t block_tables_ptr, uint64_t seq_lens_ptr,
+    uint64_t block_offsets_f16_ptr, uint32_t batch, uint32_t num_q_heads,
+    uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
+    uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
+
 /** fp32 pool: fp32 q/out, same tensor contract as
  *  kcmm_paged_attn_decode_f16 (ref kcmm.h:505).  Synchronizes before
  *  returning. */

@@ -134,6 +134,7 @@ SIGNATURES = {
     "kcmm_paged_attn_decode_bf16": (_ATTN, C.c_int),
     "kcmm_paged_attn_decode_bf16_on_stream": (_ATTN + [_U64], C.c_int),
     "kcmm_paged_attn_decode_fp8_on_stream": (_ATTN + [_U64], C.c_int),
+    "kcmm_paged_attn_decode_bf16_noalloc_on_stream": (_ATTN + [_U64], C.c_int),
     "kcmm_paged_attn_decode_f32": (_ATTN, C.c_int),
     "kcmm_paged_attn_decode_f32_on_stream": (_ATTN + [_U64], C.c_int),
     "kcmm_paged_attn_prefill_on_stream": ([_P, _U32, _U64, _U64, _U64, _U64, _U64, _U64, _U32,

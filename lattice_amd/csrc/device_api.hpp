@@ -42,6 +42,7 @@ struct AttnDecodeArgs {
     uint32_t data_bytes;    // bytes of page data before the fp8 scale footer
     float scale;
     uint64_t stream;
+    bool no_alloc = false;  // scratch from the static array, never the workspace
 };
 bool attn_decode(const AttnDecodeArgs& a, std::string* err);
 

@@ -82,7 +82,7 @@ bool layer_ok(kcmm_pool_t* p, uint32_t layer, const char* fn) {
 int attn_impl(kcmm_pool_t* pool, int32_t want_dtype, const char* fn, uint32_t layer_idx,
               uint64_t q, uint64_t out, uint64_t bt, uint64_t sl, uint64_t offs, uint32_t batch,
               uint32_t hq, uint32_t hkv, uint32_t d, uint32_t bs, uint32_t mbps, float scale,
-              uint64_t stream, bool sync_after, bool bind_device) {
+              uint64_t stream, bool sync_after, bool bind_device, bool no_alloc = false) {
     if (pool == nullptr || q == 0 || out == 0 || bt == 0 || sl == 0 || offs == 0) {
         if (pool) pool->set_error(std::string(fn) + ": null pointer argument");
         return -1;
@@ -139,6 +139,7 @@ int attn_impl(kcmm_pool_t* pool, int32_t want_dtype, const char* fn, uint32_t la
     a.data_bytes = static_cast<uint32_t>(g.data_bytes);
     a.scale = scale;
     a.stream = stream;
+    a.no_alloc = no_alloc;
     if (!kcmm::dev::attn_decode(a, &err)) {
         pool->set_error(std::string(fn) + ": launch failed: " + err);
         return -1;
@@ -560,6 +561,11 @@ int kcmm_paged_attn_decode_bf16(KCMM_ATTN_ARGS) {
 int kcmm_paged_attn_decode_bf16_on_stream(KCMM_ATTN_ARGS, uint64_t stream) {
     return attn_impl(pool, kcmm::kBF16, "kcmm_paged_attn_decode_bf16", KCMM_ATTN_PASS, stream,
                      false, true);
+}
+
+int kcmm_paged_attn_decode_bf16_noalloc_on_stream(KCMM_ATTN_ARGS, uint64_t stream) {
+    return attn_impl(pool, kcmm::kBF16, "kcmm_paged_attn_decode_bf16_noalloc_on_stream",
+                     KCMM_ATTN_PASS, stream, false, true, true);
 }
 
 int kcmm_paged_attn_decode_f32(KCMM_ATTN_ARGS) {

@@ -34,6 +34,8 @@
 //    by log-sum-exp.
 #include <algorithm>
 #include <climits>
+#include <mutex>
+#include <string>
 #include <cmath>
 #include <cstdlib>
 #include <type_traits>
@@ -43,6 +45,37 @@
 
 namespace kcmm {
 namespace {
+
+// Device scratch of the no-allocation entry point
+// (kcmm_paged_attn_decode_bf16_noalloc_on_stream): the streaming kernel's
+// idle-load region, partial results and segment table, carved from one
+// file-scope array instead of the per-stream workspace.  Every GPU holds its
+// own copy for the life of the process; host code uses only the address
+// hipGetSymbolAddress reports for the current device.
+constexpr size_t kNoAllocScratchBytes = size_t(24) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// Address of `scratch` on the current device, looked up once per device.
+bool noalloc_scratch(uint8_t** out, std::string* err) {
+    static std::mutex mu;
+    static uint8_t* ptrs[kMaxDevices] = {};
+    int dev = 0;
+    KCMM_HIP_CHECK(hipGetDevice(&dev), err);
+    if (dev < 0 || dev >= kMaxDevices) {
+        *err = "decode attention (no-alloc): device ordinal out of range";
+        return false;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    if (ptrs[dev] == nullptr) {
+        void* p = nullptr;
+        KCMM_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), err);
+        ptrs[dev] = static_cast<uint8_t*>(p);
+    }
+    *out = ptrs[dev];
+    return true;
+}
 
 struct AttnParams {
     const uint8_t* q;       // [B][Hq][D] 16-bit elements
@@ -904,7 +937,7 @@ int stream_min_tiles() { return env_int("KCMM_ATTN_MIN_TILES", 8, 1, 1 << 16); }
 int stream_depth() { return env_int("KCMM_ATTN_DEPTH", 2, 2, 3); }
 
 template <int DT, int D, int BS>
-bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
+bool launch_stream(AttnParams& p, hipStream_t s, bool no_alloc, std::string* err) {
     static_assert(D * (DT == kDtFP8 ? 1 : 2) % 128 == 0, "head rows are whole 128-byte lines");
     const long long cap = static_cast<long long>(p.mbps) * p.block_size;
     const long long tmax = static_cast<long long>(p.batch) * p.kv_heads * ((cap + 31) / 32);
@@ -932,9 +965,24 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
     const size_t info_bytes = static_cast<size_t>(p.batch) * p.kv_heads * sizeof(int2);
     void* ws = nullptr;
     void* info = nullptr;
-    if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 0, part_bytes, &ws, false, err) ||
-        !dev::stream_workspace(reinterpret_cast<uint64_t>(s), 2, info_bytes, &info, false, err))
-        return false;
+    if (no_alloc) {
+        // nothing here needs to start zeroed: every partial and segment
+        // record is written before it is read
+        uint8_t* base = nullptr;
+        if (!noalloc_scratch(&base, err)) return false;
+        if (part_bytes + info_bytes > kNoAllocScratchBytes) {
+            *err = "decode attention (no-alloc): this batch needs " +
+                   std::to_string(part_bytes + info_bytes) + " bytes of scratch, the static "
+                   "scratch holds " + std::to_string(kNoAllocScratchBytes);
+            return false;
+        }
+        ws = base;
+        info = base + part_bytes;
+    } else {
+        if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 0, part_bytes, &ws, false, err) ||
+            !dev::stream_workspace(reinterpret_cast<uint64_t>(s), 2, info_bytes, &info, false, err))
+            return false;
+    }
     const uint8_t* idle = static_cast<const uint8_t*>(ws);
     p.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + idle_bytes);
     p.part_acc = p.part_ml + units * 2;
@@ -954,15 +1002,15 @@ bool launch_stream(AttnParams& p, hipStream_t s, std::string* err) {
 }
 
 template <int DT, int D>
-bool launch_stream_bs(AttnParams& p, hipStream_t s, std::string* err) {
-    if (p.block_size == 16) return launch_stream<DT, D, 16>(p, s, err);
-    return launch_stream<DT, D, 0>(p, s, err);
+bool launch_stream_bs(AttnParams& p, hipStream_t s, bool no_alloc, std::string* err) {
+    if (p.block_size == 16) return launch_stream<DT, D, 16>(p, s, no_alloc, err);
+    return launch_stream<DT, D, 0>(p, s, no_alloc, err);
 }
 
 template <int DT>
-bool launch_dt(AttnParams& p, int head_dim, hipStream_t s, std::string* err) {
-    if (head_dim == 64) return launch_stream_bs<DT, 64>(p, s, err);
-    return launch_stream_bs<DT, 128>(p, s, err);
+bool launch_dt(AttnParams& p, int head_dim, hipStream_t s, bool no_alloc, std::string* err) {
+    if (head_dim == 64) return launch_stream_bs<DT, 64>(p, s, no_alloc, err);
+    return launch_stream_bs<DT, 128>(p, s, no_alloc, err);
 }
 
 }  // namespace
@@ -995,9 +1043,11 @@ bool attn_decode(const AttnDecodeArgs& a, std::string* err) {
     const bool stream_dim = a.head_dim == 64 || a.head_dim == 128;
     const bool force_generic = std::getenv("KCMM_ATTN_GENERIC") != nullptr;
     if (grouped && a.block_size % 8 == 0 && !force_generic) {
-        if (a.dtype == kDtFP8 && a.head_dim == 128) return launch_stream_bs<kDtFP8, 128>(p, s, err);
-        if (a.dtype == kDtF16 && stream_dim) return launch_dt<kDtF16>(p, a.head_dim, s, err);
-        if (a.dtype == kDtBF16 && stream_dim) return launch_dt<kDtBF16>(p, a.head_dim, s, err);
+        if (a.dtype == kDtFP8 && a.head_dim == 128)
+            return launch_stream_bs<kDtFP8, 128>(p, s, a.no_alloc, err);
+        if (a.dtype == kDtF16 && stream_dim) return launch_dt<kDtF16>(p, a.head_dim, s, a.no_alloc, err);
+        if (a.dtype == kDtBF16 && stream_dim)
+            return launch_dt<kDtBF16>(p, a.head_dim, s, a.no_alloc, err);
     }
     const dim3 grid(a.batch * a.num_q_heads);
     switch (a.dtype) {
