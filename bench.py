@@ -395,19 +395,24 @@ def main():
             extra[label] = float(np.mean([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]))
         log(f"layer step (one call) ms={extra['layer_step']:.4f}, append ms={extra['append']:.4f}, "
             f"32-layer decode step ms={extra['decode_step']:.4f}")
-        # the projections at M = 256 tokens (configs[3]'s second size), same weights
-        # (kcmm_gemm_bf16 hands M > 128 to hipBLASLt; KCMM_GEMM_LT=0 keeps the
-        # weight-stream kernel, timed beside it)
-        m256, m256_stream = {}, {}
+        # the projections at M = 256 tokens (configs[3]'s second size), same weights:
+        # kcmm_gemm_bf16 runs M > 128 on the LDS-tiled MFMA kernel; the
+        # weight-stream kernel (KCMM_GEMM_TILED=0) and torch.matmul (ROCm's
+        # GEMM libraries, not part of the library) are timed beside it
+        m256, m256_stream, m256_torch = {}, {}, {}
         x256 = {k: torch.randn((256, k), generator=g, device=dev).to(torch.bfloat16)
                 for k in (HIDDEN, INTER)}
         y256 = torch.empty((256, 2 * INTER), dtype=torch.bfloat16, device=dev)
-        lt_env = os.environ.get("KCMM_GEMM_LT")
-        for backend, out in (("1", m256), ("0", m256_stream)):
-            os.environ["KCMM_GEMM_LT"] = backend
+        tiled_env = os.environ.get("KCMM_GEMM_TILED")
+        for backend, out in (("1", m256), ("0", m256_stream), ("torch", m256_torch)):
+            os.environ["KCMM_GEMM_TILED"] = "0" if backend == "0" else "1"
             for name, n, k in GEMMS:
-                fn = lambda l, n=n, k=k, name=name: lib.gemm_bf16(
-                    x256[k].data_ptr(), W(l, name), y256.data_ptr(), 256, n, k, sp)
+                if backend == "torch":
+                    fn = lambda l, n=n, k=k, name=name: torch.matmul(
+                        x256[k], weights[l % len(weights)][name].t())
+                else:
+                    fn = lambda l, n=n, k=k, name=name: lib.gemm_bf16(
+                        x256[k].data_ptr(), W(l, name), y256.data_ptr(), 256, n, k, sp)
                 evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
                 for i in range(min(args.warmup, args.steps)):
                     fn(i)
@@ -419,14 +424,16 @@ def main():
                 torch.cuda.synchronize()
                 out[name] = float(np.mean([evs[i].elapsed_time(evs[i + 1])
                                            for i in range(args.steps)]))
-        if lt_env is None:
-            os.environ.pop("KCMM_GEMM_LT", None)
+        if tiled_env is None:
+            os.environ.pop("KCMM_GEMM_TILED", None)
         else:
-            os.environ["KCMM_GEMM_LT"] = lt_env
+            os.environ["KCMM_GEMM_TILED"] = tiled_env
         del x256, y256
-        log("M=256 GEMM ms (hipBLASLt): " + ", ".join(f"{k}={v:.4f}" for k, v in m256.items()))
+        log("M=256 GEMM ms (tiled MFMA kernel): " + ", ".join(f"{k}={v:.4f}" for k, v in m256.items()))
         log("M=256 GEMM ms (weight-stream kernel): " +
             ", ".join(f"{k}={v:.4f}" for k, v in m256_stream.items()))
+        log("M=256 GEMM ms (torch.matmul, reference only): " +
+            ", ".join(f"{k}={v:.4f}" for k, v in m256_torch.items()))
         assert torch.isfinite(hidden.float()).all(), "layer step produced non-finite hidden state"
 
     # attention calls back to back over the cycled KV sets (the order a decode
@@ -556,8 +563,9 @@ def main():
             return gem
         result["gemm_m64"] = gemm_report(per, B, True)
         result["gemm_m256"] = gemm_report(m256, 256, False)
-        result["gemm_m256"]["backend"] = "hipBLASLt"
+        result["gemm_m256"]["backend"] = "tiled MFMA kernel (gemm_tiled.hip)"
         result["gemm_m256_stream_kernel"] = gemm_report(m256_stream, 256, False)
+        result["gemm_m256_torch_reference"] = gemm_report(m256_torch, 256, False)
         result["tiering"] = tiering_report(lib, args)
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))

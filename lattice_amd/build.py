@@ -42,7 +42,8 @@ CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-Wno-unused-para
 HOST_SOURCES = ["pool_core.cpp", "tiering.cpp", "ffi.cpp"]
 HIP_SOURCES = ["kernels/backing.hip", "kernels/attn_decode.hip", "kernels/attn_prefill.hip",
                "kernels/kv_write.hip",
-               "kernels/page_copy.hip", "kernels/gemm.hip", "kernels/gemm_lt.hip", "kernels/glue.hip",
+               "kernels/page_copy.hip", "kernels/gemm.hip", "kernels/gemm_tiled.hip",
+               "kernels/glue.hip",
                "kernels/tier_copy.hip"]
 
 
@@ -77,8 +78,7 @@ def build_kcmm(jobs: int = 8) -> Path:
         list(ex.map(_run, cmds))
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-          *map(str, objs), f"-L{ROCM}/lib", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib",
-          "-Wl,--no-undefined"])
+          *map(str, objs), "-Wl,--no-undefined"])
     os.replace(tmp, LIB)
     return LIB
 

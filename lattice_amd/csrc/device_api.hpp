@@ -22,7 +22,7 @@ bool set_device(int device, std::string* err);
 // Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
 // attention partials, 1: GEMM split partials, 2: decode attention segment
 // table, 3: decode layer-step activations, 4: the final norm's output,
-// 5: hipBLASLt workspace, 6: tiering staging on the null stream, 7: fp8
+// 5: unused, 6: tiering staging on the null stream, 7: fp8
 // RoPE/append staging, 8: fp8 page-writer row table).  `zero_fill` buffers
 // start zeroed by a fill kernel, and their users leave them zeroed.
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
@@ -112,10 +112,14 @@ void host_pinned_free(void* p);
 bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
                uint64_t stream, std::string* err, uint64_t residual = 0);
 
-// The same product through hipBLASLt (kernels/gemm_lt.hip); *used is false
-// (and the call succeeds) when the library offers no algorithm for the shape.
-bool lt_gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
-                  uint64_t stream, bool* used, std::string* err);
+// The same product for many tokens (m > 128) on the LDS-tiled MFMA kernel
+// (kernels/gemm_tiled.hip); n % 64 == 0, k % 64 == 0.
+bool gemm_bf16_tiled(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
+                     uint64_t stream, uint64_t residual, std::string* err);
+// Y = bf16(sum of `splits` fp32 partials [splits][MN]) (+ R), in split order.
+bool gemm_split_reduce_launch(const float* part, uint16_t* y, const uint16_t* r, int mn,
+                              int splits, uint64_t stream, std::string* err);
+
 
 // Decode-step glue (kernels/glue.hip), bf16.
 bool rmsnorm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t rows, uint32_t hidden, float eps,

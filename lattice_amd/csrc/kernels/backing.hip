@@ -1,16 +1,15 @@
 // Device page backing for a KCMM pool on MI355X.
 //
-// Two backings with identical block ids and offsets:
-//  * HipFlatBacking (default): each of the 2*L regions is one hipMalloc of
-//    the pool's full capacity.  MI355X carries 288 GB of HBM per GPU, so the
-//    configured capacity is committed up front and growth costs nothing.
-//  * HipVmmBacking (KCMM_BACKING=vmm): the reference's CUDA-VMM design (ref
-//    src/cache/cuda_vmm.rs:6-234, pool.rs:211-221,287-322) on HIP VMM -- one
-//    virtual-address reservation per region, and a 2 MiB physical superblock
-//    created and mapped at byte sb*2MiB of every region when the allocator
-//    grows.  Opt-in: with the HIP runtime PyTorch-ROCm 7.0 ships, a process
-//    that created and destroyed a dozen VMM pools saw hipMemSetAccess fail
-//    with "invalid argument" and a crash inside pool teardown.
+//  * HipFlatBacking (the backing pools get): each of the 2*L regions is one
+//    hipMalloc of the pool's full capacity.  MI355X carries 288 GB of HBM per
+//    GPU, so the configured capacity is committed up front and growth costs
+//    nothing.  Block ids and offsets are the reference's either way.
+//  * VmmBacking<HipVmmOps>: the reference's CUDA-VMM design (ref
+//    src/cache/cuda_vmm.rs:6-234, pool.rs:211-221,287-322) on HIP VMM.
+//    Switched off: a process that created and destroyed about a dozen VMM
+//    pools saw hipMemSetAccess fail with "invalid argument" and then a crash
+//    in pool teardown; the cause is not known, so KCMM_BACKING=vmm makes
+//    pool creation fail.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -20,88 +19,57 @@
 #include <vector>
 
 #include "../device_api.hpp"
+#include "../vmm_backing.hpp"
 #include "common.hpp"
 
 namespace kcmm {
 namespace {
 
-class HipVmmBacking final : public PageBacking {
-public:
-    explicit HipVmmBacking(int device) : device_(device) {
-        std::memset(&prop_, 0, sizeof(prop_));
-        prop_.type = hipMemAllocationTypePinned;
-        prop_.location.type = hipMemLocationTypeDevice;
-        prop_.location.id = device;
+// HIP VMM calls for VmmBacking (vmm_backing.hpp).  Not reachable: the VMM
+// backing is switched off (make_backing); kept with the bookkeeping it
+// drives, which the host-check build tests with a fault-injecting mock.
+struct HipVmmOps {
+    using Handle = hipMemGenericAllocationHandle_t;
+    hipMemAllocationProp prop;
+    explicit HipVmmOps(int device) {
+        std::memset(&prop, 0, sizeof(prop));
+        prop.type = hipMemAllocationTypePinned;
+        prop.location.type = hipMemLocationTypeDevice;
+        prop.location.id = device;
     }
-    ~HipVmmBacking() override { release(); }
-
-    bool reserve(size_t num_regions, size_t region_bytes, std::string* err) override {
-        size_t gran = 0;
-        KCMM_HIP_CHECK(hipMemGetAllocationGranularity(&gran, &prop_,
-                                                      hipMemAllocationGranularityMinimum),
+    bool granularity(size_t* g, std::string* err) {
+        KCMM_HIP_CHECK(hipMemGetAllocationGranularity(g, &prop, hipMemAllocationGranularityMinimum),
                        err);
-        if (gran == 0 || kSuperblockBytes % gran != 0) {
-            *err = "HIP VMM granularity does not divide the 2 MiB superblock";
-            return false;
-        }
-        region_bytes_ = region_bytes;
-        for (size_t r = 0; r < num_regions; ++r) {
-            void* p = nullptr;
-            KCMM_HIP_CHECK(hipMemAddressReserve(&p, region_bytes, kSuperblockBytes, nullptr, 0),
-                           err);
-            bases_.push_back(p);
-        }
         return true;
     }
-
-    uint64_t region_base(size_t r) const override {
-        return reinterpret_cast<uint64_t>(bases_[r]);
+    bool reserve(size_t bytes, size_t align, void** va, std::string* err) {
+        KCMM_HIP_CHECK(hipMemAddressReserve(va, bytes, align, nullptr, 0), err);
+        return true;
     }
-
-    bool map_superblock(size_t sb, std::string* err) override {
-        if ((sb + 1) * kSuperblockBytes > region_bytes_) {
-            *err = "superblock beyond the reserved region";
-            return false;
-        }
+    bool create(size_t bytes, Handle* h, std::string* err) {
+        KCMM_HIP_CHECK(hipMemCreate(h, bytes, &prop, 0), err);
+        return true;
+    }
+    bool map(void* at, size_t bytes, Handle h, std::string* err) {
+        KCMM_HIP_CHECK(hipMemMap(at, bytes, 0, h, 0), err);
+        return true;
+    }
+    bool set_access(void* at, size_t bytes, std::string* err) {
         hipMemAccessDesc desc;
         std::memset(&desc, 0, sizeof(desc));
-        desc.location = prop_.location;
+        desc.location = prop.location;
         desc.flags = hipMemAccessFlagsProtReadWrite;
-        for (void* base : bases_) {
-            char* at = static_cast<char*>(base) + sb * kSuperblockBytes;
-            hipMemGenericAllocationHandle_t h;
-            KCMM_HIP_CHECK(hipMemCreate(&h, kSuperblockBytes, &prop_, 0), err);
-            hipError_t e = hipMemMap(at, kSuperblockBytes, 0, h, 0);
-            if (e != hipSuccess) {
-                (void)hipMemRelease(h);
-                *err = std::string("hipMemMap: ") + hipGetErrorString(e);
-                return false;
-            }
-            mapped_.push_back({at, h});
-            KCMM_HIP_CHECK(hipMemSetAccess(at, kSuperblockBytes, &desc, 1), err);
-        }
+        KCMM_HIP_CHECK(hipMemSetAccess(at, bytes, &desc, 1), err);
         return true;
     }
-
-    void release() override {
-        for (auto& m : mapped_) {
-            (void)hipMemUnmap(m.first, kSuperblockBytes);
-            (void)hipMemRelease(m.second);
-        }
-        mapped_.clear();
-        for (void* b : bases_) (void)hipMemAddressFree(b, region_bytes_);
-        bases_.clear();
-    }
-
-    int kind() const override { return 0; }
-
-private:
-    int device_;
-    hipMemAllocationProp prop_;
-    size_t region_bytes_ = 0;
-    std::vector<void*> bases_;
-    std::vector<std::pair<void*, hipMemGenericAllocationHandle_t>> mapped_;
+    void unmap(void* at, size_t bytes) { (void)hipMemUnmap(at, bytes); }
+    void release(Handle h) { (void)hipMemRelease(h); }
+    void free_va(void* va, size_t bytes) { (void)hipMemAddressFree(va, bytes); }
 };
+
+[[maybe_unused]] std::unique_ptr<PageBacking> make_vmm_backing(int device) {
+    return std::unique_ptr<PageBacking>(new VmmBacking<HipVmmOps>(HipVmmOps(device)));
+}
 
 class HipFlatBacking final : public PageBacking {
 public:

@@ -495,16 +495,21 @@ GemmParams base_params(uint64_t x, uint64_t w, uint32_t m, uint32_t n, uint32_t 
 
 namespace dev {
 
+bool gemm_split_reduce_launch(const float* part, uint16_t* y, const uint16_t* r, int mn,
+                              int splits, uint64_t stream, std::string* err) {
+    hipLaunchKernelGGL(gemm_split_reduce, dim3((mn / 4 + 255) / 256), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), part, y, r, mn, splits);
+    KCMM_HIP_CHECK(hipGetLastError(), err);
+    return true;
+}
+
 bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
                uint64_t stream, std::string* err, uint64_t residual) {
     if (!shape_ok(m, n, k, err)) return false;
-    // many tokens, plain store: hipBLASLt's MFMA tiling (KCMM_GEMM_LT=0 keeps
-    // the weight-stream kernel)
-    if (m > 128 && residual == 0 && env_int("KCMM_GEMM_LT", 1) != 0) {
-        bool used = false;
-        if (!lt_gemm_bf16(x, w, y, m, n, k, stream, &used, err)) return false;
-        if (used) return true;
-    }
+    // many tokens: the LDS-tiled MFMA kernel (KCMM_GEMM_TILED=0 keeps the
+    // weight-stream kernel)
+    if (m > 128 && env_int("KCMM_GEMM_TILED", 1) != 0)
+        return gemm_bf16_tiled(x, w, y, m, n, k, stream, residual, err);
     GemmParams p = base_params(x, w, m, n, k);
     p.Y = reinterpret_cast<uint16_t*>(y);
     p.R = reinterpret_cast<const uint16_t*>(residual);

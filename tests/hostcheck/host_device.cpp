@@ -93,9 +93,12 @@ bool gemm_bf16_swiglu(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t
                       std::string* err) {
     return no_device(err);
 }
-bool lt_gemm_bf16(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, bool* used,
-                  std::string* err) {
-    *used = false;
+bool gemm_bf16_tiled(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, uint64_t,
+                     std::string* err) {
+    return no_device(err);
+}
+bool gemm_split_reduce_launch(const float*, uint16_t*, const uint16_t*, int, int, uint64_t,
+                              std::string* err) {
     return no_device(err);
 }
 // The host-check backing has no page memory (fake region addresses), so the

@@ -5,7 +5,7 @@ replace (same GEMM arithmetic, then the same element arithmetic):
   kcmm_gemm_bf16_swiglu        == kcmm_gemm_bf16 -> kcmm_silu_mul_bf16
   kcmm_qkv_rope_append_bf16    == kcmm_gemm_bf16 -> kcmm_rope_append_bf16
   kcmm_gemm_bf16_add_rmsnorm   == kcmm_gemm_bf16_add -> kcmm_rmsnorm_bf16
-(the unfused GEMM on the weight-stream kernel: KCMM_GEMM_LT=0).  The
+(the unfused GEMM on the weight-stream kernel: KCMM_GEMM_TILED=0).  The
 unfused kernels are themselves checked against the oracle
 (tests/test_gpu_glue.py, tests/test_gpu_gemm.py).  Shapes cover both the
 single-pass GEMM (epilogue in its store) and the split-K path whose fp32
@@ -35,7 +35,7 @@ def _randn_bf16(torch, shape, std, seed):
                                        (100, 512, 1024), (256, 768, 2048)])
 def test_swiglu_gemm_matches_unfused(gpu_lib, monkeypatch, m, inter, k):
     import torch
-    monkeypatch.setenv("KCMM_GEMM_LT", "0")   # the unfused GEMM on the same kernel
+    monkeypatch.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
     x = _randn_bf16(torch, (m, k), 1.0, 1)
     w = _randn_bf16(torch, (2 * inter, k), 0.05, 2)
     gu = torch.empty((m, 2 * inter), dtype=torch.bfloat16, device="cuda")
@@ -65,7 +65,7 @@ def test_qkv_rope_append_matches_unfused(gpu_lib, monkeypatch, hq, hkv, d, h, ns
     with no token and one whose position lies past its table (both
     skipped: their q_out rows keep the NaN fill)."""
     import torch
-    monkeypatch.setenv("KCMM_GEMM_LT", "0")   # the unfused GEMM on the same kernel
+    monkeypatch.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
     lens = ([1, 16, 17, 300, 0, 48] * (nseq // 6 + 1))[:nseq]
     B = len(lens)
     n = (hq + 2 * hkv) * d
@@ -137,8 +137,9 @@ def test_split_k_in_kernel_reduction(gpu_lib, monkeypatch, splits):
 
 
 @pytest.mark.parametrize("m,n,k", [(64, 4096, 4096), (7, 512, 256), (64, 512, 14336), (200, 1024, 1024)])
-def test_add_rmsnorm_matches_unfused(gpu_lib, m, n, k):
+def test_add_rmsnorm_matches_unfused(gpu_lib, monkeypatch, m, n, k):
     import torch
+    monkeypatch.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
     x = _randn_bf16(torch, (m, k), 1.0, 11)
     w = _randn_bf16(torch, (n, k), 0.02, 12)
     h0 = _randn_bf16(torch, (m, n), 1.0, 13)

@@ -13,12 +13,12 @@ def rel_err(got, ref):
     return float(np.abs(got - ref).max() / np.abs(ref).max())
 
 
-@pytest.fixture(params=["lt", "stream"])
+@pytest.fixture(params=["tiled", "stream"])
 def backend(request, monkeypatch):
-    """kcmm_gemm_bf16 hands plain products with M > 128 to hipBLASLt;
-    KCMM_GEMM_LT=0 keeps them on the weight-stream kernel.  Both are
-    checked."""
-    monkeypatch.setenv("KCMM_GEMM_LT", "1" if request.param == "lt" else "0")
+    """kcmm_gemm_bf16 runs products with M > 128 on the LDS-tiled MFMA
+    kernel; KCMM_GEMM_TILED=0 keeps them on the weight-stream kernel.  Both
+    are checked."""
+    monkeypatch.setenv("KCMM_GEMM_TILED", "1" if request.param == "tiled" else "0")
     return request.param
 
 
@@ -34,10 +34,11 @@ def run(gpu_lib, x, w):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 256), (17, 192, 512), (64, 256, 1024),
-                                   (100, 128, 768), (256, 320, 2048)])
+                                   (100, 128, 768), (256, 320, 2048), (129, 192, 512),
+                                   (300, 1024, 256), (513, 640, 1024)])
 def test_vs_oracle(gpu_lib, backend, m, n, k):
     import torch
-    if backend == "lt" and m <= 128:
+    if backend == "tiled" and m <= 128:
         pytest.skip("M <= 128 always runs the weight-stream kernel")
     rng = np.random.default_rng(m + n + k)
     xb = O.encode(O.BF16, rng.standard_normal((m, k)))
@@ -55,7 +56,7 @@ def test_vs_oracle(gpu_lib, backend, m, n, k):
 @pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)])
 def test_llama3_8b_projections(gpu_lib, backend, m, n, k):
     import torch
-    if backend == "lt" and m <= 128:
+    if backend == "tiled" and m <= 128:
         pytest.skip("M <= 128 always runs the weight-stream kernel")
     g = torch.Generator(device="cuda")
     g.manual_seed(m * 7 + n + k)
@@ -89,19 +90,41 @@ def test_split_k_choices(gpu_lib, monkeypatch, target, m, n, k):
     assert err <= 1e-2
 
 
-def test_lt_repeatable_and_odd_shape(gpu_lib, monkeypatch):
-    """The hipBLASLt path: a cached plan reused for a second, different
-    input gives the oracle's product both times; a shape with M not a
-    multiple of any tile (M = 129) is covered too."""
+@pytest.mark.parametrize("tile", [str(i) for i in range(11)])
+@pytest.mark.parametrize("splits", ["1", "2", "4"])
+@pytest.mark.parametrize("residual", [False, True])
+def test_tiled_tiles_splits_residual(gpu_lib, monkeypatch, tile, splits, residual):
+    """Every configuration of the tiled kernel (tiles 128x256, 128x128,
+    128x64, 64x128, 64x64, 128x256 on 4 waves, 256x128, 128x256 with 2
+    stages) with 1, 2 or 4 K splits, M not a multiple of the tile, with and
+    without a residual (in place: R == Y), against the fp64 oracle; two
+    calls in a row give the same bits."""
     import torch
-    monkeypatch.setenv("KCMM_GEMM_LT", "1")
-    for seed, (m, n, k) in enumerate([(129, 192, 512), (129, 192, 512), (300, 1024, 256)]):
-        rng = np.random.default_rng(100 + seed)
-        xb = O.encode(O.BF16, rng.standard_normal((m, k)))
-        wb = O.encode(O.BF16, rng.standard_normal((n, k)) * 0.02)
-        x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
-        w = torch.from_numpy(wb.view(np.int16)).view(torch.bfloat16).cuda()
-        got = O.decode(O.BF16, run(gpu_lib, x, w).cpu().view(torch.int16).numpy().view(np.uint16))
-        err = rel_err(got, O.gemm_bf16_f64(xb, wb))
-        print(f"gemm lt {m}x{n}x{k} err={err:.3e}", flush=True)
-        assert err <= 1e-2
+    monkeypatch.setenv("KCMM_GEMM_TILE", tile)
+    monkeypatch.setenv("KCMM_GEMM_SPLITS", splits)
+    m, n, k = 300, 768, 1024
+    rng = np.random.default_rng(int(tile) * 10 + int(splits) + residual)
+    xb = O.encode(O.BF16, rng.standard_normal((m, k)))
+    wb = O.encode(O.BF16, rng.standard_normal((n, k)) * 0.02)
+    rb = O.encode(O.BF16, rng.standard_normal((m, n)))
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    w = torch.from_numpy(wb.view(np.int16)).view(torch.bfloat16).cuda()
+    outs = []
+    for _ in range(2):
+        y = torch.from_numpy(rb.view(np.int16)).view(torch.bfloat16).cuda().clone()
+        if residual:
+            gpu_lib.gemm_bf16_add(x.data_ptr(), w.data_ptr(), y.data_ptr(), y.data_ptr(), m, n, k,
+                                  torch.cuda.current_stream().cuda_stream)
+        else:
+            gpu_lib.gemm_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k,
+                              torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(outs[0], outs[1])
+    got = O.decode(O.BF16, outs[0]).astype(np.float64)
+    prod = O.gemm_bf16_f64(xb, wb)
+    ref = (O.decode(O.BF16, O.encode(O.BF16, prod)).astype(np.float64) +
+           O.decode(O.BF16, rb)) if residual else prod
+    err = rel_err(got, ref)
+    print(f"tiled tile={tile} splits={splits} residual={residual} err={err:.3e}", flush=True)
+    assert err <= 1e-2
