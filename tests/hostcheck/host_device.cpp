@@ -9,11 +9,15 @@
 // nothing here can stand in for the HIP kernels.
 #include <cstdint>
 #include <cstdlib>
+#include <cstring>
+#include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "../../lattice_amd/csrc/device_api.hpp"
+#include "../../lattice_amd/csrc/vmm_backing.hpp"
 
 namespace kcmm {
 namespace {
@@ -44,6 +48,81 @@ private:
     std::vector<size_t> mapped_;
 };
 
+// Recording stand-in for the HIP VMM calls (KCMM_BACKING=vmm in this build
+// only): fake addresses, live-resource counts, misuse counted as violations,
+// and one injected failure (operation, n-th call) at a time.
+struct VmmMock {
+    std::mutex mu;
+    int64_t reservations = 0, handles = 0, mappings = 0, violations = 0;
+    int64_t calls[5] = {0, 0, 0, 0, 0};   // reserve, create, map, set_access, granularity
+    int fail_op = -1;
+    int64_t fail_at = -1;
+    uint64_t next_va = 0x200000000000ull, next_handle = 0;
+    std::map<uint64_t, uint64_t> mapped;          // address -> handle
+    std::map<uint64_t, size_t> reserved;          // base -> bytes
+    bool fail(int op) { return ++calls[op] == fail_at && op == fail_op; }
+} g_vmm;
+
+struct MockVmmOps {
+    using Handle = uint64_t;
+    bool granularity(size_t* g, std::string* err) {
+        std::lock_guard<std::mutex> lk(g_vmm.mu);
+        if (g_vmm.fail(4)) { *err = "mock: granularity failed"; return false; }
+        *g = kSuperblockBytes;
+        return true;
+    }
+    bool reserve(size_t bytes, size_t, void** va, std::string* err) {
+        std::lock_guard<std::mutex> lk(g_vmm.mu);
+        if (g_vmm.fail(0)) { *err = "mock: reserve failed"; return false; }
+        *va = reinterpret_cast<void*>(g_vmm.next_va);
+        g_vmm.reserved[g_vmm.next_va] = bytes;
+        g_vmm.next_va += (bytes + kSuperblockBytes - 1) / kSuperblockBytes * kSuperblockBytes + kSuperblockBytes;
+        ++g_vmm.reservations;
+        return true;
+    }
+    bool create(size_t, Handle* h, std::string* err) {
+        std::lock_guard<std::mutex> lk(g_vmm.mu);
+        if (g_vmm.fail(1)) { *err = "mock: create failed"; return false; }
+        *h = ++g_vmm.next_handle;
+        ++g_vmm.handles;
+        return true;
+    }
+    bool map(void* at, size_t, Handle h, std::string* err) {
+        std::lock_guard<std::mutex> lk(g_vmm.mu);
+        if (g_vmm.fail(2)) { *err = "mock: map failed"; return false; }
+        const uint64_t a = reinterpret_cast<uint64_t>(at);
+        if (g_vmm.mapped.count(a)) ++g_vmm.violations;   // mapped twice
+        g_vmm.mapped[a] = h;
+        ++g_vmm.mappings;
+        return true;
+    }
+    bool set_access(void* at, size_t, std::string* err) {
+        std::lock_guard<std::mutex> lk(g_vmm.mu);
+        if (g_vmm.fail(3)) { *err = "mock: set_access failed"; return false; }
+        if (!g_vmm.mapped.count(reinterpret_cast<uint64_t>(at))) ++g_vmm.violations;
+        return true;
+    }
+    void unmap(void* at, size_t) {
+        std::lock_guard<std::mutex> lk(g_vmm.mu);
+        if (g_vmm.mapped.erase(reinterpret_cast<uint64_t>(at)) == 0) ++g_vmm.violations;
+        --g_vmm.mappings;
+    }
+    void release(Handle) {
+        std::lock_guard<std::mutex> lk(g_vmm.mu);
+        --g_vmm.handles;
+    }
+    void free_va(void* va, size_t bytes) {
+        std::lock_guard<std::mutex> lk(g_vmm.mu);
+        const uint64_t a = reinterpret_cast<uint64_t>(va);
+        auto it = g_vmm.reserved.find(a);
+        if (it == g_vmm.reserved.end() || it->second != bytes) ++g_vmm.violations;
+        else g_vmm.reserved.erase(it);
+        for (const auto& m : g_vmm.mapped)          // still mapped inside the range
+            if (m.first >= a && m.first < a + bytes) ++g_vmm.violations;
+        --g_vmm.reservations;
+    }
+};
+
 bool no_device(std::string* err) {
     *err = "no device in the host-check build";
     return false;
@@ -54,6 +133,9 @@ bool no_device(std::string* err) {
 namespace dev {
 
 std::unique_ptr<PageBacking> make_backing(int, std::string*) {
+    const char* env = std::getenv("KCMM_BACKING");
+    if (env != nullptr && std::strcmp(env, "vmm") == 0)
+        return std::unique_ptr<PageBacking>(new VmmBacking<MockVmmOps>(MockVmmOps()));
     return std::unique_ptr<PageBacking>(new HostBacking());
 }
 bool set_device(int, std::string*) { return true; }
@@ -136,3 +218,22 @@ bool residual_rmsnorm_from_partials(const float*, int, uint64_t, uint64_t, uint6
 
 }  // namespace dev
 }  // namespace kcmm
+
+// Test hooks of the mock VMM (host-check build only): reset the counters and
+// arm one failure (op 0 reserve, 1 create, 2 map, 3 set_access, 4
+// granularity; at = 1-based call index, -1 none); read reservations,
+// handles, mappings, violations.
+extern "C" void kcmm_hostcheck_vmm_reset(int fail_op, int64_t fail_at) {
+    std::lock_guard<std::mutex> lk(kcmm::g_vmm.mu);
+    std::memset(kcmm::g_vmm.calls, 0, sizeof(kcmm::g_vmm.calls));
+    kcmm::g_vmm.violations = 0;
+    kcmm::g_vmm.fail_op = fail_op;
+    kcmm::g_vmm.fail_at = fail_at;
+}
+extern "C" void kcmm_hostcheck_vmm_state(int64_t* out) {
+    std::lock_guard<std::mutex> lk(kcmm::g_vmm.mu);
+    out[0] = kcmm::g_vmm.reservations;
+    out[1] = kcmm::g_vmm.handles;
+    out[2] = kcmm::g_vmm.mappings;
+    out[3] = kcmm::g_vmm.violations;
+}
