@@ -15,15 +15,15 @@ SiLU*up -> down GEMM + residual.  HIP events on the launch stream time every
 call.  After the timed steps the same layer is timed through the single
 entry point kcmm_decode_layer_step_on_stream, the standalone slot append
 (kcmm_append_kv_device_slots) on its own, and a whole decode step -- all 32
-layers, each over its own KV -- through one kcmm_decode_layers_on_stream
-call, followed by the final RMSNorm and the lm_head GEMM (vocab 128256) to
-bf16 logits.
+layers, each over its own KV -- through the token embedding
+(kcmm_embed_tokens_bf16), one kcmm_decode_layers_on_stream call, the final
+RMSNorm and the lm_head GEMM (vocab 128256) to bf16 logits.
 
 Printed JSON: `value` is decode-attention KV GB/s (algorithmic K+V bytes of
 one layer-step / attention call time, the call's average launch duration over
 consecutive calls on the cycled KV sets); decode tokens/s = 64 / t_step with
-t_step the 32-layer call plus the final norm and lm_head (embedding and
-sampling are outside this path and excluded).
+t_step the embedding, the 32-layer call, the final norm and lm_head (sampling
+is outside this path and excluded).
 
 `roofline` prices the attention call (streaming kernel + log-sum-exp merge,
 timed by HIP events on the launch stream) against MI355X's 8 TB/s; its
@@ -136,6 +136,57 @@ def cpu_baseline(case, seconds, threads):
                         f"{t * 1e3:.1f} ms per pass"))
 
 
+def cpu_baseline_detail(lib, case, args, threads) -> dict:
+    """BASELINE's CPU plan beside the headline baseline: the Cfg2 sample on one
+    thread, and configs[0] (fp32 pages, B=4, 8/8 heads, head_dim 64, ctx
+    U[1,512] + 1, pages shuffled over the pool) on one thread and on all
+    threads, with the GPU's time for the same configs[0] call beside it."""
+    import torch
+    import oracle as O
+    from lattice_amd.bindings import KV_F32, memcpy_dtoh
+    from lattice_amd.workload import build_decode_case
+    out = {"cfg2_1_thread": cpu_baseline(case, max(2.0, args.cpu_seconds / 3), 1)}
+    rng = np.random.default_rng(args.seed + 7)
+    ctx = rng.integers(1, 513, size=4) + 1
+    c1 = build_decode_case(lib, batch=4, num_q_heads=8, kv_heads=8, head_dim=64, block_size=16,
+                           ctx_lens=ctx, dtype=KV_F32, seed=args.seed + 8)
+    try:
+        g = c1.geometry
+        kreg = memcpy_dtoh(c1.pool.va_k(0), g["mapped_bytes"])
+        vreg = memcpy_dtoh(c1.pool.va_v(0), g["mapped_bytes"])
+        kv = int(c1.seq_lens.astype(np.int64).sum()) * 2 * 8 * 64 * 4
+        stream = torch.cuda.current_stream()
+        for _ in range(5):
+            c1.run_attention(stream_ptr=stream.cuda_stream)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record(stream)
+        for _ in range(50):
+            c1.run_attention(stream_ptr=stream.cuda_stream)
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        gpu_s = ev[0].elapsed_time(ev[1]) / 50 / 1e3
+        res = O.attn_decode_ref_f32(O.F32, c1.q_bits, kreg, vreg, c1.block_tables, c1.seq_lens,
+                                    c1.offsets_f16, 8, 8, 64, 16, g["row_bytes"], 1 / math.sqrt(64),
+                                    threads=1)
+        for label, th in (("cfg1_fp32_1_thread", 1), ("cfg1_fp32_all_threads", threads)):
+            reps, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 2.0:
+                O.attn_decode_ref_f32(O.F32, c1.q_bits, kreg, vreg, c1.block_tables, c1.seq_lens,
+                                      c1.offsets_f16, 8, 8, 64, 16, g["row_bytes"],
+                                      1 / math.sqrt(64), threads=th, out=res)
+                reps += 1
+            t = (time.perf_counter() - t0) / reps
+            out[label] = dict(value=round(kv / t / 1e9, 3), unit="GB/s", cores=th, kind="port",
+                              us_per_call=round(t * 1e6, 2),
+                              sample=f"configs[0], {kv / 1e6:.2f} MB KV, {reps} reps")
+        out["cfg1_fp32_gpu"] = dict(value=round(kv / gpu_s / 1e9, 3), unit="GB/s",
+                                    us_per_call=round(gpu_s * 1e6, 2),
+                                    note="kcmm_paged_attn_decode_f32_on_stream, any-shape kernel")
+    finally:
+        c1.pool.destroy()
+    return out
+
+
 def bench_prefill(args):
     """Cfg3: causal chunked prefill over shared-prefix pages; MFMA-bound."""
     import torch
@@ -242,11 +293,13 @@ def main():
                                    ("attn_norm", "qkv", "o", "mlp_norm", "gate_up", "down")})
                for w in weights]
     inv_freq = torch.from_numpy(rope_inv_freq(ROPE_THETA, D)).to(dev)
-    # final norm + lm_head (1.05 GB) for the whole-step timing
+    # embedding table, final norm and lm_head (1.05 GB each) for the whole-step timing
     if not args.attn_only:
         final_norm = (1.0 + 0.1 * torch.randn(HIDDEN, generator=g, device=dev)).to(torch.bfloat16)
         lm_head = (torch.randn((VOCAB, HIDDEN), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         logits = torch.empty((B, VOCAB), dtype=torch.bfloat16, device=dev)
+        embed = torch.randn((VOCAB, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
+        token_ids = torch.randint(0, VOCAB, (B,), generator=g, device=dev, dtype=torch.int32)
     hidden = torch.randn((B, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
     normed = torch.empty((B, HIDDEN), dtype=torch.bfloat16, device=dev)
     qkv_out = torch.empty((B, (HQ + 2 * HKV) * D), dtype=torch.bfloat16, device=dev)
@@ -286,8 +339,10 @@ def main():
                                     max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
 
     def decode_step(_):
-        """One decode step: all 32 layers in one call (weight sets alternate),
-        then the final norm and lm_head to bf16 logits."""
+        """One decode step: token embedding, all 32 layers in one call (weight
+        sets alternate), then the final norm and lm_head to bf16 logits."""
+        lib.embed_tokens_bf16(embed.data_ptr(), token_ids.data_ptr(), hidden.data_ptr(), B, HIDDEN,
+                              VOCAB, sp)
         case.pool.decode_layers(first_layer=0, weights=[layer_w[i % nw] for i in range(MODEL_LAYERS)],
                                 hidden_ptr=hidden.data_ptr(), block_tables_ptr=dv["bt"].data_ptr(),
                                 seq_lens_ptr=dv["sl"].data_ptr(),
@@ -571,6 +626,7 @@ def main():
         threads = len(os.sched_getaffinity(0))
         log(f"cpu baseline on {threads} threads ...")
         result["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds, threads)
+        result["cpu_baseline_detail"] = cpu_baseline_detail(lib, case, args, threads)
     else:
         result["cpu_baseline"] = None
     case.pool.destroy()

@@ -203,13 +203,25 @@ int kcmm_copy_blocks_device_on_stream(kcmm_pool_t *pool, uint64_t pairs_ptr,
  *  ref llama_transformer.rs:115-120), bf16 inputs and output, fp32
  *  accumulation on MFMA.  Replaces the cuBLAS call of ref runtime.rs:17-41
  *  (whose column-major arguments equal this product only at m == 1).
- *  m <= 128 runs the weight-stream MFMA kernel; m > 128 runs hipBLASLt
- *  (same product, fp32 accumulation, not the same bits) unless the
- *  environment sets KCMM_GEMM_LT=0.  Enqueue only; requires k % 256 == 0
- *  and n % 64 == 0. */
+ *  m <= 128 runs the weight-stream MFMA kernel (weights streamed into
+ *  registers); m > 128 the LDS-tiled MFMA kernel (same product, fp32
+ *  accumulation, not the same bits; KCMM_GEMM_TILED=0 keeps the
+ *  weight-stream kernel).  Enqueue only; requires k % 256 == 0 and
+ *  n % 64 == 0. */
 int kcmm_gemm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
                              uint32_t m, uint32_t n, uint32_t k,
                              uint64_t stream_ptr);
+
+/** Y[m][n] = X[m][k] * (W8[n][k] * wscale[n])^T with fp8-e4m3 (OCP e4m3fn)
+ *  weights W8 and one fp32 scale per weight row: the projection with
+ *  weight-only fp8 quantization (half the weight bytes a decode step
+ *  streams).  bf16 activations and output, fp32 accumulation on bf16 MFMA
+ *  (the weights are converted to bf16 exactly in registers; the row scale
+ *  multiplies the accumulated dot product).  Weight-stream kernel at every
+ *  m.  Enqueue only; k % 256 == 0, n % 64 == 0. */
+int kcmm_gemm_fp8w_bf16_on_stream(uint64_t x_ptr, uint64_t w8_ptr, uint64_t wscale_ptr,
+                                  uint64_t y_ptr, uint32_t m, uint32_t n, uint32_t k,
+                                  uint64_t stream_ptr);
 
 /** Y = R + X * W^T: the O / down projections with the residual add of ref
  *  llama_transformer.rs:358-360,377-379 (add.cu) in the GEMM's store.  The product
@@ -244,6 +256,15 @@ int kcmm_rmsnorm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
                                 uint32_t rows, uint32_t hidden, float eps,
                                 uint64_t stream_ptr);
 
+/** Token embedding of a decode step (ref llama_transformer.rs:264-275, one
+ *  device copy per token there): hidden[b][:] = embed[token_ids[b]][:] for
+ *  b < batch, bf16 rows of hidden_size (% 8 == 0) elements; token_ids is a
+ *  device int32 array (e.g. the previous step's sampled tokens); an id
+ *  outside [0, vocab) gives a zero row.  Enqueue only. */
+int kcmm_embed_tokens_bf16_on_stream(uint64_t embed_ptr, uint64_t token_ids_ptr,
+                                     uint64_t hidden_ptr, uint32_t batch, uint32_t hidden_size,
+                                     uint32_t vocab, uint64_t stream_ptr);
+
 /** act[r][j] = bf16(bf16(silu(g)) * u) with g = gate_up[r][j] and
  *  u = gate_up[r][intermediate + j] (the fused [gate | up] projection
  *  output; F.silu on a bf16 tensor rounds before the multiply).
@@ -256,7 +277,7 @@ int kcmm_silu_mul_bf16_on_stream(uint64_t gate_up_ptr, uint64_t act_ptr, uint32_
  *  = bf16(bf16(silu(G)) * U) with G, U the bf16-rounded projections
  *  x * w[j]^T and x * w[intermediate + j]^T; w_gate_up = [gate rows; up
  *  rows], [2 intermediate][k].  Bit-identical to kcmm_gemm_bf16_on_stream
- *  (on the weight-stream kernel: m <= 128 or KCMM_GEMM_LT=0)
+ *  (on the weight-stream kernel: m <= 128 or KCMM_GEMM_TILED=0)
  *  followed by kcmm_silu_mul_bf16_on_stream, without the [m][2 intermediate]
  *  intermediate.  intermediate % 32 == 0, k % 256 == 0. */
 int kcmm_gemm_bf16_swiglu_on_stream(uint64_t x_ptr, uint64_t w_gate_up_ptr, uint64_t act_ptr,
@@ -289,7 +310,7 @@ int kcmm_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, uint6
  *  treated exactly as kcmm_rope_append_bf16_on_stream treats a qkv row, so
  *  the pair gives identical bits without the qkv intermediate (with the
  *  pair's GEMM on the weight-stream kernel: batch <= 128 or
- *  KCMM_GEMM_LT=0).  head_dim %
+ *  KCMM_GEMM_TILED=0).  head_dim %
  *  16 == 0, hidden % 256 == 0, (Hq + 2 Hkv) head_dim % 64 == 0. */
 int kcmm_qkv_rope_append_bf16_on_stream(kcmm_pool_t *pool, uint32_t layer_idx, uint64_t x_ptr,
                                         uint64_t w_qkv_ptr, uint64_t q_out_ptr,

@@ -167,9 +167,11 @@ SIGNATURES = {
     "kcmm_copy_blocks_on_stream": ([_P, _P, _U32, _U64], C.c_int),
     "kcmm_copy_blocks_device_on_stream": ([_P, _U64, _U64, _U32, _U64], C.c_int),
     "kcmm_gemm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
+    "kcmm_gemm_fp8w_bf16_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_gemm_bf16_add_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_rmsnorm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, C.c_float, _U64], C.c_int),
     "kcmm_silu_mul_bf16_on_stream": ([_U64, _U64, _U32, _U32, _U64], C.c_int),
+    "kcmm_embed_tokens_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_gemm_bf16_swiglu_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_decode_logits_bf16_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, C.c_float,
                                            _U64], C.c_int),
@@ -227,6 +229,12 @@ class KcmmLibrary:
         if self.lib.kcmm_gemm_bf16_on_stream(x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr) != 0:
             raise KcmmError("kcmm_gemm_bf16_on_stream failed")
 
+    def gemm_fp8w_bf16(self, x_ptr, w8_ptr, wscale_ptr, y_ptr, m, n, k, stream_ptr=0) -> None:
+        """Y = X (W8 diag(wscale))^T: fp8-e4m3 weights with an fp32 scale per row."""
+        if self.lib.kcmm_gemm_fp8w_bf16_on_stream(x_ptr, w8_ptr, wscale_ptr, y_ptr, m, n, k,
+                                                  stream_ptr) != 0:
+            raise KcmmError("kcmm_gemm_fp8w_bf16_on_stream failed")
+
     def gemm_bf16_add(self, x_ptr, w_ptr, residual_ptr, y_ptr, m, n, k, stream_ptr=0) -> None:
         """Y = R + X W^T (R may be Y)."""
         if self.lib.kcmm_gemm_bf16_add_on_stream(x_ptr, w_ptr, residual_ptr, y_ptr, m, n, k,
@@ -237,6 +245,13 @@ class KcmmLibrary:
         if self.lib.kcmm_rmsnorm_bf16_on_stream(x_ptr, w_ptr, y_ptr, rows, hidden, C.c_float(eps),
                                                 stream_ptr) != 0:
             raise KcmmError("kcmm_rmsnorm_bf16_on_stream failed")
+
+    def embed_tokens_bf16(self, embed_ptr, token_ids_ptr, hidden_ptr, batch, hidden_size, vocab,
+                          stream_ptr=0) -> None:
+        """hidden[b] = embed[token_ids[b]] (device int32 ids; out-of-range ids: zero rows)."""
+        if self.lib.kcmm_embed_tokens_bf16_on_stream(embed_ptr, token_ids_ptr, hidden_ptr, batch,
+                                                     hidden_size, vocab, stream_ptr) != 0:
+            raise KcmmError("kcmm_embed_tokens_bf16_on_stream failed")
 
     def silu_mul_bf16(self, gate_up_ptr, act_ptr, rows, intermediate, stream_ptr=0) -> None:
         if self.lib.kcmm_silu_mul_bf16_on_stream(gate_up_ptr, act_ptr, rows, intermediate,

@@ -116,6 +116,11 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
 // (kernels/gemm_tiled.hip); n % 64 == 0, k % 64 == 0.
 bool gemm_bf16_tiled(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
                      uint64_t stream, uint64_t residual, std::string* err);
+// Y = X (W8 diag(wscale))^T: fp8-e4m3 weights W8 [n][k] with an fp32 scale per
+// weight row, bf16 activations and result, fp32 accumulate (weight-stream
+// kernel; the weights are converted to bf16 exactly in registers).
+bool gemm_fp8w_bf16(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32_t m, uint32_t n,
+                    uint32_t k, uint64_t stream, std::string* err);
 // Y = bf16(sum of `splits` fp32 partials [splits][MN]) (+ R), in split order.
 bool gemm_split_reduce_launch(const float* part, uint16_t* y, const uint16_t* r, int mn,
                               int splits, uint64_t stream, std::string* err);
@@ -139,6 +144,10 @@ struct RopeAppendArgs {
                               // a larger id are skipped)
 };
 bool rope_append_bf16(const RopeAppendArgs& a, std::string* err);
+// hidden[b] = embed[ids[b]] (bf16 rows of hidden_size; ids int32 on the
+// device; an id outside [0, vocab) gives a zero row).
+bool embed_bf16(uint64_t embed, uint64_t ids, uint64_t hidden, uint32_t batch, uint32_t hidden_size,
+                uint32_t vocab, uint64_t stream, std::string* err);
 bool silu_mul_bf16(uint64_t gate_up, uint64_t act, uint32_t rows, uint32_t inter,
                    uint64_t stream, std::string* err);
 

@@ -1023,6 +1023,17 @@ int kcmm_gemm_bf16_on_stream(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uin
     return 0;
 }
 
+int kcmm_gemm_fp8w_bf16_on_stream(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32_t m,
+                                  uint32_t n, uint32_t k, uint64_t stream) {
+    if (x == 0 || w8 == 0 || wscale == 0 || y == 0) return -1;
+    std::string err;
+    if (!kcmm::dev::gemm_fp8w_bf16(x, w8, wscale, y, m, n, k, stream, &err)) {
+        std::fprintf(stderr, "kcmm_gemm_fp8w_bf16_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
 int kcmm_gemm_bf16_add_on_stream(uint64_t x, uint64_t w, uint64_t residual, uint64_t y,
                                  uint32_t m, uint32_t n, uint32_t k, uint64_t stream) {
     if (x == 0 || w == 0 || residual == 0 || y == 0 || m == 0 || n == 0 || k == 0) return -1;
@@ -1073,6 +1084,20 @@ int kcmm_rmsnorm_bf16_on_stream(uint64_t x, uint64_t w, uint64_t y, uint32_t row
     std::string err;
     if (!kcmm::dev::rmsnorm_bf16(x, w, y, rows, hidden, eps, stream, &err)) {
         std::fprintf(stderr, "kcmm_rmsnorm_bf16_on_stream: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_embed_tokens_bf16_on_stream(uint64_t embed, uint64_t token_ids, uint64_t hidden,
+                                     uint32_t batch, uint32_t hidden_size, uint32_t vocab,
+                                     uint64_t stream) {
+    if (embed == 0 || token_ids == 0 || hidden == 0 || batch == 0 || hidden_size == 0 ||
+        hidden_size % 8 != 0 || vocab == 0)
+        return -1;
+    std::string err;
+    if (!kcmm::dev::embed_bf16(embed, token_ids, hidden, batch, hidden_size, vocab, stream, &err)) {
+        std::fprintf(stderr, "kcmm_embed_tokens_bf16_on_stream: %s\n", err.c_str());
         return -1;
     }
     return 0;

@@ -58,6 +58,17 @@ __device__ __forceinline__ void fix_lines(u32x4& x, u32x4& y, bool low8) {
     y = ny;
 }
 
+// Eight e4m3 values (two dwords) -> eight bf16, exactly (every e4m3 value is
+// a bf16 value).
+__device__ __forceinline__ u32x4 fp8x8_to_bf16(uint32_t d0, uint32_t d1) {
+    u32x4 r;
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, true));
+    return r;
+}
+
 __device__ __forceinline__ u32x4 load_stream(const uint8_t* a) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a));
 }
@@ -88,6 +99,7 @@ struct GemmParams {
     uint16_t* Y;         // plain: [M][N]; swiglu: act [M][N/2]
     const uint16_t* R;   // plain: residual [M][N] or null (may equal Y)
     float* part;         // non-null: write fp32 partials [split][M][N], no epilogue
+    const float* wscale; // fp8 weights: fp32 scale per weight row [N] (row n of W times wscale[n])
     int M, N, K, klen;
     // rope_append
     uint16_t* q_out;     // [M][Hq][D]
@@ -105,10 +117,17 @@ struct GemmParams {
 // rowA + 0..7 and 8..15 = rowB + 0..7.  With p.part set: fp32 partials of
 // split blockIdx.y, else the EPI epilogue.
 template <int MB, int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x4 (&acc)[MB], int rowA,
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[MB], int rowA,
                                               int rowB, int m_base, int ln, int lg) {
     const bool hi = lg >= 2;
     const int cw = 4 * (lg & 1);
+    if (p.wscale != nullptr) {
+        // fp8 weights: the row scale multiplies the whole dot product
+        const float* sc = p.wscale + (hi ? rowB : rowA) + cw;
+        const f32x4 s4 = {sc[0], sc[1], sc[2], sc[3]};
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[j] *= s4;
+    }
     if (p.part != nullptr) {
         const int n = (hi ? rowB : rowA) + cw;
 #pragma unroll
@@ -222,11 +241,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x4 (
 // then stream each weight line: 20-40% slower); summing the split partials inside this kernel
 // by the last workgroup of each tile, whose coherent stores and arrival count
 // put several memory round trips on every tile's tail.)
-template <int MB, int KCH, int EPI>
+template <int MB, int KCH, int EPI, bool WF8 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_bf16_stream(GemmParams p) {
     constexpr int NT = 256;
-    constexpr int LINES = KCH / 64;          // 128-byte lines per weight row per chunk
+    // 128-byte lines per weight row per chunk (fp8 weights: half as many)
+    constexpr int LINES = WF8 ? KCH / 128 : KCH / 64;
     constexpr int KC = KCH / 32;             // MFMA k-steps per chunk
     constexpr int PIECES = KCH / 8;          // 16-byte pieces per activation row
     constexpr int MROWS = 16 * MB;
@@ -246,7 +266,7 @@ void gemm_bf16_stream(GemmParams p) {
     const int m_base = blockIdx.z * MROWS;
     const int kbeg = blockIdx.y * p.klen;
     const int nchunks = p.klen / KCH;
-    const uint32_t rowb = static_cast<uint32_t>(K) * 2;
+    const uint32_t rowb = static_cast<uint32_t>(K) * (WF8 ? 1 : 2);   // weight row bytes
 
     // weight rows of this wave: rowA + 0..7 (MFMA rows 0..7), rowB + 0..7 (8..15)
     const int gw = blockIdx.x * 4 + wave;
@@ -266,13 +286,13 @@ void gemm_bf16_stream(GemmParams p) {
 
     const uint32_t piece = ((ln >> 3) * 4 + lg) * 16;
     const uint8_t* wp0 = reinterpret_cast<const uint8_t*>(p.W) + (rowA + (ln & 7)) * static_cast<size_t>(rowb) +
-                         piece + static_cast<size_t>(kbeg) * 2;
+                         piece + static_cast<size_t>(kbeg) * (WF8 ? 1 : 2);
     const uint8_t* wp1 = reinterpret_cast<const uint8_t*>(p.W) + (rowB + (ln & 7)) * static_cast<size_t>(rowb) +
-                         piece + static_cast<size_t>(kbeg) * 2;
+                         piece + static_cast<size_t>(kbeg) * (WF8 ? 1 : 2);
     auto load_w = [&](u32x4* dst, int c) {
 #pragma unroll
         for (int c2 = 0; c2 < LINES; ++c2) {
-            const size_t o = static_cast<size_t>(c) * KCH * 2 + c2 * 128;
+            const size_t o = static_cast<size_t>(c) * KCH * (WF8 ? 1 : 2) + c2 * 128;
             dst[2 * c2] = load_stream(wp0 + o);
             dst[2 * c2 + 1] = load_stream(wp1 + o);
         }
@@ -298,7 +318,38 @@ void gemm_bf16_stream(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[j] = f32x4{0, 0, 0, 0};
 
+    // one MFMA k-step: A operand a (16 weight rows), B from activation piece pc
+    auto kstep = [&](const u32x4& a, int pc, int buf) {
+        u32x4 b[MB];
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            const int r = 16 * j + ln;
+            b[j] = *reinterpret_cast<const u32x4*>(xs + buf * XBUF + r * ROWB +
+                                                   ((pc ^ (r & (PIECES - 1))) * 16));
+        }
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b[j]), acc[j], 0, 0, 0);
+    };
     auto compute = [&](u32x4* wa, int buf) {
+        if constexpr (WF8) {
+            // a fixed-up half line holds 16 fp8 weights per lane, k = base +
+            // 16 lg + 0..15; each 8 of them (exactly bf16 after conversion)
+            // are one k-step, against activation piece base/8 + 2 lg (+1)
+#pragma unroll
+            for (int c2 = 0; c2 < LINES; ++c2) {
+                fix_lines(wa[2 * c2], wa[2 * c2 + 1], low8);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const u32x4& raw = wa[2 * c2 + hh];
+                    const int pc = (c2 * 128 + hh * 64) / 8 + 2 * lg;
+                    kstep(fp8x8_to_bf16(raw[0], raw[1]), pc, buf);
+                    kstep(fp8x8_to_bf16(raw[2], raw[3]), pc + 1, buf);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int c2 = 0; c2 < LINES; ++c2) {
             fix_lines(wa[2 * c2], wa[2 * c2 + 1], low8);
@@ -423,29 +474,31 @@ int choose_splits(int N, int K, int kch, int mgroups) {
 
 // Tile shape by M: token blocks per pass (the activation chunk, M x KCH
 // bf16, is 32 KiB).
+// fp8 weights need at least 128-element chunks (one 128-byte weight line).
 template <typename F>
-bool by_m(int M, F&& f) {
+bool by_m(int M, F&& f, bool wf8 = false) {
     if (M <= 16) return f(std::integral_constant<int, 1>{}, std::integral_constant<int, 256>{});
     if (M <= 32) return f(std::integral_constant<int, 2>{}, std::integral_constant<int, 256>{});
     if (M <= 64) return f(std::integral_constant<int, 4>{}, std::integral_constant<int, 256>{});
     if (M <= 128) return f(std::integral_constant<int, 8>{}, std::integral_constant<int, 128>{});
+    if (wf8) return f(std::integral_constant<int, 16>{}, std::integral_constant<int, 128>{});
     return f(std::integral_constant<int, 16>{}, std::integral_constant<int, 64>{});
 }
 
-int splits_for(int M, int N, int K) {
+int splits_for(int M, int N, int K, bool wf8 = false) {
     int s = 1;
     by_m(M, [&](auto mb, auto kch) {
         const int mgroups = (M + 16 * mb.value - 1) / (16 * mb.value);
         s = choose_splits(N, K, kch.value, mgroups);
         return true;
-    });
+    }, wf8);
     return s;
 }
 
 // Launch the streaming kernel with `splits` K splits; splits > 1 or
 // want_partials writes fp32 partials [splits][M][N] to the stream's workspace
 // (returned in *part) instead of running the epilogue.
-template <int EPI>
+template <int EPI, bool WF8 = false>
 bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, uint64_t stream,
                    std::string* err) {
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -461,11 +514,16 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
     p.klen = p.K / splits;
     return by_m(p.M, [&](auto mb, auto kch) {
         constexpr int MB = decltype(mb)::value, KCH = decltype(kch)::value;
-        const dim3 grid(p.N / 64, splits, (p.M + 16 * MB - 1) / (16 * MB));
-        hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI>), grid, dim3(256), 0, s, p);
-        KCMM_HIP_CHECK(hipGetLastError(), err);
-        return true;
-    });
+        if constexpr (WF8 && KCH < 128) {
+            *err = "fp8 weights need 128-element chunks";
+            return false;
+        } else {
+            const dim3 grid(p.N / 64, splits, (p.M + 16 * MB - 1) / (16 * MB));
+            hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8>), grid, dim3(256), 0, s, p);
+            KCMM_HIP_CHECK(hipGetLastError(), err);
+            return true;
+        }
+    }, WF8);
 }
 
 bool shape_ok(uint32_t m, uint32_t n, uint32_t k, std::string* err) {
@@ -522,6 +580,19 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
                            reinterpret_cast<hipStream_t>(stream), part, p.Y, p.R, MN, splits);
         KCMM_HIP_CHECK(hipGetLastError(), err);
     }
+    return true;
+}
+
+bool gemm_fp8w_bf16(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32_t m, uint32_t n,
+                    uint32_t k, uint64_t stream, std::string* err) {
+    if (!shape_ok(m, n, k, err)) return false;
+    GemmParams p = base_params(x, w8, m, n, k);
+    p.Y = reinterpret_cast<uint16_t*>(y);
+    p.wscale = reinterpret_cast<const float*>(wscale);
+    const int splits = splits_for(p.M, p.N, p.K, true);
+    float* part = nullptr;
+    if (!launch_stream<kEpiPlain, true>(p, splits, false, &part, stream, err)) return false;
+    if (splits > 1) return gemm_split_reduce_launch(part, p.Y, nullptr, p.M * p.N, splits, stream, err);
     return true;
 }
 

@@ -261,6 +261,23 @@ void launch_rmsnorm(uint16_t* x, const uint16_t* w, uint16_t* y, uint32_t rows, 
                            h, eps, part, splits);
 }
 
+// hidden[b] = embed[ids[b]] (ref llama_transformer.rs:264-275 copies each
+// token's row with its own driver memcpy); one workgroup per row, 16-byte
+// pieces; an id outside [0, vocab) gives a zero row.
+__global__ __launch_bounds__(256) void embed_rows(const uint8_t* __restrict__ embed,
+                                                  const int32_t* __restrict__ ids,
+                                                  uint8_t* __restrict__ hidden, uint32_t row_bytes,
+                                                  uint32_t vocab) {
+    const int b = blockIdx.x;
+    const int32_t id = ids[b];
+    const bool ok = id >= 0 && static_cast<uint32_t>(id) < vocab;
+    const uint8_t* src = embed + static_cast<size_t>(ok ? id : 0) * row_bytes;
+    uint8_t* dst = hidden + static_cast<size_t>(b) * row_bytes;
+    for (uint32_t o = threadIdx.x * 16; o < row_bytes; o += 256 * 16)
+        *reinterpret_cast<u32x4*>(dst + o) = ok ? *reinterpret_cast<const u32x4*>(src + o)
+                                                : u32x4{0, 0, 0, 0};
+}
+
 }  // namespace
 
 namespace dev {
@@ -372,6 +389,16 @@ bool rope_append_bf16(const RopeAppendArgs& a, std::string* err) {
 bool rope_append_from_partials(const RopeAppendArgs& a, const float* part, int splits,
                                std::string* err) {
     return launch_rope(a, part, splits, err);
+}
+
+bool embed_bf16(uint64_t embed, uint64_t ids, uint64_t hidden, uint32_t batch, uint32_t hidden_size,
+                uint32_t vocab, uint64_t stream, std::string* err) {
+    if (batch == 0) return true;
+    hipLaunchKernelGGL(embed_rows, dim3(batch), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       reinterpret_cast<const uint8_t*>(embed), reinterpret_cast<const int32_t*>(ids),
+                       reinterpret_cast<uint8_t*>(hidden), hidden_size * 2u, vocab);
+    KCMM_HIP_CHECK(hipGetLastError(), err);
+    return true;
 }
 
 bool silu_mul_bf16(uint64_t gate_up, uint64_t act, uint32_t rows, uint32_t inter,

@@ -97,6 +97,7 @@ def _bind(l: C.CDLL) -> None:
         "oracle_attn_prefill_f64": ([C.c_int, P, P, P, P, P, P, P, P] + [U32] * 8 + [C.c_double],
                                     C.c_int),
         "oracle_gemm_bf16_f64": ([P, P, P, U32, U32, U32], None),
+        "oracle_gemm_fp8w_f64": ([P, P, P, P, U32, U32, U32], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(l, name)
@@ -421,6 +422,28 @@ def gemm_bf16_f64(x_bits: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
     y = np.zeros((m, n), dtype=np.float64)
     lib().oracle_gemm_bf16_f64(_p(x), _p(w), _p(y), m, n, k)
     return y
+
+
+def gemm_fp8w_f64(x_bits: np.ndarray, w8: np.ndarray, wscale: np.ndarray) -> np.ndarray:
+    """Y = X (decode(W8) diag(wscale))^T in fp64 (bf16 X, e4m3 W8, fp32 scale per row)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(w8, dtype=np.uint8)
+    s = np.ascontiguousarray(wscale, dtype=np.float32)
+    m, k = x.shape
+    n, k2 = w.shape
+    assert k == k2 and s.shape == (n,)
+    y = np.zeros((m, n), dtype=np.float64)
+    lib().oracle_gemm_fp8w_f64(_p(x), _p(w), _p(s), _p(y), m, n, k)
+    return y
+
+
+def quantize_fp8_rows(w: np.ndarray):
+    """Per-row e4m3 weights: scale = amax/448 (1 for an all-zero row), codes =
+    RNE of w/scale with saturation (the page writer's rule, applied per row)."""
+    w = np.asarray(w, dtype=np.float32)
+    amax = np.abs(w).max(axis=1)
+    scale = np.where(amax > 0, amax / np.float32(448.0), np.float32(1.0)).astype(np.float32)
+    return encode(FP8, w / scale[:, None]), scale
 
 
 # ---- decode-step glue and one decoder layer ----------------------------------

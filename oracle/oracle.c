@@ -1195,7 +1195,7 @@ int oracle_attn_decode_ref_f32(int dtype, const void *q, float *out, const uint8
                                uint32_t batch, uint32_t hq, uint32_t hkv, uint32_t D,
                                uint32_t bs, uint32_t mbps, uint32_t row_bytes, float scale,
                                int threads) {
-    if (D > 256 || (dtype != 0 && dtype != 1)) return -1;
+    if (D > 256 || (dtype != 0 && dtype != 1 && dtype != 3)) return -1;
 #ifdef _OPENMP
     if (threads > 0) omp_set_num_threads(threads);
 #endif
@@ -1208,19 +1208,28 @@ int oracle_attn_decode_ref_f32(int dtype, const void *q, float *out, const uint8
         if (L <= 0) { for (uint32_t d = 0; d < D; ++d) o[d] = 0.0f; continue; }
         float qv[256], acc[256];
         for (uint32_t d = 0; d < D; ++d) {
-            uint16_t x = ((const uint16_t *)q)[((size_t)b * hq + h) * D + d];
-            qv[d] = dtype == 0 ? oracle_f16_to_f32(x) : oracle_bf16_to_f32(x);
+            if (dtype == 3) {
+                qv[d] = ((const float *)q)[((size_t)b * hq + h) * D + d];
+            } else {
+                uint16_t x = ((const uint16_t *)q)[((size_t)b * hq + h) * D + d];
+                qv[d] = dtype == 0 ? oracle_f16_to_f32(x) : oracle_bf16_to_f32(x);
+            }
             acc[d] = 0.0f;
         }
+        const uint32_t es = dtype == 3 ? 4 : 2;
         float m = -1e30f, s = 0.0f;
         for (int32_t pos = 0; pos < L; ++pos) {
             int32_t blk = block_tables[(size_t)b * mbps + pos / bs];
             uint64_t base = offsets_f16[blk] * 2 + (uint64_t)(pos % bs) * row_bytes +
-                            (uint64_t)kvh * D * 2;
+                            (uint64_t)kvh * D * es;
             const uint16_t *kr = (const uint16_t *)(k_region + base);
             const uint16_t *vr = (const uint16_t *)(v_region + base);
+            const float *kf = (const float *)(k_region + base);
+            const float *vf = (const float *)(v_region + base);
             float dot = 0.0f;
-            if (dtype == 1) {
+            if (dtype == 3) {
+                for (uint32_t d = 0; d < D; ++d) dot += qv[d] * kf[d];
+            } else if (dtype == 1) {
                 for (uint32_t d = 0; d < D; ++d) dot += qv[d] * u2f((uint32_t)kr[d] << 16);
             } else {
                 for (uint32_t d = 0; d < D; ++d) dot += qv[d] * oracle_f16_to_f32(kr[d]);
@@ -1231,7 +1240,9 @@ int oracle_attn_decode_ref_f32(int dtype, const void *q, float *out, const uint8
             float e = expf(dot - m);
             float corr = expf(old_m - m);
             s = s * corr + e;
-            if (dtype == 1) {
+            if (dtype == 3) {
+                for (uint32_t d = 0; d < D; ++d) acc[d] = acc[d] * corr + e * vf[d];
+            } else if (dtype == 1) {
                 for (uint32_t d = 0; d < D; ++d) acc[d] = acc[d] * corr + e * u2f((uint32_t)vr[d] << 16);
             } else {
                 for (uint32_t d = 0; d < D; ++d) acc[d] = acc[d] * corr + e * oracle_f16_to_f32(vr[d]);
@@ -1247,6 +1258,24 @@ int oracle_attn_decode_ref_f32(int dtype, const void *q, float *out, const uint8
  * GEMM: Y = X W^T (the HF Linear product ref llama_transformer.rs:115-120
  * intends; ref runtime.rs:17-41 delegates it to cuBLAS).
  * ====================================================================== */
+/* Y = X (W8 diag(s))^T with e4m3 weights and an fp32 scale per weight row:
+ * the fp64 sum of x * decode(w8) times the row's scale. */
+void oracle_gemm_fp8w_f64(const uint16_t *x, const uint8_t *w8, const float *s, double *y,
+                          uint32_t m, uint32_t n, uint32_t k) {
+    #pragma omp parallel for schedule(static)
+    for (long long i = 0; i < (long long)m; ++i) {
+        double *xr = (double *)malloc(k * sizeof(double));
+        for (uint32_t t = 0; t < k; ++t) xr[t] = oracle_bf16_to_f32(x[(size_t)i * k + t]);
+        for (uint32_t j = 0; j < n; ++j) {
+            const uint8_t *wr = w8 + (size_t)j * k;
+            double acc = 0.0;
+            for (uint32_t t = 0; t < k; ++t) acc += xr[t] * (double)oracle_e4m3_to_f32(wr[t]);
+            y[(size_t)i * n + j] = acc * (double)s[j];
+        }
+        free(xr);
+    }
+}
+
 void oracle_gemm_bf16_f64(const uint16_t *x, const uint16_t *w, double *y, uint32_t m,
                           uint32_t n, uint32_t k) {
     #pragma omp parallel for schedule(static)

@@ -134,6 +134,8 @@ int oracle_attn_decode_ref_f32(int dtype, const void *q, float *out, const uint8
 
 /* ---- projection GEMM (intended semantics of ref runtime.rs:17-41) ---- */
 /* Y[m][n] = sum_k X[m][k] W[n][k], bf16 inputs, fp64 accumulation. */
+void oracle_gemm_fp8w_f64(const uint16_t *x, const uint8_t *w8, const float *s, double *y,
+                          uint32_t m, uint32_t n, uint32_t k);
 void oracle_gemm_bf16_f64(const uint16_t *x, const uint16_t *w, double *y, uint32_t m,
                           uint32_t n, uint32_t k);
 

@@ -164,6 +164,10 @@ bool rmsnorm_bf16(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, float, uint6
     return no_device(err);
 }
 bool rope_append_bf16(const RopeAppendArgs&, std::string* err) { return no_device(err); }
+bool embed_bf16(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t,
+                std::string* err) {
+    return no_device(err);
+}
 bool silu_mul_bf16(uint64_t, uint64_t, uint32_t, uint32_t, uint64_t, std::string* err) {
     return no_device(err);
 }
@@ -177,6 +181,10 @@ bool gemm_bf16_swiglu(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t
 }
 bool gemm_bf16_tiled(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, uint64_t,
                      std::string* err) {
+    return no_device(err);
+}
+bool gemm_fp8w_bf16(uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t,
+                    std::string* err) {
     return no_device(err);
 }
 bool gemm_split_reduce_launch(const float*, uint16_t*, const uint16_t*, int, int, uint64_t,

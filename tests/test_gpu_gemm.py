@@ -78,7 +78,6 @@ def test_split_k_choices(gpu_lib, monkeypatch, target, m, n, k):
     partials and their reduction are exact up to fp32 rounding."""
     import torch
     monkeypatch.setenv("KCMM_GEMM_WGS", target)
-    monkeypatch.setenv("KCMM_GEMM_LT", "0")
     g = torch.Generator(device="cuda")
     g.manual_seed(m * 31 + n + k + len(target))
     x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
@@ -128,3 +127,72 @@ def test_tiled_tiles_splits_residual(gpu_lib, monkeypatch, tile, splits, residua
     err = rel_err(got, ref)
     print(f"tiled tile={tile} splits={splits} residual={residual} err={err:.3e}", flush=True)
     assert err <= 1e-2
+
+
+def _fp8_weights(torch, rng, n, k, std):
+    w8, s = O.quantize_fp8_rows(rng.standard_normal((n, k)).astype(np.float32) * std)
+    return w8, s, torch.from_numpy(w8).cuda(), torch.from_numpy(s).cuda()
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 256), (17, 192, 512), (64, 256, 1024),
+                                   (100, 128, 768), (129, 192, 512), (256, 640, 2048)])
+def test_fp8_weights_vs_oracle(gpu_lib, m, n, k):
+    """kcmm_gemm_fp8w_bf16: e4m3 weights with per-row scales against the fp64
+    oracle (relative 1e-2, the bf16 output's tolerance); a second call gives
+    the same bits."""
+    import torch
+    rng = np.random.default_rng(m * 3 + n + k)
+    xb = O.encode(O.BF16, rng.standard_normal((m, k)))
+    w8, s, w8d, sd = _fp8_weights(torch, rng, n, k, 0.02)
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    outs = []
+    for _ in range(2):
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        gpu_lib.gemm_fp8w_bf16(x.data_ptr(), w8d.data_ptr(), sd.data_ptr(), y.data_ptr(), m, n, k,
+                               torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(outs[0], outs[1])
+    got = O.decode(O.BF16, outs[0]).astype(np.float64)
+    err = rel_err(got, O.gemm_fp8w_f64(xb, w8, s))
+    print(f"fp8w gemm {m}x{n}x{k} err={err:.3e}", flush=True)
+    assert err <= 1e-2
+
+
+@pytest.mark.parametrize("m", [64, 128, 256])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)])
+def test_fp8_weights_llama3_8b_projections(gpu_lib, m, n, k):
+    """The four Llama-3-8B projections with fp8 weights vs a torch fp32 product
+    of the dequantized weights."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m + n + k)
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    w = torch.randn((n, k), generator=g, device="cuda") * 0.02
+    s = (w.abs().amax(dim=1) / 448.0).clamp_min(1e-30)
+    w8 = (w / s[:, None]).to(torch.float8_e4m3fn)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.gemm_fp8w_bf16(x.data_ptr(), w8.view(torch.uint8).data_ptr(), s.data_ptr(),
+                           y.data_ptr(), m, n, k, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref = x.float() @ (w8.float() * s[:, None]).t()
+    err = float((y.float() - ref).abs().max() / ref.abs().max())
+    print(f"fp8w gemm {m}x{n}x{k} err={err:.3e}", flush=True)
+    assert err <= 1e-2
+
+
+@pytest.mark.parametrize("splits", ["1", "2", "4", "8"])
+def test_fp8_weights_split_k(gpu_lib, monkeypatch, splits):
+    import torch
+    monkeypatch.setenv("KCMM_GEMM_SPLITS", splits)
+    rng = np.random.default_rng(int(splits))
+    m, n, k = 64, 512, 4096
+    xb = O.encode(O.BF16, rng.standard_normal((m, k)))
+    w8, s, w8d, sd = _fp8_weights(torch, rng, n, k, 0.02)
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.gemm_fp8w_bf16(x.data_ptr(), w8d.data_ptr(), sd.data_ptr(), y.data_ptr(), m, n, k,
+                           torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = O.decode(O.BF16, y.cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+    assert rel_err(got, O.gemm_fp8w_f64(xb, w8, s)) <= 1e-2

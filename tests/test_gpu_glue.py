@@ -378,3 +378,25 @@ def test_decode_logits(gpu_lib, b, h, vocab):
     assert rel_err(got, ref) <= 1e-2
     # hidden is not modified
     assert np.array_equal(bits_of(xd), x)
+
+
+def test_embed_tokens(gpu_lib):
+    """hidden[b] = embed[ids[b]] bit for bit (ref llama_transformer.rs:264-275),
+    ids on the device; ids outside [0, vocab) give zero rows; a repeated id
+    and the first/last rows of the table included."""
+    import torch
+    rng = np.random.default_rng(41)
+    vocab, H = 1000, 4096
+    table = O.encode(O.BF16, rng.standard_normal((vocab, H)))
+    ids = np.array([5, 999, 0, -1, 1000, 17, 5, 2 ** 31 - 1, 512], np.int32)
+    tdev = bf16_dev(torch, table)
+    idd = torch.from_numpy(ids).cuda()
+    out = torch.full((len(ids), H), float("nan"), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.embed_tokens_bf16(tdev.data_ptr(), idd.data_ptr(), out.data_ptr(), len(ids), H, vocab,
+                              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = bits_of(out)
+    ok = (ids >= 0) & (ids < vocab)
+    ref = np.zeros((len(ids), H), np.uint16)
+    ref[ok] = table[ids[ok]]
+    assert np.array_equal(got, ref)

@@ -88,7 +88,7 @@ def test_page_placement_does_not_matter(oracle_lib):
     assert np.array_equal(ra, rb)
 
 
-@pytest.mark.parametrize("dtype", [O.F16, O.BF16])
+@pytest.mark.parametrize("dtype", [O.F16, O.BF16, O.F32])
 def test_reference_loop_within_fp32_tolerance(oracle_lib, dtype):
     hq, hkv, d, bs = 8, 8, 64, 16                         # BASELINE configs[0] shape
     rng = np.random.default_rng(11)
