@@ -832,85 +832,201 @@ void launch_merge(AttnParams& p, hipStream_t s) {
         hipLaunchKernelGGL((attn_decode_merge<DT, D, 32>), grid, block, 0, s, p, p.seg_info);
 }
 
-// Any-shape fallback (head_dim <= 256, any GQA map, any block size, fp8
-// pages): one wavefront per (b, query head), lanes split the head dimension,
-// the same online-softmax recurrence as the reference kernel.
-template <int DT>
-__global__ __launch_bounds__(64) void attn_decode_generic(AttnParams p, int head_dim,
-                                                          float scale) {
+// Any-shape decode attention (head_dim <= 256, any GQA map, any block size;
+// f16, bf16, fp32 and fp8 pages): one workgroup per (sequence, query head),
+// the same online-softmax recurrence as the reference kernel
+// (ref kcmm_vllm_paged_attn.cu:10-102), with the positions spread over the
+// workgroup instead of walked by one thread:
+//  * lanes form teams of T (a power of two, 4..64) with 4 consecutive head
+//    dims per lane; teams take positions round-robin, kGenUnroll at a time
+//    (every K and V load of those positions issued before the first is
+//    used), each team keeping its own running max, denominator and
+//    accumulator;
+//  * the page offsets (and fp8 scales) of kGenChunk positions are staged in
+//    LDS before the chunk is walked, so a position costs one dependent load
+//    (its K/V row), not three (table entry, offset, row);
+//  * at the end the teams' states are rescaled to the common max and summed
+//    through LDS.
+constexpr int kGenThreads = 512;
+constexpr int kGenChunk = 1024;
+constexpr int kGenUnroll = 4;
+constexpr int kGenMaxTeams = kGenThreads / 4;
+
+// Four consecutive elements d0..d0+3 of a K/V row (zeros past head_dim);
+// VEC: head_dim % 4 == 0, so the four are one aligned vector load.
+template <int DT, bool VEC>
+__device__ __forceinline__ void gen_load4(const uint8_t* row, int d0, int head_dim, float sc,
+                                          float (&x)[4]) {
+    if constexpr (VEC) {
+        if (d0 >= head_dim) {
+            x[0] = x[1] = x[2] = x[3] = 0.0f;
+            return;
+        }
+        if constexpr (DT == kDtF32) {
+            const float4 v = *reinterpret_cast<const float4*>(row + d0 * 4);
+            x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+        } else if constexpr (DT == kDtFP8) {
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(row + d0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = fp8e4m3_to_f32((w >> (8 * i)) & 0xFFu) * sc;
+        } else {
+            const uint2 w = *reinterpret_cast<const uint2*>(row + d0 * 2);
+            x[0] = elem_to_f32<DT>(w.x & 0xFFFFu);
+            x[1] = elem_to_f32<DT>(w.x >> 16);
+            x[2] = elem_to_f32<DT>(w.y & 0xFFFFu);
+            x[3] = elem_to_f32<DT>(w.y >> 16);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = d0 + i;
+            if (d >= head_dim) {
+                x[i] = 0.0f;
+            } else if constexpr (DT == kDtF32) {
+                x[i] = reinterpret_cast<const float*>(row)[d];
+            } else if constexpr (DT == kDtFP8) {
+                x[i] = fp8e4m3_to_f32(row[d]) * sc;
+            } else {
+                x[i] = elem_to_f32<DT>(reinterpret_cast<const uint16_t*>(row)[d]);
+            }
+        }
+    }
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kGenThreads) void attn_decode_generic(AttnParams p, int head_dim,
+                                                                   float scale, int tlog2) {
+    constexpr bool F8 = DT == kDtFP8;
+    __shared__ uint64_t s_page[kGenChunk + 1];
+    __shared__ float s_ks[F8 ? kGenChunk + 1 : 1], s_vs[F8 ? kGenChunk + 1 : 1];
+    __shared__ float s_m[kGenMaxTeams], s_s[kGenMaxTeams];
+    __shared__ float s_acc[kGenThreads * 4];
+
     const int bh = blockIdx.x;
     const int b = bh / p.num_q_heads;
     const int h = bh - b * p.num_q_heads;
     const int kvh = h * p.kv_heads / p.num_q_heads;  // ref kcmm_vllm_paged_attn.cu:40
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int T = 1 << tlog2;
+    const int nteams = blockDim.x >> tlog2;
+    const int team = tid >> tlog2;
+    const int d0 = (tid & (T - 1)) * 4;
     const int L = min(p.seq_lens[b], p.mbps * p.block_size);
     // q/out: f16 for f16 pools, fp32 for fp32 pools, bf16 otherwise
     const size_t io_off = (static_cast<size_t>(b) * p.num_q_heads + h) * head_dim * io_bytes<DT>();
     const uint8_t* qrow = p.q + io_off;
     uint8_t* orow = p.out + io_off;
     if (L <= 0) {
-        for (int d = lane; d < head_dim; d += 64) io_store<DT>(orow, d, 0.0f);
+        for (int d = tid; d < head_dim; d += blockDim.x) io_store<DT>(orow, d, 0.0f);
         return;
     }
     float qv[4], acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        qv[i] = d < head_dim ? io_load<DT>(qrow, d) : 0.0f;
+        qv[i] = d0 + i < head_dim ? io_load<DT>(qrow, d0 + i) : 0.0f;
         acc[i] = 0.0f;
     }
-    const int esize = kv_elem_bytes<DT>();
+    const uint64_t head_off = static_cast<uint64_t>(kvh) * head_dim * kv_elem_bytes<DT>();
+    const int32_t* table = p.block_tables + static_cast<size_t>(b) * p.mbps;
     float m = -INFINITY, s = 0.0f;
-    for (int pos = 0; pos < L; ++pos) {
-        const int lb = pos / p.block_size;
-        const int off = pos - lb * p.block_size;
-        const int blk = p.block_tables[static_cast<size_t>(b) * p.mbps + lb];
-        const uint64_t page = p.offsets_f16[blk] * 2ull;
-        const uint64_t roff = page + static_cast<uint64_t>(off) * p.row_bytes +
-                              static_cast<uint64_t>(kvh) * head_dim * esize;
-        float ks = 1.0f, vs = 1.0f;
-        if constexpr (DT == kDtFP8) {
-            ks = *reinterpret_cast<const float*>(p.k_base + page + p.data_bytes + kvh * 4);
-            vs = *reinterpret_cast<const float*>(p.v_base + page + p.data_bytes + kvh * 4);
+    for (int c0 = 0; c0 < L; c0 += kGenChunk) {
+        const int c1 = min(L, c0 + kGenChunk);
+        const int lb0 = c0 / p.block_size;
+        const int nb = (c1 - 1) / p.block_size - lb0 + 1;   // <= kGenChunk + 1
+        __syncthreads();                                    // the last chunk's readers are done
+        for (int i = tid; i < nb; i += blockDim.x) {
+            const uint64_t page = p.offsets_f16[table[lb0 + i]] * 2ull;
+            s_page[i] = page;
+            if constexpr (F8) {
+                s_ks[i] = *reinterpret_cast<const float*>(p.k_base + page + p.data_bytes + kvh * 4);
+                s_vs[i] = *reinterpret_cast<const float*>(p.v_base + page + p.data_bytes + kvh * 4);
+            }
         }
-        float dot = 0.0f;
-        float vv[4];
+        __syncthreads();
+        for (int pos = c0 + team; pos < c1; pos += nteams * kGenUnroll) {
+            float kx[kGenUnroll][4], vx[kGenUnroll][4], dot[kGenUnroll];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int d = lane + 64 * i;
-            float kx = 0.0f, vx = 0.0f;
-            if (d < head_dim) {
-                if constexpr (DT == kDtFP8) {
-                    kx = fp8e4m3_to_f32(p.k_base[roff + d]) * ks;
-                    vx = fp8e4m3_to_f32(p.v_base[roff + d]) * vs;
-                } else if constexpr (DT == kDtF32) {
-                    kx = reinterpret_cast<const float*>(p.k_base + roff)[d];
-                    vx = reinterpret_cast<const float*>(p.v_base + roff)[d];
+            for (int u = 0; u < kGenUnroll; ++u) {
+                const int pp = pos + u * nteams;
+                if (pp < c1) {
+                    const int lb = pp / p.block_size;
+                    const int j = lb - lb0;
+                    const uint64_t roff = s_page[j] +
+                                          static_cast<uint64_t>(pp - lb * p.block_size) * p.row_bytes +
+                                          head_off;
+                    gen_load4<DT, VEC>(p.k_base + roff, d0, head_dim, F8 ? s_ks[j] : 1.0f, kx[u]);
+                    gen_load4<DT, VEC>(p.v_base + roff, d0, head_dim, F8 ? s_vs[j] : 1.0f, vx[u]);
                 } else {
-                    kx = elem_to_f32<DT>(reinterpret_cast<const uint16_t*>(p.k_base + roff)[d]);
-                    vx = elem_to_f32<DT>(reinterpret_cast<const uint16_t*>(p.v_base + roff)[d]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) kx[u][i] = vx[u][i] = 0.0f;
                 }
             }
-            dot += qv[i] * kx;
-            vv[i] = vx;
+#pragma unroll
+            for (int u = 0; u < kGenUnroll; ++u)
+                dot[u] = qv[0] * kx[u][0] + qv[1] * kx[u][1] + qv[2] * kx[u][2] + qv[3] * kx[u][3];
+            for (int o = T >> 1; o > 0; o >>= 1) {
+#pragma unroll
+                for (int u = 0; u < kGenUnroll; ++u) dot[u] += __shfl_xor(dot[u], o);
+            }
+            float mx = m;
+#pragma unroll
+            for (int u = 0; u < kGenUnroll; ++u) {
+                dot[u] = pos + u * nteams < c1 ? dot[u] * scale : -INFINITY;
+                mx = fmaxf(mx, dot[u]);
+            }
+            const float corr = kexp<DT>(m - mx);            // m = -inf: 0
+            s *= corr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] *= corr;
+#pragma unroll
+            for (int u = 0; u < kGenUnroll; ++u) {
+                const float e = kexp<DT>(dot[u] - mx);      // -inf (past the chunk): 0
+                s += e;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] += e * vx[u][i];
+            }
+            m = mx;
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
-        dot *= scale;
-        const float m_new = fmaxf(m, dot);
-        const float e = kexp<DT>(dot - m_new);
-        const float corr = kexp<DT>(m - m_new);
-        s = s * corr + e;
-        m = m_new;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = acc[i] * corr + e * vv[i];
     }
-    const float inv = 1.0f / s;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        if (d < head_dim) io_store<DT>(orow, d, acc[i] * inv);
+    // combine the teams: rescale each to the common max, sum through LDS
+    if ((tid & (T - 1)) == 0) {
+        s_m[team] = m;
+        s_s[team] = s;
     }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int t = 0; t < nteams; ++t) M = fmaxf(M, s_m[t]);
+    const float f = m == -INFINITY ? 0.0f : kexp<DT>(m - M);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_acc[team * T * 4 + d0 + i] = acc[i] * f;
+    __syncthreads();
+    float S = 0.0f;
+    for (int t = 0; t < nteams; ++t)
+        if (s_m[t] != -INFINITY) S += s_s[t] * kexp<DT>(s_m[t] - M);
+    const float inv = 1.0f / S;
+    for (int d = tid; d < head_dim; d += blockDim.x) {
+        float o = 0.0f;
+        for (int t = 0; t < nteams; ++t) o += s_acc[t * T * 4 + d];
+        io_store<DT>(orow, d, o * inv);
+    }
+}
+
+template <int DT>
+void launch_generic(const AttnParams& p, int head_dim, float scale, hipStream_t s) {
+    int tlog2 = 2;
+    while ((4 << tlog2) < head_dim) ++tlog2;               // 4 * T >= head_dim, T <= 64
+    // few (sequence, head) pairs: the whole 512-lane workgroup per pair;
+    // enough pairs to fill the chip: 256 lanes each
+    const long long pairs = static_cast<long long>(p.batch) * p.num_q_heads;
+    if (pairs == 0) return;
+    const int threads = pairs >= 1024 ? 256 : kGenThreads;
+    const dim3 grid(static_cast<unsigned>(pairs));
+    if (head_dim % 4 == 0)
+        hipLaunchKernelGGL((attn_decode_generic<DT, true>), grid, dim3(threads), 0, s, p, head_dim,
+                           scale, tlog2);
+    else
+        hipLaunchKernelGGL((attn_decode_generic<DT, false>), grid, dim3(threads), 0, s, p, head_dim,
+                           scale, tlog2);
 }
 
 int env_int(const char* name, int dflt, int lo, int hi) {
@@ -1049,24 +1165,12 @@ bool attn_decode(const AttnDecodeArgs& a, std::string* err) {
         if (a.dtype == kDtBF16 && stream_dim)
             return launch_dt<kDtBF16>(p, a.head_dim, s, a.no_alloc, err);
     }
-    const dim3 grid(a.batch * a.num_q_heads);
+    const int hd = static_cast<int>(a.head_dim);
     switch (a.dtype) {
-        case kDtF16:
-            hipLaunchKernelGGL(attn_decode_generic<kDtF16>, grid, dim3(64), 0, s, p,
-                               static_cast<int>(a.head_dim), a.scale);
-            break;
-        case kDtBF16:
-            hipLaunchKernelGGL(attn_decode_generic<kDtBF16>, grid, dim3(64), 0, s, p,
-                               static_cast<int>(a.head_dim), a.scale);
-            break;
-        case kDtF32:
-            hipLaunchKernelGGL(attn_decode_generic<kDtF32>, grid, dim3(64), 0, s, p,
-                               static_cast<int>(a.head_dim), a.scale);
-            break;
-        default:
-            hipLaunchKernelGGL(attn_decode_generic<kDtFP8>, grid, dim3(64), 0, s, p,
-                               static_cast<int>(a.head_dim), a.scale);
-            break;
+        case kDtF16: launch_generic<kDtF16>(p, hd, a.scale, s); break;
+        case kDtBF16: launch_generic<kDtBF16>(p, hd, a.scale, s); break;
+        case kDtF32: launch_generic<kDtF32>(p, hd, a.scale, s); break;
+        default: launch_generic<kDtFP8>(p, hd, a.scale, s); break;
     }
     KCMM_HIP_CHECK(hipGetLastError(), err);
     return true;

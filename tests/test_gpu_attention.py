@@ -113,12 +113,43 @@ def test_head_block_not_dividing(gpu_lib, monkeypatch, hw, hq, hkv, dtype):
         case.pool.destroy()
 
 
-@pytest.mark.parametrize("hq,hkv,d,bs", [(6, 4, 80, 8), (32, 1, 96, 16), (40, 8, 128, 16)])
+@pytest.mark.parametrize("hq,hkv,d,bs", [(6, 4, 80, 8), (32, 1, 96, 16), (40, 8, 128, 16),
+                                        (4, 2, 66, 3), (8, 8, 256, 5), (3, 3, 8, 16)])
 def test_generic_path_shapes(gpu_lib, hq, hkv, d, bs):
-    # head_dim not in {64,128,256}, Hq not a multiple of Hkv, or group > 16
+    # head_dim not in {64,128,256} (66: not a multiple of 4, element loads),
+    # Hq not a multiple of Hkv, group > 16, block sizes not a multiple of 8
     ctx = [1, 40, 129, 0]
     case = build_decode_case(gpu_lib, batch=4, num_q_heads=hq, kv_heads=hkv, head_dim=d,
                              block_size=bs, ctx_lens=ctx, dtype=KV_F16, seed=4)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_F16, KV_FP8])
+@pytest.mark.parametrize("bs,ctx", [(16, [2500, 1, 1024, 1025, 0, 700]), (1, [1100, 3, 2049])])
+def test_generic_kernel_forced(gpu_lib, monkeypatch, dtype, bs, ctx):
+    """KCMM_ATTN_GENERIC forces the any-shape kernel at the Llama-3-8B head
+    shape: contexts across its 1024-position staging chunks (and exactly at
+    their edges), one-token pages, an empty sequence."""
+    monkeypatch.setenv("KCMM_ATTN_GENERIC", "1")
+    case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=bs, ctx_lens=ctx, dtype=dtype, seed=21 + bs)
+    try:
+        check(case)
+    finally:
+        case.pool.destroy()
+
+
+def test_generic_kernel_many_pairs(gpu_lib, monkeypatch):
+    """1280 (sequence, head) pairs: the any-shape kernel's 256-lane
+    workgroups."""
+    monkeypatch.setenv("KCMM_ATTN_GENERIC", "1")
+    rng = np.random.default_rng(77)
+    ctx = rng.integers(0, 700, size=40)
+    case = build_decode_case(gpu_lib, batch=40, num_q_heads=32, kv_heads=8, head_dim=64,
+                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=77)
     try:
         check(case)
     finally:
