@@ -19,12 +19,16 @@ std::unique_ptr<PageBacking> make_backing(int device, std::string* err);
 
 bool set_device(int device, std::string* err);
 
-// Per-(device, stream, slot) device scratch; grown on demand (slot 0: decode
-// attention partials, 1: GEMM split partials, 2: decode attention segment
-// table, 3: decode layer-step activations, 4: the final norm's output,
-// 5: unused, 6: tiering staging on the null stream, 7: fp8
-// RoPE/append staging, 8: fp8 page-writer row table).  `zero_fill` buffers
-// start zeroed by a fill kernel, and their users leave them zeroed.
+// Per-(device, stream, slot, host thread) device scratch; grown on demand
+// (slot 0: decode attention partials, 1: GEMM split partials, 2: decode
+// attention segment table, 3: decode layer-step activations, 4: the final
+// norm's output, 5: unused, 6: tiering staging on
+// the null stream, 7: fp8 RoPE/append staging, 8: fp8 page-writer row
+// table).  `zero_fill` buffers start zeroed by a fill kernel, and their
+// users leave them zeroed.  Keyed by host thread as well, so a thread that
+// grows a buffer never frees one another thread has been handed.  Growth
+// synchronizes the stream and calls hipMalloc, so it cannot happen under
+// graph capture: run each shape once before capturing it.
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
 bool synchronize_device(int device, std::string* err);

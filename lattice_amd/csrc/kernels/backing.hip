@@ -15,6 +15,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <thread>
 #include <tuple>
 #include <vector>
 
@@ -126,9 +127,12 @@ bool set_device(int device, std::string* err) {
 }
 
 // Device scratch for split-K partials and arrival counters, one buffer per
-// (device, stream, user slot) so launches on different streams never share
-// one.  Grows on demand; the old buffer is released only after its stream has
-// drained; `zero_fill` buffers start zeroed (their users restore zero).
+// (device, stream, user slot, host thread): launches on different streams
+// never share one, and a buffer is only ever handed to the thread that
+// grows it, so a growth (which frees the old buffer once its stream has
+// drained) cannot free a buffer another thread is about to launch with.
+// `zero_fill` buffers start zeroed (their users restore zero).  Buffers of
+// threads that have exited stay allocated until the process ends.
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err) {
     struct Ws {
@@ -136,11 +140,11 @@ bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool 
         size_t bytes = 0;
     };
     static std::mutex mu;
-    static std::map<std::tuple<int, uint64_t, int>, Ws> table;
+    static std::map<std::tuple<int, uint64_t, int, std::thread::id>, Ws> table;
     int dev = 0;
     KCMM_HIP_CHECK(hipGetDevice(&dev), err);
     std::lock_guard<std::mutex> lk(mu);
-    Ws& w = table[std::make_tuple(dev, stream, slot)];
+    Ws& w = table[std::make_tuple(dev, stream, slot, std::this_thread::get_id())];
     if (w.bytes < bytes) {
         if (w.ptr) {
             KCMM_HIP_CHECK(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)), err);

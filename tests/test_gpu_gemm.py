@@ -196,3 +196,47 @@ def test_fp8_weights_split_k(gpu_lib, monkeypatch, splits):
     torch.cuda.synchronize()
     got = O.decode(O.BF16, y.cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
     assert rel_err(got, O.gemm_fp8w_f64(xb, w8, s)) <= 1e-2
+
+
+def test_workspace_two_host_threads(gpu_lib):
+    """Two host threads launch split-K GEMMs on the same (null) stream with
+    growing shapes: each thread has its own split-partial workspace, so one
+    thread growing (and freeing) its buffer never frees the buffer the other
+    is about to launch with.  Every product is checked."""
+    import threading
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    shapes = [(64, n, 4096) for n in (256, 512, 1024, 2048, 3072)]
+    data = {}
+    for m, n, k in shapes:
+        x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+        w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        data[n] = (x, w, (x.float() @ w.float().t()))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(order):
+        try:
+            torch.cuda.set_device(0)
+            for rep in range(3):
+                for n in order:
+                    x, w, ref = data[n]
+                    y = torch.empty((64, n), dtype=torch.bfloat16, device="cuda")
+                    gpu_lib.gemm_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), 64, n, 4096, 0)
+                    torch.cuda.synchronize()
+                    err = float((y.float() - ref).abs().max() / ref.abs().max())
+                    if not err <= 1e-2:
+                        errors.append((n, rep, err))
+        except Exception as e:          # reported below
+            errors.append(repr(e))
+
+    ns = [n for _, n, _ in shapes]
+    threads = [threading.Thread(target=worker, args=(ns,)),
+               threading.Thread(target=worker, args=(ns[::-1],))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert errors == []
