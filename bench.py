@@ -76,6 +76,9 @@ def parse():
                          "16 seqs x 256-token chunk over a shared 1024-token prefix; cfg5: "
                          "fp8-e4m3 pages, B=128, ctx 80%% U[1024,8192] + 20%% U[16384,32768] "
                          "(attention only)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="time the four M=64 projection GEMMs alone, as the layer's component "
+                         "pass calls them (for HBM counter runs under rocprofv3)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
     return ap.parse_args()
@@ -187,6 +190,69 @@ def cpu_baseline_detail(lib, case, args, threads) -> dict:
     return out
 
 
+def gemm_bytes(lib, name, n, k, m):
+    """Algorithmic HBM bytes of one projection call (W, X, Y; O and down also
+    read their residual) and the fp32 split-K partials its plan writes and
+    the reduction reads back (not algorithmic: the cost of the split)."""
+    res = 2 if name in ("o", "down") else 1
+    plan = lib.gemm_plan(m, n, k)
+    return 2.0 * (n * k + m * k + m * n * res), plan
+
+
+def bench_gemm(args):
+    """--gemm-only: the four Llama-3-8B projections at M = 64, each called as
+    in the layer's component pass (QKV and gate/up plain, O and down with the
+    residual added in place), two weight sets alternating so that the weights
+    come from HBM; HIP events per call."""
+    import torch
+    from lattice_amd.bindings import KcmmLibrary
+    lib = KcmmLibrary()
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 2)
+    sets = [{name: (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+             for name, n, k in GEMMS} for _ in range(2)]
+    x = {k: torch.randn((B, k), generator=g, device=dev).to(torch.bfloat16) for k in (HIDDEN, INTER)}
+    y = torch.empty((B, 2 * INTER), dtype=torch.bfloat16, device=dev)
+    hidden = torch.randn((B, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
+    sp = torch.cuda.current_stream().cuda_stream
+    if args.calib_copy:
+        src = torch.empty(128 << 20, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        dst.copy_(src)                               # 256 MiB read + 256 MiB written
+        torch.cuda.synchronize()
+        del src, dst
+
+    def call(name, n, k, i):
+        w = sets[i % 2][name].data_ptr()
+        if name in ("o", "down"):
+            lib.gemm_bf16_add(x[k].data_ptr(), w, hidden.data_ptr(), hidden.data_ptr(), B, n, k, sp)
+        else:
+            lib.gemm_bf16(x[k].data_ptr(), w, y.data_ptr(), B, n, k, sp)
+
+    out = {}
+    for name, n, k in GEMMS:
+        for i in range(args.warmup):
+            call(name, n, k, i)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            ev[i].record()
+            call(name, n, k, i)
+        ev[-1].record()
+        torch.cuda.synchronize()
+        us = float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)])) * 1e3
+        alg, plan = gemm_bytes(lib, name, n, k, B)
+        out[name] = {"us": round(us, 2), "algorithmic_bytes": int(alg), "plan": plan,
+                     "gbs": round(alg / us / 1e3, 1),
+                     "frac_of_hbm_peak": round(alg / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"{name}: {us:.2f} us, plan {plan}")
+    print(json.dumps({"metric": "M=64 projection GEMM time", "unit": "us", "steps": args.steps,
+                      "warmup": args.warmup, "m": B, "gemms": out}), flush=True)
+
+
 def bench_prefill(args):
     """Cfg3: causal chunked prefill over shared-prefix pages; MFMA-bound."""
     import torch
@@ -238,6 +304,8 @@ def main():
         sys.exit(2)
     if args.config == "cfg3":
         return bench_prefill(args)
+    if args.gemm_only:
+        return bench_gemm(args)
     import torch
     from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, KcmmLibrary
     from lattice_amd.workload import build_decode_case, rope_inv_freq
@@ -601,7 +669,7 @@ def main():
         result["t_logits_us"] = round(extra["logits"] * 1e3, 2)
         result["t_layer_single_call_us"] = round(extra["layer_step"] * 1e3, 2)
         result["t_layer_components_us"] = {n: round(per[n] * 1e3, 2) for n in names}
-        def gemm_report(times_ms, M, residual):
+        def gemm_report(times_ms, M, residual, plan=True):
             gem = {}
             for name, n, k in GEMMS:
                 s = times_ms[name] / 1e3
@@ -615,12 +683,18 @@ def main():
                              "gbs": round(byts / s / 1e9, 1),
                              "frac_of_min_roofline": round(flops / s / ceiling, 4),
                              "frac_of_mfma_peak": round(flops / s / (BF16_PEAK_TFLOPS * 1e12), 4)}
+                if plan:
+                    # split-K partials: written by the GEMM, read back by the reduction
+                    p = lib.gemm_plan(M, n, k)
+                    gem[name]["splits"] = p["splits"]
+                    gem[name]["partial_bytes"] = 2 * p["partial_bytes"]
+                    gem[name]["gbs_incl_partials"] = round((byts + 2 * p["partial_bytes"]) / s / 1e9, 1)
             return gem
         result["gemm_m64"] = gemm_report(per, B, True)
         result["gemm_m256"] = gemm_report(m256, 256, False)
         result["gemm_m256"]["backend"] = "tiled MFMA kernel (gemm_tiled.hip)"
         result["gemm_m256_stream_kernel"] = gemm_report(m256_stream, 256, False)
-        result["gemm_m256_torch_reference"] = gemm_report(m256_torch, 256, False)
+        result["gemm_m256_torch_reference"] = gemm_report(m256_torch, 256, False, plan=False)
         result["tiering"] = tiering_report(lib, args)
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))

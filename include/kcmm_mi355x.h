@@ -212,6 +212,17 @@ int kcmm_gemm_bf16_on_stream(uint64_t x_ptr, uint64_t w_ptr, uint64_t y_ptr,
                              uint32_t m, uint32_t n, uint32_t k,
                              uint64_t stream_ptr);
 
+/** How kcmm_gemm_bf16_on_stream (fp8_weights = 0) or
+ *  kcmm_gemm_fp8w_bf16_on_stream (fp8_weights = 1) runs a product of this
+ *  shape under the current KCMM_GEMM_* settings, written to out[4]: kernel
+ *  (0 weight-stream, 1 LDS-tiled), K splits, tiling of the tiled kernel (-1
+ *  otherwise), bytes of fp32 split partials written and read back by the
+ *  reduction (0 without a split).  No reference counterpart (the reference's
+ *  cuBLAS call, runtime.rs:17-41, exposes no plan); for sizing workspaces and
+ *  for counting a product's HBM bytes.  Host-only, no device work.  0 on
+ *  success, -1 on a shape the kernels do not take. */
+int kcmm_gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t fp8_weights, int64_t* out);
+
 /** Y[m][n] = X[m][k] * (W8[n][k] * wscale[n])^T with fp8-e4m3 (OCP e4m3fn)
  *  weights W8 and one fp32 scale per weight row: the projection with
  *  weight-only fp8 quantization (half the weight bytes a decode step

@@ -168,6 +168,7 @@ SIGNATURES = {
     "kcmm_copy_blocks_device_on_stream": ([_P, _U64, _U64, _U32, _U64], C.c_int),
     "kcmm_gemm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_gemm_fp8w_bf16_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
+    "kcmm_gemm_plan": ([_U32, _U32, _U32, _U32, C.POINTER(C.c_int64)], C.c_int),
     "kcmm_gemm_bf16_add_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_rmsnorm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, C.c_float, _U64], C.c_int),
     "kcmm_silu_mul_bf16_on_stream": ([_U64, _U64, _U32, _U32, _U64], C.c_int),
@@ -228,6 +229,15 @@ class KcmmLibrary:
     def gemm_bf16(self, x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr=0) -> None:
         if self.lib.kcmm_gemm_bf16_on_stream(x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr) != 0:
             raise KcmmError("kcmm_gemm_bf16_on_stream failed")
+
+    def gemm_plan(self, m, n, k, fp8_weights=False) -> dict:
+        """How a plain product of this shape runs: kernel ('stream' / 'tiled'),
+        K splits, tiling, bytes of fp32 split partials."""
+        out = (C.c_int64 * 4)()
+        if self.lib.kcmm_gemm_plan(m, n, k, int(bool(fp8_weights)), out) != 0:
+            raise KcmmError("kcmm_gemm_plan failed")
+        return {"kernel": ("stream", "tiled")[out[0]], "splits": int(out[1]), "tile": int(out[2]),
+                "partial_bytes": int(out[3])}
 
     def gemm_fp8w_bf16(self, x_ptr, w8_ptr, wscale_ptr, y_ptr, m, n, k, stream_ptr=0) -> None:
         """Y = X (W8 diag(wscale))^T: fp8-e4m3 weights with an fp32 scale per row."""

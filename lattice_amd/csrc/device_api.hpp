@@ -120,6 +120,18 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
 // (kernels/gemm_tiled.hip); n % 64 == 0, k % 64 == 0.
 bool gemm_bf16_tiled(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
                      uint64_t stream, uint64_t residual, std::string* err);
+void gemm_tiled_plan(uint32_t m, uint32_t n, uint32_t k, int* splits, int* tile);
+
+// How a plain product of this shape runs (under the current KCMM_GEMM_*
+// settings): kernel 0 = weight-stream, 1 = LDS-tiled; K splits; tiling (tiled
+// kernel only, else -1); bytes of fp32 split partials written (and read
+// back by the reduction), 0 without a split.
+struct GemmPlan {
+    int kernel = 0, splits = 1, tile = -1;
+    uint64_t partial_bytes = 0;
+};
+bool gemm_plan(uint32_t m, uint32_t n, uint32_t k, bool fp8_weights, GemmPlan* plan,
+               std::string* err);
 // Y = X (W8 diag(wscale))^T: fp8-e4m3 weights W8 [n][k] with an fp32 scale per
 // weight row, bf16 activations and result, fp32 accumulate (weight-stream
 // kernel; the weights are converted to bf16 exactly in registers).

@@ -1023,6 +1023,21 @@ int kcmm_gemm_bf16_on_stream(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uin
     return 0;
 }
 
+int kcmm_gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t fp8_weights, int64_t* out) {
+    if (out == nullptr) return -1;
+    std::string err;
+    kcmm::dev::GemmPlan plan;
+    if (!kcmm::dev::gemm_plan(m, n, k, fp8_weights != 0, &plan, &err)) {
+        std::fprintf(stderr, "kcmm_gemm_plan: %s\n", err.c_str());
+        return -1;
+    }
+    out[0] = plan.kernel;
+    out[1] = plan.splits;
+    out[2] = plan.tile;
+    out[3] = static_cast<int64_t>(plan.partial_bytes);
+    return 0;
+}
+
 int kcmm_gemm_fp8w_bf16_on_stream(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32_t m,
                                   uint32_t n, uint32_t k, uint64_t stream) {
     if (x == 0 || w8 == 0 || wscale == 0 || y == 0) return -1;

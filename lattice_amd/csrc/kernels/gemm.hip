@@ -583,6 +583,25 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
     return true;
 }
 
+bool gemm_plan(uint32_t m, uint32_t n, uint32_t k, bool fp8_weights, GemmPlan* plan,
+               std::string* err) {
+    if (!shape_ok(m, n, k, err)) return false;
+    *plan = GemmPlan{};
+    if (!fp8_weights && m > 128 && env_int("KCMM_GEMM_TILED", 1) != 0) {
+        plan->kernel = 1;
+        gemm_tiled_plan(m, n, k, &plan->splits, &plan->tile);
+    } else {
+        plan->kernel = 0;
+        plan->splits = splits_for(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                                  fp8_weights);
+        plan->tile = -1;
+    }
+    plan->partial_bytes = plan->splits > 1
+                              ? static_cast<uint64_t>(plan->splits) * m * n * sizeof(float)
+                              : 0;
+    return true;
+}
+
 bool gemm_fp8w_bf16(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32_t m, uint32_t n,
                     uint32_t k, uint64_t stream, std::string* err) {
     if (!shape_ok(m, n, k, err)) return false;

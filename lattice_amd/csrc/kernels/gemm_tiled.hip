@@ -314,6 +314,12 @@ TiledConfig choose(int M, int N, int K) {
 
 namespace dev {
 
+void gemm_tiled_plan(uint32_t m, uint32_t n, uint32_t k, int* splits, int* tile) {
+    const TiledConfig c = choose(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k));
+    *splits = c.splits;
+    *tile = c.id;
+}
+
 bool gemm_bf16_tiled(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
                      uint64_t stream, uint64_t residual, std::string* err) {
     if (m == 0 || n % 64 != 0 || k % 64 != 0) {

@@ -191,6 +191,13 @@ bool gemm_split_reduce_launch(const float*, uint16_t*, const uint16_t*, int, int
                               std::string* err) {
     return no_device(err);
 }
+void gemm_tiled_plan(uint32_t, uint32_t, uint32_t, int* splits, int* tile) {
+    *splits = 1;
+    *tile = -1;
+}
+bool gemm_plan(uint32_t, uint32_t, uint32_t, bool, GemmPlan*, std::string* err) {
+    return no_device(err);
+}
 // The host-check backing has no page memory (fake region addresses), so the
 // tiering moves carry no bytes here: they succeed, and the CPU tier checks
 // the bookkeeping around them (victims, swap slots, locations, new pages).
