@@ -240,3 +240,18 @@ def test_workspace_two_host_threads(gpu_lib):
         t.join(timeout=120)
     assert not any(t.is_alive() for t in threads)
     assert errors == []
+
+
+def test_gemm_plan(gpu_lib, monkeypatch):
+    """kcmm_gemm_plan reports what the product entry points run."""
+    p = gpu_lib.gemm_plan(64, 6144, 4096)
+    assert p["kernel"] == "stream" and p["tile"] == -1
+    assert p["partial_bytes"] == (p["splits"] * 64 * 6144 * 4 if p["splits"] > 1 else 0)
+    assert gpu_lib.gemm_plan(256, 6144, 4096)["kernel"] == "tiled"
+    assert gpu_lib.gemm_plan(256, 6144, 4096, fp8_weights=True)["kernel"] == "stream"
+    monkeypatch.setenv("KCMM_GEMM_SPLITS", "2")
+    assert gpu_lib.gemm_plan(64, 512, 4096)["splits"] == 2
+    monkeypatch.setenv("KCMM_GEMM_TILED", "0")
+    assert gpu_lib.gemm_plan(256, 6144, 4096)["kernel"] == "stream"
+    with pytest.raises(Exception):
+        gpu_lib.gemm_plan(64, 100, 4096)          # n not a multiple of 64
