@@ -54,6 +54,7 @@ CTX_LO, CTX_HI = 512, 4096
 MODEL_LAYERS = 32
 HIDDEN, INTER, VOCAB = 4096, 14336, 128256
 KV_BF16_CODE = 1
+KV_FP8_CODE = 2
 ROPE_THETA, RMS_EPS = 500000.0, 1e-5      # Llama-3-8B config.json
 BEAM_WIDTH = 4                             # configs[4]
 GEMMS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
@@ -259,25 +260,33 @@ def bench_prefill(args):
     from lattice_amd.bindings import KcmmLibrary
     from lattice_amd.workload import build_prefix_shared_case
     lib = KcmmLibrary()
-    case = build_prefix_shared_case(lib, batch=16, prefix_tokens=1024, suffix_tokens=256,
-                                    chunk=256, num_q_heads=HQ, kv_heads=HKV, head_dim=D,
-                                    block_size=BS, dtype=KV_BF16_CODE, num_layers=args.layers,
-                                    seed=args.seed)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
-    for i in range(args.warmup):
-        case.run(layer=i % args.layers, stream_ptr=sp)
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    ev[0].record(stream)
-    for i in range(args.steps):
-        case.run(layer=i % args.layers, stream_ptr=sp)
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    ms = float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]))
-    flops = case.flops()
+
+    def timed(dtype):
+        case = build_prefix_shared_case(lib, batch=16, prefix_tokens=1024, suffix_tokens=256,
+                                        chunk=256, num_q_heads=HQ, kv_heads=HKV, head_dim=D,
+                                        block_size=BS, dtype=dtype, num_layers=args.layers,
+                                        seed=args.seed)
+        for i in range(args.warmup):
+            case.run(layer=i % args.layers, stream_ptr=sp)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        ev[0].record(stream)
+        for i in range(args.steps):
+            case.run(layer=i % args.layers, stream_ptr=sp)
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        ms = float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]))
+        flops = case.flops()
+        case.pool.destroy()
+        return ms, flops
+
+    ms, flops = timed(KV_BF16_CODE)
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"prefill per-call ms: {ms:.4f}, {flops / 1e9:.1f} GFLOP")
+    ms8, _ = timed(KV_FP8_CODE)
+    log(f"prefill per-call ms with fp8-e4m3 pages: {ms8:.4f}")
     result = {
         "metric": "chunked prefill attention TFLOP/s (% bf16 MFMA peak), 1 GPU",
         "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -290,9 +299,11 @@ def bench_prefill(args):
                      "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": None},
         "gflop_per_call": round(flops / 1e9, 2),
+        # the same chunk over fp8-e4m3 pages (dequantized to bf16 in LDS by
+        # the same MFMA kernel): half the K/V bytes, the same flops
+        "fp8_pages": {"ms": round(ms8, 4), "tflops": round(flops / (ms8 * 1e-3) / 1e12, 1)},
         "cpu_baseline": None,
     }
-    case.pool.destroy()
     print(json.dumps(result), flush=True)
 
 

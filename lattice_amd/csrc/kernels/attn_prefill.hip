@@ -8,13 +8,15 @@
 // p = seq_lens[b] - len_b + i and attends to keys 0..p.  q/out rows are
 // [qsl[b] + i][Hq][D]; GQA head map g = h / (Hq/Hkv).  Accumulation is fp32.
 //
-// MI355X design (flash attention over LDS-staged pages):
-//  * workgroup = 4 waves on one (sequence b, kv head g, block of query
-//    tokens); wave w owns 64 MFMA columns (4 blocks of 16), a column being
-//    one (query token, head of the GQA group) pair, heads fastest, with its
-//    Q rows held in registers for the whole key loop;
+// MI355X design (flash attention over LDS-staged pages; f16 / bf16 pages,
+// and fp8-e4m3 pages at head_dim 128, dequantized to bf16 as their rows are
+// stored to LDS):
+//  * workgroup = 8 waves (2 per SIMD) on one (sequence b, kv head g, block
+//    of query tokens); wave w owns 32 MFMA columns (2 blocks of 16), a
+//    column being one (query token, head of the GQA group) pair, heads
+//    fastest, with its Q rows held in registers for the whole key loop;
 //  * the workgroup walks 32-key tiles up to its last query's position: the
-//    256 threads gather a tile's K and V rows (16 B each, coalesced per row)
+//    512 threads gather a tile's K and V rows (16 B each, coalesced per row)
 //    into registers one tile ahead, store them to a double-buffered,
 //    XOR-swizzled LDS tile, and every wave computes from LDS, so each key
 //    row leaves L2 once per workgroup instead of once per wave;
@@ -131,7 +133,14 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                        const int32_t* __restrict__ sl, const int32_t* __restrict__ qsl,
                        const uint64_t* __restrict__ offs) {
     using S = Shape<D, KT>;
-    constexpr int KC = S::KC, DB = S::DB, CH = S::CH;
+    constexpr int KC = S::KC, DB = S::DB;
+    // fp8-e4m3 pages: rows are gathered as 8-bit codes (half the bytes) and
+    // dequantized with their page's scale to bf16 as they are stored to LDS;
+    // from there on the tile is a bf16 tile (MFMA, q and out in bf16)
+    constexpr bool F8 = DT == kDtFP8;
+    constexpr int MDT = F8 ? kDtBF16 : DT;
+    constexpr int EB = F8 ? 1 : 2;                // bytes per K/V element in the page
+    constexpr int CH = D * EB / 16;               // 16-byte chunks per key row in the page
     constexpr int NKB = KT / 16;         // 16-key blocks of S^T per tile
     constexpr int NKS = KT / 32;         // 32-key k-steps of P V per tile
     constexpr int NT = NW * 64;          // threads
@@ -233,7 +242,7 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     const int tc = tid % CH;
     const int32_t* row = bt + static_cast<size_t>(b) * p.mbps;
     const int bmask = (1 << p.bs_shift) - 1;
-    const uint32_t head_off = static_cast<uint32_t>(g * D * 2 + tc * 16);
+    const uint32_t head_off = static_cast<uint32_t>(g * D * EB + tc * 16);
     auto key_tok = [&](int kt, int i) { return min(kt * KT + c_key(i), L - 1); };
     auto page_entry = [&](int kt, int i) { return row[key_tok(kt, i) >> p.bs_shift]; };
     // Loaded values pass through an empty asm where they are used, so the
@@ -244,14 +253,19 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         return offs[entry];
     };
     u32x4 gch[CPT];
+    float gsc[F8 ? CPT : 1];   // fp8: the chunk's page scale for kv head g
     auto gather = [&](int kt, const uint64_t (&pg)[CPT]) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             uint64_t page = pg[i];
             asm volatile("" : "+v"(page));
+            const uint8_t* reg = c_tensor(i) ? vreg : kreg;
             const uint64_t a =
                 page * 2ull + (__umul24(key_tok(kt, i) & bmask, p.row_bytes) + head_off);
-            gch[i] = *reinterpret_cast<const u32x4*>((c_tensor(i) ? vreg : kreg) + a);
+            gch[i] = *reinterpret_cast<const u32x4*>(reg + a);
+            if constexpr (F8)
+                gsc[i] = *reinterpret_cast<const float*>(reg + page * 2ull +
+                                                         static_cast<uint32_t>(p.data_bytes + g * 4));
         }
     };
     auto store_tile = [&](int buf) {
@@ -259,13 +273,34 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         for (int i = 0; i < CPT; ++i) {
             const int k = c_key(i);
             const int off = c_tensor(i) ? S::KTILE + k * S::VROW : k * S::KROW;
-            *reinterpret_cast<u32x4*>(&lds[buf * S::BUF + off + tc * 16]) = gch[i];
+            if constexpr (F8) {
+                // 16 codes -> 16 bf16 = bf16(e4m3 value * scale), 32 bytes
+                u32x4 lo, hi;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const auto a = __builtin_amdgcn_cvt_pk_f32_fp8(gch[i][w], false);
+                    const auto b = __builtin_amdgcn_cvt_pk_f32_fp8(gch[i][w], true);
+                    const uint32_t x = pack2<kDtBF16>(a[0] * gsc[i], a[1] * gsc[i]);
+                    const uint32_t y = pack2<kDtBF16>(b[0] * gsc[i], b[1] * gsc[i]);
+                    if (w < 2) {
+                        lo[2 * w] = x;
+                        lo[2 * w + 1] = y;
+                    } else {
+                        hi[2 * w - 4] = x;
+                        hi[2 * w - 3] = y;
+                    }
+                }
+                *reinterpret_cast<u32x4*>(&lds[buf * S::BUF + off + tc * 32]) = lo;
+                *reinterpret_cast<u32x4*>(&lds[buf * S::BUF + off + tc * 32 + 16]) = hi;
+            } else {
+                *reinterpret_cast<u32x4*>(&lds[buf * S::BUF + off + tc * 16]) = gch[i];
+            }
         }
     };
 
     // l (the softmax denominator) accumulates on the MFMA as ones x P^T: every
     // row of lsum[cb] holds the column sums of the 16-bit P used for O
-    const u32x4 ones = DT == kDtF16 ? u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}
+    const u32x4 ones = MDT == kDtF16 ? u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}
                                     : u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
     float m_run[NCB];
     f32x4 lsum[NCB];
@@ -302,7 +337,7 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                 s[cb][hb] = f32x4{0, 0, 0, 0};
 #pragma unroll
                 for (int kc = 0; kc < KC; ++kc)
-                    s[cb][hb] = mfma16<DT>(kf[kc], qf[cb][kc], s[cb][hb]);
+                    s[cb][hb] = mfma16<MDT>(kf[kc], qf[cb][kc], s[cb][hb]);
             }
         }
         if (kt * KT + KT - 1 > qmin) {
@@ -357,8 +392,8 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                         pv[4 * h + r] =
                             __builtin_amdgcn_exp2f(fmaf(s[cb][2 * j + h][r], p.scale_log2, nmu));
 #pragma unroll
-                for (int i = 0; i < 4; ++i) pf[cb][j][i] = pack2<DT>(pv[2 * i], pv[2 * i + 1]);
-                lsum[cb] = mfma16<DT>(ones, pf[cb][j], lsum[cb]);
+                for (int i = 0; i < 4; ++i) pf[cb][j][i] = pack2<MDT>(pv[2 * i], pv[2 * i + 1]);
+                lsum[cb] = mfma16<MDT>(ones, pf[cb][j], lsum[cb]);
             }
         }
     };
@@ -377,7 +412,7 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
             for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
                 for (int db = 0; db < DB; ++db)
-                    acc[cb][db] = mfma16<DT>(vf[db], pf[cb][j], acc[cb][db]);
+                    acc[cb][db] = mfma16<MDT>(vf[db], pf[cb][j], acc[cb][db]);
         }
     };
 
@@ -437,8 +472,8 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 u32x2 w;
-                w[0] = pack2<DT>(acc[cb][db][0] * inv, acc[cb][db][1] * inv);
-                w[1] = pack2<DT>(acc[cb][db][2] * inv, acc[cb][db][3] * inv);
+                w[0] = pack2<MDT>(acc[cb][db][0] * inv, acc[cb][db][1] * inv);
+                w[1] = pack2<MDT>(acc[cb][db][2] * inv, acc[cb][db][3] * inv);
                 *reinterpret_cast<u32x2*>(o + 16 * db) = w;
             }
         }
@@ -598,9 +633,11 @@ bool attn_prefill(const AttnPrefillArgs& a, std::string* err) {
     const bool mfma_dim = a.head_dim == 64 || a.head_dim == 128;
     const bool pow2_bs = (1u << p.bs_shift) == a.block_size;
     // (the MFMA kernel takes column maxima of the raw scores: scale > 0)
-    if ((a.dtype == kDtF16 || a.dtype == kDtBF16) && mfma_group && mfma_dim && pow2_bs &&
-        a.scale > 0.0f &&
+    const bool mfma_type = a.dtype == kDtF16 || a.dtype == kDtBF16 ||
+                           (a.dtype == kDtFP8 && a.head_dim == 128);
+    if (mfma_type && mfma_group && mfma_dim && pow2_bs && a.scale > 0.0f &&
         std::getenv("KCMM_ATTN_GENERIC") == nullptr) {
+        if (a.dtype == kDtFP8) return launch_group<kDtFP8, 128>(a, p, s, err);
         if (a.dtype == kDtF16)
             return a.head_dim == 64 ? launch_group<kDtF16, 64>(a, p, s, err)
                                     : launch_group<kDtF16, 128>(a, p, s, err);

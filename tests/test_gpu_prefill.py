@@ -90,10 +90,43 @@ def test_dtypes_and_block_sizes(gpu_lib, dtype, bs):
         case.pool.destroy()
 
 
-@pytest.mark.parametrize("dtype,hq,hkv,d", [(KV_FP8, 32, 8, 128), (KV_BF16, 12, 4, 80),
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (32, 4), (32, 2)])
+@pytest.mark.parametrize("bs", [16, 8, 32])
+def test_fp8_pages_on_mfma(gpu_lib, hq, hkv, bs):
+    """fp8-e4m3 pages at head_dim 128 take the MFMA kernel: codes gathered,
+    dequantized with their page's per-kv-head scale to bf16 in LDS; against
+    the oracle on the same pages (3e-2), every GQA group, three block sizes
+    (a 32-key tile spans 1, 2 or 4 pages, each with its own scale)."""
+    case = build_decode_case(gpu_lib, batch=len(CTX), num_q_heads=hq, kv_heads=hkv, head_dim=128,
+                             block_size=bs, ctx_lens=CTX, dtype=KV_FP8, seed=hq + bs)
+    try:
+        got, ref = run_prefill(case, LENS, hq, seed=hq * bs)
+        err = rel_err(got, ref)
+        print(f"prefill fp8 mfma G={hq // hkv} bs={bs} err={err:.3e}", flush=True)
+        assert np.isfinite(got).all() and err <= TOL[KV_FP8]
+    finally:
+        case.pool.destroy()
+
+
+def test_fp8_mfma_matches_generic(gpu_lib, monkeypatch):
+    """The fp8 MFMA path and the generic kernel (KCMM_ATTN_GENERIC) agree
+    within the fp8 tolerance on the same pages and queries."""
+    case = build_decode_case(gpu_lib, batch=len(CTX), num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=CTX, dtype=KV_FP8, seed=31)
+    try:
+        got, ref = run_prefill(case, LENS, 32, seed=32)
+        monkeypatch.setenv("KCMM_ATTN_GENERIC", "1")
+        gen, _ = run_prefill(case, LENS, 32, seed=32)
+        assert rel_err(got, gen) <= TOL[KV_FP8] and rel_err(gen, ref) <= TOL[KV_FP8]
+    finally:
+        case.pool.destroy()
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d", [(KV_FP8, 32, 8, 64), (KV_BF16, 12, 4, 80),
                                             (KV_F16, 24, 8, 64)])
 def test_generic_path(gpu_lib, dtype, hq, hkv, d):
-    """fp8 pages, head_dim 80 and a group of 3 run on the generic kernel."""
+    """fp8 pages at head_dim 64, head_dim 80 and a group of 3 run on the
+    generic kernel."""
     ctx, lens = [40, 9, 77], [13, 9, 30]
     case = build_decode_case(gpu_lib, batch=3, num_q_heads=hq, kv_heads=hkv, head_dim=d,
                              block_size=16, ctx_lens=ctx, dtype=dtype, seed=d)
@@ -145,14 +178,15 @@ def test_more_queries_than_tokens_gives_zero_rows(gpu_lib):
         case.pool.destroy()
 
 
-def test_shared_prefix_chunked_prefill(gpu_lib):
+@pytest.mark.parametrize("dtype", [KV_BF16, KV_FP8])
+def test_shared_prefix_chunked_prefill(gpu_lib, dtype):
     """BASELINE configs[2] layout at reduced batch: sequences share refcounted
     prefix pages (kcmm_share_prefix) and own their suffix; the chunk is the
-    suffix.  Regions are read back for the oracle."""
+    suffix.  Regions are read back for the oracle.  bf16 and fp8 pages."""
     import torch
     case = build_prefix_shared_case(gpu_lib, batch=4, prefix_tokens=1024, suffix_tokens=256,
                                     chunk=256, num_q_heads=32, kv_heads=8, head_dim=128,
-                                    block_size=16, dtype=KV_BF16, seed=24)
+                                    block_size=16, dtype=dtype, seed=24)
     try:
         pre = case.block_tables[:, :64]
         assert (pre == pre[0]).all()                       # same physical prefix pages
@@ -165,12 +199,13 @@ def test_shared_prefix_chunked_prefill(gpu_lib):
         kreg = memcpy_dtoh(case.pool.va_k(0), mapped)
         vreg = memcpy_dtoh(case.pool.va_v(0), mapped)
         got = O.decode(O.BF16, case.dev["out"].cpu().view(torch.int16).numpy().view(np.uint16))
-        ref = O.attn_prefill_f64(KV_BF16, case.q_bits, kreg, vreg, case.block_tables,
+        eb = 1 if dtype == KV_FP8 else 2
+        ref = O.attn_prefill_f64(dtype, case.q_bits, kreg, vreg, case.block_tables,
                                  case.seq_lens, case.qsl, case.offsets_f16, 32, 8, 128, 16,
-                                 8 * 128 * 2, 8 * 128 * 2 * 16, 1 / math.sqrt(128))
+                                 8 * 128 * eb, 8 * 128 * eb * 16, 1 / math.sqrt(128))
         err = rel_err(got.astype(np.float64), ref)
-        print(f"shared-prefix prefill err={err:.3e}", flush=True)
-        assert np.isfinite(got).all() and err <= TOL[KV_BF16]
+        print(f"shared-prefix prefill dtype={dtype} err={err:.3e}", flush=True)
+        assert np.isfinite(got).all() and err <= TOL[dtype]
     finally:
         case.pool.destroy()
 
