@@ -197,6 +197,58 @@ int kcmm_copy_blocks_device_on_stream(kcmm_pool_t *pool, uint64_t pairs_ptr,
                                       uint64_t block_offsets_f16_ptr,
                                       uint32_t num_pairs, uint64_t stream_ptr);
 
+/* ---- prefix cache ------------------------------------------------------- */
+
+/* The reference's prefix-sharing manager (src/kcmm/sharing.rs:9-65: content
+ * hash -> the blocks of a prefix, reference counted for sharing; a
+ * placeholder there) over the copy-on-write pages above.  Keys are chained
+ * content hashes of full blocks; every cache entry holds one reference on its
+ * block, so a cached prefix outlives the sequence that registered it and a
+ * later request with the same tokens attaches the same pages instead of
+ * recomputing them.  Cached blocks are full and shared: writes into them are
+ * refused like writes into any shared block. */
+
+/** Chained content hashes of the full blocks of tokens[0..n_tokens): hash i
+ *  = FNV-1a-64 over the 8 little-endian bytes of hash i-1 (seed for i = 0)
+ *  followed by the 4 little-endian bytes of each of the block's block_size
+ *  token ids.  Writes min(n_tokens / block_size, max_hashes) hashes to
+ *  out_hashes and their count to *count.  Host-only.  -1 on null pointers or
+ *  block_size 0. */
+int kcmm_prefix_hash_blocks(const int32_t *tokens, uint32_t n_tokens, uint32_t block_size,
+                            uint64_t seed, uint64_t *out_hashes, uint32_t max_hashes,
+                            uint32_t *count);
+
+/** Cache the first num_blocks blocks of seq_idx's table under
+ *  hashes[0..num_blocks).  Only full blocks: num_blocks * block_size must not
+ *  exceed the sequence's seq_len.  A key already cached is left as it is (the
+ *  first registration wins); each new entry takes one reference on its block.
+ *  *out_added = entries created.  -1 on an unknown sequence, too many blocks,
+ *  a partial block or a block not in use (nothing cached then). */
+int kcmm_prefix_register(kcmm_pool_t *pool, uint32_t seq_idx, const uint64_t *hashes,
+                         uint32_t num_blocks, uint32_t *out_added);
+
+/** The longest cached run hashes[0..m): block ids to out_blocks[0..m)
+ *  (out_blocks may be NULL), m to *out_matched.  Marks the run as used now
+ *  (eviction order).  No reference changes. */
+int kcmm_prefix_match(kcmm_pool_t *pool, const uint64_t *hashes, uint32_t num_blocks,
+                      uint32_t *out_blocks, uint32_t *out_matched);
+
+/** kcmm_prefix_match, then append the m matched blocks to dst_seq's table
+ *  with one reference each (as kcmm_share_prefix).  out_blocks may be NULL.
+ *  The caller sets dst_seq's seq_len; blocks swapped out to host memory must
+ *  be restored before attention reads them. */
+int kcmm_prefix_attach(kcmm_pool_t *pool, uint32_t dst_seq, const uint64_t *hashes,
+                       uint32_t num_blocks, uint32_t *out_blocks, uint32_t *out_matched);
+
+/** Drop up to max_entries cache entries, least recently used first (the
+ *  deepest first among entries registered or matched together), releasing
+ *  each entry's reference (a block no sequence holds is freed).
+ *  UINT32_MAX drops every entry.  *out_evicted = entries dropped. */
+int kcmm_prefix_evict(kcmm_pool_t *pool, uint32_t max_entries, uint32_t *out_evicted);
+
+/** Number of cache entries (0 for NULL). */
+uint32_t kcmm_prefix_cached_blocks(kcmm_pool_t *pool);
+
 /* ---- projection GEMM ---------------------------------------------------- */
 
 /** Y[m][n] = X[m][k] * W[n][k]^T (row major, the HF Linear layout used by

@@ -169,6 +169,12 @@ SIGNATURES = {
     "kcmm_gemm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_gemm_fp8w_bf16_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_gemm_plan": ([_U32, _U32, _U32, _U32, C.POINTER(C.c_int64)], C.c_int),
+    "kcmm_prefix_hash_blocks": ([_P, _U32, _U32, _U64, _P, _U32, C.POINTER(_U32)], C.c_int),
+    "kcmm_prefix_register": ([_P, _U32, _P, _U32, C.POINTER(_U32)], C.c_int),
+    "kcmm_prefix_match": ([_P, _P, _U32, _P, C.POINTER(_U32)], C.c_int),
+    "kcmm_prefix_attach": ([_P, _U32, _P, _U32, _P, C.POINTER(_U32)], C.c_int),
+    "kcmm_prefix_evict": ([_P, _U32, C.POINTER(_U32)], C.c_int),
+    "kcmm_prefix_cached_blocks": ([_P], _U32),
     "kcmm_gemm_bf16_add_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_rmsnorm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, C.c_float, _U64], C.c_int),
     "kcmm_silu_mul_bf16_on_stream": ([_U64, _U64, _U32, _U32, _U64], C.c_int),
@@ -229,6 +235,18 @@ class KcmmLibrary:
     def gemm_bf16(self, x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr=0) -> None:
         if self.lib.kcmm_gemm_bf16_on_stream(x_ptr, w_ptr, y_ptr, m, n, k, stream_ptr) != 0:
             raise KcmmError("kcmm_gemm_bf16_on_stream failed")
+
+    def prefix_hash_blocks(self, tokens, block_size, seed=0):
+        """Chained content hashes of the full blocks of a token sequence
+        (numpy uint64 array)."""
+        import numpy as np
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros(max(len(t) // block_size, 1), dtype=np.uint64)
+        cnt = _U32(0)
+        if self.lib.kcmm_prefix_hash_blocks(t.ctypes.data if t.size else None, t.size, block_size,
+                                            seed, out.ctypes.data, out.size, C.byref(cnt)) != 0:
+            raise KcmmError("kcmm_prefix_hash_blocks failed")
+        return out[: cnt.value]
 
     def gemm_plan(self, m, n, k, fp8_weights=False) -> dict:
         """How a plain product of this shape runs: kernel ('stream' / 'tiled'),
@@ -604,6 +622,44 @@ class KcmmPool:
 
     def refcount(self, blk: int) -> int:
         return self.lib.kcmm_get_block_refcount(self.handle, blk)
+
+    # ---- prefix cache (kcmm_prefix_*) ----
+    @staticmethod
+    def _hashes(hashes):
+        import numpy as np
+        h = np.ascontiguousarray(hashes, dtype=np.uint64)
+        return h, (h.ctypes.data if h.size else None)
+
+    def prefix_register(self, seq: int, hashes) -> int:
+        h, hp = self._hashes(hashes)
+        added = C.c_uint32(0)
+        self._check(self.lib.kcmm_prefix_register(self.handle, seq, hp, h.size, C.byref(added)),
+                    "kcmm_prefix_register")
+        return added.value
+
+    def prefix_match(self, hashes) -> list[int]:
+        h, hp = self._hashes(hashes)
+        out = (C.c_uint32 * max(1, h.size))()
+        m = C.c_uint32(0)
+        self._check(self.lib.kcmm_prefix_match(self.handle, hp, h.size, out, C.byref(m)),
+                    "kcmm_prefix_match")
+        return list(out[: m.value])
+
+    def prefix_attach(self, dst: int, hashes) -> list[int]:
+        h, hp = self._hashes(hashes)
+        out = (C.c_uint32 * max(1, h.size))()
+        m = C.c_uint32(0)
+        self._check(self.lib.kcmm_prefix_attach(self.handle, dst, hp, h.size, out, C.byref(m)),
+                    "kcmm_prefix_attach")
+        return list(out[: m.value])
+
+    def prefix_evict(self, n: int = 0xFFFFFFFF) -> int:
+        k = C.c_uint32(0)
+        self._check(self.lib.kcmm_prefix_evict(self.handle, n, C.byref(k)), "kcmm_prefix_evict")
+        return k.value
+
+    def prefix_entries(self) -> int:
+        return self.lib.kcmm_prefix_cached_blocks(self.handle)
 
     def cow_block_for_append(self, seq: int, logical: int):
         s, d = C.c_uint32(0), C.c_uint32(0)

@@ -912,6 +912,67 @@ int kcmm_share_prefix(kcmm_pool_t* pool, uint32_t src, uint32_t dst, uint32_t n,
     return 0;
 }
 
+int kcmm_prefix_hash_blocks(const int32_t* tokens, uint32_t n_tokens, uint32_t block_size,
+                            uint64_t seed, uint64_t* out, uint32_t max_out, uint32_t* count) {
+    if ((tokens == nullptr && n_tokens > 0) || out == nullptr || count == nullptr ||
+        block_size == 0)
+        return -1;
+    *count = static_cast<uint32_t>(
+        kcmm::prefix_hash_blocks(tokens, n_tokens, block_size, seed, out, max_out));
+    return 0;
+}
+
+int kcmm_prefix_register(kcmm_pool_t* pool, uint32_t seq, const uint64_t* hashes, uint32_t n,
+                         uint32_t* out_added) {
+    if (pool == nullptr || (hashes == nullptr && n > 0) || out_added == nullptr) {
+        if (pool) pool->set_error("kcmm_prefix_register: null arguments");
+        return -1;
+    }
+    std::string err;
+    if (!pool->core->prefix_register(seq, hashes, n, out_added, &err)) {
+        pool->set_error(err);
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_prefix_match(kcmm_pool_t* pool, const uint64_t* hashes, uint32_t n, uint32_t* out_blocks,
+                      uint32_t* out_matched) {
+    if (pool == nullptr || (hashes == nullptr && n > 0) || out_matched == nullptr) {
+        if (pool) pool->set_error("kcmm_prefix_match: null arguments");
+        return -1;
+    }
+    *out_matched = pool->core->prefix_match(hashes, n, out_blocks);
+    return 0;
+}
+
+int kcmm_prefix_attach(kcmm_pool_t* pool, uint32_t dst, const uint64_t* hashes, uint32_t n,
+                       uint32_t* out_blocks, uint32_t* out_matched) {
+    if (pool == nullptr || (hashes == nullptr && n > 0) || out_matched == nullptr) {
+        if (pool) pool->set_error("kcmm_prefix_attach: null arguments");
+        return -1;
+    }
+    std::string err;
+    if (!pool->core->prefix_attach(dst, hashes, n, out_blocks, out_matched, &err)) {
+        pool->set_error(err);
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_prefix_evict(kcmm_pool_t* pool, uint32_t max_entries, uint32_t* out_evicted) {
+    if (pool == nullptr || out_evicted == nullptr) {
+        if (pool) pool->set_error("kcmm_prefix_evict: null arguments");
+        return -1;
+    }
+    *out_evicted = pool->core->prefix_evict(max_entries);
+    return 0;
+}
+
+uint32_t kcmm_prefix_cached_blocks(kcmm_pool_t* pool) {
+    return pool ? pool->core->prefix_entries() : 0;
+}
+
 int kcmm_fork_sequence(kcmm_pool_t* pool, uint32_t src, uint32_t* out_seq) {
     if (pool == nullptr || out_seq == nullptr) {
         if (pool) pool->set_error("kcmm_fork_sequence: null arguments");

@@ -321,6 +321,128 @@ bool PoolCore::share_prefix(uint32_t src, uint32_t dst, uint32_t n, uint32_t* ou
     return true;
 }
 
+// FNV-1a (64-bit) over the little-endian bytes of the previous block's hash
+// (the seed for block 0) followed by the block's token ids (int32, LE).
+size_t prefix_hash_blocks(const int32_t* tokens, size_t n_tokens, size_t block_size,
+                          uint64_t seed, uint64_t* out, size_t max_out) {
+    const size_t nb = block_size ? n_tokens / block_size : 0;
+    uint64_t prev = seed;
+    size_t i = 0;
+    for (; i < nb && i < max_out; ++i) {
+        uint64_t h = 0xcbf29ce484222325ull;
+        auto mix = [&h](uint32_t b) {
+            h ^= b;
+            h *= 0x100000001b3ull;
+        };
+        for (int k = 0; k < 8; ++k) mix(static_cast<uint32_t>((prev >> (8 * k)) & 0xFF));
+        for (size_t t = 0; t < block_size; ++t) {
+            const uint32_t v = static_cast<uint32_t>(tokens[i * block_size + t]);
+            for (int k = 0; k < 4; ++k) mix((v >> (8 * k)) & 0xFF);
+        }
+        out[i] = h;
+        prev = h;
+    }
+    return i;
+}
+
+bool PoolCore::prefix_register(uint32_t seq, const uint64_t* hashes, uint32_t n,
+                               uint32_t* added, std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    *added = 0;
+    if (seq >= seqs_.size()) {
+        *err = fmt("kcmm_prefix_register: seq_idx %llu out of bounds", seq);
+        return false;
+    }
+    const SequenceState& s = seqs_[seq];
+    if (n > s.table.size()) {
+        *err = fmt("kcmm_prefix_register: seq %llu holds %llu blocks, %llu requested", seq,
+                   s.table.size(), n);
+        return false;
+    }
+    if (static_cast<uint64_t>(n) * geo_.block_size > s.seq_len) {
+        *err = fmt("kcmm_prefix_register: only full blocks are cached (%llu blocks of %llu "
+                   "tokens > seq_len %llu)", n, geo_.block_size, s.seq_len);
+        return false;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t id = s.table[i];
+        if (id >= blocks_.size() || !blocks_[id].in_use) {
+            *err = fmt("kcmm_prefix_register: block %llu not in use", id);
+            return false;
+        }
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        if (prefix_.count(hashes[i])) continue;
+        const uint32_t id = s.table[i];
+        prefix_.emplace(hashes[i], PrefixEntry{id, i, ++prefix_tick_});
+        ++blocks_[id].refcount;
+        ++*added;
+    }
+    return true;
+}
+
+uint32_t PoolCore::prefix_match_locked(const uint64_t* hashes, uint32_t n, uint32_t* blocks) {
+    const uint64_t now = ++prefix_tick_;
+    uint32_t m = 0;
+    for (; m < n; ++m) {
+        auto it = prefix_.find(hashes[m]);
+        if (it == prefix_.end()) break;
+        it->second.last_use = now;
+        if (blocks) blocks[m] = it->second.block;
+    }
+    return m;
+}
+
+uint32_t PoolCore::prefix_match(const uint64_t* hashes, uint32_t n, uint32_t* blocks) {
+    std::lock_guard<std::mutex> lk(mu_);
+    return prefix_match_locked(hashes, n, blocks);
+}
+
+bool PoolCore::prefix_attach(uint32_t dst, const uint64_t* hashes, uint32_t n, uint32_t* blocks,
+                             uint32_t* matched, std::string* err) {
+    std::lock_guard<std::mutex> lk(mu_);
+    *matched = 0;
+    if (dst >= seqs_.size()) {
+        *err = fmt("kcmm_prefix_attach: seq_idx %llu out of bounds", dst);
+        return false;
+    }
+    std::vector<uint32_t> ids(n);
+    const uint32_t m = prefix_match_locked(hashes, n, ids.data());
+    for (uint32_t i = 0; i < m; ++i) {
+        ++blocks_[ids[i]].refcount;
+        seqs_[dst].table.push_back(ids[i]);
+        if (blocks) blocks[i] = ids[i];
+    }
+    *matched = m;
+    return true;
+}
+
+uint32_t PoolCore::prefix_evict(uint32_t n) {
+    std::lock_guard<std::mutex> lk(mu_);
+    std::vector<std::pair<uint64_t, const PrefixEntry*>> order;
+    order.reserve(prefix_.size());
+    for (const auto& kv : prefix_) order.emplace_back(kv.first, &kv.second);
+    std::sort(order.begin(), order.end(), [](const auto& a, const auto& b) {
+        if (a.second->last_use != b.second->last_use) return a.second->last_use < b.second->last_use;
+        return a.second->depth > b.second->depth;
+    });
+    const uint32_t k = static_cast<uint32_t>(std::min<size_t>(n, order.size()));
+    std::vector<uint64_t> keys(k);
+    std::vector<uint32_t> ids(k);
+    for (uint32_t i = 0; i < k; ++i) {
+        keys[i] = order[i].first;
+        ids[i] = order[i].second->block;
+    }
+    for (uint32_t i = 0; i < k; ++i) prefix_.erase(keys[i]);
+    if (k) release_locked(ids.data(), k);     // in eviction order
+    return k;
+}
+
+uint32_t PoolCore::prefix_entries() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return static_cast<uint32_t>(prefix_.size());
+}
+
 bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
                           uint32_t* children, std::vector<uint32_t>* pairs, std::string* err) {
     if (width == 0) {

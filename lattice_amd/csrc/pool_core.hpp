@@ -27,6 +27,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "tiering.hpp"
@@ -121,6 +122,12 @@ struct RowDst {
     uint32_t slot;         // token offset inside the page
 };
 
+// Chained content hashes of the full blocks of a token sequence (the keys of
+// the prefix cache): hash i covers tokens [0, (i+1) * block_size) through
+// hash i-1.  Writes min(n_tokens / block_size, max_out) hashes, returns that.
+size_t prefix_hash_blocks(const int32_t* tokens, size_t n_tokens, size_t block_size,
+                          uint64_t seed, uint64_t* out, size_t max_out);
+
 class PoolCore {
 public:
     PoolCore(const PoolGeometry& g, std::unique_ptr<PageBacking> backing);
@@ -156,6 +163,30 @@ public:
     // Copy-on-write support.
     bool fork_sequence(uint32_t src, uint32_t* out_seq, std::string* err);
     bool share_prefix(uint32_t src, uint32_t dst, uint32_t n, uint32_t* out, std::string* err);
+
+    // Prefix cache: the reference's SharingManager contract (content hash ->
+    // the blocks of a prefix, with a reference held for sharing; ref
+    // src/kcmm/sharing.rs:9-65, a placeholder there).  Keys are the chained
+    // per-block content hashes of prefix_hash_blocks; every entry holds one
+    // reference on its block, so a cached prefix outlives the sequence that
+    // registered it.
+    // Cache the first n blocks of seq under hashes[0..n) (full blocks only:
+    // n * block_size <= seq_len).  Existing keys are left as they are; each
+    // new entry takes a reference.  *added = entries created.
+    bool prefix_register(uint32_t seq, const uint64_t* hashes, uint32_t n, uint32_t* added,
+                         std::string* err);
+    // Longest cached run hashes[0..m) -> blocks[0..m); marks those entries as
+    // used now.  Returns m.
+    uint32_t prefix_match(const uint64_t* hashes, uint32_t n, uint32_t* blocks);
+    // prefix_match, then append the m blocks to dst's table, one reference
+    // each (as share_prefix).  blocks may be null.
+    bool prefix_attach(uint32_t dst, const uint64_t* hashes, uint32_t n, uint32_t* blocks,
+                       uint32_t* matched, std::string* err);
+    // Drop up to n entries, least recently used first (the deepest first
+    // among entries used together), releasing their references.  Returns
+    // the number dropped.
+    uint32_t prefix_evict(uint32_t n);
+    uint32_t prefix_entries();
     int cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src, uint32_t* dst,
                              std::string* err);
     // Beam fork of a decode step: for each parent, width - 1 children, each
@@ -234,6 +265,14 @@ private:
     std::vector<BlockInfo> blocks_;
     std::vector<uint32_t> free_ids_;
     std::vector<SequenceState> seqs_;
+    struct PrefixEntry {
+        uint32_t block;
+        uint32_t depth;       // position in the prefix it was registered at
+        uint64_t last_use;    // prefix_tick_ when registered or last matched
+    };
+    std::unordered_map<uint64_t, PrefixEntry> prefix_;
+    uint64_t prefix_tick_ = 0;
+    uint32_t prefix_match_locked(const uint64_t* hashes, uint32_t n, uint32_t* blocks);
     uint64_t epoch_ = 0;
     // tiering (null policy: disabled)
     std::unique_ptr<EvictionPolicy> policy_;

@@ -65,6 +65,8 @@ def _bind(l: C.CDLL) -> None:
         "opool_share_prefix": ([P, U32, U32, U32, P], C.c_int),
         "opool_cow": ([P, U32, U32, P, P], C.c_int),
         "opool_refcount": ([P, U32], U32),
+        "opool_incref": ([P, U32], C.c_int),
+        "opool_seq_len": ([P, U32], U32),
         "opool_stats": ([P, P], None),
         "opool_metrics": ([P, P], None),
         "opool_below_low_watermark": ([P, F], C.c_int),
@@ -134,6 +136,7 @@ class OraclePool:
                  dtype=F16, rollback_on_failure=True):
         self._h = lib().opool_new(block_size, num_layers, kv_heads, head_dim, max_batch,
                                   max_seq_len, dtype, int(rollback_on_failure))
+        self.block_size = block_size
 
     def __del__(self):
         if getattr(self, "_h", None):
@@ -202,6 +205,12 @@ class OraclePool:
 
     def refcount(self, blk) -> int:
         return lib().opool_refcount(self._h, blk)
+
+    def incref(self, blk) -> bool:
+        return lib().opool_incref(self._h, blk) == 0
+
+    def seq_len(self, seq) -> int:
+        return lib().opool_seq_len(self._h, seq)
 
     def stats(self) -> dict:
         st = np.zeros(14, dtype=np.uint64)
@@ -305,6 +314,90 @@ class OracleTier:
 
     def arc_p(self):
         return lib().otier_arc_p(self._h)
+
+
+# ---- prefix cache ------------------------------------------------------------------
+# The reference's prefix-sharing manager contract (src/kcmm/sharing.rs:9-65:
+# content hash -> prefix blocks, reference counted; a placeholder there),
+# restated over OraclePool.
+
+FNV64_OFFSET, FNV64_PRIME = 0xCBF29CE484222325, 0x100000001B3
+
+
+def fnv1a64(data: bytes, h: int = FNV64_OFFSET) -> int:
+    """FNV-1a, 64-bit (the published algorithm: xor each byte, multiply by
+    the FNV prime, modulo 2^64)."""
+    for b in data:
+        h = ((h ^ b) * FNV64_PRIME) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def prefix_hash_blocks(tokens, block_size: int, seed: int = 0) -> list[int]:
+    """Chained hashes of the full blocks of a token sequence: hash i is
+    FNV-1a-64 of (hash i-1 as 8 LE bytes, seed for block 0) + the block's
+    token ids as int32 LE."""
+    t = np.asarray(tokens, dtype=np.int32)
+    out, prev = [], seed & 0xFFFFFFFFFFFFFFFF
+    for i in range(len(t) // block_size):
+        prev = fnv1a64(prev.to_bytes(8, "little") +
+                       t[i * block_size:(i + 1) * block_size].astype("<i4").tobytes())
+        out.append(prev)
+    return out
+
+
+class OraclePrefixCache:
+    """Prefix cache over an OraclePool: key -> (block, depth, last_use); each
+    entry holds one reference on its block."""
+
+    def __init__(self, pool: OraclePool):
+        self.pool, self.entries, self.tick = pool, {}, 0
+
+    def register(self, seq, hashes) -> int | None:
+        table = self.pool.block_table(seq)
+        n = len(hashes)
+        if table is None or n > len(table):
+            return None
+        if n * self.pool.block_size > self.pool.seq_len(seq):
+            return None
+        if any(self.pool.refcount(b) == 0 for b in table[:n]):
+            return None
+        added = 0
+        for i, h in enumerate(hashes):
+            if h in self.entries:
+                continue
+            self.tick += 1
+            self.entries[h] = [table[i], i, self.tick]
+            self.pool.incref(table[i])
+            added += 1
+        return added
+
+    def match(self, hashes) -> list[int]:
+        self.tick += 1
+        out = []
+        for h in hashes:
+            e = self.entries.get(h)
+            if e is None:
+                break
+            e[2] = self.tick
+            out.append(e[0])
+        return out
+
+    def attach(self, dst, hashes) -> list[int] | None:
+        if self.pool.block_table(dst) is None:
+            return None
+        blocks = self.match(hashes)
+        for b in blocks:
+            self.pool.incref(b)
+            self.pool.append_block(dst, b)
+        return blocks
+
+    def evict(self, n) -> int:
+        order = sorted(self.entries.items(), key=lambda kv: (kv[1][2], -kv[1][1]))[:n]
+        for h, _ in order:
+            del self.entries[h]
+        if order:
+            self.pool.release([e[0] for _, e in order])
+        return len(order)
 
 
 # ---- KV write / page copy ------------------------------------------------------

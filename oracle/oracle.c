@@ -436,6 +436,18 @@ int opool_cow(OPool *p, uint32_t seq, uint32_t logical, uint32_t *src, uint32_t 
     return 1;
 }
 
+/* One more reference on an in-use block (the prefix cache's hold); -1 if the
+ * block is not in use. */
+int opool_incref(OPool *p, uint32_t blk) {
+    if (blk >= p->nblocks || !p->blocks[blk].in_use) return -1;
+    p->blocks[blk].refcount++;
+    return 0;
+}
+
+uint32_t opool_seq_len(OPool *p, uint32_t seq) {
+    return seq < p->nseqs ? p->seqs[seq].seq_len : 0;
+}
+
 uint32_t opool_refcount(OPool *p, uint32_t blk) {
     if (blk >= p->nblocks || !p->blocks[blk].in_use) return 0;
     return p->blocks[blk].refcount;

@@ -54,6 +54,8 @@ int opool_fork(OPool *p, uint32_t src, uint32_t *out_seq);
 int opool_share_prefix(OPool *p, uint32_t src, uint32_t dst, uint32_t n, uint32_t *out);
 int opool_cow(OPool *p, uint32_t seq, uint32_t logical, uint32_t *src, uint32_t *dst);
 uint32_t opool_refcount(OPool *p, uint32_t blk);
+int opool_incref(OPool *p, uint32_t blk);
+uint32_t opool_seq_len(OPool *p, uint32_t seq);
 /* stats[14]: blocks_in_use, total_blocks, total_physical, free_physical,
  * active_sequences, num_layers, bps, superblocks, block_size,
  * max_blocks_per_seq, block_bytes, (float bits) idle ratio,
