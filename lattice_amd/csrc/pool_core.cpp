@@ -99,7 +99,6 @@ bool PoolCore::alloc_one_locked(uint32_t* id_out, std::string* err) {
                    static_cast<uint64_t>(h.second) * geo_.block_bytes;
     bi.superblock_idx = h.first;
     bi.block_index = h.second;
-    bi.refcount = 1;
     bi.in_use = true;
     bi.location = kLocGpu;
     uint32_t id;
@@ -110,7 +109,9 @@ bool PoolCore::alloc_one_locked(uint32_t* id_out, std::string* err) {
     } else {
         id = static_cast<uint32_t>(blocks_.size());
         blocks_.push_back(bi);
+        rc_.push_back(0);
     }
+    rc_[id] = 1;
     ++epoch_;
     *id_out = id;
     if (policy_) policy_->on_allocate(h);   // ref pool.rs:446-449
@@ -148,15 +149,15 @@ void PoolCore::release_locked(const uint32_t* ids, size_t n) {
         if (id >= blocks_.size()) continue;
         BlockInfo& bi = blocks_[id];
         if (!bi.in_use) continue;
-        if (bi.refcount > 1) {
-            --bi.refcount;
+        if (rc_[id] > 1) {
+            --rc_[id];
             continue;
         }
         // ref pool.rs:491-545: a swapped-out block gives back its swap slot,
         // one in transit is left alone
         if (bi.location == kLocEvicting || bi.location == kLocRestoring) continue;
         bi.in_use = false;
-        bi.refcount = 0;
+        rc_[id] = 0;
         if (bi.location == kLocCpu) {
             if (slots_) slots_->free(bi.cpu_offset, block_swap_bytes_);
         } else {
@@ -273,7 +274,7 @@ bool PoolCore::table_va_offsets(uint32_t seq, std::vector<uint64_t>* out) {
 uint32_t PoolCore::refcount(uint32_t block) {
     std::lock_guard<std::mutex> lk(mu_);
     if (block >= blocks_.size() || !blocks_[block].in_use) return 0;
-    return blocks_[block].refcount;
+    return rc_[block];
 }
 
 bool PoolCore::fork_sequence(uint32_t src, uint32_t* out_seq, std::string* err) {
@@ -286,7 +287,7 @@ bool PoolCore::fork_sequence(uint32_t src, uint32_t* out_seq, std::string* err) 
     s.table = seqs_[src].table;
     s.seq_len = seqs_[src].seq_len;
     for (uint32_t id : s.table)
-        if (id < blocks_.size() && blocks_[id].in_use) ++blocks_[id].refcount;
+        if (id < blocks_.size() && blocks_[id].in_use) ++rc_[id];
     seqs_.push_back(std::move(s));
     *out_seq = static_cast<uint32_t>(seqs_.size() - 1);
     return true;
@@ -314,7 +315,7 @@ bool PoolCore::share_prefix(uint32_t src, uint32_t dst, uint32_t n, uint32_t* ou
     }
     for (uint32_t i = 0; i < n; ++i) {
         const uint32_t id = seqs_[src].table[i];
-        ++blocks_[id].refcount;
+        ++rc_[id];
         seqs_[dst].table.push_back(id);
         out[i] = id;
     }
@@ -375,7 +376,7 @@ bool PoolCore::prefix_register(uint32_t seq, const uint64_t* hashes, uint32_t n,
         if (prefix_.count(hashes[i])) continue;
         const uint32_t id = s.table[i];
         prefix_.emplace(hashes[i], PrefixEntry{id, i, ++prefix_tick_});
-        ++blocks_[id].refcount;
+        ++rc_[id];
         ++*added;
     }
     return true;
@@ -409,7 +410,7 @@ bool PoolCore::prefix_attach(uint32_t dst, const uint64_t* hashes, uint32_t n, u
     std::vector<uint32_t> ids(n);
     const uint32_t m = prefix_match_locked(hashes, n, ids.data());
     for (uint32_t i = 0; i < m; ++i) {
-        ++blocks_[ids[i]].refcount;
+        ++rc_[ids[i]];
         seqs_[dst].table.push_back(ids[i]);
         if (blocks) blocks[i] = ids[i];
     }
@@ -488,7 +489,7 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
         const uint32_t p = parents[i];
         // the forks' references, all at once (ref fork: same ids, refcount + 1)
         for (uint32_t id : seqs_[p].table)
-            if (id < blocks_.size() && blocks_[id].in_use) blocks_[id].refcount += forks;
+            if (id < rc_.size() && rc_[id] != 0) rc_[id] += forks;   // in use <=> rc > 0
         const uint32_t logical = seqs_[p].seq_len / bs;
         for (uint32_t c = 0; c < forks; ++c) {
             SequenceState s;
@@ -506,19 +507,19 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
                 // list is LIFO), references and children removed.
                 for (size_t q = pairs->size(); q > pairs0; q -= 2) {
                     const uint32_t nid = (*pairs)[q - 1];
-                    blocks_[nid].refcount = 1;
+                    rc_[nid] = 1;
                     release_locked(&nid, 1);
-                    ++blocks_[(*pairs)[q - 2]].refcount;
+                    ++rc_[(*pairs)[q - 2]];
                 }
                 pairs->resize(pairs0);
                 for (uint32_t j = 0; j <= i; ++j)
                     for (uint32_t id : seqs_[parents[j]].table)
-                        if (id < blocks_.size() && blocks_[id].in_use) blocks_[id].refcount -= forks;
+                        if (id < rc_.size() && rc_[id] != 0) rc_[id] -= forks;
                 seqs_.resize(seqs0);
                 return false;
             }
             seqs_[child].table[logical] = new_id;
-            --blocks_[old_id].refcount;
+            --rc_[old_id];
             pairs->push_back(old_id);
             pairs->push_back(new_id);
         }
@@ -543,7 +544,7 @@ int PoolCore::cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src
         *err = fmt("kcmm_cow_block_for_append: block %llu not in use", old_id);
         return -1;
     }
-    if (blocks_[old_id].refcount <= 1) return 0;
+    if (rc_[old_id] <= 1) return 0;
     if (blocks_[old_id].location != kLocGpu) {
         *err = fmt("kcmm_cow_block_for_append: block %llu is not resident in HBM "
                    "(restore it first)", old_id);
@@ -552,7 +553,7 @@ int PoolCore::cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src
     uint32_t new_id;
     if (!alloc_one_locked(&new_id, err)) return -1;
     seqs_[seq].table[logical] = new_id;
-    --blocks_[old_id].refcount;
+    --rc_[old_id];
     *src = old_id;
     *dst = new_id;
     return 1;
@@ -600,10 +601,10 @@ bool PoolCore::resolve_positions(const uint32_t* seqs, const uint32_t* pos, uint
             *err = fmt("kcmm_append_kv_step: block_idx %llu not in use", id);
             return false;
         }
-        if (blocks_[id].refcount > 1) {
+        if (rc_[id] > 1) {
             *err = fmt("kcmm_append_kv_step: block_idx %llu is shared (refcount %llu); "
                        "make it private with kcmm_cow_block_for_append first",
-                       id, blocks_[id].refcount);
+                       id, rc_[id]);
             return false;
         }
         if (blocks_[id].location != kLocGpu) {
@@ -631,9 +632,9 @@ bool PoolCore::resolve_slots(const int64_t* slots, uint32_t batch, std::vector<R
                        s);
             return false;
         }
-        if (blocks_[id].refcount > 1) {
+        if (rc_[id] > 1) {
             *err = fmt("kcmm_append_kv_slots: block_idx %llu is shared (refcount %llu)", id,
-                       blocks_[id].refcount);
+                       rc_[id]);
             return false;
         }
         if (blocks_[id].location != kLocGpu) {

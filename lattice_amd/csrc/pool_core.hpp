@@ -81,7 +81,6 @@ struct BlockInfo {
     uint64_t va_offset = 0;
     uint32_t superblock_idx = 0;
     uint32_t block_index = 0;
-    uint32_t refcount = 0;
     bool in_use = false;
     int location = kLocGpu;
     uint64_t cpu_offset = 0;   // swap offset while kLocCpu / kLocEvicting
@@ -263,6 +262,9 @@ private:
     std::vector<std::pair<uint32_t, uint32_t>> free_handles_;
     size_t superblock_count_ = 0;
     std::vector<BlockInfo> blocks_;
+    // Reference count per block id, beside blocks_ (kept out of BlockInfo so
+    // the fork and release passes over a table touch 4 bytes per entry).
+    std::vector<uint32_t> rc_;
     std::vector<uint32_t> free_ids_;
     std::vector<SequenceState> seqs_;
     struct PrefixEntry {
