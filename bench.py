@@ -318,7 +318,7 @@ def main():
     if args.gemm_only:
         return bench_gemm(args)
     import torch
-    from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, KcmmLibrary
+    from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, KcmmLayerWeightsFp8, KcmmLibrary
     from lattice_amd.workload import build_decode_case, rope_inv_freq
 
     assert torch.cuda.is_available(), "bench needs a GPU"
@@ -432,6 +432,38 @@ def main():
         lib.decode_logits_bf16(hidden.data_ptr(), final_norm.data_ptr(), lm_head.data_ptr(),
                                logits.data_ptr(), B, HIDDEN, VOCAB, RMS_EPS, sp)
 
+    # the same two weight sets with fp8-e4m3 projections (per-row amax/448
+    # scales, quantized on the device), for the fp8-weight decode step
+    weights8, layer_w8 = [], []
+    if args.config == "cfg2" and not args.attn_only:
+        for w in weights:
+            w8 = {"attn_norm": w["attn_norm"], "mlp_norm": w["mlp_norm"]}
+            for name, n, k in GEMMS:
+                wf = w[name].float()
+                sc = (wf.abs().amax(dim=1) / 448.0).clamp_min(1e-30)
+                w8[name] = (wf / sc[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn) \
+                    .view(torch.uint8)
+                w8[name + "_scale"] = sc.contiguous()
+                del wf
+            weights8.append(w8)
+            layer_w8.append(KcmmLayerWeightsFp8(**{k: t.data_ptr() for k, t in w8.items()}))
+
+    def decode_step_fp8w(_):
+        """decode_step with the fp8-weight layers (kcmm_decode_layers_fp8w_on_stream)."""
+        lib.embed_tokens_bf16(embed.data_ptr(), token_ids.data_ptr(), hidden.data_ptr(), B, HIDDEN,
+                              VOCAB, sp)
+        case.pool.decode_layers_fp8w(first_layer=0,
+                                     weights=[layer_w8[i % nw] for i in range(MODEL_LAYERS)],
+                                     hidden_ptr=hidden.data_ptr(),
+                                     block_tables_ptr=dv["bt"].data_ptr(),
+                                     seq_lens_ptr=dv["sl"].data_ptr(),
+                                     block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                     inv_freq_ptr=inv_freq.data_ptr(), batch=B,
+                                     hidden_size=HIDDEN, num_q_heads=HQ, intermediate_size=INTER,
+                                     max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
+        lib.decode_logits_bf16(hidden.data_ptr(), final_norm.data_ptr(), lm_head.data_ptr(),
+                               logits.data_ptr(), B, HIDDEN, VOCAB, RMS_EPS, sp)
+
     W = lambda layer, name: weights[layer % nw][name].data_ptr()
     calls = {
         "norm1": lambda l: norm("attn_norm", l),
@@ -514,9 +546,11 @@ def main():
             lib.decode_logits_bf16(hidden.data_ptr(), final_norm.data_ptr(), lm_head.data_ptr(),
                                    logits.data_ptr(), B, HIDDEN, VOCAB, RMS_EPS, sp)
 
-        for label, fn, steps in (("layer_step", layer_step, args.steps), ("append", append, args.steps),
-                                 ("logits", logits_step, args.steps),
-                                 ("decode_step", decode_step, full_steps)):
+        timings = [("layer_step", layer_step, args.steps), ("append", append, args.steps),
+                   ("logits", logits_step, args.steps), ("decode_step", decode_step, full_steps)]
+        if layer_w8:
+            timings.append(("decode_step_fp8w", decode_step_fp8w, full_steps))
+        for label, fn, steps in timings:
             evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
             for i in range(min(args.warmup, steps)):
                 fn(i % args.layers)
@@ -680,6 +714,17 @@ def main():
         result["t_logits_us"] = round(extra["logits"] * 1e3, 2)
         result["t_layer_single_call_us"] = round(extra["layer_step"] * 1e3, 2)
         result["t_layer_components_us"] = {n: round(per[n] * 1e3, 2) for n in names}
+        if "decode_step_fp8w" in extra:
+            t8 = extra["decode_step_fp8w"] / 1e3
+            wbytes8 = sum(n * k + 4 * n for _, n, k in GEMMS)
+            result["fp8_weight_decode"] = {
+                "decode_tokens_per_s": round(B / t8, 1), "t_decode_step_us": round(t8 * 1e6, 1),
+                "t_layer_us": round((t8 - extra["logits"] / 1e3) / MODEL_LAYERS * 1e6, 2),
+                "projection_weight_bytes_per_layer": wbytes8,
+                "note": "kcmm_decode_layers_fp8w_on_stream: the decode step with fp8-e4m3 "
+                        "projection weights (fp32 row scales), bf16 KV pool, embedding and "
+                        "bf16 lm_head as in decode_tokens_per_s; HIP events around each step"}
+            log(f"fp8-weight decode step ms={extra['decode_step_fp8w']:.4f}")
         def gemm_report(times_ms, M, residual, plan=True):
             gem = {}
             for name, n, k in GEMMS:

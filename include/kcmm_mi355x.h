@@ -437,6 +437,41 @@ int kcmm_decode_layers_on_stream(kcmm_pool_t *pool, uint32_t first_layer, uint32
                                  uint32_t intermediate_size, uint32_t max_blocks_per_seq,
                                  float rms_eps, uint64_t stream_ptr);
 
+/** Device addresses of one layer's weights with fp8-e4m3 (OCP e4m3fn)
+ *  projections: each projection matrix as e4m3 codes, row-major [out][in],
+ *  with an fp32 scale per output row (weight[r][c] = decode(code[r][c]) *
+ *  scale[r]); the RMSNorm weights stay bf16.  Shapes as kcmm_layer_weights_t. */
+typedef struct kcmm_layer_weights_fp8 {
+    uint64_t attn_norm;     /**< bf16 [hidden] */
+    uint64_t qkv;           /**< e4m3 [(Hq + 2 Hkv) head_dim][hidden] */
+    uint64_t qkv_scale;     /**< fp32 [(Hq + 2 Hkv) head_dim] */
+    uint64_t o;             /**< e4m3 [hidden][Hq head_dim] */
+    uint64_t o_scale;       /**< fp32 [hidden] */
+    uint64_t mlp_norm;      /**< bf16 [hidden] */
+    uint64_t gate_up;       /**< e4m3 [2 intermediate][hidden]: gate rows, then up rows */
+    uint64_t gate_up_scale; /**< fp32 [2 intermediate] */
+    uint64_t down;          /**< e4m3 [hidden][intermediate] */
+    uint64_t down_scale;    /**< fp32 [hidden] */
+} kcmm_layer_weights_fp8_t;
+
+/** kcmm_decode_layers_on_stream with fp8-e4m3 projection weights (the same
+ *  layer loop, ref LlamaTransformer::forward_step_paged,
+ *  llama_transformer.rs:262-391, whose GEMMs are bf16 cuBLAS calls there; the
+ *  fp8-weight form has no counterpart in the reference).  Every projection
+ *  streams half the weight bytes of the bf16 form; activations, the RMSNorm
+ *  weights and the pool's pages are as in kcmm_decode_layers_on_stream, and
+ *  each product is sum(x * code) * scale in fp32 before the same bf16
+ *  rounding.  All four scale pointers of every layer must be set. */
+int kcmm_decode_layers_fp8w_on_stream(kcmm_pool_t *pool, uint32_t first_layer,
+                                      uint32_t num_layers,
+                                      const kcmm_layer_weights_fp8_t *weights,
+                                      uint64_t hidden_ptr, uint64_t block_tables_ptr,
+                                      uint64_t seq_lens_ptr, uint64_t block_offsets_f16_ptr,
+                                      uint64_t inv_freq_ptr, uint32_t batch,
+                                      uint32_t hidden_size, uint32_t num_q_heads,
+                                      uint32_t intermediate_size, uint32_t max_blocks_per_seq,
+                                      float rms_eps, uint64_t stream_ptr);
+
 #ifdef __cplusplus
 }
 #endif

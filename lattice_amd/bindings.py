@@ -93,6 +93,15 @@ class KcmmLayerWeights(C.Structure):
                 ("mlp_norm", C.c_uint64), ("gate_up", C.c_uint64), ("down", C.c_uint64)]
 
 
+class KcmmLayerWeightsFp8(C.Structure):
+    """kcmm_layer_weights_fp8_t (include/kcmm_mi355x.h): device addresses of
+    one layer's weights with fp8-e4m3 projections (codes [out][in] plus an
+    fp32 scale per output row) and bf16 RMSNorm weights."""
+    _fields_ = [(name, C.c_uint64) for name in
+                ("attn_norm", "qkv", "qkv_scale", "o", "o_scale", "mlp_norm", "gate_up",
+                 "gate_up_scale", "down", "down_scale")]
+
+
 _P, _U32, _U64, _I32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int32
 _ATTN = [_P, _U32, _U64, _U64, _U64, _U64, _U64] + [_U32] * 6 + [C.c_float]
 
@@ -194,6 +203,9 @@ SIGNATURES = {
     "kcmm_decode_layers_on_stream": ([_P, _U32, _U32, C.POINTER(KcmmLayerWeights), _U64, _U64,
                                       _U64, _U64, _U64, _U32, _U32, _U32, _U32, _U32, C.c_float,
                                       _U64], C.c_int),
+    "kcmm_decode_layers_fp8w_on_stream": ([_P, _U32, _U32, C.POINTER(KcmmLayerWeightsFp8), _U64,
+                                           _U64, _U64, _U64, _U64, _U32, _U32, _U32, _U32, _U32,
+                                           C.c_float, _U64], C.c_int),
     "kcmm_below_low_watermark": ([_P, C.c_float], C.c_int),
     "kcmm_synchronize": ([_P], C.c_int),
     "kcmm_get_block_size": ([_P], _U32),
@@ -598,6 +610,18 @@ class KcmmPool:
             seq_lens_ptr, block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size, num_q_heads,
             intermediate_size, max_blocks_per_seq, C.c_float(rms_eps), stream_ptr)
         self._check(rc, "decode_layers")
+
+    def decode_layers_fp8w(self, *, first_layer, weights, hidden_ptr, block_tables_ptr,
+                           seq_lens_ptr, block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size,
+                           num_q_heads, intermediate_size, max_blocks_per_seq, rms_eps,
+                           stream_ptr=0) -> None:
+        """decode_layers with fp8-e4m3 projection weights (KcmmLayerWeightsFp8)."""
+        arr = (KcmmLayerWeightsFp8 * len(weights))(*weights)
+        rc = self.lib.kcmm_decode_layers_fp8w_on_stream(
+            self.handle, first_layer, len(weights), arr, hidden_ptr, block_tables_ptr,
+            seq_lens_ptr, block_offsets_f16_ptr, inv_freq_ptr, batch, hidden_size, num_q_heads,
+            intermediate_size, max_blocks_per_seq, C.c_float(rms_eps), stream_ptr)
+        self._check(rc, "decode_layers_fp8w")
 
     # -- copy-on-write --
     def fork_sequence(self, src: int) -> int:

@@ -132,11 +132,12 @@ struct GemmPlan {
 };
 bool gemm_plan(uint32_t m, uint32_t n, uint32_t k, bool fp8_weights, GemmPlan* plan,
                std::string* err);
-// Y = X (W8 diag(wscale))^T: fp8-e4m3 weights W8 [n][k] with an fp32 scale per
-// weight row, bf16 activations and result, fp32 accumulate (weight-stream
-// kernel; the weights are converted to bf16 exactly in registers).
+// Y = X (W8 diag(wscale))^T (+ R when residual != 0, as gemm_bf16): fp8-e4m3
+// weights W8 [n][k] with an fp32 scale per weight row, bf16 activations and
+// result, fp32 accumulate (weight-stream kernel; the weights are converted to
+// bf16 exactly in registers, the row scale multiplies each dot product).
 bool gemm_fp8w_bf16(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32_t m, uint32_t n,
-                    uint32_t k, uint64_t stream, std::string* err);
+                    uint32_t k, uint64_t stream, std::string* err, uint64_t residual = 0);
 // Y = bf16(sum of `splits` fp32 partials [splits][MN]) (+ R), in split order.
 bool gemm_split_reduce_launch(const float* part, uint16_t* y, const uint16_t* r, int mn,
                               int splits, uint64_t stream, std::string* err);
@@ -178,9 +179,11 @@ bool residual_rmsnorm_from_partials(const float* part, int splits, uint64_t hidd
                                     uint64_t stream, std::string* err);
 
 // X W^T as fp32 partials [*splits][m][n] in the stream's workspace (slot 1),
-// for a consumer that finishes the sum itself.
+// for a consumer that finishes the sum itself.  The projections below take
+// fp8-e4m3 weights with fp32 row scales when wscale != 0 (as gemm_fp8w_bf16).
 bool gemm_bf16_partials(uint64_t x, uint64_t w, uint32_t m, uint32_t n, uint32_t k,
-                        uint64_t stream, float** part, int* splits, std::string* err);
+                        uint64_t stream, float** part, int* splits, std::string* err,
+                        uint64_t wscale = 0);
 
 // Fused projections (kernels/gemm.hip): the QKV GEMM whose store does what
 // rope_append_bf16 does with its result (a.qkv unused; one token per
@@ -188,9 +191,9 @@ bool gemm_bf16_partials(uint64_t x, uint64_t w, uint32_t m, uint32_t n, uint32_t
 // store does what silu_mul_bf16 does (w_gate_up = [gate; up], [2 inter][k]).
 // With a K split the finishing step runs as a second kernel over the partials.
 bool gemm_bf16_rope_append(uint64_t x, uint64_t w_qkv, uint32_t m, uint32_t k,
-                           const RopeAppendArgs& a, std::string* err);
+                           const RopeAppendArgs& a, std::string* err, uint64_t wscale = 0);
 bool gemm_bf16_swiglu(uint64_t x, uint64_t w_gate_up, uint64_t act, uint32_t m, uint32_t inter,
-                      uint32_t k, uint64_t stream, std::string* err);
+                      uint32_t k, uint64_t stream, std::string* err, uint64_t wscale = 0);
 
 }  // namespace dev
 }  // namespace kcmm

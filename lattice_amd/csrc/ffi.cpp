@@ -11,6 +11,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/kcmm.h"
@@ -1296,29 +1297,53 @@ int kcmm_qkv_rope_append_bf16_on_stream(kcmm_pool_t* pool, uint32_t layer_idx, u
     return 0;
 }
 
+extern "C++" {
 namespace {
+
+// One layer's weights as the layer driver takes them: bf16 projections (every
+// *_scale 0), or fp8-e4m3 projections with an fp32 scale per output row.
+struct LayerView {
+    uint64_t attn_norm, qkv, qkv_scale, o, o_scale, mlp_norm, gate_up, gate_up_scale, down,
+        down_scale;
+};
+
+LayerView layer_view(const kcmm_layer_weights_t& l) {
+    return {l.attn_norm, l.qkv, 0, l.o, 0, l.mlp_norm, l.gate_up, 0, l.down, 0};
+}
+
+LayerView layer_view(const kcmm_layer_weights_fp8_t& l) {
+    return {l.attn_norm, l.qkv, l.qkv_scale, l.o, l.o_scale, l.mlp_norm, l.gate_up,
+            l.gate_up_scale, l.down, l.down_scale};
+}
 
 // Layers first .. first + n - 1 of a decode step, in place on hidden.  Per
 // layer: RMSNorm -> QKV projection with RoPE + KV append -> paged attention
 // -> O projection (fp32 partials) -> residual add + RMSNorm -> gate/up with
 // SwiGLU -> down projection.  Between layers the down projection also leaves
 // partials, and the next layer's first RMSNorm finishes its residual add;
-// the last layer's down projection adds its residual itself.
+// the last layer's down projection adds its residual itself.  W is
+// kcmm_layer_weights_t (bf16 projections) or kcmm_layer_weights_fp8_t.
+template <typename W>
 int run_decode_layers(kcmm_pool_t* pool, const char* fn, uint32_t first, uint32_t n,
-                      const kcmm_layer_weights_t* w, uint64_t hidden, uint64_t block_tables,
+                      const W* weights, uint64_t hidden, uint64_t block_tables,
                       uint64_t seq_lens, uint64_t offsets_f16, uint64_t inv_freq, uint32_t batch,
                       uint32_t hidden_size, uint32_t num_q_heads, uint32_t intermediate_size,
                       uint32_t max_blocks_per_seq, float rms_eps, uint64_t stream) {
-    if (pool == nullptr || w == nullptr || n == 0 || hidden == 0 || block_tables == 0 ||
+    if (pool == nullptr || weights == nullptr || n == 0 || hidden == 0 || block_tables == 0 ||
         seq_lens == 0 || offsets_f16 == 0 || inv_freq == 0) {
         if (pool) pool->set_error(std::string(fn) + ": null pointer argument or no layers");
         return -1;
     }
+    constexpr bool kFp8 = std::is_same<W, kcmm_layer_weights_fp8_t>::value;
+    std::vector<LayerView> w(n);
     for (uint32_t i = 0; i < n; ++i) {
-        const kcmm_layer_weights_t& l = w[i];
+        const LayerView& l = w[i] = layer_view(weights[i]);
         if (l.attn_norm == 0 || l.qkv == 0 || l.o == 0 || l.mlp_norm == 0 || l.gate_up == 0 ||
-            l.down == 0) {
-            pool->set_error(std::string(fn) + ": null weight pointer");
+            l.down == 0 ||
+            (kFp8 && (l.qkv_scale == 0 || l.o_scale == 0 || l.gate_up_scale == 0 ||
+                      l.down_scale == 0))) {
+            pool->set_error(std::string(fn) + ": null weight pointer at layer " +
+                            std::to_string(first + i));
             return -1;
         }
     }
@@ -1363,7 +1388,7 @@ int run_decode_layers(kcmm_pool_t* pool, const char* fn, uint32_t first, uint32_
     int down_splits = 0;
     for (uint32_t i = 0; i < n; ++i) {
         const uint32_t layer = first + i;
-        const kcmm_layer_weights_t& l = w[i];
+        const LayerView& l = w[i];
         kcmm::dev::AttnDecodeArgs at{};
         at.dtype = g.dtype;
         at.q = q;
@@ -1397,10 +1422,15 @@ int run_decode_layers(kcmm_pool_t* pool, const char* fn, uint32_t first, uint32_
         // 0), else the projection then the standalone RoPE/append kernel
         auto qkv_step = [&]() {
             if (D % 16 == 0)
-                return kcmm::dev::gemm_bf16_rope_append(normed, l.qkv, B, hidden_size, ra, &err);
-            return kcmm::dev::gemm_bf16(normed, l.qkv, qkv, B, static_cast<uint32_t>(qkv_n),
-                                        hidden_size, stream, &err) &&
-                   kcmm::dev::rope_append_bf16(ra, &err);
+                return kcmm::dev::gemm_bf16_rope_append(normed, l.qkv, B, hidden_size, ra, &err,
+                                                        l.qkv_scale);
+            const bool proj =
+                kFp8 ? kcmm::dev::gemm_fp8w_bf16(normed, l.qkv, l.qkv_scale, qkv, B,
+                                                 static_cast<uint32_t>(qkv_n), hidden_size,
+                                                 stream, &err)
+                     : kcmm::dev::gemm_bf16(normed, l.qkv, qkv, B, static_cast<uint32_t>(qkv_n),
+                                            hidden_size, stream, &err);
+            return proj && kcmm::dev::rope_append_bf16(ra, &err);
         };
         // O projection as partials; the residual add is finished by the
         // RMSNorm kernel that reads them
@@ -1409,7 +1439,7 @@ int run_decode_layers(kcmm_pool_t* pool, const char* fn, uint32_t first, uint32_
             int splits = 1;
             return kcmm::dev::gemm_bf16_partials(attn, l.o, B, hidden_size,
                                                  static_cast<uint32_t>(attn_k), stream, &part,
-                                                 &splits, &err) &&
+                                                 &splits, &err, l.o_scale) &&
                    kcmm::dev::residual_rmsnorm_from_partials(part, splits, hidden, l.mlp_norm,
                                                              normed, B, hidden_size, rms_eps,
                                                              stream, &err);
@@ -1417,15 +1447,20 @@ int run_decode_layers(kcmm_pool_t* pool, const char* fn, uint32_t first, uint32_
         auto down_step = [&]() {
             if (i + 1 == n) {
                 down_part = nullptr;
+                if (kFp8)
+                    return kcmm::dev::gemm_fp8w_bf16(act, l.down, l.down_scale, hidden, B,
+                                                     hidden_size, intermediate_size, stream, &err,
+                                                     hidden);
                 return kcmm::dev::gemm_bf16(act, l.down, hidden, B, hidden_size,
                                             intermediate_size, stream, &err, hidden);
             }
             return kcmm::dev::gemm_bf16_partials(act, l.down, B, hidden_size, intermediate_size,
-                                                 stream, &down_part, &down_splits, &err);
+                                                 stream, &down_part, &down_splits, &err,
+                                                 l.down_scale);
         };
         const bool ok = norm1() && qkv_step() && kcmm::dev::attn_decode(at, &err) && o_step() &&
                         kcmm::dev::gemm_bf16_swiglu(normed, l.gate_up, act, B, intermediate_size,
-                                                    hidden_size, stream, &err) &&
+                                                    hidden_size, stream, &err, l.gate_up_scale) &&
                         down_step();
         if (!ok) {
             pool->set_error(std::string(fn) + ": launch failed at layer " + std::to_string(layer) +
@@ -1437,6 +1472,7 @@ int run_decode_layers(kcmm_pool_t* pool, const char* fn, uint32_t first, uint32_
 }
 
 }  // namespace
+}  // extern "C++"
 
 int kcmm_decode_layer_step_on_stream(kcmm_pool_t* pool, uint32_t layer_idx,
                                      const kcmm_layer_weights_t* w, uint64_t hidden,
@@ -1457,6 +1493,19 @@ int kcmm_decode_layers_on_stream(kcmm_pool_t* pool, uint32_t first_layer, uint32
                                  uint32_t num_q_heads, uint32_t intermediate_size,
                                  uint32_t max_blocks_per_seq, float rms_eps, uint64_t stream) {
     return run_decode_layers(pool, "kcmm_decode_layers_on_stream", first_layer, num_layers,
+                             weights, hidden, block_tables, seq_lens, offsets_f16, inv_freq, batch,
+                             hidden_size, num_q_heads, intermediate_size, max_blocks_per_seq,
+                             rms_eps, stream);
+}
+
+int kcmm_decode_layers_fp8w_on_stream(kcmm_pool_t* pool, uint32_t first_layer, uint32_t num_layers,
+                                      const kcmm_layer_weights_fp8_t* weights, uint64_t hidden,
+                                      uint64_t block_tables, uint64_t seq_lens,
+                                      uint64_t offsets_f16, uint64_t inv_freq, uint32_t batch,
+                                      uint32_t hidden_size, uint32_t num_q_heads,
+                                      uint32_t intermediate_size, uint32_t max_blocks_per_seq,
+                                      float rms_eps, uint64_t stream) {
+    return run_decode_layers(pool, "kcmm_decode_layers_fp8w_on_stream", first_layer, num_layers,
                              weights, hidden, block_tables, seq_lens, offsets_f16, inv_freq, batch,
                              hidden_size, num_q_heads, intermediate_size, max_blocks_per_seq,
                              rms_eps, stream);

@@ -526,6 +526,15 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
     }, WF8);
 }
 
+// launch_stream on bf16 weights, or on fp8-e4m3 weights when p.wscale is set
+template <int EPI>
+bool launch_weights(const GemmParams& p, int splits, bool want_partials, float** part,
+                    uint64_t stream, std::string* err) {
+    if (p.wscale != nullptr)
+        return launch_stream<EPI, true>(p, splits, want_partials, part, stream, err);
+    return launch_stream<EPI>(p, splits, want_partials, part, stream, err);
+}
+
 bool shape_ok(uint32_t m, uint32_t n, uint32_t k, std::string* err) {
     if (m == 0 || n % 64 != 0 || k % 256 != 0 || n == 0 || k == 0) {
         *err = "gemm_bf16 needs m > 0, n % 64 == 0 and k % 256 == 0";
@@ -603,28 +612,35 @@ bool gemm_plan(uint32_t m, uint32_t n, uint32_t k, bool fp8_weights, GemmPlan* p
 }
 
 bool gemm_fp8w_bf16(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32_t m, uint32_t n,
-                    uint32_t k, uint64_t stream, std::string* err) {
+                    uint32_t k, uint64_t stream, std::string* err, uint64_t residual) {
     if (!shape_ok(m, n, k, err)) return false;
+    if (wscale == 0) {
+        *err = "fp8 weights need their row scales";
+        return false;
+    }
     GemmParams p = base_params(x, w8, m, n, k);
     p.Y = reinterpret_cast<uint16_t*>(y);
+    p.R = reinterpret_cast<const uint16_t*>(residual);
     p.wscale = reinterpret_cast<const float*>(wscale);
     const int splits = splits_for(p.M, p.N, p.K, true);
     float* part = nullptr;
     if (!launch_stream<kEpiPlain, true>(p, splits, false, &part, stream, err)) return false;
-    if (splits > 1) return gemm_split_reduce_launch(part, p.Y, nullptr, p.M * p.N, splits, stream, err);
+    if (splits > 1) return gemm_split_reduce_launch(part, p.Y, p.R, p.M * p.N, splits, stream, err);
     return true;
 }
 
 bool gemm_bf16_partials(uint64_t x, uint64_t w, uint32_t m, uint32_t n, uint32_t k,
-                        uint64_t stream, float** part, int* splits, std::string* err) {
+                        uint64_t stream, float** part, int* splits, std::string* err,
+                        uint64_t wscale) {
     if (!shape_ok(m, n, k, err)) return false;
     GemmParams p = base_params(x, w, m, n, k);
-    *splits = splits_for(p.M, p.N, p.K);
-    return launch_stream<kEpiPlain>(p, *splits, true, part, stream, err);
+    p.wscale = reinterpret_cast<const float*>(wscale);
+    *splits = splits_for(p.M, p.N, p.K, wscale != 0);
+    return launch_weights<kEpiPlain>(p, *splits, true, part, stream, err);
 }
 
 bool gemm_bf16_swiglu(uint64_t x, uint64_t w_gate_up, uint64_t act, uint32_t m, uint32_t inter,
-                      uint32_t k, uint64_t stream, std::string* err) {
+                      uint32_t k, uint64_t stream, std::string* err, uint64_t wscale) {
     if (inter == 0 || inter % 32 != 0) {
         *err = "gemm_bf16_swiglu needs intermediate % 32 == 0";
         return false;
@@ -632,9 +648,10 @@ bool gemm_bf16_swiglu(uint64_t x, uint64_t w_gate_up, uint64_t act, uint32_t m, 
     if (!shape_ok(m, 2 * inter, k, err)) return false;
     GemmParams p = base_params(x, w_gate_up, m, 2 * inter, k);
     p.Y = reinterpret_cast<uint16_t*>(act);
-    const int splits = splits_for(p.M, p.N, p.K);
+    p.wscale = reinterpret_cast<const float*>(wscale);
+    const int splits = splits_for(p.M, p.N, p.K, wscale != 0);
     float* part = nullptr;
-    if (!launch_stream<kEpiSwiglu>(p, splits, false, &part, stream, err)) return false;
+    if (!launch_weights<kEpiSwiglu>(p, splits, false, &part, stream, err)) return false;
     if (splits > 1) {
         const int n = p.M * static_cast<int>(inter);
         hipLaunchKernelGGL(gemm_split_swiglu, dim3((n / 4 + 255) / 256), dim3(256), 0,
@@ -646,7 +663,7 @@ bool gemm_bf16_swiglu(uint64_t x, uint64_t w_gate_up, uint64_t act, uint32_t m, 
 }
 
 bool gemm_bf16_rope_append(uint64_t x, uint64_t w_qkv, uint32_t m, uint32_t k,
-                           const RopeAppendArgs& a, std::string* err) {
+                           const RopeAppendArgs& a, std::string* err, uint64_t wscale) {
     const uint32_t D = a.head_dim;
     const uint64_t n = static_cast<uint64_t>(a.num_q_heads + 2 * a.kv_heads) * D;
     if (D == 0 || D % 16 != 0 || n % 64 != 0 || a.num_q_heads == 0 || a.kv_heads == 0 ||
@@ -662,7 +679,7 @@ bool gemm_bf16_rope_append(uint64_t x, uint64_t w_qkv, uint32_t m, uint32_t k,
         float* part = nullptr;
         int splits = 1;
         return gemm_bf16_partials(x, w_qkv, m, static_cast<uint32_t>(n), k, a.stream, &part,
-                                  &splits, err) &&
+                                  &splits, err, wscale) &&
                rope_append_from_partials(a, part, splits, err);
     }
     GemmParams p = base_params(x, w_qkv, m, static_cast<uint32_t>(n), k);
@@ -679,9 +696,10 @@ bool gemm_bf16_rope_append(uint64_t x, uint64_t w_qkv, uint32_t m, uint32_t k,
     p.block_size = static_cast<int>(a.block_size);
     p.mbps = static_cast<int>(a.mbps);
     p.row_bytes = static_cast<int>(a.row_bytes);
-    const int splits = splits_for(p.M, p.N, p.K);
+    p.wscale = reinterpret_cast<const float*>(wscale);
+    const int splits = splits_for(p.M, p.N, p.K, wscale != 0);
     float* part = nullptr;
-    if (!launch_stream<kEpiRope>(p, splits, false, &part, a.stream, err)) return false;
+    if (!launch_weights<kEpiRope>(p, splits, false, &part, a.stream, err)) return false;
     if (splits > 1) return rope_append_from_partials(a, part, splits, err);
     return true;
 }

@@ -594,6 +594,17 @@ def fp8_page_rows(region, page_byte, slots, kv_heads, head_dim, row_bytes, data_
     return out
 
 
+def layer_weight_f64(w, name):
+    """Layer weight `name` of dict w in fp64: bf16 bits, or, for fp8-weight
+    projections, a (e4m3 codes [out][in], fp32 scale [out]) pair whose
+    weight is code * scale row by row."""
+    v = w[name]
+    if isinstance(v, tuple):
+        codes, scale = v
+        return decode(FP8, codes).astype(np.float64) * np.asarray(scale, np.float64)[:, None]
+    return decode(BF16, v).astype(np.float64)
+
+
 def decode_layer_step_f64(hidden_bits, w, k_region, v_region, block_tables, seq_lens,
                           offsets_f16, inv_freq, num_q_heads, kv_heads, head_dim,
                           intermediate, block_size, row_bytes, eps, round_bf16=True,
@@ -603,7 +614,9 @@ def decode_layer_step_f64(hidden_bits, w, k_region, v_region, block_tables, seq_
     read back dequantized).
 
     hidden_bits [B][H] uint16 (bf16); w: dict of bf16-bit arrays attn_norm [H],
-    qkv [(Hq+2Hkv)D][H], o [H][Hq D], mlp_norm [H], gate_up [2I][H], down [H][I].
+    qkv [(Hq+2Hkv)D][H], o [H][Hq D], mlp_norm [H], gate_up [2I][H], down [H][I]
+    (a projection may instead be an fp8 (codes, row scales) pair, see
+    layer_weight_f64).
     Sequence b's new token is at position seq_lens[b] - 1; its rotated k and v
     are written (as bf16) into k_region / v_region (uint8 copies of the
     layer's regions) and attention runs over rows 0..pos of its pages (the
@@ -611,7 +624,7 @@ def decode_layer_step_f64(hidden_bits, w, k_region, v_region, block_tables, seq_
     stored activation to bf16 as a bf16 model does; without it the layer is
     computed in fp64 throughout.  Returns the new hidden state (float64)."""
     rnd = bf16_round if round_bf16 else (lambda a: np.asarray(a, dtype=np.float64))
-    f = lambda name: decode(BF16, w[name]).astype(np.float64)
+    f = lambda name: layer_weight_f64(w, name)
     hq, hkv, d = num_q_heads, kv_heads, head_dim
     grp = hq // hkv
     x = decode(BF16, hidden_bits).astype(np.float64)

@@ -172,11 +172,11 @@ bool silu_mul_bf16(uint64_t, uint64_t, uint32_t, uint32_t, uint64_t, std::string
     return no_device(err);
 }
 bool gemm_bf16_rope_append(uint64_t, uint64_t, uint32_t, uint32_t, const RopeAppendArgs&,
-                           std::string* err) {
+                           std::string* err, uint64_t) {
     return no_device(err);
 }
 bool gemm_bf16_swiglu(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t,
-                      std::string* err) {
+                      std::string* err, uint64_t) {
     return no_device(err);
 }
 bool gemm_bf16_tiled(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, uint64_t,
@@ -184,7 +184,7 @@ bool gemm_bf16_tiled(uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t,
     return no_device(err);
 }
 bool gemm_fp8w_bf16(uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t,
-                    std::string* err) {
+                    std::string* err, uint64_t) {
     return no_device(err);
 }
 bool gemm_split_reduce_launch(const float*, uint16_t*, const uint16_t*, int, int, uint64_t,
@@ -220,7 +220,7 @@ bool host_pinned_alloc(size_t bytes, void** out, std::string* err) {
 }
 void host_pinned_free(void* p) { std::free(p); }
 bool gemm_bf16_partials(uint64_t, uint64_t, uint32_t, uint32_t, uint32_t, uint64_t, float**, int*,
-                        std::string* err) {
+                        std::string* err, uint64_t) {
     return no_device(err);
 }
 bool rope_append_from_partials(const RopeAppendArgs&, const float*, int, std::string* err) {

@@ -150,7 +150,7 @@ def test_null_and_argument_checks(hostcheck_lib):
 def test_decode_layer_entry_points_validate_before_device_work(hostcheck_lib):
     """The decode-layer, fused-GEMM and beam-fork entry points reject bad
     arguments (and say why) before any device work, on the host-check build."""
-    from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, make_config
+    from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, KcmmLayerWeightsFp8, make_config
     L = hostcheck_lib.lib
     # pool-free entry points: shape rules
     assert L.kcmm_gemm_bf16_swiglu_on_stream(1, 1, 1, 4, 100, 256, 0) == -1      # inter % 32
@@ -183,6 +183,21 @@ def test_decode_layer_entry_points_validate_before_device_work(hostcheck_lib):
         assert "layer" in bf.last_error()
         with pytest.raises(Exception):
             bf.decode_layers(first_layer=0, weights=[], **kw)
+        # fp8-weight layers: every row-scale pointer is required
+        w8 = KcmmLayerWeightsFp8(attn_norm=1, qkv=1, qkv_scale=1, o=1, o_scale=1, mlp_norm=1,
+                                 gate_up=1, gate_up_scale=1, down=1, down_scale=1)
+        for missing in ("qkv_scale", "o_scale", "gate_up_scale", "down_scale"):
+            bad = KcmmLayerWeightsFp8(**{f: getattr(w8, f) for f, _ in w8._fields_})
+            setattr(bad, missing, 0)
+            with pytest.raises(Exception):
+                bf.decode_layers_fp8w(first_layer=0, weights=[w8, bad], **kw)
+            assert "null weight pointer at layer 1" in bf.last_error()
+        with pytest.raises(Exception):
+            bf.decode_layers_fp8w(first_layer=0, weights=[w8], **{**kw, "hidden_size": 500})
+        assert "multiples of 256" in bf.last_error()
+        with pytest.raises(Exception):
+            f16.decode_layers_fp8w(first_layer=0, weights=[w8], **kw)
+        assert "bf16" in f16.last_error()
         # beam fork: bad width and an unknown parent are errors; a parent whose
         # next token opens a new page forks with no copy (so no device work)
         ids = bf.alloc_blocks(2)

@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lattice_amd.bindings import KV_BF16, KV_FP8, KcmmLayerWeights, memcpy_dtoh
+from lattice_amd.bindings import (KV_BF16, KV_FP8, KcmmLayerWeights, KcmmLayerWeightsFp8,
+                                  memcpy_dtoh)
 from lattice_amd.workload import build_decode_case
 
 pytestmark = pytest.mark.gpu
@@ -355,6 +356,155 @@ def test_decode_layers_matches_layer_steps(gpu_lib, hq, hkv, d, h, inter, dtype)
     assert np.array_equal(res[0][0], res[1][0])
     for a, b in zip(res[0][1], res[1][1]):
         assert np.array_equal(a, b)
+
+
+_PROJ = ("qkv", "o", "gate_up", "down")
+
+
+def _layer_weights_fp8(torch, rng, h, inter, hq, hkv, d, pow2=False):
+    """fp8-e4m3 projections: per-row amax/448 quantization of N(0, 0.05)
+    weights (pow2: power-of-two row scales, so that code * scale is a bf16
+    value); returns the oracle's dict ((codes, scale) pairs), the bf16 bits of
+    the dequantized projections, the device tensors and the ABI struct."""
+    shapes = {"qkv": ((hq + 2 * hkv) * d, h), "o": (h, hq * d), "gate_up": (2 * inter, h),
+              "down": (h, inter)}
+    w = {"attn_norm": O.encode(O.BF16, 1.0 + 0.1 * rng.standard_normal(h)),
+         "mlp_norm": O.encode(O.BF16, 1.0 + 0.1 * rng.standard_normal(h))}
+    exact = dict(w)
+    dev = {k: bf16_dev(torch, v) for k, v in w.items()}
+    for name in _PROJ:
+        x = rng.standard_normal(shapes[name]) * 0.05
+        if pow2:
+            scale = (2.0 ** np.ceil(np.log2(np.abs(x).max(axis=1) / 448.0))).astype(np.float32)
+            codes = O.encode(O.FP8, x / scale[:, None])
+        else:
+            codes, scale = O.quantize_fp8_rows(x)
+        w[name] = (codes, scale)
+        exact[name] = O.encode(O.BF16, O.layer_weight_f64(w, name))
+        dev[name] = torch.from_numpy(np.ascontiguousarray(codes)).cuda()
+        dev[name + "_scale"] = torch.from_numpy(scale).cuda()
+    lw = KcmmLayerWeightsFp8(**{k: t.data_ptr() for k, t in dev.items()})
+    return w, exact, dev, lw
+
+
+@pytest.mark.parametrize("hq,hkv,d,h,inter,dtype", [
+    (8, 2, 64, 512, 768, KV_BF16), (32, 8, 128, 4096, 1024, KV_BF16),
+    (32, 8, 72, 512, 768, KV_BF16), (32, 8, 128, 4096, 1024, KV_FP8)])
+def test_decode_layers_fp8_weights(gpu_lib, hq, hkv, d, h, inter, dtype):
+    """Two layers through kcmm_decode_layers_fp8w_on_stream (fp8-e4m3
+    projections, fp32 row scales) vs the oracle's layer applied twice with
+    the dequantized weights: layer 0's down projection leaves partials that
+    layer 1's RMSNorm finishes, layer 1's adds its residual itself.  head_dim
+    72 takes the unfused QKV path.  Tolerances as the bf16 layer step's (fp8
+    pages: the fp8 attention's)."""
+    import torch
+    lens = [1, 16, 17, 130]
+    fp8 = dtype == KV_FP8
+    case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=16, ctx_lens=lens, dtype=dtype, seed=h, num_layers=2)
+    try:
+        g = case.geometry
+        rng = np.random.default_rng(21)
+        ws = [_layer_weights_fp8(torch, rng, h, inter, hq, hkv, d) for _ in range(2)]
+        hid = O.encode(O.BF16, rng.standard_normal((len(lens), h)))
+        hd = bf16_dev(torch, hid)
+        inv = O.default_inv_freq(500000.0, d)
+        invd = torch.from_numpy(inv.astype(np.float32)).cuda()
+        dv = case.dev
+        mb = g["mapped_bytes"]
+        regs = [(memcpy_dtoh(case.pool.va_k(l), mb), memcpy_dtoh(case.pool.va_v(l), mb))
+                for l in range(2)]
+        case.pool.decode_layers_fp8w(first_layer=0, weights=[w[3] for w in ws],
+                                     hidden_ptr=hd.data_ptr(),
+                                     block_tables_ptr=dv["bt"].data_ptr(),
+                                     seq_lens_ptr=dv["sl"].data_ptr(),
+                                     block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                     inv_freq_ptr=invd.data_ptr(), batch=len(lens),
+                                     hidden_size=h, num_q_heads=hq, intermediate_size=inter,
+                                     max_blocks_per_seq=case.mbps, rms_eps=1e-5,
+                                     stream_ptr=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        got = O.decode(O.BF16, bits_of(hd)).astype(np.float64)
+        ref_bits = hid
+        for layer in range(2):
+            ref = O.decode_layer_step_f64(ref_bits, ws[layer][0], *regs[layer], case.block_tables,
+                                          case.seq_lens, case.offsets_f16, inv, hq, hkv, d,
+                                          inter, 16, g["row_bytes"], 1e-5, dtype=dtype,
+                                          data_bytes=g["data_bytes"])
+            ref_bits = O.encode(O.BF16, ref)
+        x = O.decode(O.BF16, hid).astype(np.float64)
+        err = rel_err(got, ref)
+        upd = rel_err(got - x, ref - x)
+        print(f"fp8-weight layers hq={hq} d={d} h={h} dtype={dtype}: err {err:.2e}, "
+              f"update err {upd:.2e}", flush=True)
+        assert np.isfinite(got).all() and err <= (3e-2 if fp8 else 1e-2)
+        assert upd <= (8e-2 if fp8 else 5e-2)
+        # the new tokens' K/V rows of both layers hold what the oracle wrote
+        for layer in range(2):
+            k1 = memcpy_dtoh(case.pool.va_k(layer), mb)
+            v1 = memcpy_dtoh(case.pool.va_v(layer), mb)
+            for b, L in enumerate(lens):
+                pos = L - 1
+                pg = int(case.offsets_f16[case.block_tables[b, pos // 16]]) * 2
+                for got_r, ref_r in ((k1, regs[layer][0]), (v1, regs[layer][1])):
+                    if fp8:
+                        a = O.fp8_page_rows(got_r, pg, [pos % 16], hkv, d, g["row_bytes"],
+                                            g["data_bytes"])
+                        r = O.fp8_page_rows(ref_r, pg, [pos % 16], hkv, d, g["row_bytes"],
+                                            g["data_bytes"])
+                        assert rel_err(a, r) <= 1.3e-1, (layer, b)
+                        continue
+                    base = pg + (pos % 16) * g["row_bytes"]
+                    seg = slice(base, base + hkv * d * 2)
+                    a = O.decode(O.BF16, got_r[seg].view(np.uint16)).astype(np.float64)
+                    r = O.decode(O.BF16, ref_r[seg].view(np.uint16)).astype(np.float64)
+                    assert rel_err(a, r) <= 2e-2, (layer, b)
+    finally:
+        case.pool.destroy()
+
+
+@pytest.mark.parametrize("hq,hkv,d,h,inter", [(32, 8, 128, 4096, 1024), (8, 2, 64, 512, 768)])
+def test_fp8_weight_layers_match_bf16_layers_on_exact_weights(gpu_lib, hq, hkv, d, h, inter):
+    """With power-of-two row scales every fp8 weight is a bf16 value: two
+    fp8-weight layers and two bf16 layers on those values must agree to
+    within the fp32 accumulation order (the fp8 GEMMs multiply by the row
+    scale after the dot product); a scale dropped or applied to the wrong row
+    is off by powers of two."""
+    import torch
+    lens = [1, 16, 17, 130]
+    outs = []
+    for fp8w in (True, False):
+        case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv,
+                                 head_dim=d, block_size=16, ctx_lens=lens, dtype=KV_BF16, seed=h,
+                                 num_layers=2)
+        try:
+            rng = np.random.default_rng(33)
+            ws = [_layer_weights_fp8(torch, rng, h, inter, hq, hkv, d, pow2=True)
+                  for _ in range(2)]
+            hid = O.encode(O.BF16, rng.standard_normal((len(lens), h)))
+            hd = bf16_dev(torch, hid)
+            invd = torch.from_numpy(O.default_inv_freq(500000.0, d).astype(np.float32)).cuda()
+            dv = case.dev
+            kw = dict(hidden_ptr=hd.data_ptr(), block_tables_ptr=dv["bt"].data_ptr(),
+                      seq_lens_ptr=dv["sl"].data_ptr(), block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                      inv_freq_ptr=invd.data_ptr(), batch=len(lens), hidden_size=h,
+                      num_q_heads=hq, intermediate_size=inter, max_blocks_per_seq=case.mbps,
+                      rms_eps=1e-5)
+            if fp8w:
+                case.pool.decode_layers_fp8w(first_layer=0, weights=[w[3] for w in ws], **kw)
+            else:
+                bf = [{k: bf16_dev(torch, v) for k, v in w[1].items()} for w in ws]
+                lws = [KcmmLayerWeights(**{k: t.data_ptr() for k, t in b.items()}) for b in bf]
+                case.pool.decode_layers(first_layer=0, weights=lws, **kw)
+            torch.cuda.synchronize()
+            outs.append(O.decode(O.BF16, bits_of(hd)).astype(np.float64))
+        finally:
+            case.pool.destroy()
+    same = float(np.mean(outs[0] == outs[1]))
+    err = rel_err(outs[0], outs[1])
+    print(f"fp8w vs bf16 on exact weights: {same:.4f} identical, max rel err {err:.2e}",
+          flush=True)
+    assert np.isfinite(outs[0]).all() and err <= 1e-2 and same >= 0.5
 
 
 @pytest.mark.parametrize("b,h,vocab", [(5, 512, 1024), (64, 4096, 2048), (8, 256, 128256)])

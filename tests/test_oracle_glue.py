@@ -204,3 +204,35 @@ def test_layer_step_rounding_is_small_and_writes_pages():
         want.add((int(cs["offs"][cs["bt"][bb, p // bs]]) * 2 + (p % bs) * cs["row_bytes"])
                  // cs["row_bytes"])
     assert rows <= want
+
+
+def test_layer_step_fp8_weights_equal_exact_bf16_weights():
+    """fp8-weight projections given as (e4m3 codes, row scales): with
+    power-of-two row scales every weight code * scale is a bf16 value, so the
+    layer must equal the bf16 layer on those values bit for bit; a dropped or
+    misapplied row scale (scales differ per row) breaks the equality."""
+    h, inter, hq, hkv, d, bs, eps = 256, 512, 4, 2, 64, 16, 1e-5
+    lens = [1, 16, 20]
+    rng = np.random.default_rng(8)
+    cs = _layer_case(rng, h, inter, hq, hkv, d, bs, lens)
+    inv = O.default_inv_freq(500000.0, d)
+    w8, wexact = dict(cs["w"]), dict(cs["w"])
+    for name in ("qkv", "o", "gate_up", "down"):
+        n, k = cs["w"][name].shape
+        codes = rng.integers(0, 256, size=(n, k), dtype=np.uint8)
+        codes[(codes & 0x7F) == 0x7F] = 0x38          # no NaN codes
+        scale = (2.0 ** rng.integers(-9, -5, size=n)).astype(np.float32)
+        w8[name] = (codes, scale)
+        deq = O.decode(O.FP8, codes).astype(np.float64) * scale[:, None]
+        wexact[name] = O.encode(O.BF16, deq)
+        assert np.array_equal(O.decode(O.BF16, wexact[name]).astype(np.float64), deq)
+    args = (cs["bt"], cs["sl"], cs["offs"], inv, hq, hkv, d, inter, bs, cs["row_bytes"], eps)
+    k1, v1, k2, v2 = (cs["kreg"].copy(), cs["vreg"].copy(), cs["kreg"].copy(),
+                      cs["vreg"].copy())
+    a = O.decode_layer_step_f64(cs["hidden"], w8, k1, v1, *args)
+    b = O.decode_layer_step_f64(cs["hidden"], wexact, k2, v2, *args)
+    assert np.array_equal(a, b) and np.array_equal(k1, k2) and np.array_equal(v1, v2)
+    # the scale matters: the same codes at scale 1 give another layer
+    w1 = {k: ((v[0], np.ones_like(v[1])) if isinstance(v, tuple) else v) for k, v in w8.items()}
+    c = O.decode_layer_step_f64(cs["hidden"], w1, cs["kreg"].copy(), cs["vreg"].copy(), *args)
+    assert not np.allclose(a, c)
