@@ -177,9 +177,19 @@ void PoolCore::free_blocks(const uint32_t* ids, size_t n) {
     release_locked(ids, n);
 }
 
+std::vector<uint32_t> PoolCore::take_table_locked() {
+    std::vector<uint32_t> t;
+    if (!spare_tables_.empty()) {
+        t.swap(spare_tables_.back());
+        spare_tables_.pop_back();
+    }
+    return t;
+}
+
 uint32_t PoolCore::register_sequence(const uint32_t* table, size_t n) {
     std::lock_guard<std::mutex> lk(mu_);
     SequenceState s;
+    s.table = take_table_locked();
     s.table.assign(table, table + n);
     seqs_.push_back(std::move(s));
     return static_cast<uint32_t>(seqs_.size() - 1);
@@ -192,6 +202,10 @@ void PoolCore::unregister_sequence(uint32_t seq) {
     table.swap(seqs_[seq].table);
     seqs_[seq].seq_len = 0;
     if (!table.empty()) release_locked(table.data(), table.size());
+    if (table.capacity() != 0 && spare_tables_.size() < kMaxSpareTables) {
+        table.clear();
+        spare_tables_.push_back(std::move(table));
+    }
 }
 
 void PoolCore::touch(uint32_t seq) {
@@ -284,7 +298,8 @@ bool PoolCore::fork_sequence(uint32_t src, uint32_t* out_seq, std::string* err) 
         return false;
     }
     SequenceState s;
-    s.table = seqs_[src].table;
+    s.table = take_table_locked();
+    s.table.assign(seqs_[src].table.begin(), seqs_[src].table.end());
     s.seq_len = seqs_[src].seq_len;
     for (uint32_t id : s.table)
         if (id < blocks_.size() && blocks_[id].in_use) ++rc_[id];
@@ -484,7 +499,11 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
         return false;
     }
     const size_t seqs0 = seqs_.size(), pairs0 = pairs->size();
-    seqs_.reserve(seqs0 + static_cast<size_t>(n) * forks);
+    // (geometric growth: sequence indices are never reused, so a loop of
+    // forks keeps appending; an exact reserve would move every sequence on
+    // every call)
+    const size_t want = seqs0 + static_cast<size_t>(n) * forks;
+    if (seqs_.capacity() < want) seqs_.reserve(std::max(want, 2 * seqs_.capacity()));
     for (uint32_t i = 0; i < n; ++i) {
         const uint32_t p = parents[i];
         // the forks' references, all at once (ref fork: same ids, refcount + 1)
@@ -493,7 +512,8 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
         const uint32_t logical = seqs_[p].seq_len / bs;
         for (uint32_t c = 0; c < forks; ++c) {
             SequenceState s;
-            s.table = seqs_[p].table;
+            s.table = take_table_locked();
+            s.table.assign(seqs_[p].table.begin(), seqs_[p].table.end());
             s.seq_len = seqs_[p].seq_len;
             seqs_.push_back(std::move(s));
             const uint32_t child = static_cast<uint32_t>(seqs_.size() - 1);

@@ -267,6 +267,12 @@ private:
     std::vector<uint32_t> rc_;
     std::vector<uint32_t> free_ids_;
     std::vector<SequenceState> seqs_;
+    // Block-table buffers of unregistered sequences, kept (emptied) for the
+    // next sequence that needs one, so that forks and registrations of a
+    // steady serving loop do not go to the heap for every table.
+    static constexpr size_t kMaxSpareTables = 1024;
+    std::vector<std::vector<uint32_t>> spare_tables_;
+    std::vector<uint32_t> take_table_locked();
     struct PrefixEntry {
         uint32_t block;
         uint32_t depth;       // position in the prefix it was registered at

@@ -172,3 +172,68 @@ def test_fork_beams_matches_separate_calls(gpu_lib, dtype, width):
             assert np.array_equal(got[l][0], regs[l][0]) and np.array_equal(got[l][1], regs[l][1])
     finally:
         pool.destroy()
+
+
+def test_fork_beams_repeated_steps(gpu_lib):
+    """Four beam steps in a row, each forking every parent into 3 children
+    whose last partial page is made private, then releasing the children (so
+    later forks take recycled table buffers): after every step the child ids,
+    tables, refcounts and the allocator's next ids equal the oracle pool's
+    fork + CoW + unregister; the regions hold every copy at the end."""
+    import torch
+    rng = np.random.default_rng(19)
+    L, hk, d, bs, B, width = 2, 8, 128, 16, 5, 4
+    pool = gpu_lib.create_pool(make_config(num_layers=L, kv_heads=hk, head_dim=d,
+                                           max_batch=B * width, max_seq_len=512), KV_BF16)
+    opool = O.OraclePool(bs, L, hk, d, B * width, 512, KV_BF16)
+    try:
+        seqs, lens = [], {}
+        for b in range(B):
+            n = int(rng.integers(2, 9))
+            ids = pool.alloc_blocks(n)
+            assert ids == opool.alloc(n)
+            s = pool.register_sequence(ids)
+            assert s == opool.register(ids)
+            ln = n * bs - int(rng.integers(1, bs))       # a partial last page
+            pool.update_seq_len(s, ln)
+            opool.update_seq_len(s, ln)
+            seqs.append(s)
+            lens[s] = ln
+        regs = fill_random(pool, rng)
+        stream = torch.cuda.current_stream()
+        all_pairs = []
+        for step in range(4):
+            children, ncopy = pool.fork_beams(seqs, width, stream_ptr=stream.cuda_stream)
+            stream.synchronize()
+            ochildren = []
+            for s in seqs:
+                for _ in range(width - 1):
+                    c = opool.fork(s)
+                    ochildren.append(c)
+                    rc, pair = opool.cow(c, lens[s] // bs)
+                    assert rc == 1
+                    all_pairs.append(tuple(pair))
+            assert children == ochildren and ncopy == B * (width - 1), step
+            for s in seqs + children:
+                assert pool.block_table(s) == opool.block_table(s), (step, s)
+                for blk in pool.block_table(s):
+                    assert pool.refcount(blk) == opool.refcount(blk), (step, blk)
+            # the copies of this step land before its children are released
+            flat = [r for pair in regs for r in pair]
+            O.copy_pages(flat, [(opool.block_offset(a), opool.block_offset(b))
+                                for a, b in all_pairs[-ncopy:]], pool.stats()["block_bytes"])
+            got = read_all(pool)
+            for l in range(L):
+                assert np.array_equal(got[l][0], regs[l][0]), (step, l)
+                assert np.array_equal(got[l][1], regs[l][1]), (step, l)
+            for c in children:
+                pool.unregister_sequence(c)
+                opool.unregister(c)
+            for s in seqs:
+                for blk in pool.block_table(s):
+                    assert pool.refcount(blk) == opool.refcount(blk) == 1, (step, blk)
+        # the freed private pages come back in the oracle's order
+        ids = pool.alloc_blocks(3)
+        assert ids == opool.alloc(3)
+    finally:
+        pool.destroy()
