@@ -11,14 +11,17 @@
 namespace kcmm {
 namespace {
 
+// One launch carries up to kMaxPairs pairs for up to kMaxRegions regions in
+// its kernel arguments (3.6 KB, under the 4 KB argument limit).
 constexpr int kMaxRegions = 64;
-constexpr int kMaxPairs = 96;
+constexpr int kMaxPairs = 192;
 
 struct CopyBatch {
     uint64_t region[kMaxRegions];
     uint64_t pair[2 * kMaxPairs];  // (src, dst) byte offsets inside each region
     uint32_t n_regions;
 };
+static_assert(sizeof(CopyBatch) + 8 <= 4096, "page-copy kernel arguments over 4 KB");
 
 __device__ __forceinline__ void copy_page(uint8_t* base, uint64_t src, uint64_t dst,
                                           uint32_t bytes) {
