@@ -484,7 +484,7 @@ def main():
     names = ["norm1", "qkv", "rope_append", "attn", "o", "norm2", "gate_up", "silu", "down"]
     if args.attn_only:
         names = ["append", "attn"]
-    beam = {"children": [], "copies": 0}
+    beam = {"children": [], "copies": 0, "host_us": []}
     if args.config == "cfg5":
         # beam search, width 4: every step each of the B sequences is forked
         # into 3 more beams whose last partial page is made private (one
@@ -492,7 +492,9 @@ def main():
         parents = list(range(B))
 
         def beam_fork(_):
+            t0 = time.perf_counter()
             children, ncopy = case.pool.fork_beams(parents, BEAM_WIDTH, stream_ptr=sp)
+            beam["host_us"].append((time.perf_counter() - t0) * 1e6)
             beam["children"].extend(children)
             beam["copies"] = ncopy
 
@@ -662,7 +664,12 @@ def main():
     if args.config == "cfg5":
         geo5 = case.geometry
         result["beam_fork_us"] = round(per["beam_fork"] * 1e3, 2)
+        fork_ms = [ev[i][names.index("beam_fork")].elapsed_time(ev[i][names.index("beam_fork") + 1])
+                   for i in range(args.steps)]
+        host = beam["host_us"][-args.steps:]
         result["beam_fork"] = {"beam_width": BEAM_WIDTH, "parents": B,
+                               "median_us": round(float(np.median(fork_ms)) * 1e3, 2),
+                               "host_call_us_median": round(float(np.median(host)), 2),
                                "cow_pages_per_step": beam["copies"],
                                "cow_copy_bytes_per_step": beam["copies"] * 2 * args.layers *
                                geo5["block_bytes"],

@@ -499,11 +499,7 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
         return false;
     }
     const size_t seqs0 = seqs_.size(), pairs0 = pairs->size();
-    // (geometric growth: sequence indices are never reused, so a loop of
-    // forks keeps appending; an exact reserve would move every sequence on
-    // every call)
-    const size_t want = seqs0 + static_cast<size_t>(n) * forks;
-    if (seqs_.capacity() < want) seqs_.reserve(std::max(want, 2 * seqs_.capacity()));
+    pairs->reserve(pairs0 + 2 * needed);
     for (uint32_t i = 0; i < n; ++i) {
         const uint32_t p = parents[i];
         // the forks' references, all at once (ref fork: same ids, refcount + 1)

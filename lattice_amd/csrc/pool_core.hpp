@@ -28,6 +28,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <deque>
 #include <vector>
 
 #include "tiering.hpp"
@@ -266,7 +267,9 @@ private:
     // the fork and release passes over a table touch 4 bytes per entry).
     std::vector<uint32_t> rc_;
     std::vector<uint32_t> free_ids_;
-    std::vector<SequenceState> seqs_;
+    // Sequence indices are never reused, so a serving loop that forks keeps
+    // appending; a deque never moves the sequences it already holds.
+    std::deque<SequenceState> seqs_;
     // Block-table buffers of unregistered sequences, kept (emptied) for the
     // next sequence that needs one, so that forks and registrations of a
     // steady serving loop do not go to the heap for every table.
