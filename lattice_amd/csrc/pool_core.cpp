@@ -110,6 +110,7 @@ bool PoolCore::alloc_one_locked(uint32_t* id_out, std::string* err) {
         id = static_cast<uint32_t>(blocks_.size());
         blocks_.push_back(bi);
         rc_.push_back(0);
+        in_base_.push_back(0);
     }
     rc_[id] = 1;
     ++epoch_;
@@ -130,6 +131,8 @@ bool PoolCore::alloc_blocks(uint32_t n, uint32_t* out, std::string* err) {
                 free_handles_.emplace_back(bi.superblock_idx, bi.block_index);
                 if (out[j] >= ids_before) {
                     blocks_.pop_back();
+                    rc_.pop_back();
+                    in_base_.pop_back();
                 } else {
                     bi = BlockInfo{};
                     free_ids_.push_back(out[j]);
@@ -149,6 +152,7 @@ void PoolCore::release_locked(const uint32_t* ids, size_t n) {
         if (id >= blocks_.size()) continue;
         BlockInfo& bi = blocks_[id];
         if (!bi.in_use) continue;
+        exact_rc_locked(id);
         if (rc_[id] > 1) {
             --rc_[id];
             continue;
@@ -158,6 +162,7 @@ void PoolCore::release_locked(const uint32_t* ids, size_t n) {
         if (bi.location == kLocEvicting || bi.location == kLocRestoring) continue;
         bi.in_use = false;
         rc_[id] = 0;
+        if (in_base_[id] != 0) poison_bases_locked(id);
         if (bi.location == kLocCpu) {
             if (slots_) slots_->free(bi.cpu_offset, block_swap_bytes_);
         } else {
@@ -198,6 +203,8 @@ uint32_t PoolCore::register_sequence(const uint32_t* table, size_t n) {
 void PoolCore::unregister_sequence(uint32_t seq) {
     std::lock_guard<std::mutex> lk(mu_);
     if (seq >= seqs_.size()) return;
+    // table order: the shared base's ids, then the sequence's own
+    if (seqs_[seq].base >= 0) leave_base_locked(seqs_[seq], false);
     std::vector<uint32_t> table;
     table.swap(seqs_[seq].table);
     seqs_[seq].seq_len = 0;
@@ -248,7 +255,9 @@ bool PoolCore::append_block_to_sequence(uint32_t seq, uint32_t block) {
 bool PoolCore::get_block_table(uint32_t seq, std::vector<uint32_t>* out) {
     std::lock_guard<std::mutex> lk(mu_);
     if (seq >= seqs_.size()) return false;
-    *out = seqs_[seq].table;
+    out->clear();
+    out->reserve(table_size(seqs_[seq]));
+    for_each_id(seqs_[seq], [out](uint32_t id) { out->push_back(id); });
     return true;
 }
 
@@ -278,7 +287,9 @@ bool PoolCore::table_va_offsets(uint32_t seq, std::vector<uint64_t>* out) {
     std::lock_guard<std::mutex> lk(mu_);
     if (seq >= seqs_.size()) return false;
     out->clear();
-    for (uint32_t id : seqs_[seq].table) {
+    const SequenceState& s = seqs_[seq];
+    for (size_t i = 0, n = table_size(s); i < n; ++i) {
+        const uint32_t id = table_at(s, i);
         if (id >= blocks_.size() || !blocks_[id].in_use) return false;
         out->push_back(blocks_[id].va_offset);
     }
@@ -288,6 +299,7 @@ bool PoolCore::table_va_offsets(uint32_t seq, std::vector<uint64_t>* out) {
 uint32_t PoolCore::refcount(uint32_t block) {
     std::lock_guard<std::mutex> lk(mu_);
     if (block >= blocks_.size() || !blocks_[block].in_use) return 0;
+    if (lazy_total_ != 0 && in_base_[block] != 0) flush_lazy_locked();
     return rc_[block];
 }
 
@@ -299,7 +311,8 @@ bool PoolCore::fork_sequence(uint32_t src, uint32_t* out_seq, std::string* err) 
     }
     SequenceState s;
     s.table = take_table_locked();
-    s.table.assign(seqs_[src].table.begin(), seqs_[src].table.end());
+    s.table.reserve(table_size(seqs_[src]));
+    for_each_id(seqs_[src], [&s](uint32_t id) { s.table.push_back(id); });
     s.seq_len = seqs_[src].seq_len;
     for (uint32_t id : s.table)
         if (id < blocks_.size() && blocks_[id].in_use) ++rc_[id];
@@ -316,20 +329,21 @@ bool PoolCore::share_prefix(uint32_t src, uint32_t dst, uint32_t n, uint32_t* ou
                    dst);
         return false;
     }
-    const auto& st = seqs_[src].table;
-    if (st.size() < n) {
+    const SequenceState& st = seqs_[src];
+    if (table_size(st) < n) {
         *err = fmt("kcmm_share_prefix: src seq %llu holds %llu blocks, %llu requested", src,
-                   st.size(), n);
+                   table_size(st), n);
         return false;
     }
     for (uint32_t i = 0; i < n; ++i) {
-        if (st[i] >= blocks_.size() || !blocks_[st[i]].in_use) {
-            *err = fmt("kcmm_share_prefix: block %llu not in use", st[i]);
+        const uint32_t id = table_at(st, i);
+        if (id >= blocks_.size() || !blocks_[id].in_use) {
+            *err = fmt("kcmm_share_prefix: block %llu not in use", id);
             return false;
         }
     }
     for (uint32_t i = 0; i < n; ++i) {
-        const uint32_t id = seqs_[src].table[i];
+        const uint32_t id = table_at(seqs_[src], i);
         ++rc_[id];
         seqs_[dst].table.push_back(id);
         out[i] = id;
@@ -370,9 +384,9 @@ bool PoolCore::prefix_register(uint32_t seq, const uint64_t* hashes, uint32_t n,
         return false;
     }
     const SequenceState& s = seqs_[seq];
-    if (n > s.table.size()) {
+    if (n > table_size(s)) {
         *err = fmt("kcmm_prefix_register: seq %llu holds %llu blocks, %llu requested", seq,
-                   s.table.size(), n);
+                   table_size(s), n);
         return false;
     }
     if (static_cast<uint64_t>(n) * geo_.block_size > s.seq_len) {
@@ -381,7 +395,7 @@ bool PoolCore::prefix_register(uint32_t seq, const uint64_t* hashes, uint32_t n,
         return false;
     }
     for (uint32_t i = 0; i < n; ++i) {
-        const uint32_t id = s.table[i];
+        const uint32_t id = table_at(s, i);
         if (id >= blocks_.size() || !blocks_[id].in_use) {
             *err = fmt("kcmm_prefix_register: block %llu not in use", id);
             return false;
@@ -389,7 +403,7 @@ bool PoolCore::prefix_register(uint32_t seq, const uint64_t* hashes, uint32_t n,
     }
     for (uint32_t i = 0; i < n; ++i) {
         if (prefix_.count(hashes[i])) continue;
-        const uint32_t id = s.table[i];
+        const uint32_t id = table_at(s, i);
         prefix_.emplace(hashes[i], PrefixEntry{id, i, ++prefix_tick_});
         ++rc_[id];
         ++*added;
@@ -459,6 +473,84 @@ uint32_t PoolCore::prefix_entries() {
     return static_cast<uint32_t>(prefix_.size());
 }
 
+void PoolCore::flush_lazy_locked() {
+    for (SharedBase& b : bases_) {
+        if (b.lazy == 0) continue;
+        for (uint32_t id : b.ids) rc_[id] += b.lazy;   // every id of such a base is in use
+        lazy_total_ -= b.lazy;
+        b.lazy = 0;
+    }
+}
+
+int32_t PoolCore::new_base_locked(SequenceState& s, size_t cut) {
+    int32_t idx;
+    if (!free_bases_.empty()) {
+        idx = free_bases_.back();
+        free_bases_.pop_back();
+    } else {
+        idx = static_cast<int32_t>(bases_.size());
+        bases_.emplace_back();
+    }
+    SharedBase& b = bases_[idx];
+    b.ids = std::move(s.table);
+    s.table = take_table_locked();
+    s.table.assign(b.ids.begin() + cut, b.ids.end());
+    b.ids.resize(cut);
+    b.holders = 1;
+    b.lazy = 0;
+    b.eager_only = false;
+    for (uint32_t id : b.ids) {
+        if (id < in_base_.size()) ++in_base_[id];
+        if (id >= blocks_.size() || !blocks_[id].in_use) b.eager_only = true;
+    }
+    s.base = idx;
+    return idx;
+}
+
+void PoolCore::leave_base_locked(SequenceState& s, bool keep_refs) {
+    const int32_t idx = s.base;
+    s.base = -1;
+    SharedBase& b = bases_[idx];
+    if (keep_refs) {
+        if (b.lazy > 0) {   // this holder's references become counted ones
+            --b.lazy;
+            --lazy_total_;
+            for (uint32_t id : b.ids) ++rc_[id];
+        }
+        std::vector<uint32_t> t = take_table_locked();
+        t.reserve(b.ids.size() + s.table.size());
+        t.assign(b.ids.begin(), b.ids.end());
+        t.insert(t.end(), s.table.begin(), s.table.end());
+        s.table.swap(t);
+        if (t.capacity() != 0 && spare_tables_.size() < kMaxSpareTables) {
+            t.clear();
+            spare_tables_.push_back(std::move(t));
+        }
+    } else if (b.lazy > 0) {
+        --b.lazy;           // (every id keeps a count of 2 or more: nothing is freed)
+        --lazy_total_;
+    } else {
+        release_locked(b.ids.data(), b.ids.size());
+    }
+    if (--b.holders == 0) {
+        for (uint32_t id : b.ids)
+            if (id < in_base_.size()) --in_base_[id];
+        b.ids.clear();
+        if (b.ids.capacity() != 0 && spare_tables_.size() < kMaxSpareTables) {
+            spare_tables_.push_back(std::move(b.ids));
+            b.ids = std::vector<uint32_t>();
+        }
+        free_bases_.push_back(idx);
+    }
+}
+
+void PoolCore::poison_bases_locked(uint32_t id) {
+    for (SharedBase& b : bases_) {
+        if (b.holders == 0 || b.eager_only) continue;
+        if (std::find(b.ids.begin(), b.ids.end(), id) != b.ids.end()) b.eager_only = true;
+    }
+}
+
 bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
                           uint32_t* children, std::vector<uint32_t>* pairs, std::string* err) {
     if (width == 0) {
@@ -480,8 +572,8 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
         }
         const SequenceState& ps = seqs_[parents[i]];
         const uint32_t logical = ps.seq_len / bs;
-        if (forks == 0 || logical >= ps.table.size()) continue;   // the next token opens a new page
-        const uint32_t id = ps.table[logical];
+        if (forks == 0 || logical >= table_size(ps)) continue;   // the next token opens a new page
+        const uint32_t id = table_at(ps, logical);
         if (id >= blocks_.size() || !blocks_[id].in_use) {
             *err = fmt("kcmm_fork_beams: block %llu of parent %llu not in use", id, parents[i]);
             return false;
@@ -498,29 +590,69 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
                    needed, free_handles_.size() + grow);
         return false;
     }
+    if (forks == 0) return true;
     const size_t seqs0 = seqs_.size(), pairs0 = pairs->size();
     pairs->reserve(pairs0 + 2 * needed);
+    // parents whose forks' references are taken: (parent, through its base)
+    std::vector<std::pair<uint32_t, bool>> done;
+    done.reserve(n);
+    auto add_refs = [&](const std::vector<uint32_t>& ids, int64_t d) {
+        for (uint32_t id : ids)
+            if (id < rc_.size() && rc_[id] != 0)   // in use <=> rc > 0
+                rc_[id] = static_cast<uint32_t>(static_cast<int64_t>(rc_[id]) + d);
+    };
     for (uint32_t i = 0; i < n; ++i) {
         const uint32_t p = parents[i];
-        // the forks' references, all at once (ref fork: same ids, refcount + 1)
-        for (uint32_t id : seqs_[p].table)
-            if (id < rc_.size() && rc_[id] != 0) rc_[id] += forks;   // in use <=> rc > 0
-        const uint32_t logical = seqs_[p].seq_len / bs;
+        SequenceState& ps = seqs_[p];
+        const size_t total = table_size(ps);
+        const uint32_t logical = ps.seq_len / bs;
+        // The table up to the next-token page is shared through a base (made
+        // from the parent's own table the first time; remade when the parent
+        // has grown far past it); what follows is copied into each child.
+        const size_t cut = std::min<size_t>(logical, total);
+        if (ps.base >= 0 && !bases_[ps.base].eager_only &&
+            (bases_[ps.base].ids.size() > cut || cut - bases_[ps.base].ids.size() > kMaxSharedTail))
+            leave_base_locked(ps, true);
+        if (ps.base < 0 && cut > 0) new_base_locked(ps, cut);
+        const bool shared = ps.base >= 0 && !bases_[ps.base].eager_only;
+        if (shared) {
+            // the forks' references: through the base (counted lazily) and,
+            // for the parent's own entries, one each
+            SharedBase& b = bases_[ps.base];
+            b.holders += forks;
+            b.lazy += forks;
+            lazy_total_ += forks;
+            add_refs(ps.table, forks);
+        } else {
+            for_each_id(ps, [&](uint32_t id) {
+                if (id < rc_.size() && rc_[id] != 0) rc_[id] += forks;
+            });
+        }
+        done.emplace_back(p, shared);
+        const size_t bl = shared ? bases_[ps.base].ids.size() : 0;
         for (uint32_t c = 0; c < forks; ++c) {
             SequenceState s;
             s.table = take_table_locked();
-            s.table.assign(seqs_[p].table.begin(), seqs_[p].table.end());
-            s.seq_len = seqs_[p].seq_len;
+            if (shared) {
+                s.base = ps.base;
+                s.table.assign(ps.table.begin(), ps.table.end());
+            } else {
+                s.table.reserve(total);
+                for_each_id(ps, [&s](uint32_t id) { s.table.push_back(id); });
+            }
+            s.seq_len = ps.seq_len;
             seqs_.push_back(std::move(s));
             const uint32_t child = static_cast<uint32_t>(seqs_.size() - 1);
             children[static_cast<size_t>(i) * forks + c] = child;
-            if (logical >= seqs_[child].table.size()) continue;
-            const uint32_t old_id = seqs_[child].table[logical];
+            if (logical >= total) continue;
+            // (logical >= bl: the base ends at the next-token page)
+            const uint32_t old_id = seqs_[child].table[logical - bl];
             uint32_t new_id = 0;
             if (!alloc_one_locked(&new_id, err)) {
                 // Only a page backing that fails to map memory gets here.
                 // Undo the call: new pages back in reverse order (the free
-                // list is LIFO), references and children removed.
+                // list is LIFO), references and children removed (the
+                // parents keep their bases: the same tables).
                 for (size_t q = pairs->size(); q > pairs0; q -= 2) {
                     const uint32_t nid = (*pairs)[q - 1];
                     rc_[nid] = 1;
@@ -528,13 +660,24 @@ bool PoolCore::fork_beams(const uint32_t* parents, uint32_t n, uint32_t width,
                     ++rc_[(*pairs)[q - 2]];
                 }
                 pairs->resize(pairs0);
-                for (uint32_t j = 0; j <= i; ++j)
-                    for (uint32_t id : seqs_[parents[j]].table)
-                        if (id < rc_.size() && rc_[id] != 0) rc_[id] -= forks;
-                seqs_.resize(seqs0);
+                for (const auto& d : done) {
+                    SequenceState& q = seqs_[d.first];
+                    if (d.second) {
+                        SharedBase& b = bases_[q.base];
+                        b.holders -= forks;
+                        b.lazy -= forks;
+                        lazy_total_ -= forks;
+                        add_refs(q.table, -static_cast<int64_t>(forks));
+                    } else {
+                        for_each_id(q, [&](uint32_t id) {
+                            if (id < rc_.size() && rc_[id] != 0) rc_[id] -= forks;
+                        });
+                    }
+                }
+                while (seqs_.size() > seqs0) seqs_.pop_back();
                 return false;
             }
-            seqs_[child].table[logical] = new_id;
+            seqs_[child].table[logical - bl] = new_id;
             --rc_[old_id];
             pairs->push_back(old_id);
             pairs->push_back(new_id);
@@ -550,16 +693,18 @@ int PoolCore::cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src
         *err = fmt("kcmm_cow_block_for_append: seq_idx %llu out of bounds", seq);
         return -1;
     }
-    if (logical >= seqs_[seq].table.size()) {
+    SequenceState& s = seqs_[seq];
+    if (logical >= table_size(s)) {
         *err = fmt("kcmm_cow_block_for_append: logical block %llu >= allocated %llu", logical,
-                   seqs_[seq].table.size());
+                   table_size(s));
         return -1;
     }
-    const uint32_t old_id = seqs_[seq].table[logical];
+    const uint32_t old_id = table_at(s, logical);
     if (old_id >= blocks_.size() || !blocks_[old_id].in_use) {
         *err = fmt("kcmm_cow_block_for_append: block %llu not in use", old_id);
         return -1;
     }
+    exact_rc_locked(old_id);
     if (rc_[old_id] <= 1) return 0;
     if (blocks_[old_id].location != kLocGpu) {
         *err = fmt("kcmm_cow_block_for_append: block %llu is not resident in HBM "
@@ -568,7 +713,9 @@ int PoolCore::cow_block_for_append(uint32_t seq, uint32_t logical, uint32_t* src
     }
     uint32_t new_id;
     if (!alloc_one_locked(&new_id, err)) return -1;
-    seqs_[seq].table[logical] = new_id;
+    if (s.base >= 0 && logical < bases_[s.base].ids.size()) leave_base_locked(s, true);
+    const size_t bl = s.base >= 0 ? bases_[s.base].ids.size() : 0;
+    s.table[logical - bl] = new_id;
     --rc_[old_id];
     *src = old_id;
     *dst = new_id;
@@ -604,20 +751,22 @@ bool PoolCore::resolve_positions(const uint32_t* seqs, const uint32_t* pos, uint
             *err = fmt("kcmm_append_kv_step: seq_idx %llu out of bounds", seqs[b]);
             return false;
         }
-        const auto& table = seqs_[seqs[b]].table;
+        const SequenceState& sq = seqs_[seqs[b]];
         const size_t lb = pos[b] / geo_.block_size;
         const size_t off = pos[b] % geo_.block_size;
-        if (lb >= table.size()) {
+        if (lb >= table_size(sq)) {
             *err = fmt("kcmm_append_kv_step: logical_block %llu >= allocated %llu for seq %llu",
-                       lb, table.size(), seqs[b]);
+                       lb, table_size(sq), seqs[b]);
             return false;
         }
-        const uint32_t id = table[lb];
+        const uint32_t id = table_at(sq, lb);
         if (id >= blocks_.size() || !blocks_[id].in_use) {
             *err = fmt("kcmm_append_kv_step: block_idx %llu not in use", id);
             return false;
         }
+        exact_rc_locked(id);
         if (rc_[id] > 1) {
+            if (lazy_total_ != 0 && in_base_[id] != 0) flush_lazy_locked();   // exact count
             *err = fmt("kcmm_append_kv_step: block_idx %llu is shared (refcount %llu); "
                        "make it private with kcmm_cow_block_for_append first",
                        id, rc_[id]);
@@ -648,7 +797,9 @@ bool PoolCore::resolve_slots(const int64_t* slots, uint32_t batch, std::vector<R
                        s);
             return false;
         }
+        exact_rc_locked(static_cast<uint32_t>(id));
         if (rc_[id] > 1) {
+            if (lazy_total_ != 0 && in_base_[id] != 0) flush_lazy_locked();   // exact count
             *err = fmt("kcmm_append_kv_slots: block_idx %llu is shared (refcount %llu)", id,
                        rc_[id]);
             return false;
@@ -894,7 +1045,7 @@ Metrics PoolCore::metrics() {
     const uint64_t in_use = blocks_in_use_locked();
     uint64_t blocks_used = 0, tokens = 0;
     for (const auto& s : seqs_) {
-        blocks_used += s.table.size();
+        blocks_used += table_size(s);
         tokens += s.seq_len;
     }
     const uint64_t layers2 = geo_.num_layers * 2;

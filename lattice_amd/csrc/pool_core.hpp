@@ -97,7 +97,10 @@ struct TierMove {
 };
 
 struct SequenceState {
+    // The block table: with base >= 0 it is the shared base's ids followed by
+    // `table`, else `table` alone.
     std::vector<uint32_t> table;
+    int32_t base = -1;
     uint32_t seq_len = 0;
     bool active = true;
     int priority = 2;  // Evictable 0, Low 1, Normal 2, High 3 (ref pool.rs:69-86)
@@ -276,6 +279,61 @@ private:
     static constexpr size_t kMaxSpareTables = 1024;
     std::vector<std::vector<uint32_t>> spare_tables_;
     std::vector<uint32_t> take_table_locked();
+
+    // Shared table bases of beam forks.  fork_beams moves a parent's table
+    // up to its next-token page into a base that the parent and its
+    // children all start with, so a child costs its short tail, not a copy
+    // of the table.  The base's references are counted lazily: rc_ holds
+    // (holders - lazy) references per base id and `lazy` holders own theirs
+    // only through the base, so a fork adds holders in O(1) and a holder
+    // that leaves while lazy > 0 just decrements lazy (no block of the base
+    // can reach zero then).  The count an id would have with eager counting
+    // is rc_ + the lazy counts of the bases that list it; every path that
+    // needs it exactly (a refcount query, a release or privacy check of an
+    // id that rc_ alone puts at 1) first makes all bases eager
+    // (flush_lazy_locked), which is rare in a beam loop.  A base one of
+    // whose ids is freed while it lives (a caller freeing a block a table
+    // still holds) stays eager for good.
+    struct SharedBase {
+        std::vector<uint32_t> ids;
+        uint32_t holders = 0;
+        uint32_t lazy = 0;
+        bool eager_only = false;
+    };
+    std::vector<SharedBase> bases_;
+    std::vector<int32_t> free_bases_;
+    std::vector<uint32_t> in_base_;     // per block id: how many bases list it
+    uint64_t lazy_total_ = 0;           // sum of lazy over the bases
+    static constexpr size_t kMaxSharedTail = 64;
+
+    size_t table_size(const SequenceState& s) const {
+        return (s.base >= 0 ? bases_[s.base].ids.size() : 0) + s.table.size();
+    }
+    uint32_t table_at(const SequenceState& s, size_t i) const {
+        if (s.base >= 0) {
+            const auto& b = bases_[s.base].ids;
+            if (i < b.size()) return b[i];
+            return s.table[i - b.size()];
+        }
+        return s.table[i];
+    }
+    template <typename F>
+    void for_each_id(const SequenceState& s, F&& f) const {
+        if (s.base >= 0)
+            for (uint32_t id : bases_[s.base].ids) f(id);
+        for (uint32_t id : s.table) f(id);
+    }
+    void flush_lazy_locked();
+    // make sure rc_[id] is the exact count of an id that rc_ puts at 1
+    void exact_rc_locked(uint32_t id) {
+        if (lazy_total_ != 0 && id < in_base_.size() && in_base_[id] != 0 && rc_[id] == 1)
+            flush_lazy_locked();
+    }
+    int32_t new_base_locked(SequenceState& s, size_t cut);
+    // the sequence stops using its base: keep_refs moves the base's ids into
+    // its own table (references kept), else its references are released
+    void leave_base_locked(SequenceState& s, bool keep_refs);
+    void poison_bases_locked(uint32_t id);
     struct PrefixEntry {
         uint32_t block;
         uint32_t depth;       // position in the prefix it was registered at
