@@ -168,7 +168,7 @@ int kcmm_cow_block_for_append(kcmm_pool_t *pool, uint32_t seq_idx,
                               uint32_t *out_dst);
 
 /** Copy whole pages src->dst for every layer's K and V region (and fp8
- *  scale footers), one HIP kernel per call.  `src_dst` is a host array of
+ *  scale footers), one HIP kernel launch per 192 pairs.  `src_dst` is a host array of
  *  num_pairs (src, dst) block ids; both ids must be in use.  Enqueue only. */
 int kcmm_copy_blocks_on_stream(kcmm_pool_t *pool, const uint32_t *src_dst,
                                uint32_t num_pairs, uint64_t stream_ptr);
@@ -181,8 +181,11 @@ int kcmm_copy_blocks_on_stream(kcmm_pool_t *pool, const uint32_t *src_dst,
  *  seq_len / block_size, when already allocated) is made private as
  *  kcmm_cow_block_for_append does, in the same order as the separate calls
  *  (fork child, CoW child, next child), and all the page copies (every
- *  layer's K and V) are enqueued on stream_ptr in one kernel.  The parent
- *  keeps the original page, private again once its children have copied.
+ *  layer's K and V) are enqueued on stream_ptr (one kernel launch per 192
+ *  pages).  The parent keeps the original page, private again once its
+ *  children have copied.  The children share the parent's table up to that
+ *  page instead of copying it, so the call costs O(children) on the host,
+ *  not O(table length); refcounts reported afterwards are exact.
  *  Returns the number of pages copied, or -1. */
 int kcmm_fork_beams_on_stream(kcmm_pool_t *pool, const uint32_t *parents, uint32_t n_parents,
                               uint32_t beam_width, uint32_t *children_out,
