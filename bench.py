@@ -85,14 +85,16 @@ def parse():
     return ap.parse_args()
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "attn_decode_cfg2_hbm_traffic.txt"
+TRAFFIC_FILES = {"cfg2": ROOT / "profiles" / "attn_decode_cfg2_hbm_traffic.txt",
+                 "cfg3": ROOT / "profiles" / "attn_prefill_cfg3_hbm_traffic.txt",
+                 "cfg5": ROOT / "profiles" / "attn_decode_fp8_cfg5_hbm_traffic.txt"}
 
 
-def measured_traffic():
+def measured_traffic(config="cfg2"):
     """HBM bytes per attention call from the committed rocprofv3 counter
-    summary (None if the file is absent)."""
+    summary of that config (None if the file is absent)."""
     try:
-        for line in TRAFFIC_FILE.read_text().splitlines():
+        for line in TRAFFIC_FILES[config].read_text().splitlines():
             if line.startswith("traffic_bytes_per_call:"):
                 return int(line.split(":")[1])
     except OSError:
@@ -262,6 +264,16 @@ def bench_prefill(args):
     lib = KcmmLibrary()
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
+    if args.calib_copy:
+        # a 256 MiB device copy (256 MiB read + 256 MiB written) that the
+        # counter runs scale their FETCH_SIZE / WRITE_SIZE readings by
+        src = torch.empty(128 << 20, dtype=torch.int16, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     def timed(dtype):
         case = build_prefix_shared_case(lib, batch=16, prefix_tokens=1024, suffix_tokens=256,
@@ -297,7 +309,8 @@ def bench_prefill(args):
                    "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "block_size": BS},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic("cfg3"),
+                     "kernel": "attn_prefill_mfma (bf16 pages)"},
         "gflop_per_call": round(flops / 1e9, 2),
         # the same chunk over fp8-e4m3 pages (dequantized to bf16 in LDS by
         # the same MFMA kernel): half the K/V bytes, the same flops
@@ -655,7 +668,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(kv_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kv_gbs / HBM_PEAK_GBS, 4),
                      # counter-measured HBM bytes exist for the Cfg2 call only
-                     "traffic": measured_traffic() if args.config == "cfg2" else None,
+                     "traffic": measured_traffic(args.config),
                      "kernel": "paged decode attention call (attn_decode_stream + attn_decode_merge)",
                      "algorithmic_bytes": kv_bytes},
         "append_us": round((per["append"] if args.attn_only else extra["append"]) * 1e3, 2),
