@@ -213,19 +213,22 @@ def _layer_weights(torch, rng, h, inter, hq, hkv, d):
     return w, dev, lw
 
 
-@pytest.mark.parametrize("hq,hkv,d,h,inter,dtype", [
-    (8, 2, 64, 512, 768, KV_BF16), (32, 8, 128, 4096, 1024, KV_BF16), (32, 8, 72, 512, 768, KV_BF16),
-    (32, 8, 128, 4096, 1024, KV_FP8), (8, 2, 64, 512, 768, KV_FP8)])
-def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter, dtype):
+@pytest.mark.parametrize("hq,hkv,d,h,inter,dtype,nseq", [
+    (8, 2, 64, 512, 768, KV_BF16, 4), (32, 8, 128, 4096, 1024, KV_BF16, 4),
+    (32, 8, 72, 512, 768, KV_BF16, 4), (32, 8, 128, 4096, 1024, KV_FP8, 4),
+    (8, 2, 64, 512, 768, KV_FP8, 4), (8, 2, 64, 512, 768, KV_BF16, 136)])
+def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter, dtype, nseq):
     """One decoder layer through kcmm_decode_layer_step_on_stream vs the
     oracle's layer (RMSNorm, QKV, RoPE + append, paged attention,
     O + residual, RMSNorm, gate/up, SiLU*up, down + residual).  head_dim 72
     takes the unfused QKV path (projection, then the RoPE/append kernel).
     fp8 pools: the new rows go through the fp8 page writer (bf16 activations,
     fp8 K/V); tolerances are the fp8 attention's (3e-2 on the layer output,
-    8e-2 on its update)."""
+    8e-2 on its update).  136 tokens take the 256-token tiles of the fused
+    projections."""
     import torch
-    lens = [1, 16, 17, 130]
+    lens = ([1, 16, 17, 130] if nseq == 4 else
+            np.random.default_rng(nseq).integers(1, 70, size=nseq).tolist())
     fp8 = dtype == KV_FP8
     case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
                              block_size=16, ctx_lens=lens, dtype=dtype, seed=h)
@@ -387,18 +390,21 @@ def _layer_weights_fp8(torch, rng, h, inter, hq, hkv, d, pow2=False):
     return w, exact, dev, lw
 
 
-@pytest.mark.parametrize("hq,hkv,d,h,inter,dtype", [
-    (8, 2, 64, 512, 768, KV_BF16), (32, 8, 128, 4096, 1024, KV_BF16),
-    (32, 8, 72, 512, 768, KV_BF16), (32, 8, 128, 4096, 1024, KV_FP8)])
-def test_decode_layers_fp8_weights(gpu_lib, hq, hkv, d, h, inter, dtype):
+@pytest.mark.parametrize("hq,hkv,d,h,inter,dtype,nseq", [
+    (8, 2, 64, 512, 768, KV_BF16, 4), (32, 8, 128, 4096, 1024, KV_BF16, 4),
+    (32, 8, 72, 512, 768, KV_BF16, 4), (32, 8, 128, 4096, 1024, KV_FP8, 4),
+    (8, 2, 64, 512, 768, KV_BF16, 128), (8, 2, 64, 512, 768, KV_BF16, 136)])
+def test_decode_layers_fp8_weights(gpu_lib, hq, hkv, d, h, inter, dtype, nseq):
     """Two layers through kcmm_decode_layers_fp8w_on_stream (fp8-e4m3
     projections, fp32 row scales) vs the oracle's layer applied twice with
     the dequantized weights: layer 0's down projection leaves partials that
     layer 1's RMSNorm finishes, layer 1's adds its residual itself.  head_dim
-    72 takes the unfused QKV path.  Tolerances as the bf16 layer step's (fp8
+    72 takes the unfused QKV path; 128 and 136 tokens take the fp8 GEMM's
+    128-token and 256-token tiles.  Tolerances as the bf16 layer step's (fp8
     pages: the fp8 attention's)."""
     import torch
-    lens = [1, 16, 17, 130]
+    lens = ([1, 16, 17, 130] if nseq == 4 else
+            np.random.default_rng(nseq).integers(1, 70, size=nseq).tolist())
     fp8 = dtype == KV_FP8
     case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
                              block_size=16, ctx_lens=lens, dtype=dtype, seed=h, num_layers=2)
