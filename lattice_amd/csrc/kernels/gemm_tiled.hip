@@ -275,39 +275,59 @@ void by_config(int id, F&& f) {
     }
 }
 
-// Configuration 0 (128 x 256), 1 (128 x 128) or 4 (64 x 64), the first that
-// reaches 224 workgroups -- about one per CU -- with a K split whose fp32
-// partials stay within 30% of the weight bytes (2 s M / K <= 0.3) and whose
-// splits are at least 8 chunks long.  KCMM_GEMM_TILE (configuration index)
-// and KCMM_GEMM_SPLITS override.
+// Tile and K split by a cost model fitted to cold-cache timings (weights
+// not resident in the Infinity Cache, as in a model's layer loop): among
+// the nontemporal-weight configurations 0 (128 x 256), 9 (128 x 128) and
+// 10 (64 x 64), and splits whose parts are at least 8 chunks long, the one
+// that minimises
+//   (weight bytes + 3 x fp32 partial bytes + L2->LDS bytes / 2) / efficiency
+// where L2->LDS bytes = 2 N M K (1/BM + 1/BN) (each tile loads its weight
+// rows and tokens) and efficiency = the fraction of workgroup slots the grid
+// fills in its last round (one workgroup per CU for configurations 0 and 9,
+// two for 10) times the fraction of each token tile that is real tokens
+// (partials count three times: written, read back, and the reduction's own
+// launch).
+// At the Llama-3-8B shapes this picks 9 x 2 / 9 x 4 for QKV / O at M = 256
+// (32.5 / 24.7 us against 46.8 / 30.2 for 64 x 64 unsplit, caches flushed),
+// 9 x 1 / 9 x 2 at M = 512, and keeps 0 for gate/up and 0 x 8 (M = 256) /
+// 0 x 4 (M = 512) for down.  KCMM_GEMM_TILE
+// (configuration index) and KCMM_GEMM_SPLITS override.
 TiledConfig choose(int M, int N, int K) {
     const int chunks = K / 64;
-    auto max_splits = [&](int tiles) {
-        int s = 1;
-        while (tiles * s < 224 && s < 16 && chunks % (2 * s) == 0 && chunks / (2 * s) >= 8 &&
-               2.0 * (2 * s) * M / K <= 0.3)
-            s *= 2;
-        return s;
-    };
     const int forced_tile = env_int("KCMM_GEMM_TILE", -1);
-    int id = -1, splits = 1;
+    auto ok_split = [&](int s) { return chunks % s == 0 && chunks / s >= 8; };
+    TiledConfig best{-1, 0, 0, 1};
     if (forced_tile >= 0 && forced_tile < kCfgs && N % kCfgBN[forced_tile] == 0) {
-        id = forced_tile;
-        splits = max_splits((N / kCfgBN[id]) * ((M + kCfgBM[id] - 1) / kCfgBM[id]));
+        best = TiledConfig{forced_tile, kCfgBN[forced_tile], kCfgBM[forced_tile], 1};
     } else {
-        for (int cand : {0, 1, 4}) {
-            if (N % kCfgBN[cand]) continue;
-            const int tiles = (N / kCfgBN[cand]) * ((M + kCfgBM[cand] - 1) / kCfgBM[cand]);
-            id = cand;
-            splits = max_splits(tiles);
-            if (tiles * splits >= 224) break;
+        double best_cost = 0.0;
+        const double wbytes = 2.0 * N * K;
+        for (int cand : {0, 9, 10}) {
+            const int bn = kCfgBN[cand], bm = kCfgBM[cand];
+            if (N % bn) continue;
+            const int tiles_m = (M + bm - 1) / bm;
+            const int tiles = (N / bn) * tiles_m;
+            const int slots = cand == 10 ? 512 : 256;
+            const double real = static_cast<double>(M) / (tiles_m * bm);
+            const double l2 = 2.0 * N * M * K * (1.0 / bm + 1.0 / bn);
+            for (int s = 1; s <= 16; s *= 2) {
+                if (!ok_split(s)) break;
+                const int wgs = tiles * s;
+                const int rounds = (wgs + slots - 1) / slots;
+                const double eff = static_cast<double>(wgs) / (rounds * slots) * real;
+                const double part = s > 1 ? 4.0 * s * M * N : 0.0;
+                const double cost = (wbytes + 3.0 * part + 0.5 * l2) / eff;
+                if (best.id < 0 || cost < best_cost) {
+                    best = TiledConfig{cand, bn, bm, s};
+                    best_cost = cost;
+                }
+            }
         }
-        if (id < 0) id = 3;   // N % 64 == 0 only
+        if (best.id < 0) best = TiledConfig{3, kCfgBN[3], kCfgBM[3], 1};   // N % 64 == 0 only
     }
-    TiledConfig c{id, kCfgBN[id], kCfgBM[id], splits};
     const int forced = env_int("KCMM_GEMM_SPLITS", 0);
-    if (forced >= 1 && forced <= 16 && chunks % forced == 0) c.splits = forced;
-    return c;
+    if (forced >= 1 && forced <= 16 && chunks % forced == 0) best.splits = forced;
+    return best;
 }
 
 }  // namespace
