@@ -106,6 +106,21 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def quantize_layer_fp8(w):
+    """fp8-e4m3 copies of a layer's four projections (per-row amax/448 scales,
+    quantized on the device) and the ABI struct of the fp8-weight layer."""
+    import torch
+    from lattice_amd.bindings import KcmmLayerWeightsFp8
+    w8 = {"attn_norm": w["attn_norm"], "mlp_norm": w["mlp_norm"]}
+    for name, _, _ in GEMMS:
+        wf = w[name].float()
+        sc = (wf.abs().amax(dim=1) / 448.0).clamp_min(1e-30)
+        w8[name] = (wf / sc[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+        w8[name + "_scale"] = sc.contiguous()
+        del wf
+    return w8, KcmmLayerWeightsFp8(**{k: t.data_ptr() for k, t in w8.items()})
+
+
 def cpu_baseline(case, seconds, threads):
     """The reference kernel's loop (oracle restatement) on host cores, on a
     bounded sample: layer 0 of the same workload, the first sequences that
@@ -331,7 +346,7 @@ def main():
     if args.gemm_only:
         return bench_gemm(args)
     import torch
-    from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, KcmmLayerWeightsFp8, KcmmLibrary
+    from lattice_amd.bindings import KV_BF16, KcmmLayerWeights, KcmmLibrary
     from lattice_amd.workload import build_decode_case, rope_inv_freq
 
     assert torch.cuda.is_available(), "bench needs a GPU"
@@ -450,16 +465,9 @@ def main():
     weights8, layer_w8 = [], []
     if args.config == "cfg2" and not args.attn_only:
         for w in weights:
-            w8 = {"attn_norm": w["attn_norm"], "mlp_norm": w["mlp_norm"]}
-            for name, n, k in GEMMS:
-                wf = w[name].float()
-                sc = (wf.abs().amax(dim=1) / 448.0).clamp_min(1e-30)
-                w8[name] = (wf / sc[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn) \
-                    .view(torch.uint8)
-                w8[name + "_scale"] = sc.contiguous()
-                del wf
+            w8, lw8 = quantize_layer_fp8(w)
             weights8.append(w8)
-            layer_w8.append(KcmmLayerWeightsFp8(**{k: t.data_ptr() for k, t in w8.items()}))
+            layer_w8.append(lw8)
 
     def decode_step_fp8w(_):
         """decode_step with the fp8-weight layers (kcmm_decode_layers_fp8w_on_stream)."""
@@ -724,13 +732,40 @@ def main():
         torch.cuda.synchronize()
         t_l = e0.elapsed_time(e1) / reps / args.layers
         assert torch.isfinite(hid5.float()).all(), "fp8 layer step produced non-finite hidden state"
+        # the same with fp8-e4m3 projection weights (kcmm_decode_layers_fp8w_on_stream)
+        w8, lw8 = quantize_layer_fp8(w)
+
+        def fp8_layers_fp8w():
+            case.pool.decode_layers_fp8w(first_layer=0, weights=[lw8] * args.layers,
+                                         hidden_ptr=hid5.data_ptr(),
+                                         block_tables_ptr=dv["bt"].data_ptr(),
+                                         seq_lens_ptr=dv["sl"].data_ptr(),
+                                         block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                         inv_freq_ptr=inv_freq.data_ptr(), batch=B,
+                                         hidden_size=HIDDEN, num_q_heads=HQ,
+                                         intermediate_size=INTER, max_blocks_per_seq=case.mbps,
+                                         rms_eps=RMS_EPS, stream_ptr=sp)
+        fp8_layers_fp8w()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            fp8_layers_fp8w()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t_l8 = e0.elapsed_time(e1) / reps / args.layers
+        assert torch.isfinite(hid5.float()).all(), "fp8-weight layer step produced non-finite state"
+        del w8
         result["fp8_layer_step"] = {
             "t_layer_us": round(t_l * 1e3, 2), "layers_per_call": args.layers, "batch": B,
             "kv_bytes_per_layer": kv_bytes,
             "note": "kcmm_decode_layers_on_stream on the fp8 pool: RMSNorm, QKV (partials) + "
                     "RoPE + fp8 append, fp8 attention, O + residual + RMSNorm, gate/up + SwiGLU, "
-                    "down + residual; HIP events around the calls"}
-        log(f"fp8 layer step: {t_l * 1e3:.1f} us per layer ({args.layers} layers per call)")
+                    "down + residual; HIP events around the calls",
+            "t_layer_fp8_weights_us": round(t_l8 * 1e3, 2),
+            "note_fp8_weights": "the same layers through kcmm_decode_layers_fp8w_on_stream with "
+                                "fp8-e4m3 projection weights (per-row amax/448 scales)"}
+        log(f"fp8 layer step: {t_l * 1e3:.1f} us per layer ({args.layers} layers per call); "
+            f"with fp8 weights {t_l8 * 1e3:.1f} us")
         del w, hid5
     if not args.attn_only:
         t_step_s = extra["decode_step"] / 1e3
