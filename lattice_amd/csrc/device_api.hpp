@@ -121,6 +121,10 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
 bool gemm_bf16_tiled(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
                      uint64_t stream, uint64_t residual, std::string* err);
 void gemm_tiled_plan(uint32_t m, uint32_t n, uint32_t k, int* splits, int* tile);
+// The tiled kernel for either weight type: bf16 W (wscale == 0) or fp8-e4m3
+// W [n][k] with an fp32 scale per row (as gemm_fp8w_bf16).
+bool gemm_tiled(uint64_t x, uint64_t w, uint64_t wscale, uint64_t y, uint32_t m, uint32_t n,
+                uint32_t k, uint64_t stream, uint64_t residual, std::string* err);
 
 // How a plain product of this shape runs (under the current KCMM_GEMM_*
 // settings): kernel 0 = weight-stream, 1 = LDS-tiled; K splits; tiling (tiled

@@ -596,7 +596,7 @@ bool gemm_plan(uint32_t m, uint32_t n, uint32_t k, bool fp8_weights, GemmPlan* p
                std::string* err) {
     if (!shape_ok(m, n, k, err)) return false;
     *plan = GemmPlan{};
-    if (!fp8_weights && m > 128 && env_int("KCMM_GEMM_TILED", 1) != 0) {
+    if (m > 128 && env_int("KCMM_GEMM_TILED", 1) != 0) {
         plan->kernel = 1;
         gemm_tiled_plan(m, n, k, &plan->splits, &plan->tile);
     } else {
@@ -618,6 +618,10 @@ bool gemm_fp8w_bf16(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32
         *err = "fp8 weights need their row scales";
         return false;
     }
+    // many tokens: the LDS-tiled kernel (KCMM_GEMM_TILED=0 keeps the
+    // weight-stream kernel)
+    if (m > 128 && env_int("KCMM_GEMM_TILED", 1) != 0)
+        return gemm_tiled(x, w8, wscale, y, m, n, k, stream, residual, err);
     GemmParams p = base_params(x, w8, m, n, k);
     p.Y = reinterpret_cast<uint16_t*>(y);
     p.R = reinterpret_cast<const uint16_t*>(residual);

@@ -22,7 +22,12 @@
 //    tile then comes from HBM once and from that XCD's L2 for the rest;
 //  * optional K split: each split writes fp32 partials, summed in split
 //    order by gemm_split_reduce (the same partial layout as the streaming
-//    kernel).
+//    kernel);
+//  * fp8-e4m3 weights (WF8): the weight tile is staged as codes, 64-byte
+//    LDS rows of four 16-byte pieces (piece p of row r at slot
+//    p ^ ((r >> 2) & 3)), each MFMA operand read as 8 codes and converted
+//    exactly to bf16 in registers; the fp32 row scale multiplies the
+//    accumulator before the store.
 #include <algorithm>
 #include <cstdlib>
 #include <string>
@@ -62,7 +67,8 @@ __device__ __forceinline__ void wait_lgkm0() {
 
 struct TiledParams {
     const uint8_t* X;    // [M][K] bf16
-    const uint8_t* W;    // [N][K] bf16
+    const uint8_t* W;    // [N][K] bf16, or e4m3 codes with WF8
+    const float* wscale; // WF8: fp32 scale per weight row [N]
     uint16_t* Y;         // [M][N]
     const uint16_t* R;   // residual [M][N] or null (may equal Y)
     float* part;         // non-null: fp32 partials [split][M][N]
@@ -78,16 +84,28 @@ __device__ __forceinline__ u32x2 pack4(f32x4 v) {
     return o;
 }
 
+// Eight e4m3 codes (two dwords) -> eight bf16, exactly.
+__device__ __forceinline__ u32x4 fp8x8_bf16(u32x2 d) {
+    u32x4 r;
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[0], 1.0f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[0], 1.0f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[1], 1.0f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[1], 1.0f, true));
+    return r;
+}
+
 // WN x WM waves, each accumulating (BN/WN) x (BM/WM) of the tile.
-template <int BN, int BM, int WN, int WM, int NS, bool WNT>
+template <int BN, int BM, int WN, int WM, int NS, bool WNT, bool WF8 = false>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_tiled_kernel(TiledParams p) {
     constexpr int NWAVES = WN * WM;
-    constexpr int KT = 64;                  // k per chunk: 128-byte LDS rows
-    constexpr int WB = BN * 128, XB = BM * 128, SB = WB + XB;
-    constexpr int WL = BN / (8 * NWAVES), XL = BM / (8 * NWAVES);   // loads per wave per chunk
+    constexpr int KT = 64;                  // k per chunk: 128-byte LDS rows (fp8 weights: 64)
+    constexpr int WROW = WF8 ? 64 : 128;    // LDS bytes per weight row per chunk
+    constexpr int WRI = 1024 / WROW;        // weight rows per load instruction
+    constexpr int WB = BN * WROW, XB = BM * 128, SB = WB + XB;
+    constexpr int WL = BN / (WRI * NWAVES), XL = BM / (8 * NWAVES);   // loads per wave per chunk
     constexpr int TN = BN / WN, TM = BM / WM;                     // wave tile
     constexpr int FA = TN / 16, FB = TM / 16;                     // MFMA fragments per k-step
-    static_assert(WL * 8 * NWAVES == BN && XL * 8 * NWAVES == BM, "tile rows split over the waves");
+    static_assert(WL * WRI * NWAVES == BN && XL * 8 * NWAVES == BM, "tile rows split over the waves");
     static_assert(TN % 16 == 0 && TM % 16 == 0, "wave tile");
     static_assert(NS * SB <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * SB];
@@ -105,6 +123,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_tiled_kernel(TiledParams p)
     const int kbeg = blockIdx.y * p.klen;
     const int nchunks = p.klen / KT;
     const size_t rowb = static_cast<size_t>(p.K) * 2;
+    const size_t wrowb = static_cast<size_t>(p.K) * (WF8 ? 1 : 2);
 
     // Direct loads: instruction i of wave w fills LDS rows 8*(NWAVES*i + w)
     // .. +8 of the W (then X) tile; lane l writes slot l & 7 of row
@@ -115,8 +134,16 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_tiled_kernel(TiledParams p)
     const uint8_t* xsrc[XL];
 #pragma unroll
     for (int i = 0; i < WL; ++i) {
-        const int r = 8 * (NWAVES * i + wave) + lrow;
-        wsrc[i] = p.W + (n0 + r) * rowb + static_cast<size_t>(kbeg) * 2 + lpiece * 16;
+        if constexpr (WF8) {
+            // 16 rows x 64 bytes per instruction: lane l fills slot l & 3 of
+            // row 16*(NWAVES*i + w) + (l >> 2) with piece (l & 3) ^ ((row >> 2) & 3)
+            const int r = 16 * (NWAVES * i + wave) + (lane >> 2);
+            const int pc = (lane & 3) ^ ((lane >> 4) & 3);
+            wsrc[i] = p.W + (n0 + r) * wrowb + static_cast<size_t>(kbeg) + pc * 16;
+        } else {
+            const int r = 8 * (NWAVES * i + wave) + lrow;
+            wsrc[i] = p.W + (n0 + r) * wrowb + static_cast<size_t>(kbeg) * 2 + lpiece * 16;
+        }
     }
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
@@ -126,10 +153,11 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_tiled_kernel(TiledParams p)
     auto issue = [&](int c) {
         uint8_t* st = lds + (c % NS) * SB;
         const size_t ko = static_cast<size_t>(c) * KT * 2;
+        const size_t kw = static_cast<size_t>(c) * KT * (WF8 ? 1 : 2);
 #pragma unroll
         for (int i = 0; i < WL; ++i) {
-            if constexpr (WNT) load_lds16_nt(wsrc[i] + ko, st + (NWAVES * i + wave) * 1024);
-            else load_lds16(wsrc[i] + ko, st + (NWAVES * i + wave) * 1024);
+            if constexpr (WNT) load_lds16_nt(wsrc[i] + kw, st + (NWAVES * i + wave) * 1024);
+            else load_lds16(wsrc[i] + kw, st + (NWAVES * i + wave) * 1024);
         }
 #pragma unroll
         for (int i = 0; i < XL; ++i) load_lds16(xsrc[i] + ko, st + WB + (NWAVES * i + wave) * 1024);
@@ -151,7 +179,14 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_tiled_kernel(TiledParams p)
 #pragma unroll
         for (int i = 0; i < FA; ++i) {
             const int r = wn * TN + 16 * i + ln;
-            a[i] = *reinterpret_cast<const u32x4*>(st + r * 128 + ((pc ^ (r & 7)) * 16));
+            if constexpr (WF8) {
+                // codes k = ks*32 + 8*lg .. +8: piece 2 ks + lg/2, half lg & 1
+                const int pp = 2 * ks + (lg >> 1);
+                a[i] = fp8x8_bf16(*reinterpret_cast<const u32x2*>(
+                    st + r * 64 + ((pp ^ ((r >> 2) & 3)) * 16) + (lg & 1) * 8));
+            } else {
+                a[i] = *reinterpret_cast<const u32x4*>(st + r * 128 + ((pc ^ (r & 7)) * 16));
+            }
         }
 #pragma unroll
         for (int j = 0; j < FB; ++j) {
@@ -216,6 +251,10 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_tiled_kernel(TiledParams p)
 #pragma unroll
         for (int i = 0; i < FA; ++i) {
             const int n = n0 + wn * TN + 16 * i + 4 * lg;
+            if constexpr (WF8) {
+                const f32x4 s4 = {p.wscale[n], p.wscale[n + 1], p.wscale[n + 2], p.wscale[n + 3]};
+                acc[i][j] *= s4;
+            }
             if (p.part != nullptr) {
                 *reinterpret_cast<f32x4*>(p.part + (static_cast<size_t>(blockIdx.y) * p.M + m) * p.N + n) =
                     acc[i][j];
@@ -340,16 +379,17 @@ void gemm_tiled_plan(uint32_t m, uint32_t n, uint32_t k, int* splits, int* tile)
     *tile = c.id;
 }
 
-bool gemm_bf16_tiled(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
-                     uint64_t stream, uint64_t residual, std::string* err) {
+bool gemm_tiled(uint64_t x, uint64_t w, uint64_t wscale, uint64_t y, uint32_t m, uint32_t n,
+                uint32_t k, uint64_t stream, uint64_t residual, std::string* err) {
     if (m == 0 || n % 64 != 0 || k % 64 != 0) {
-        *err = "tiled gemm_bf16 needs m > 0, n % 64 == 0 and k % 64 == 0";
+        *err = "tiled gemm needs m > 0, n % 64 == 0 and k % 64 == 0";
         return false;
     }
     const TiledConfig c = choose(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k));
     TiledParams p{};
     p.X = reinterpret_cast<const uint8_t*>(x);
     p.W = reinterpret_cast<const uint8_t*>(w);
+    p.wscale = reinterpret_cast<const float*>(wscale);
     p.Y = reinterpret_cast<uint16_t*>(y);
     p.R = reinterpret_cast<const uint16_t*>(residual);
     p.M = static_cast<int>(m);
@@ -371,13 +411,22 @@ bool gemm_bf16_tiled(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n,
         constexpr int BN = decltype(bn)::value, BM = decltype(bm)::value;
         constexpr int WN = decltype(wn)::value, WM = decltype(wm)::value, NS = decltype(ns)::value;
         constexpr bool NT = decltype(nt)::value;
-        hipLaunchKernelGGL((gemm_tiled_kernel<BN, BM, WN, WM, NS, NT>), dim3(tiles, c.splits),
-                           dim3(64 * WN * WM), 0, s, p);
+        if (wscale != 0)
+            hipLaunchKernelGGL((gemm_tiled_kernel<BN, BM, WN, WM, NS, NT, true>),
+                               dim3(tiles, c.splits), dim3(64 * WN * WM), 0, s, p);
+        else
+            hipLaunchKernelGGL((gemm_tiled_kernel<BN, BM, WN, WM, NS, NT>), dim3(tiles, c.splits),
+                               dim3(64 * WN * WM), 0, s, p);
     });
     KCMM_HIP_CHECK(hipGetLastError(), err);
     if (c.splits > 1)
         return gemm_split_reduce_launch(p.part, p.Y, p.R, p.M * p.N, c.splits, stream, err);
     return true;
+}
+
+bool gemm_bf16_tiled(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
+                     uint64_t stream, uint64_t residual, std::string* err) {
+    return gemm_tiled(x, w, 0, y, m, n, k, stream, residual, err);
 }
 
 }  // namespace dev

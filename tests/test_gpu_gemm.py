@@ -181,6 +181,45 @@ def test_fp8_weights_llama3_8b_projections(gpu_lib, m, n, k):
     assert err <= 1e-2
 
 
+@pytest.mark.parametrize("tile", [str(i) for i in range(11)])
+@pytest.mark.parametrize("splits", ["1", "2", "4"])
+def test_fp8_weights_tiled(gpu_lib, monkeypatch, tile, splits):
+    """fp8 weights with more than 128 tokens take the LDS-tiled kernel (codes
+    staged in 64-byte LDS rows, converted to bf16 as they are read): every
+    tiling with 1, 2 or 4 K splits, M not a multiple of the tile, against the
+    fp64 oracle; two calls give the same bits; the weight-stream kernel
+    (KCMM_GEMM_TILED=0) agrees within the same tolerance."""
+    import torch
+    monkeypatch.setenv("KCMM_GEMM_TILE", tile)
+    monkeypatch.setenv("KCMM_GEMM_SPLITS", splits)
+    m, n, k = 300, 768, 1024
+    rng = np.random.default_rng(int(tile) * 10 + int(splits) + 5)
+    xb = O.encode(O.BF16, rng.standard_normal((m, k)))
+    w8, s, w8d, sd = _fp8_weights(torch, rng, n, k, 0.02)
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    assert gpu_lib.gemm_plan(m, n, k, fp8_weights=True)["kernel"] == "tiled"
+    outs = []
+    for _ in range(2):
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        gpu_lib.gemm_fp8w_bf16(x.data_ptr(), w8d.data_ptr(), sd.data_ptr(), y.data_ptr(), m, n, k,
+                               torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(outs[0], outs[1])
+    got = O.decode(O.BF16, outs[0]).astype(np.float64)
+    ref = O.gemm_fp8w_f64(xb, w8, s)
+    err = rel_err(got, ref)
+    print(f"fp8w tiled tile={tile} splits={splits} err={err:.3e}", flush=True)
+    assert err <= 1e-2
+    monkeypatch.setenv("KCMM_GEMM_TILED", "0")
+    y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.gemm_fp8w_bf16(x.data_ptr(), w8d.data_ptr(), sd.data_ptr(), y.data_ptr(), m, n, k,
+                           torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    stream = O.decode(O.BF16, y.cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+    assert rel_err(stream, ref) <= 1e-2
+
+
 @pytest.mark.parametrize("splits", ["1", "2", "4", "8"])
 def test_fp8_weights_split_k(gpu_lib, monkeypatch, splits):
     import torch
