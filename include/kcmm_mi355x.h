@@ -283,8 +283,10 @@ int kcmm_gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t fp8_weights, int
  *  weight-only fp8 quantization (half the weight bytes a decode step
  *  streams).  bf16 activations and output, fp32 accumulation on bf16 MFMA
  *  (the weights are converted to bf16 exactly in registers; the row scale
- *  multiplies the accumulated dot product).  Weight-stream kernel at every
- *  m.  Enqueue only; k % 256 == 0, n % 64 == 0. */
+ *  multiplies the accumulated dot product).  m <= 128 runs the
+ *  weight-stream kernel, m > 128 the LDS-tiled kernel (codes staged in LDS,
+ *  converted as they are read; KCMM_GEMM_TILED=0 keeps the weight-stream
+ *  kernel).  Enqueue only; k % 256 == 0, n % 64 == 0. */
 int kcmm_gemm_fp8w_bf16_on_stream(uint64_t x_ptr, uint64_t w8_ptr, uint64_t wscale_ptr,
                                   uint64_t y_ptr, uint32_t m, uint32_t n, uint32_t k,
                                   uint64_t stream_ptr);

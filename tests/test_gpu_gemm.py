@@ -287,7 +287,8 @@ def test_gemm_plan(gpu_lib, monkeypatch):
     assert p["kernel"] == "stream" and p["tile"] == -1
     assert p["partial_bytes"] == (p["splits"] * 64 * 6144 * 4 if p["splits"] > 1 else 0)
     assert gpu_lib.gemm_plan(256, 6144, 4096)["kernel"] == "tiled"
-    assert gpu_lib.gemm_plan(256, 6144, 4096, fp8_weights=True)["kernel"] == "stream"
+    assert gpu_lib.gemm_plan(256, 6144, 4096, fp8_weights=True)["kernel"] == "tiled"
+    assert gpu_lib.gemm_plan(128, 6144, 4096, fp8_weights=True)["kernel"] == "stream"
     monkeypatch.setenv("KCMM_GEMM_SPLITS", "2")
     assert gpu_lib.gemm_plan(64, 512, 4096)["splits"] == 2
     monkeypatch.setenv("KCMM_GEMM_TILED", "0")
