@@ -302,12 +302,14 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     // row of lsum[cb] holds the column sums of the 16-bit P used for O
     const u32x4 ones = MDT == kDtF16 ? u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}
                                     : u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-    float m_run[NCB];
+    float m_run[NCB], nmu[NCB];
+    bool all_seen = false;   // every column of the wave has a finite maximum
     f32x4 lsum[NCB];
     f32x4 acc[NCB][DB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
         m_run[cb] = -INFINITY;
+        nmu[cb] = 0.0f;
         lsum[cb] = f32x4{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < DB; ++i) acc[cb][i] = f32x4{0, 0, 0, 0};
@@ -350,37 +352,71 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                     for (int r = 0; r < 4; ++r)
                         if (key0 + 16 * hb + r > qpos[cb]) s[cb][hb][r] = -INFINITY;
         }
-        // column maxima of the raw scores (scale > 0), masked keys -inf
-        float mt[NCB];
-        bool grow[NCB];
-        bool any_grow = false;
+        // exp arguments s * scale_log2 - m with the running column maxima m
+        // (-m kept in nmu; 0 for a column with no visible key yet, whose P is
+        // then 0 through its masked scores).  The maxima are recomputed only
+        // when some argument exceeds 7.99 -- a column maximum may have grown
+        // by more than 8 -- or while some column has seen no key: for
+        // |m| < 2^16 (the rounding of m + 8 below 0.01) this takes the exact
+        // rule below on every tile where it would rescale, and skips the
+        // cross-lane maxima on the others.
+        float arg[NCB][NKB][4];
+        auto args = [&]() {
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-            float x = -INFINITY;
+            for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+                for (int hb = 0; hb < NKB; ++hb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        arg[cb][hb][r] = fmaf(s[cb][hb][r], p.scale_log2, nmu[cb]);
+        };
+        args();
+        float amax = -INFINITY;
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
             for (int hb = 0; hb < NKB; ++hb)
-                x = vmax(x, vmax(vmax(s[cb][hb][0], s[cb][hb][1]), vmax(s[cb][hb][2], s[cb][hb][3])));
-            mt[cb] = col_max(x) * p.scale_log2;
-            // rescale only when the column maximum grows by more than 8
-            grow[cb] = mt[cb] > m_run[cb] + 8.0f;
-            any_grow |= grow[cb];
-        }
-        if (__builtin_amdgcn_ballot_w64(any_grow)) {
+                amax = vmax(amax, vmax(vmax(arg[cb][hb][0], arg[cb][hb][1]),
+                                       vmax(arg[cb][hb][2], arg[cb][hb][3])));
+        if (__builtin_amdgcn_ballot_w64(amax > 7.99f) || !all_seen) {
+            // column maxima of the raw scores (scale > 0), masked keys -inf
+            float mt[NCB];
+            bool grow[NCB];
+            bool any_grow = false;
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
-                if (!__builtin_amdgcn_ballot_w64(grow[cb])) continue;
-                // (a column that does not grow keeps its scale exactly)
-                const float corr = grow[cb] ? __builtin_amdgcn_exp2f(m_run[cb] - mt[cb]) : 1.0f;
-                lsum[cb] *= corr;
+                float x = -INFINITY;
 #pragma unroll
-                for (int db = 0; db < DB; ++db) acc[cb][db] *= corr;
-                m_run[cb] = grow[cb] ? mt[cb] : m_run[cb];
+                for (int hb = 0; hb < NKB; ++hb)
+                    x = vmax(x, vmax(vmax(s[cb][hb][0], s[cb][hb][1]), vmax(s[cb][hb][2], s[cb][hb][3])));
+                mt[cb] = col_max(x) * p.scale_log2;
+                // rescale only when the column maximum grows by more than 8
+                grow[cb] = mt[cb] > m_run[cb] + 8.0f;
+                any_grow |= grow[cb];
+            }
+            if (__builtin_amdgcn_ballot_w64(any_grow)) {
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) {
+                    if (!__builtin_amdgcn_ballot_w64(grow[cb])) continue;
+                    // (a column that does not grow keeps its scale exactly)
+                    const float corr = grow[cb] ? __builtin_amdgcn_exp2f(m_run[cb] - mt[cb]) : 1.0f;
+                    lsum[cb] *= corr;
+#pragma unroll
+                    for (int db = 0; db < DB; ++db) acc[cb][db] *= corr;
+                    m_run[cb] = grow[cb] ? mt[cb] : m_run[cb];
+                }
+                bool unseen = false;
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) {
+                    nmu[cb] = m_run[cb] == -INFINITY ? 0.0f : -m_run[cb];
+                    unseen |= m_run[cb] == -INFINITY;
+                }
+                all_seen = !__builtin_amdgcn_ballot_w64(unseen);
+                args();
             }
         }
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) {
-            // a column with no visible key yet keeps m = -inf and P = 0
-            const float nmu = m_run[cb] == -INFINITY ? 0.0f : -m_run[cb];
 #pragma unroll
             for (int j = 0; j < NKS; ++j) {
                 // k-step j: keys 4lg..+3 of block 2j, then of block 2j + 1
@@ -389,8 +425,7 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        pv[4 * h + r] =
-                            __builtin_amdgcn_exp2f(fmaf(s[cb][2 * j + h][r], p.scale_log2, nmu));
+                        pv[4 * h + r] = __builtin_amdgcn_exp2f(arg[cb][2 * j + h][r]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) pf[cb][j][i] = pack2<MDT>(pv[2 * i], pv[2 * i + 1]);
                 lsum[cb] = mfma16<MDT>(ones, pf[cb][j], lsum[cb]);
