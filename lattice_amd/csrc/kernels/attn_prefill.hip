@@ -252,20 +252,34 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         asm volatile("" : "+v"(entry));
         return offs[entry];
     };
+    // With two chunks per thread (KT * CH == NT: 16-bit pages at head_dim
+    // 128) chunk 0 is a K row piece and chunk 1 the V piece of the same key
+    // at the same place, so one page lookup and one address serve both.
+    constexpr int NPG = CPT == 2 ? 1 : CPT;   // page lookups per thread per tile
+    static_assert(CPT != 2 || KT * CH == NT, "chunks 0 and 1 share their key");
     u32x4 gch[CPT];
     float gsc[F8 ? CPT : 1];   // fp8: the chunk's page scale for kv head g
-    auto gather = [&](int kt, const uint64_t (&pg)[CPT]) {
-#pragma unroll
-        for (int i = 0; i < CPT; ++i) {
-            uint64_t page = pg[i];
+    auto gather = [&](int kt, const uint64_t (&pg)[NPG]) {
+        if constexpr (NPG == 1 && CPT == 2) {
+            uint64_t page = pg[0];
             asm volatile("" : "+v"(page));
-            const uint8_t* reg = c_tensor(i) ? vreg : kreg;
             const uint64_t a =
-                page * 2ull + (__umul24(key_tok(kt, i) & bmask, p.row_bytes) + head_off);
-            gch[i] = *reinterpret_cast<const u32x4*>(reg + a);
-            if constexpr (F8)
-                gsc[i] = *reinterpret_cast<const float*>(reg + page * 2ull +
-                                                         static_cast<uint32_t>(p.data_bytes + g * 4));
+                page * 2ull + (__umul24(key_tok(kt, 0) & bmask, p.row_bytes) + head_off);
+            gch[0] = *reinterpret_cast<const u32x4*>(kreg + a);
+            gch[1] = *reinterpret_cast<const u32x4*>(vreg + a);
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) {
+                uint64_t page = pg[i];
+                asm volatile("" : "+v"(page));
+                const uint8_t* reg = c_tensor(i) ? vreg : kreg;
+                const uint64_t a =
+                    page * 2ull + (__umul24(key_tok(kt, i) & bmask, p.row_bytes) + head_off);
+                gch[i] = *reinterpret_cast<const u32x4*>(reg + a);
+                if constexpr (F8)
+                    gsc[i] = *reinterpret_cast<const float*>(
+                        reg + page * 2ull + static_cast<uint32_t>(p.data_bytes + g * 4));
+            }
         }
     };
     auto store_tile = [&](int buf) {
@@ -452,21 +466,21 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
     };
 
     if (nt_wg > 0) {   // (no tile at all: no column has a visible key)
-        uint64_t pg[CPT];
-        int ent[CPT];
+        uint64_t pg[NPG];
+        int ent[NPG];
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) pg[i] = page_offs(page_entry(0, i));
+        for (int i = 0; i < NPG; ++i) pg[i] = page_offs(page_entry(0, i));
         gather(0, pg);
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) pg[i] = page_offs(page_entry(1, i));
+        for (int i = 0; i < NPG; ++i) pg[i] = page_offs(page_entry(1, i));
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) ent[i] = page_entry(2, i);
+        for (int i = 0; i < NPG; ++i) ent[i] = page_entry(2, i);
         store_tile(0);
         gather(1, pg);
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) pg[i] = page_offs(ent[i]);       // tile 2
+        for (int i = 0; i < NPG; ++i) pg[i] = page_offs(ent[i]);       // tile 2
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) ent[i] = page_entry(3, i);        // tile 3
+        for (int i = 0; i < NPG; ++i) ent[i] = page_entry(3, i);        // tile 3
         __syncthreads();
         // Gathers past the last tile read clamped (valid) rows and are never
         // consumed; issuing them unconditionally keeps every iteration's
@@ -483,9 +497,9 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
             __syncthreads();
             gather(kt + 2, pg);
 #pragma unroll
-            for (int i = 0; i < CPT; ++i) pg[i] = page_offs(ent[i]);   // tile kt + 3
+            for (int i = 0; i < NPG; ++i) pg[i] = page_offs(ent[i]);   // tile kt + 3
 #pragma unroll
-            for (int i = 0; i < CPT; ++i) ent[i] = page_entry(kt + 4, i);
+            for (int i = 0; i < NPG; ++i) ent[i] = page_entry(kt + 4, i);
         };
         for (int kt = 0; kt < nt_wg; kt += 2) {
             step(kt, 0);
