@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lattice_amd.bindings import KV_BF16, KV_F16, KV_FP8, memcpy_dtoh
+from lattice_amd.bindings import KV_BF16, KV_F16, KV_FP8, memcpy_dtoh, memcpy_htod
 from lattice_amd.workload import (build_decode_case, build_prefix_shared_case, encode16,
                                   io_dtype, torch_io_dtype)
 
@@ -225,6 +225,37 @@ def test_many_sequences_ragged_chunks(gpu_lib):
         got, ref = run_prefill(case, lens, 32, 73)
         err = rel_err(got, ref)
         print(f"70 sequences, {int(lens.sum())} queries, err={err:.3e}", flush=True)
+        assert np.isfinite(got).all() and err <= TOL[KV_BF16]
+    finally:
+        case.pool.destroy()
+
+
+def test_running_max_grows_on_most_tiles(gpu_lib):
+    """Keys whose size grows along the sequence (row t scaled by 1 + t/8) make
+    each column maximum grow by more than 8 (log2 units) on about a third of
+    the tiles (6-9 of 22 at 700 keys), so a wave of 32 columns takes the
+    rescale path on most tiles, where N(0,1) data stays on the fast path after
+    the first; a spike (rows 300..363 four times larger) then holds the maxima
+    for the tiles after it.  Against the oracle,
+    ragged chunks, one sequence whose chunk is all of it."""
+    ctx = [700, 257, 96, 33]
+    lens = [200, 64, 96, 33]
+    case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=91)
+    try:
+        g = case.geometry
+        mk = case.k_mirror[0]
+        rb = g["row_bytes"]
+        for b, L in enumerate(ctx):
+            for t in range(L):
+                at = int(case.offsets_f16[case.block_tables[b, t // 16]]) * 2 + (t % 16) * rb
+                vals = O.decode(O.BF16, mk[at:at + rb].view(np.uint16)).astype(np.float32)
+                vals *= (1.0 + t / 8.0) * (4.0 if 300 <= t < 364 else 1.0)
+                mk[at:at + rb] = encode16(KV_BF16, vals).view(np.uint8).reshape(-1)
+        memcpy_htod(case.pool.va_k(0), mk)
+        got, ref = run_prefill(case, lens, 32, seed=92)
+        err = rel_err(got, ref)
+        print(f"growing maxima: err={err:.3e}", flush=True)
         assert np.isfinite(got).all() and err <= TOL[KV_BF16]
     finally:
         case.pool.destroy()
