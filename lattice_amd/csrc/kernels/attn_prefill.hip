@@ -253,8 +253,10 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
         return offs[entry];
     };
     // With two chunks per thread (KT * CH == NT: 16-bit pages at head_dim
-    // 128) chunk 0 is a K row piece and chunk 1 the V piece of the same key
-    // at the same place, so one page lookup and one address serve both.
+    // 128 with 32-key tiles, fp8 pages with 64-key tiles) chunk 0 is a K row
+    // piece and chunk 1 the V piece of the same key at the same place, so one
+    // page lookup and one address serve both (for fp8, with the page's two
+    // scales).
     constexpr int NPG = CPT == 2 ? 1 : CPT;   // page lookups per thread per tile
     static_assert(CPT != 2 || KT * CH == NT, "chunks 0 and 1 share their key");
     u32x4 gch[CPT];
@@ -267,6 +269,11 @@ void attn_prefill_mfma(PrefillParams p, const uint8_t* __restrict__ kreg,
                 page * 2ull + (__umul24(key_tok(kt, 0) & bmask, p.row_bytes) + head_off);
             gch[0] = *reinterpret_cast<const u32x4*>(kreg + a);
             gch[1] = *reinterpret_cast<const u32x4*>(vreg + a);
+            if constexpr (F8) {
+                const uint64_t sa = page * 2ull + static_cast<uint32_t>(p.data_bytes + g * 4);
+                gsc[0] = *reinterpret_cast<const float*>(kreg + sa);
+                gsc[1] = *reinterpret_cast<const float*>(vreg + sa);
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < CPT; ++i) {
@@ -620,7 +627,8 @@ __global__ __launch_bounds__(64) void attn_prefill_generic(PrefillParams p,
 template <int DT, int D, int G>
 bool launch_mfma(const dev::AttnPrefillArgs& a, PrefillParams& p, hipStream_t s, std::string* err) {
     // 8 waves of 32 columns (2 waves per SIMD), 32 keys per tile.  Measured
-    // on Cfg3 (MI355X): 64-key tiles ~2% slower; 4-wave workgroups (two per
+    // on the Cfg3 shape (MI355X): 64-key tiles ~4% slower on bf16 pages, equal
+    // on fp8 pages, ~11% slower at head_dim 64; 4-wave workgroups (two per
     // CU) ~10% slower; 64 columns per wave does not fit 2 waves per SIMD.
     constexpr int NW = 8, NCB = 2, KT = 32;
     constexpr int TWG = NW * NCB * (16 / G);
