@@ -32,6 +32,20 @@ typedef enum {
  * footer of kv_heads fp32 scales at byte bs*kv_heads*head_dim and are padded
  * to a multiple of 256 bytes, so a page copy moves its scales with it.
  * Extends kcmm_pool_create (ref kcmm.h:193), which is the KCMM_KV_F16 case.
+ *
+ * fp8 page writes (every KV append on an fp8 pool) take bf16 rows.  The rows
+ * one call writes into a page are applied as one set -- for each token slot
+ * the call's last row for it -- so the bytes do not depend on row order.
+ * Per (page, kv head), with amax = max |x| over the rows written:
+ *   - a call that writes slot 0, or that finds a footer scale that is not a
+ *     finite positive number, starts the page: scale = amax / 448 (1 if 0);
+ *     the page's other slots are undefined afterwards;
+ *   - any other call keeps the scale, or raises it to amax / 448 when
+ *     amax > 448 * scale and then re-encodes every slot it does not write;
+ * each written element is e4m3(x / scale), round to nearest even, so no
+ * value is clipped.  A page must therefore be started by a write of slot 0.
+ * Limits: block_size <= 4096 and head_dim <= 256; a host-slot call writes at
+ * most 64 distinct slots of one page.
  */
 kcmm_pool_t *kcmm_pool_create_typed(const kcmm_config_t *config, int32_t kv_dtype);
 

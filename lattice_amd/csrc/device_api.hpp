@@ -72,7 +72,7 @@ bool attn_prefill(const AttnPrefillArgs& a, std::string* err);
 struct KvRowsArgs {
     int32_t dtype;
     uint64_t k_base, v_base, k_src, v_src;
-    uint32_t kv_heads, head_dim, row_bytes, data_bytes;
+    uint32_t block_size, kv_heads, head_dim, row_bytes, data_bytes;
     const RowDst* rows;
     size_t num_rows;
     uint64_t stream;

@@ -172,6 +172,7 @@ int write_rows(kcmm_pool_t* pool, const char* fn, uint32_t layer_idx,
     a.v_base = pool->core->va_v(layer_idx);
     a.k_src = k_src;
     a.v_src = v_src;
+    a.block_size = static_cast<uint32_t>(g.block_size);
     a.kv_heads = static_cast<uint32_t>(g.kv_heads);
     a.head_dim = static_cast<uint32_t>(g.head_dim);
     a.row_bytes = static_cast<uint32_t>(g.row_bytes);

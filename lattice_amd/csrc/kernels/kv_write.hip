@@ -9,11 +9,14 @@
 // per 16-bit element (device path); here one launch moves every row with
 // 16-byte vector copies.
 //
-// fp8-e4m3 pools take bf16 source rows and quantize per (page, kv head): the
-// row written at slot 0 sets the page scale to amax/448 (1 for an all-zero
-// row); a later row whose amax exceeds 448*scale raises the scale to
-// amax/448 and re-encodes the rows already in the page, so no value is ever
-// clipped.  Encoding is round-to-nearest-even with saturation to +-448.
+// fp8-e4m3 pools take bf16 source rows and quantize per (page, kv head) with
+// one fp32 scale in the page footer.  The rows one call writes into a page
+// are applied as a set (the call's last row for each slot), so the result
+// does not depend on their order: a call that writes slot 0 starts the page
+// with scale amax/448 over its rows (1 if all zero); a later call raises the
+// scale to amax/448 when its rows exceed 448*scale and re-encodes every slot
+// it does not write, so no value is ever clipped (fp8_write_page_head).
+// Encoding is round-to-nearest-even with saturation to +-448.
 #include <algorithm>
 #include <cmath>
 #include <vector>
@@ -76,55 +79,65 @@ __device__ __forceinline__ uint32_t f32_to_fp8e4m3(float x) {
     return sign | code;
 }
 
-// Writes the bf16 head row `src` at token row `slot` of an fp8 page (kv head
-// kvh) with one wavefront.  `scale` is the page scale before this row (unused
-// when slot == 0); returns the scale after it, which the caller stores in the
-// footer once its last row is written.  Rows of one page must go through one
-// wavefront in call order: each may raise the scale and re-encode the rows
-// before it.
-__device__ float fp8_put_row(uint8_t* page, uint32_t slot, uint32_t kvh, const uint16_t* src,
-                             uint32_t head_dim, uint32_t row_bytes, float scale) {
+// fp8 page write of one (page, kv head) for one call.  `row_of` (bs entries,
+// LDS) gives, for each token slot, the source row this call writes there (the
+// call's last row for that slot), or -1.  The rows a call writes into a page
+// are applied as one set, so the bytes do not depend on their order:
+//   amax  = max |x| over the written rows of this kv head;
+//   fresh = the call writes slot 0, or the footer scale is not a finite
+//           positive number (a page never started);
+//   fresh:  scale = amax / 448 (1 for amax 0); the slots the call does not
+//           write are left as they are and are undefined from then on;
+//   else:   scale = old, raised to amax / 448 when amax > 448 * old, and then
+//           every slot the call does not write is re-encoded from old to the
+//           new scale (e4m3(decode(code) * old / scale));
+// and each written row is stored as e4m3(x / scale).  One wavefront.
+__device__ void fp8_write_page_head(uint8_t* page, uint32_t kvh, const uint16_t* src_base,
+                                    const int32_t* row_of, uint32_t bs, uint32_t kv_heads,
+                                    uint32_t head_dim, uint32_t row_bytes, uint32_t data_bytes) {
     const int lane = threadIdx.x & 63;
-    float x[4];
     float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t d = lane + 64 * i;
-        x[i] = d < head_dim ? bf16_bits_to_f32(src[d]) : 0.0f;
-        amax = fmaxf(amax, fabsf(x[i]));
+    for (uint32_t u = 0; u < bs; ++u) {
+        const int32_t r = row_of[u];
+        if (r < 0) continue;
+        const uint16_t* src = src_base + (static_cast<uint64_t>(r) * kv_heads + kvh) * head_dim;
+        for (uint32_t d = lane; d < head_dim; d += 64) amax = fmaxf(amax, fabsf(bf16_bits_to_f32(src[d])));
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    if (slot == 0) {
+    float* sp = reinterpret_cast<float*>(page + data_bytes) + kvh;
+    const float old = *sp;
+    const bool fresh = row_of[0] >= 0 || !(old > 0.0f && old <= 3.40282347e38f);
+    float scale;
+    if (fresh) {
         scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-    } else if (amax > 448.0f * scale) {
-        const float old = scale;
-        scale = amax / 448.0f;
-        // re-encode the rows already in this page with the larger scale
-        for (uint32_t u = 0; u < slot; ++u) {
-            uint8_t* row = page + static_cast<uint64_t>(u) * row_bytes + kvh * head_dim;
-            for (uint32_t d = lane; d < head_dim; d += 64) {
-                const float y = fp8e4m3_to_f32(row[d]) * old;
-                row[d] = static_cast<uint8_t>(f32_to_fp8e4m3(y / scale));
+    } else {
+        scale = old;
+        if (amax > 448.0f * old) {
+            scale = amax / 448.0f;
+            for (uint32_t u = 0; u < bs; ++u) {
+                if (row_of[u] >= 0) continue;
+                uint8_t* row = page + static_cast<uint64_t>(u) * row_bytes + kvh * head_dim;
+                for (uint32_t d = lane; d < head_dim; d += 64) {
+                    const float y = fp8e4m3_to_f32(row[d]) * old;
+                    row[d] = static_cast<uint8_t>(f32_to_fp8e4m3(y / scale));
+                }
             }
         }
     }
-    uint8_t* row = page + static_cast<uint64_t>(slot) * row_bytes + kvh * head_dim;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t d = lane + 64 * i;
-        if (d < head_dim) row[d] = static_cast<uint8_t>(f32_to_fp8e4m3(x[i] / scale));
+    for (uint32_t u = 0; u < bs; ++u) {
+        const int32_t r = row_of[u];
+        if (r < 0) continue;
+        const uint16_t* src = src_base + (static_cast<uint64_t>(r) * kv_heads + kvh) * head_dim;
+        uint8_t* row = page + static_cast<uint64_t>(u) * row_bytes + kvh * head_dim;
+        for (uint32_t d = lane; d < head_dim; d += 64)
+            row[d] = static_cast<uint8_t>(f32_to_fp8e4m3(bf16_bits_to_f32(src[d]) / scale));
     }
-    return scale;
-}
-
-__device__ __forceinline__ float* fp8_scale_ptr(uint8_t* page, uint32_t data_bytes, uint32_t kvh) {
-    return reinterpret_cast<float*>(page + data_bytes) + kvh;
+    if (lane == 0) *sp = scale;
 }
 
 // Host-resolved fp8 rows grouped by page: rows start[g] .. start[g+1]-1 of the
-// batch target one page, in call order.  A page's rows may continue in the
-// next launch of the same call (launches on one stream run in order).
+// batch target one page, in call order.  A page's rows never span launches.
 struct Fp8RowBatch {
     uint64_t page[kRowsPerLaunch];
     uint32_t slot[kRowsPerLaunch];
@@ -134,27 +147,28 @@ struct Fp8RowBatch {
 
 // Waves per fp8 writer workgroup: one per (kv head, K|V) pair, at most 16.
 constexpr int kFp8MaxWaves = 16;
+// Token slots per page the fp8 writer handles (its slot table lives in LDS).
+constexpr uint32_t kFp8MaxBlockSize = 4096;
 
-// grid (groups); wave w takes the (kv head, K|V) pairs w, w + waves, ...
+// grid (groups), dynamic LDS bs * 4 bytes; wave w takes the (kv head, K|V)
+// pairs w, w + waves, ...
 __global__ __launch_bounds__(64 * kFp8MaxWaves) void kv_rows_fp8(
     Fp8RowBatch rb, uint8_t* k_base, uint8_t* v_base, const uint16_t* k_src,
-    const uint16_t* v_src, uint32_t kv_heads, uint32_t head_dim, uint32_t row_bytes,
+    const uint16_t* v_src, uint32_t bs, uint32_t kv_heads, uint32_t head_dim, uint32_t row_bytes,
     uint32_t data_bytes) {
+    extern __shared__ int32_t row_of[];
     const uint32_t g = blockIdx.x;
     const uint32_t r0 = rb.start[g], r1 = rb.start[g + 1];
+    for (uint32_t u = threadIdx.x; u < bs; u += blockDim.x) row_of[u] = -1;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (uint32_t r = r0; r < r1; ++r) row_of[rb.slot[r]] = static_cast<int32_t>(rb.src[r]);
+    __syncthreads();
     const uint32_t waves = blockDim.x >> 6;
     for (uint32_t j = threadIdx.x >> 6; j < 2 * kv_heads; j += waves) {
-        const uint32_t kvh = j >> 1;
         const bool is_v = j & 1;
-        uint8_t* page = (is_v ? v_base : k_base) + rb.page[r0];
-        float* sp = fp8_scale_ptr(page, data_bytes, kvh);
-        float scale = rb.slot[r0] == 0 ? 1.0f : *sp;
-        for (uint32_t r = r0; r < r1; ++r) {
-            const uint16_t* src = (is_v ? v_src : k_src) +
-                                  (static_cast<uint64_t>(rb.src[r]) * kv_heads + kvh) * head_dim;
-            scale = fp8_put_row(page, rb.slot[r], kvh, src, head_dim, row_bytes, scale);
-        }
-        if ((threadIdx.x & 63) == 0) *sp = scale;
+        fp8_write_page_head((is_v ? v_base : k_base) + rb.page[r0], j >> 1, is_v ? v_src : k_src,
+                            row_of, bs, kv_heads, head_dim, row_bytes, data_bytes);
     }
 }
 
@@ -210,13 +224,14 @@ __global__ __launch_bounds__(256) void kv_slots_copy(SlotArgs a) {
     }
 }
 
-// fp8 pages through device slot ids, in two kernels so that the rows of one
-// page are applied in call order by one wavefront per (kv head, K|V), as a
-// sequential writer would.  `lead` / `cnt` (int32 per block id, zero between
-// calls) collect, per page, batch - (first row) and the number of rows.
-// Pass 1: one thread per row resolves the slot (status as above) and enters
-// the row; pass 2: the workgroup of a page's first row writes all its rows,
-// then restores both entries to zero.
+// fp8 pages through device slot ids, in two kernels so that all rows of a
+// page are applied as one set by one workgroup (fp8_write_page_head).
+// `lead` / `cnt` (int32 per block id, zero between calls) collect, per page,
+// batch - (first row) and the number of rows.  Pass 1: one thread per row
+// resolves the slot (status as above) and enters the row; pass 2: the
+// workgroup of a page's first row builds the page's slot table in LDS (rows
+// in call order, so the last row for a slot wins), writes the page, then
+// restores both entries to zero.
 __global__ __launch_bounds__(256) void kv_slots_fp8_collect(SlotArgs a, uint32_t batch,
                                                             int32_t* lead, int32_t* cnt) {
     const uint32_t r = blockIdx.x * 256 + threadIdx.x;
@@ -236,11 +251,12 @@ __global__ __launch_bounds__(256) void kv_slots_fp8_collect(SlotArgs a, uint32_t
     atomicAdd(cnt + id, 1);
 }
 
-// grid (batch); 64 * min(2 kv_heads, 16) threads.
+// grid (batch); 64 * min(2 kv_heads, 16) threads; dynamic LDS block_size * 4.
 __global__ __launch_bounds__(64 * kFp8MaxWaves) void kv_slots_fp8_write(SlotArgs a,
                                                                          uint32_t batch,
                                                                          int32_t* lead,
                                                                          int32_t* cnt) {
+    extern __shared__ int32_t row_of[];
     __shared__ int32_t s_rows;
     const uint32_t r = blockIdx.x;
     const int64_t slot = a.slots[r];
@@ -253,44 +269,37 @@ __global__ __launch_bounds__(64 * kFp8MaxWaves) void kv_slots_fp8_write(SlotArgs
         s_rows = __atomic_load_n(lead + id, __ATOMIC_RELAXED) == static_cast<int32_t>(batch - r)
                      ? __atomic_load_n(cnt + id, __ATOMIC_RELAXED)
                      : 0;
+    for (uint32_t u = threadIdx.x; u < a.block_size; u += blockDim.x) row_of[u] = -1;
     __syncthreads();
     const int32_t rows = s_rows;
     if (rows == 0) return;
-    const uint64_t page_off = a.offsets_f16[id] * 2ull;
-    const uint32_t waves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
-    for (uint32_t j = threadIdx.x >> 6; j < 2 * a.kv_heads; j += waves) {
-        const uint32_t kvh = j >> 1;
-        const bool is_v = j & 1;
-        uint8_t* page = (is_v ? a.v_base : a.k_base) + page_off;
-        const uint16_t* src_base = reinterpret_cast<const uint16_t*>(is_v ? a.v_src : a.k_src);
-        float* sp = fp8_scale_ptr(page, a.data_bytes, kvh);
-        float scale = 1.0f;
-        bool have_scale = false;
-        int32_t done = 0;
+    if (threadIdx.x < 64) {
         // rows of this page, in call order, from this one on
+        int32_t done = 0;
         for (uint32_t base = r; done < rows && base < batch; base += 64) {
             const uint32_t rr = base + lane;
             const int64_t s2 = rr < batch ? a.slots[rr] : -1;
-            const bool mine = s2 >= 0 && s2 / a.block_size == id;
-            uint64_t mask = __ballot(mine);
+            uint64_t mask = __ballot(s2 >= 0 && s2 / a.block_size == id);
             while (mask != 0 && done < rows) {
                 const int i = __builtin_ctzll(mask);
                 mask &= mask - 1;
                 const uint32_t row = base + i;
-                const uint32_t in_page = static_cast<uint32_t>(a.slots[row] % a.block_size);
-                if (!have_scale) {
-                    scale = in_page == 0 ? 1.0f : *sp;
-                    have_scale = true;
-                }
-                scale = fp8_put_row(page, in_page, kvh,
-                                    src_base + (static_cast<uint64_t>(row) * a.kv_heads + kvh) *
-                                                   a.head_dim,
-                                    a.head_dim, a.row_bytes, scale);
+                if (lane == 0)
+                    row_of[static_cast<uint32_t>(a.slots[row] % a.block_size)] =
+                        static_cast<int32_t>(row);
                 ++done;
             }
         }
-        if (lane == 0) *sp = scale;
+    }
+    __syncthreads();
+    const uint64_t page_off = a.offsets_f16[id] * 2ull;
+    const uint32_t waves = blockDim.x >> 6;
+    for (uint32_t j = threadIdx.x >> 6; j < 2 * a.kv_heads; j += waves) {
+        const bool is_v = j & 1;
+        fp8_write_page_head((is_v ? a.v_base : a.k_base) + page_off, j >> 1,
+                            reinterpret_cast<const uint16_t*>(is_v ? a.v_src : a.k_src), row_of,
+                            a.block_size, a.kv_heads, a.head_dim, a.row_bytes, a.data_bytes);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -303,48 +312,81 @@ __global__ __launch_bounds__(64 * kFp8MaxWaves) void kv_slots_fp8_write(SlotArgs
 
 namespace dev {
 
+// Row indices sorted by (page, slot), keeping only the last row of the call
+// for each (page, slot): a call that names a slot twice stores its last row
+// there, as the reference's sequential row copies do (ref pool.rs:1084-1091).
+static std::vector<uint32_t> last_row_per_slot(const RowDst* rows, size_t n) {
+    std::vector<uint32_t> order(n);
+    for (size_t i = 0; i < n; ++i) order[i] = static_cast<uint32_t>(i);
+    std::sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
+        if (rows[x].page_offset != rows[y].page_offset)
+            return rows[x].page_offset < rows[y].page_offset;
+        if (rows[x].slot != rows[y].slot) return rows[x].slot < rows[y].slot;
+        return x < y;
+    });
+    size_t m = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const bool superseded = i + 1 < n && rows[order[i]].page_offset == rows[order[i + 1]].page_offset &&
+                                rows[order[i]].slot == rows[order[i + 1]].slot;
+        if (!superseded) order[m++] = order[i];
+    }
+    order.resize(m);
+    return order;
+}
+
 bool kv_write_rows(const KvRowsArgs& a, std::string* err) {
     hipStream_t s = reinterpret_cast<hipStream_t>(a.stream);
     auto* kb = reinterpret_cast<uint8_t*>(a.k_base);
     auto* vb = reinterpret_cast<uint8_t*>(a.v_base);
+    const std::vector<uint32_t> order = last_row_per_slot(a.rows, a.num_rows);
+    const size_t num = order.size();
     if (a.dtype == kDtFP8) {
         if (a.head_dim > 256) {
             *err = "fp8 KV write supports head_dim <= 256";
             return false;
         }
-        // Rows grouped by page, call order kept inside a page (pages are
-        // independent, so groups may run in any order).
-        std::vector<uint32_t> order(a.num_rows);
-        for (size_t i = 0; i < a.num_rows; ++i) order[i] = static_cast<uint32_t>(i);
-        std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
-            return a.rows[x].page_offset < a.rows[y].page_offset;
-        });
+        if (a.block_size == 0 || a.block_size > kFp8MaxBlockSize) {
+            *err = "fp8 KV write supports block_size <= 4096";
+            return false;
+        }
+        // One workgroup per page; a page's rows (distinct slots) go to one
+        // launch, whole groups packed kRowsPerLaunch rows at a time.
         const int waves = static_cast<int>(std::min<uint32_t>(2 * a.kv_heads, kFp8MaxWaves));
-        for (size_t base = 0; base < a.num_rows; base += kRowsPerLaunch) {
-            const size_t n = std::min<size_t>(kRowsPerLaunch, a.num_rows - base);
+        const size_t lds = static_cast<size_t>(a.block_size) * 4;
+        size_t i = 0;
+        while (i < num) {
             Fp8RowBatch rb{};
-            uint32_t groups = 0;
-            for (size_t i = 0; i < n; ++i) {
-                const RowDst& r = a.rows[order[base + i]];
-                if (i == 0 || r.page_offset != rb.page[i - 1]) rb.start[groups++] = static_cast<uint16_t>(i);
-                rb.page[i] = r.page_offset;
-                rb.slot[i] = r.slot;
-                rb.src[i] = r.src_row;
+            uint32_t groups = 0, n = 0;
+            while (i < num) {
+                size_t j = i;
+                while (j < num && a.rows[order[j]].page_offset == a.rows[order[i]].page_offset) ++j;
+                if (j - i > static_cast<size_t>(kRowsPerLaunch)) {
+                    *err = "fp8 KV write: more than 64 rows into one page in one call";
+                    return false;
+                }
+                if (n + (j - i) > static_cast<size_t>(kRowsPerLaunch)) break;
+                rb.start[groups++] = static_cast<uint16_t>(n);
+                for (; i < j; ++i, ++n) {
+                    const RowDst& r = a.rows[order[i]];
+                    rb.page[n] = r.page_offset;
+                    rb.slot[n] = r.slot;
+                    rb.src[n] = r.src_row;
+                }
             }
             rb.start[groups] = static_cast<uint16_t>(n);
-            hipLaunchKernelGGL(kv_rows_fp8, dim3(groups), dim3(64 * waves), 0, s, rb, kb, vb,
+            hipLaunchKernelGGL(kv_rows_fp8, dim3(groups), dim3(64 * waves), lds, s, rb, kb, vb,
                                reinterpret_cast<const uint16_t*>(a.k_src),
-                               reinterpret_cast<const uint16_t*>(a.v_src), a.kv_heads, a.head_dim,
-                               a.row_bytes, a.data_bytes);
+                               reinterpret_cast<const uint16_t*>(a.v_src), a.block_size,
+                               a.kv_heads, a.head_dim, a.row_bytes, a.data_bytes);
             KCMM_HIP_CHECK(hipGetLastError(), err);
         }
         return true;
     }
-    for (size_t base = 0; base < a.num_rows; base += kRowsPerLaunch) {
-        const size_t n = std::min<size_t>(kRowsPerLaunch, a.num_rows - base);
+    for (size_t base = 0; base < num; base += kRowsPerLaunch) {
+        const size_t n = std::min<size_t>(kRowsPerLaunch, num - base);
         RowBatch rb{};
         for (size_t i = 0; i < n; ++i) {
-            const RowDst& r = a.rows[base + i];
+            const RowDst& r = a.rows[order[base + i]];
             rb.dst[i] = r.page_offset + static_cast<uint64_t>(r.slot) * a.row_bytes;
             rb.src[i] = r.src_row;
         }
@@ -382,6 +424,10 @@ bool kv_write_device_slots(const KvDeviceSlotsArgs& a, std::string* err) {
             *err = "fp8 KV write: batch or offset table too large";
             return false;
         }
+        if (a.block_size == 0 || a.block_size > kFp8MaxBlockSize) {
+            *err = "fp8 KV write supports block_size <= 4096";
+            return false;
+        }
         // per block id: batch - first row, row count (zero between calls)
         void* ws = nullptr;
         if (!stream_workspace(a.stream, 8, static_cast<size_t>(a.offsets_len) * 8, &ws, true, err))
@@ -392,8 +438,8 @@ bool kv_write_device_slots(const KvDeviceSlotsArgs& a, std::string* err) {
                            a.batch, lead, cnt);
         KCMM_HIP_CHECK(hipGetLastError(), err);
         const int waves = static_cast<int>(std::min<uint32_t>(2 * a.kv_heads, kFp8MaxWaves));
-        hipLaunchKernelGGL(kv_slots_fp8_write, dim3(a.batch), dim3(64 * waves), 0, s, sa, a.batch,
-                           lead, cnt);
+        hipLaunchKernelGGL(kv_slots_fp8_write, dim3(a.batch), dim3(64 * waves),
+                           static_cast<size_t>(a.block_size) * 4, s, sa, a.batch, lead, cnt);
     } else {
         hipLaunchKernelGGL(kv_slots_copy, dim3(a.batch), dim3(256), 0, s, sa);
     }

@@ -983,54 +983,64 @@ size_t otier_arc_p(OTier *t) { return t->arc_p; }
  * KV write
  * ====================================================================== */
 
-/* fp8 page write of one kv head row (this build's fp8 contract, stated in
- * include/kcmm_mi355x.h and the kernel source; no reference counterpart). */
-static void fp8_write_head(uint8_t *page, uint32_t slot, uint32_t kvh, const uint16_t *src,
-                           uint32_t D, uint32_t row_bytes, uint32_t data_bytes) {
-    float x[512];
-    float amax = 0.0f;
-    for (uint32_t d = 0; d < D; ++d) {
-        x[d] = oracle_bf16_to_f32(src[d]);
-        float a = fabsf(x[d]);
-        if (a > amax) amax = a;
-    }
-    uint8_t *sp = page + data_bytes + kvh * 4;
-    float scale;
-    if (slot == 0) {
-        scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-    } else {
+/* fp8 page write (this build's fp8 contract, stated in include/kcmm_mi355x.h
+ * at kcmm_pool_create_typed; the reference has no fp8 pages).  The rows one
+ * call writes into a page act as one set: row_of[slot] is the source row the
+ * call writes at that slot (its last one for the slot), or -1.  Per kv head:
+ * amax over the written rows; writing slot 0, or a footer scale that is not a
+ * finite positive number, starts the page (scale amax/448, 1 if 0, unwritten
+ * slots left as they are); otherwise the scale grows to amax/448 when
+ * amax > 448*old and every unwritten slot is re-encoded from old to new.
+ * Written rows are stored as e4m3(x/scale). */
+static void fp8_write_page(uint8_t *page, const int32_t *row_of, uint32_t bs,
+                           const uint16_t *src, uint32_t kv_heads, uint32_t D,
+                           uint32_t row_bytes, uint32_t data_bytes) {
+    for (uint32_t g = 0; g < kv_heads; ++g) {
+        float amax = 0.0f;
+        for (uint32_t u = 0; u < bs; ++u) {
+            if (row_of[u] < 0) continue;
+            const uint16_t *x = src + ((uint64_t)row_of[u] * kv_heads + g) * D;
+            for (uint32_t d = 0; d < D; ++d) {
+                float a = fabsf(oracle_bf16_to_f32(x[d]));
+                if (a > amax) amax = a;
+            }
+        }
+        uint8_t *sp = page + data_bytes + g * 4;
         float old;
         memcpy(&old, sp, 4);
-        scale = old;
-        if (amax > 448.0f * old) {
-            scale = amax / 448.0f;
-            for (uint32_t u = 0; u < slot; ++u) {
-                uint8_t *row = page + (uint64_t)u * row_bytes + kvh * D;
-                for (uint32_t d = 0; d < D; ++d) {
-                    float y = oracle_e4m3_to_f32(row[d]) * old;
-                    row[d] = oracle_f32_to_e4m3(y / scale);
+        const int fresh = row_of[0] >= 0 || !(old > 0.0f && old <= 3.40282347e38f);
+        float scale;
+        if (fresh) {
+            scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+        } else {
+            scale = old;
+            if (amax > 448.0f * old) {
+                scale = amax / 448.0f;
+                for (uint32_t u = 0; u < bs; ++u) {
+                    if (row_of[u] >= 0) continue;
+                    uint8_t *row = page + (uint64_t)u * row_bytes + g * D;
+                    for (uint32_t d = 0; d < D; ++d) {
+                        float y = oracle_e4m3_to_f32(row[d]) * old;
+                        row[d] = oracle_f32_to_e4m3(y / scale);
+                    }
                 }
             }
         }
+        for (uint32_t u = 0; u < bs; ++u) {
+            if (row_of[u] < 0) continue;
+            const uint16_t *x = src + ((uint64_t)row_of[u] * kv_heads + g) * D;
+            uint8_t *row = page + (uint64_t)u * row_bytes + g * D;
+            for (uint32_t d = 0; d < D; ++d) row[d] = oracle_f32_to_e4m3(oracle_bf16_to_f32(x[d]) / scale);
+        }
+        memcpy(sp, &scale, 4);
     }
-    uint8_t *row = page + (uint64_t)slot * row_bytes + kvh * D;
-    for (uint32_t d = 0; d < D; ++d) row[d] = oracle_f32_to_e4m3(x[d] / scale);
-    memcpy(sp, &scale, 4);
 }
 
-static void write_row(int dtype, uint8_t *k_region, uint8_t *v_region, const uint8_t *k_src,
-                      const uint8_t *v_src, uint64_t page, uint32_t slot, uint32_t src_row,
-                      uint32_t kv_heads, uint32_t D, uint32_t row_bytes, uint32_t data_bytes) {
-    if (dtype == 2) {
-        for (uint32_t g = 0; g < kv_heads; ++g) {
-            const uint16_t *ks = (const uint16_t *)k_src + ((uint64_t)src_row * kv_heads + g) * D;
-            const uint16_t *vs = (const uint16_t *)v_src + ((uint64_t)src_row * kv_heads + g) * D;
-            fp8_write_head(k_region + page, slot, g, ks, D, row_bytes, data_bytes);
-            fp8_write_head(v_region + page, slot, g, vs, D, row_bytes, data_bytes);
-        }
-        return;
-    }
-    /* ref pool.rs:1073-1091: dst = region + va_offset + off*step*2, one row copy */
+/* ref pool.rs:1073-1091: dst = region + va_offset + off*step*2, one row copy
+ * per row in call order (a repeated slot keeps the last row). */
+static void copy_row(uint8_t *k_region, uint8_t *v_region, const uint8_t *k_src,
+                     const uint8_t *v_src, uint64_t page, uint32_t slot, uint32_t src_row,
+                     uint32_t row_bytes) {
     uint64_t dst = page + (uint64_t)slot * row_bytes;
     memcpy(k_region + dst, k_src + (uint64_t)src_row * row_bytes, row_bytes);
     memcpy(v_region + dst, v_src + (uint64_t)src_row * row_bytes, row_bytes);
@@ -1041,9 +1051,30 @@ int oracle_kv_write_rows(int dtype, uint8_t *k_region, uint8_t *v_region, const 
                          const uint32_t *slots, const uint32_t *src_rows, uint32_t n,
                          uint32_t kv_heads, uint32_t head_dim, uint32_t row_bytes,
                          uint32_t data_bytes) {
-    for (uint32_t i = 0; i < n; ++i)
-        write_row(dtype, k_region, v_region, k_src, v_src, page_offsets[i], slots[i],
-                  src_rows[i], kv_heads, head_dim, row_bytes, data_bytes);
+    if (dtype != 2) {
+        for (uint32_t i = 0; i < n; ++i)
+            copy_row(k_region, v_region, k_src, v_src, page_offsets[i], slots[i], src_rows[i],
+                     row_bytes);
+        return 0;
+    }
+    const uint32_t bs = data_bytes / row_bytes;
+    int32_t *row_of = (int32_t *)malloc(bs * sizeof(int32_t));
+    uint8_t *done = (uint8_t *)calloc(n ? n : 1, 1);
+    for (uint32_t i = 0; i < n; ++i) {
+        if (done[i]) continue;
+        for (uint32_t u = 0; u < bs; ++u) row_of[u] = -1;
+        for (uint32_t j = i; j < n; ++j)
+            if (page_offsets[j] == page_offsets[i]) {
+                row_of[slots[j]] = (int32_t)src_rows[j];
+                done[j] = 1;
+            }
+        fp8_write_page(k_region + page_offsets[i], row_of, bs, (const uint16_t *)k_src, kv_heads,
+                       head_dim, row_bytes, data_bytes);
+        fp8_write_page(v_region + page_offsets[i], row_of, bs, (const uint16_t *)v_src, kv_heads,
+                       head_dim, row_bytes, data_bytes);
+    }
+    free(done);
+    free(row_of);
     return 0;
 }
 
@@ -1055,15 +1086,34 @@ int oracle_kv_write_device_slots(int dtype, uint8_t *k_region, uint8_t *v_region
                                  const uint8_t *valid, uint32_t offsets_len, uint32_t block_size,
                                  uint32_t kv_heads, uint32_t head_dim, uint32_t row_bytes,
                                  uint32_t data_bytes, int32_t *status) {
+    int32_t *row_of = (int32_t *)malloc(block_size * sizeof(int32_t));
+    uint8_t *done = (uint8_t *)calloc(batch ? batch : 1, 1);
     for (uint32_t r = 0; r < batch; ++r) {
         int64_t slot = slots[r];
-        if (slot < 0) continue;
+        if (slot < 0 || done[r]) continue;
         int64_t id = slot / block_size;
         if (id >= (int64_t)offsets_len) { if (status && *status == 0) *status = 1; continue; }
         if (valid && valid[id] == 0) { if (status && *status == 0) *status = 2; continue; }
-        write_row(dtype, k_region, v_region, k_src, v_src, offsets_f16[id] * 2,
-                  (uint32_t)(slot % block_size), r, kv_heads, head_dim, row_bytes, data_bytes);
+        const uint64_t page = offsets_f16[id] * 2;
+        if (dtype != 2) {
+            copy_row(k_region, v_region, k_src, v_src, page, (uint32_t)(slot % block_size), r,
+                     row_bytes);
+            continue;
+        }
+        /* fp8: all rows of this page in the call, as one set */
+        for (uint32_t u = 0; u < block_size; ++u) row_of[u] = -1;
+        for (uint32_t j = r; j < batch; ++j)
+            if (slots[j] >= 0 && slots[j] / block_size == id) {
+                row_of[slots[j] % block_size] = (int32_t)j;
+                done[j] = 1;
+            }
+        fp8_write_page(k_region + page, row_of, block_size, (const uint16_t *)k_src, kv_heads,
+                       head_dim, row_bytes, data_bytes);
+        fp8_write_page(v_region + page, row_of, block_size, (const uint16_t *)v_src, kv_heads,
+                       head_dim, row_bytes, data_bytes);
     }
+    free(done);
+    free(row_of);
     return 0;
 }
 

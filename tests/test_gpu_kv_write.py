@@ -203,9 +203,11 @@ def _prefill_rows(rng, tables, bs, tokens, order):
 @pytest.mark.parametrize("path", ["device", "host"])
 def test_fp8_multi_token_pages_vs_oracle(gpu_lib, order, path):
     """fp8 pages written by calls that put many tokens of a sequence (two and
-    a half pages' worth) into the same pages: every row of a page must be
-    applied in call order (each one may raise the page scale and re-encode
-    the rows before it), bit-exact with the oracle's sequential writer."""
+    a half pages' worth) into the same pages, in several row orders: the rows
+    a call writes into a page act as one set (the last row for a repeated
+    slot), bit-exact with the oracle, and every row the call wrote decodes
+    (torch's e4m3 cast times the footer scale) within one e4m3 step of its
+    bf16 input."""
     import torch
     rng = np.random.default_rng(77 + len(order) + (path == "host"))
     B, hk, d, bs, L = 5, 8, 128, 16, 1
@@ -255,6 +257,17 @@ def test_fp8_multi_token_pages_vs_oracle(gpu_lib, order, path):
             gk, gv = region_bytes(pool)
             assert np.array_equal(gk, ok), f"K after call {call}"
             assert np.array_equal(gv, ov), f"V after call {call}"
+            last = {sl_: i for i, sl_ in enumerate(slots) if sl_ >= 0}
+            for which, reg in ((0, gk), (1, gv)):
+                for sl_, i in last.items():
+                    page = int(offs[sl_ // bs]) * 2
+                    at = page + (sl_ % bs) * g_row
+                    sc = reg[page + data_bytes:page + data_bytes + 4 * hk].view(np.float32)
+                    codes = torch.from_numpy(reg[at:at + g_row].copy()).view(torch.float8_e4m3fn)
+                    got = codes.float().numpy().reshape(hk, d) * sc[:, None]
+                    want = O.decode(O.BF16, bits[which][i]).reshape(hk, d)
+                    bound = 2.0 ** -3 * np.abs(want) + 2.0 ** -9 * sc[:, None]
+                    assert np.all(np.abs(got - want) <= bound * (1 + 1e-6)), (call, which, sl_)
     finally:
         pool.destroy()
 
