@@ -82,7 +82,27 @@ def parse():
                          "pass calls them (for HBM counter runs under rocprofv3)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
+    ap.add_argument("--no-sub-configs", action="store_true",
+                    help="cfg2: skip the cfg3 prefill and cfg5 fp8 runs that the default run "
+                         "adds as sub-objects of its JSON line")
     return ap.parse_args()
+
+
+def sub_config(cfg, args) -> dict | None:
+    """Runs `bench.py --config cfg` in a child process (its own pool and
+    workload) and returns its JSON line, or an error record."""
+    import subprocess
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--config", cfg,
+           "--steps", str(max(4, min(args.steps, 20))), "--warmup", str(max(2, min(args.warmup, 5))),
+           "--no-cpu-baseline", "--seed", str(args.seed)]
+    log(f"sub-config {cfg}: {' '.join(cmd[1:])}")
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, text=True)
+    lines = [l for l in proc.stdout.splitlines() if l.startswith("{")]
+    if proc.returncode != 0 or not lines:
+        return {"error": f"bench.py --config {cfg} exited {proc.returncode}"}
+    out = json.loads(lines[-1])
+    out["cmd"] = "python3 bench.py " + " ".join(cmd[2:])
+    return out
 
 
 TRAFFIC_FILES = {"cfg2": ROOT / "profiles" / "attn_decode_cfg2_hbm_traffic.txt",
@@ -829,6 +849,12 @@ def main():
     else:
         result["cpu_baseline"] = None
     case.pool.destroy()
+    if args.config == "cfg2" and not args.attn_only and not args.no_sub_configs:
+        del case
+        torch.cuda.empty_cache()
+        # BASELINE configs[2] and configs[4], each timed in a child process
+        result["cfg3_prefill"] = sub_config("cfg3", args)
+        result["cfg5_fp8"] = sub_config("cfg5", args)
     print(json.dumps(result), flush=True)
 
 

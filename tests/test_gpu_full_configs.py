@@ -11,8 +11,9 @@ against the oracle:
 * chunked prefill with a shared 1024-token prefix at its full
   batch of 16 (256-token suffix chunks), within 1e-2;
 * configs[1]'s decoder layer: kcmm_decode_layer_step_on_stream at B = 64,
-  hidden 4096, 32/8 heads, intermediate 14336, contexts U[512, 4096] + 1,
-  against the oracle's layer (1e-2 on the output).
+  hidden 4096, 32/8 heads, intermediate 14336, contexts U[512, 4096] + 1:
+  every stage against the oracle's stage at 1e-2, the layer step equal to
+  its components bit for bit, and the layer against the oracle's layer.
 """
 import math
 
@@ -20,8 +21,9 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lattice_amd.bindings import KV_BF16, KV_FP8, KcmmLayerWeights, memcpy_dtoh
+from lattice_amd.bindings import KV_BF16, KV_FP8, KcmmLayerWeights, memcpy_dtoh, memcpy_htod
 from lattice_amd.workload import build_decode_case, build_prefix_shared_case
+from tests import layer_stages as LS
 
 pytestmark = pytest.mark.gpu
 
@@ -133,6 +135,9 @@ def test_cfg3_prefix_shared_prefill_full_batch(gpu_lib):
 
 
 def test_cfg2_decoder_layer_full_size(gpu_lib):
+    """The Cfg2 layer (B = 64, Llama-3-8B dims) stage by stage against the
+    oracle at 1e-2 (tests/layer_stages.py), then the layer step from the same
+    pages: the components' bits, and the whole layer against the oracle's."""
     import torch
     rng = np.random.default_rng(21)
     B, H, I = 64, 4096, 14336
@@ -150,10 +155,17 @@ def test_cfg2_decoder_layer_full_size(gpu_lib):
                 for k, v in w.items()}
         lw = KcmmLayerWeights(**{k: t.data_ptr() for k, t in wdev.items()})
         hid = O.encode(O.BF16, rng.standard_normal((B, H)))
-        hd = torch.from_numpy(hid.view(np.int16)).view(torch.bfloat16).cuda()
         inv = O.default_inv_freq(500000.0, D)
         invd = torch.from_numpy(inv.astype(np.float32)).cuda()
-        kreg, vreg = regions(case.pool)
+        stream = torch.cuda.current_stream().cuda_stream
+        st = LS.run_stages(gpu_lib, case, wdev, hid, invd, HQ, H, I, 1e-5, stream)
+        errs = LS.check_stages(st, case, w, inv, HQ, I, 1e-5, KV_BF16)
+        print("cfg2 layer stages: " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()),
+              flush=True)
+        kreg, vreg = st["kv0"]
+        memcpy_htod(case.pool.va_k(0), kreg)
+        memcpy_htod(case.pool.va_v(0), vreg)
+        hd = torch.from_numpy(hid.view(np.int16)).view(torch.bfloat16).cuda()
         dv = case.dev
         case.pool.decode_layer_step(layer_idx=0, weights=lw, hidden_ptr=hd.data_ptr(),
                                     block_tables_ptr=dv["bt"].data_ptr(),
@@ -162,15 +174,19 @@ def test_cfg2_decoder_layer_full_size(gpu_lib):
                                     inv_freq_ptr=invd.data_ptr(), batch=B, hidden_size=H,
                                     num_q_heads=HQ, intermediate_size=I,
                                     max_blocks_per_seq=case.mbps, rms_eps=1e-5,
-                                    stream_ptr=torch.cuda.current_stream().cuda_stream)
+                                    stream_ptr=stream)
         torch.cuda.synchronize()
-        got = O.decode(O.BF16, hd.cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+        out_bits = hd.cpu().view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(out_bits, st["out"]), "layer step != its components"
+        got = O.decode(O.BF16, out_bits).astype(np.float64)
         ref = O.decode_layer_step_f64(hid, w, kreg, vreg, case.block_tables, case.seq_lens,
                                       case.offsets_f16, inv, HQ, HKV, D, I, BS, g["row_bytes"],
                                       1e-5, dtype=KV_BF16, data_bytes=g["data_bytes"])
         x = O.decode(O.BF16, hid).astype(np.float64)
         err, upd = rel_err(got, ref), rel_err(got - x, ref - x)
         print(f"cfg2 layer B={B} I={I}: err {err:.2e}, update err {upd:.2e}", flush=True)
-        assert np.isfinite(got).all() and err <= 1e-2 and upd <= 5e-2
+        # every stage above holds 1e-2; the whole layer's update is bounded
+        # at twice its measured error (MI355X: 1.03e-2)
+        assert np.isfinite(got).all() and err <= 1e-2 and upd <= 2.1e-2
     finally:
         case.pool.destroy()

@@ -12,8 +12,9 @@ import pytest
 
 import oracle as O
 from lattice_amd.bindings import (KV_BF16, KV_FP8, KcmmLayerWeights, KcmmLayerWeightsFp8,
-                                  memcpy_dtoh)
+                                  memcpy_dtoh, memcpy_htod)
 from lattice_amd.workload import build_decode_case
+from tests import layer_stages as LS
 
 pytestmark = pytest.mark.gpu
 
@@ -35,6 +36,16 @@ def within_ulp(got, ref, n=1):
 
 def rel_err(got, ref):
     return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def fp8_rows_close(a, r, region, page, g, hkv, tol=1e-2):
+    """Dequantized fp8 rows a (GPU) and r (oracle) [Hkv][D]: within one e4m3
+    step each way (2^-3 of the value, 2^-9 of the page scale near zero) plus
+    tol of the row's max |value| for the inputs' own difference."""
+    db = g["data_bytes"]
+    sc = region[page + db:page + db + 4 * hkv].view(np.float32).astype(np.float64)[:, None]
+    bound = 2.0 ** -3 * np.abs(r) + 2.0 ** -8 * sc + tol * np.abs(r).max()
+    return bool(np.all(np.abs(a - r) <= bound))
 
 
 @pytest.mark.parametrize("rows,hidden", [(7, 4096), (64, 4096), (3, 520)])
@@ -218,14 +229,16 @@ def _layer_weights(torch, rng, h, inter, hq, hkv, d):
     (32, 8, 72, 512, 768, KV_BF16, 4), (32, 8, 128, 4096, 1024, KV_FP8, 4),
     (8, 2, 64, 512, 768, KV_FP8, 4), (8, 2, 64, 512, 768, KV_BF16, 136)])
 def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter, dtype, nseq):
-    """One decoder layer through kcmm_decode_layer_step_on_stream vs the
-    oracle's layer (RMSNorm, QKV, RoPE + append, paged attention,
-    O + residual, RMSNorm, gate/up, SiLU*up, down + residual).  head_dim 72
-    takes the unfused QKV path (projection, then the RoPE/append kernel).
-    fp8 pools: the new rows go through the fp8 page writer (bf16 activations,
-    fp8 K/V); tolerances are the fp8 attention's (3e-2 on the layer output,
-    8e-2 on its update).  136 tokens take the 256-token tiles of the fused
-    projections."""
+    """One decoder layer through kcmm_decode_layer_step_on_stream.  First the
+    same layer one component entry point at a time, every stage against the
+    oracle's stage on the GPU's own input (tests/layer_stages.py: 1e-2, the
+    attention on an fp8 pool 3e-2); then, from the same pages, the layer step
+    itself must give the components' bits (hidden state and K/V regions), and
+    its output is compared with the oracle's whole layer (RMSNorm, QKV, RoPE +
+    append, paged attention, O + residual, RMSNorm, gate/up, SiLU*up, down +
+    residual).  head_dim 72 takes the unfused QKV path (projection, then the
+    RoPE/append kernel); fp8 pools take the new rows through the fp8 page
+    writer; 136 tokens take the 256-token tiles of the fused projections."""
     import torch
     lens = ([1, 16, 17, 130] if nseq == 4 else
             np.random.default_rng(nseq).integers(1, 70, size=nseq).tolist())
@@ -237,11 +250,18 @@ def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter, dtype, nseq):
         rng = np.random.default_rng(11)
         w, wdev, lw = _layer_weights(torch, rng, h, inter, hq, hkv, d)
         hid = O.encode(O.BF16, rng.standard_normal((len(lens), h)))
-        hd = bf16_dev(torch, hid)
         inv = O.default_inv_freq(500000.0, d)
         invd = torch.from_numpy(inv.astype(np.float32)).cuda()
         dv = case.dev
-        kreg, vreg = _region(case, "k"), _region(case, "v")
+        stream = torch.cuda.current_stream().cuda_stream
+        st = LS.run_stages(gpu_lib, case, wdev, hid, invd, hq, h, inter, 1e-5, stream)
+        errs = LS.check_stages(st, case, w, inv, hq, inter, 1e-5, dtype)
+        print(f"layer stages hq={hq} d={d} h={h} dtype={dtype} nseq={nseq}: " +
+              ", ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
+        kreg, vreg = st["kv0"]
+        memcpy_htod(case.pool.va_k(0), kreg)
+        memcpy_htod(case.pool.va_v(0), vreg)
+        hd = bf16_dev(torch, hid)
         case.pool.decode_layer_step(layer_idx=0, weights=lw, hidden_ptr=hd.data_ptr(),
                                     block_tables_ptr=dv["bt"].data_ptr(),
                                     seq_lens_ptr=dv["sl"].data_ptr(),
@@ -249,11 +269,14 @@ def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter, dtype, nseq):
                                     inv_freq_ptr=invd.data_ptr(), batch=len(lens),
                                     hidden_size=h, num_q_heads=hq, intermediate_size=inter,
                                     max_blocks_per_seq=case.mbps, rms_eps=1e-5,
-                                    stream_ptr=torch.cuda.current_stream().cuda_stream)
+                                    stream_ptr=stream)
         torch.cuda.synchronize()
+        assert np.array_equal(bits_of(hd), st["out"]), "layer step != its components"
+        assert np.array_equal(_region(case, "k"), st["kv1"][0])
+        assert np.array_equal(_region(case, "v"), st["kv1"][1])
         got = O.decode(O.BF16, bits_of(hd)).astype(np.float64)
-        ref = O.decode_layer_step_f64(hid, w, kreg, vreg, case.block_tables, case.seq_lens,
-                                      case.offsets_f16, inv, hq, hkv, d, inter, 16,
+        ref = O.decode_layer_step_f64(hid, w, kreg.copy(), vreg.copy(), case.block_tables,
+                                      case.seq_lens, case.offsets_f16, inv, hq, hkv, d, inter, 16,
                                       g["row_bytes"], 1e-5, dtype=dtype,
                                       data_bytes=g["data_bytes"])
         x = O.decode(O.BF16, hid).astype(np.float64)
@@ -262,26 +285,9 @@ def test_decode_layer_step(gpu_lib, hq, hkv, d, h, inter, dtype, nseq):
         print(f"layer step hq={hq} d={d} h={h} dtype={dtype}: err {err:.2e}, update err {upd:.2e}",
               flush=True)
         assert np.isfinite(got).all() and err <= (3e-2 if fp8 else 1e-2)
-        assert upd <= (8e-2 if fp8 else 5e-2)
-        # the new token's K / V rows hold what the oracle wrote (within bf16 /
-        # one fp8 step)
-        k1, v1 = _region(case, "k"), _region(case, "v")
-        for b, L in enumerate(lens):
-            pos = L - 1
-            pg = int(case.offsets_f16[case.block_tables[b, pos // 16]]) * 2
-            for got_r, ref_r in ((k1, kreg), (v1, vreg)):
-                if fp8:
-                    a = O.fp8_page_rows(got_r, pg, [pos % 16], hkv, d, g["row_bytes"],
-                                        g["data_bytes"])
-                    r = O.fp8_page_rows(ref_r, pg, [pos % 16], hkv, d, g["row_bytes"],
-                                        g["data_bytes"])
-                    assert rel_err(a, r) <= 1.3e-1, b
-                    continue
-                base = pg + (pos % 16) * g["row_bytes"]
-                seg = slice(base, base + hkv * d * 2)
-                a = O.decode(O.BF16, got_r[seg].view(np.uint16)).astype(np.float64)
-                r = O.decode(O.BF16, ref_r[seg].view(np.uint16)).astype(np.float64)
-                assert rel_err(a, r) <= 2e-2, b
+        # twice the largest update error measured over these cases (MI355X:
+        # bf16 pools 6.2e-3, fp8 pools 8.8e-3); the stages above hold 1e-2
+        assert upd <= (1.75e-2 if fp8 else 1.25e-2)
     finally:
         case.pool.destroy()
 
@@ -444,27 +450,38 @@ def test_decode_layers_fp8_weights(gpu_lib, hq, hkv, d, h, inter, dtype, nseq):
         print(f"fp8-weight layers hq={hq} d={d} h={h} dtype={dtype}: err {err:.2e}, "
               f"update err {upd:.2e}", flush=True)
         assert np.isfinite(got).all() and err <= (3e-2 if fp8 else 1e-2)
-        assert upd <= (8e-2 if fp8 else 5e-2)
-        # the new tokens' K/V rows of both layers hold what the oracle wrote
+        # two layers deep: twice the largest update error measured over these
+        # cases (MI355X: bf16 pools 8.6e-3; the fp8 pool 2.2e-2, where each
+        # side re-quantizes its own new K/V rows to e4m3)
+        assert upd <= (4.5e-2 if fp8 else 1.75e-2)
+        # the new tokens' K/V rows of both layers hold what the oracle wrote:
+        # layer 0's within the bf16 tolerance, layer 1's within twice that
+        # (its input carries layer 0's error); fp8 pools one e4m3 step more
         for layer in range(2):
+            tol = 1e-2 * (layer + 1)
             k1 = memcpy_dtoh(case.pool.va_k(layer), mb)
             v1 = memcpy_dtoh(case.pool.va_v(layer), mb)
+            worst = 0.0
             for b, L in enumerate(lens):
                 pos = L - 1
                 pg = int(case.offsets_f16[case.block_tables[b, pos // 16]]) * 2
                 for got_r, ref_r in ((k1, regs[layer][0]), (v1, regs[layer][1])):
                     if fp8:
+                        # both rows are one e4m3 rounding of bf16 rows that
+                        # agree to the layer tolerance
                         a = O.fp8_page_rows(got_r, pg, [pos % 16], hkv, d, g["row_bytes"],
-                                            g["data_bytes"])
+                                            g["data_bytes"])[0]
                         r = O.fp8_page_rows(ref_r, pg, [pos % 16], hkv, d, g["row_bytes"],
-                                            g["data_bytes"])
-                        assert rel_err(a, r) <= 1.3e-1, (layer, b)
+                                            g["data_bytes"])[0]
+                        assert fp8_rows_close(a, r, got_r, pg, g, hkv, tol), (layer, b)
                         continue
                     base = pg + (pos % 16) * g["row_bytes"]
                     seg = slice(base, base + hkv * d * 2)
                     a = O.decode(O.BF16, got_r[seg].view(np.uint16)).astype(np.float64)
                     r = O.decode(O.BF16, ref_r[seg].view(np.uint16)).astype(np.float64)
-                    assert rel_err(a, r) <= 2e-2, (layer, b)
+                    worst = max(worst, rel_err(a, r))
+            print(f"  layer {layer} new K/V rows: max rel err {worst:.2e}", flush=True)
+            assert worst <= tol, (layer, worst)
     finally:
         case.pool.destroy()
 
