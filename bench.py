@@ -621,6 +621,7 @@ def main():
         tiled_env = os.environ.get("KCMM_GEMM_TILED")
         for backend, out in (("1", m256), ("0", m256_stream), ("torch", m256_torch)):
             os.environ["KCMM_GEMM_TILED"] = "0" if backend == "0" else "1"
+            lib.reload_tunables()       # the library reads KCMM_* once
             for name, n, k in GEMMS:
                 if backend == "torch":
                     fn = lambda l, n=n, k=k, name=name: torch.matmul(
@@ -645,6 +646,7 @@ def main():
             os.environ.pop("KCMM_GEMM_TILED", None)
         else:
             os.environ["KCMM_GEMM_TILED"] = tiled_env
+        lib.reload_tunables()
         del x256, y256
         log("M=256 GEMM ms (tiled MFMA kernel): " + ", ".join(f"{k}={v:.4f}" for k, v in m256.items()))
         log("M=256 GEMM ms (weight-stream kernel): " +
@@ -834,11 +836,13 @@ def main():
                                        "(512 MiB write outside the events), as in a layer loop")
         prev = os.environ.get("KCMM_GEMM_TILED")
         os.environ["KCMM_GEMM_TILED"] = "0"        # the weight-stream kernel's own plan
+        lib.reload_tunables()
         result["gemm_m256_stream_kernel"] = gemm_report(m256_stream, 256, False)
         if prev is None:
             os.environ.pop("KCMM_GEMM_TILED", None)
         else:
             os.environ["KCMM_GEMM_TILED"] = prev
+        lib.reload_tunables()
         result["gemm_m256_torch_reference"] = gemm_report(m256_torch, 256, False, plan=False)
         result["tiering"] = tiering_report(lib, args)
     if not args.no_cpu_baseline:

@@ -103,8 +103,13 @@ int kcmm_paged_attn_decode_fp8_on_stream(
  * capture, tight serving loops, harnesses that forbid hipMalloc).  A batch
  * whose scratch would exceed 24 MiB is refused (-1, error text names the
  * sizes); at the Llama-3-8B decode shape (32/8 heads, head_dim 128) that is
- * about 300 sequences.  Every call on a GPU shares that GPU's array: calls
- * that overlap on one GPU (other streams, other threads) race.  Enqueue only.
+ * about 300 sequences.  Every call on a GPU shares that GPU's array, so
+ * calls take turns with it: a call on a different stream from the previous
+ * call on that GPU first waits (hipStreamWaitEvent on one event per GPU,
+ * created with the array's address on the first call) for that call's
+ * kernels, and the array keeps the last call's contents.  Under HIP graph
+ * capture no event is recorded or waited on: a graph that holds two such
+ * calls on parallel branches must order them itself.  Enqueue only.
  */
 int kcmm_paged_attn_decode_bf16_noalloc_on_stream(
     kcmm_pool_t *pool, uint32_t layer_idx, uint64_t query_ptr, uint64_t out_ptr,
@@ -112,6 +117,13 @@ int kcmm_paged_attn_decode_bf16_noalloc_on_stream(
     uint64_t block_offsets_f16_ptr, uint32_t batch, uint32_t num_q_heads,
     uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
     uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
+
+/** Reads the KCMM_* tuning variables (KCMM_ATTN_*, KCMM_GEMM_*) again.  The
+ *  library reads them once, on first use, so that launch paths make no
+ *  getenv call; tests and tuning runs that change them call this after the
+ *  change.  Not to be called while other threads launch.  No counterpart
+ *  in the reference. */
+void kcmm_reload_tunables(void);
 
 /** fp32 pool: fp32 q/out, same tensor contract as
  *  kcmm_paged_attn_decode_f16 (ref kcmm.h:505).  Synchronizes before

@@ -214,6 +214,7 @@ SIGNATURES = {
     "kcmm_get_num_layers": ([_P], _U32),
     "kcmm_get_max_batch": ([_P], _U32),
     "kcmm_get_max_seq_len": ([_P], _U32),
+    "kcmm_reload_tunables": ([], None),
 }
 
 
@@ -235,6 +236,10 @@ class KcmmLibrary:
             fn = getattr(self.lib, name)
             fn.argtypes = args
             fn.restype = res
+
+    def reload_tunables(self) -> None:
+        """Re-read the KCMM_* tuning variables (the library reads them once)."""
+        self.lib.kcmm_reload_tunables()
 
     def create_pool(self, config: KcmmConfig, kv_dtype: int = KV_F16) -> "KcmmPool":
         h = self.lib.kcmm_pool_create_typed(C.byref(config), kv_dtype)

@@ -39,7 +39,7 @@ HIP_FLAGS = [
 ]
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 
-HOST_SOURCES = ["pool_core.cpp", "tiering.cpp", "ffi.cpp"]
+HOST_SOURCES = ["pool_core.cpp", "tiering.cpp", "ffi.cpp", "tunables.cpp"]
 HIP_SOURCES = ["kernels/backing.hip", "kernels/attn_decode.hip", "kernels/attn_prefill.hip",
                "kernels/kv_write.hip",
                "kernels/page_copy.hip", "kernels/gemm.hip", "kernels/gemm_tiled.hip",

@@ -19,6 +19,24 @@ std::unique_ptr<PageBacking> make_backing(int device, std::string* err);
 
 bool set_device(int device, std::string* err);
 
+// KCMM_* tunables, read once per process on first use (tunables.cpp).
+enum class Tun {
+    kAttnWaves,     // KCMM_ATTN_WAVES
+    kAttnHw,        // KCMM_ATTN_HW
+    kAttnMinTiles,  // KCMM_ATTN_MIN_TILES
+    kAttnDepth,     // KCMM_ATTN_DEPTH
+    kAttnGeneric,   // KCMM_ATTN_GENERIC (set: force the any-shape kernels)
+    kGemmSplits,    // KCMM_GEMM_SPLITS
+    kGemmWgs,       // KCMM_GEMM_WGS
+    kGemmTiled,     // KCMM_GEMM_TILED
+    kGemmTile,      // KCMM_GEMM_TILE
+    kCount
+};
+// true and *value = atoi(variable) when the variable is set.
+bool tunable(Tun t, int* value);
+int tunable_or(Tun t, int dflt);
+void reload_tunables();
+
 // Per-(device, stream, slot, host thread) device scratch; grown on demand
 // (slot 0: decode attention partials, 1: GEMM split partials, 2: decode
 // attention segment table, 3: decode layer-step activations, 4: the final
@@ -31,6 +49,10 @@ bool set_device(int device, std::string* err);
 // graph capture: run each shape once before capturing it.
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err);
+// Buffers of exited threads are freed by the next workspace allocation;
+// this frees them now (device synchronize first).  Count of those pending.
+bool release_orphaned_workspaces(std::string* err);
+size_t orphaned_workspaces();
 bool synchronize_device(int device, std::string* err);
 
 // Paged decode attention over one layer's K/V regions.

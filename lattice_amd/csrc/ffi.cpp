@@ -265,6 +265,8 @@ void kcmm_pool_destroy(kcmm_pool_t* pool) {
     if (pool == nullptr) return;
     std::string err;
     kcmm::dev::synchronize_device(pool->device, &err);  // ref ffi.rs:552-553
+    // scratch of host threads that have exited since the last allocation
+    kcmm::dev::release_orphaned_workspaces(&err);
     delete pool;
 }
 

@@ -57,23 +57,37 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
 
-// Address of `scratch` on the current device, looked up once per device.
-bool noalloc_scratch(uint8_t** out, std::string* err) {
-    static std::mutex mu;
-    static uint8_t* ptrs[kMaxDevices] = {};
+// Per device: the address of `scratch` there (hipGetSymbolAddress, once),
+// and one event (created once) that marks the end of the last no-alloc
+// call's kernels.  A call on a different stream waits on that event first,
+// so calls on two streams of one GPU take turns with the array instead of
+// overwriting each other's partials.  All no-alloc calls hold g_noalloc_mu
+// from that wait until their own event record.
+struct NoAllocDevice {
+    uint8_t* scratch = nullptr;
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool used = false;
+};
+std::mutex g_noalloc_mu;
+NoAllocDevice g_noalloc[kMaxDevices];
+
+// The current device's state, set up on its first call; g_noalloc_mu held.
+bool noalloc_device(NoAllocDevice** out, std::string* err) {
     int dev = 0;
     KCMM_HIP_CHECK(hipGetDevice(&dev), err);
     if (dev < 0 || dev >= kMaxDevices) {
         *err = "decode attention (no-alloc): device ordinal out of range";
         return false;
     }
-    std::lock_guard<std::mutex> lk(mu);
-    if (ptrs[dev] == nullptr) {
+    NoAllocDevice& d = g_noalloc[dev];
+    if (d.scratch == nullptr) {
         void* p = nullptr;
         KCMM_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), err);
-        ptrs[dev] = static_cast<uint8_t*>(p);
+        KCMM_HIP_CHECK(hipEventCreateWithFlags(&d.done, hipEventDisableTiming), err);
+        d.scratch = static_cast<uint8_t*>(p);
     }
-    *out = ptrs[dev];
+    *out = &d;
     return true;
 }
 
@@ -1029,28 +1043,27 @@ void launch_generic(const AttnParams& p, int head_dim, float scale, hipStream_t 
                            scale, tlog2);
 }
 
-int env_int(const char* name, int dflt, int lo, int hi) {
-    const char* e = std::getenv(name);
-    if (!e) return dflt;
-    const int x = std::atoi(e);
+int env_int(dev::Tun t, int dflt, int lo, int hi) {
+    int x = 0;
+    if (!dev::tunable(t, &x)) return dflt;
     return x < lo || x > hi ? dflt : x;
 }
 
-// Tunables, read on every call (getenv is cheap next to a launch):
+// Tunables (read once per process, dev::tunable):
 // KCMM_ATTN_WAVES waves of the streaming kernel (default by page type),
 // KCMM_ATTN_HW waves per workgroup (kv heads read together; the largest
 // divisor of Hkv not above it is used), KCMM_ATTN_MIN_TILES the smallest
 // slice a workgroup takes, KCMM_ATTN_DEPTH tiles in flight (2 or 3; 3 keeps
 // at most 4 waves per workgroup).
 int stream_waves(int dtype) {
-    return env_int("KCMM_ATTN_WAVES", dtype == kDtFP8 ? 2048 : 1024, 1, 1 << 20);
+    return env_int(dev::Tun::kAttnWaves, dtype == kDtFP8 ? 2048 : 1024, 1, 1 << 20);
 }
 // Measured in the full decode step (Llama-3-8B shape, three runs each):
 // 16-bit pages are as fast with one-wave workgroups as with head blocks (the
 // layer step is 1% faster with HW = 1), fp8 pages gain 3% at HW = 8.
-int stream_hw(int dtype) { return env_int("KCMM_ATTN_HW", dtype == kDtFP8 ? 8 : 1, 1, 8); }
-int stream_min_tiles() { return env_int("KCMM_ATTN_MIN_TILES", 8, 1, 1 << 16); }
-int stream_depth() { return env_int("KCMM_ATTN_DEPTH", 2, 2, 3); }
+int stream_hw(int dtype) { return env_int(dev::Tun::kAttnHw, dtype == kDtFP8 ? 8 : 1, 1, 8); }
+int stream_min_tiles() { return env_int(dev::Tun::kAttnMinTiles, 8, 1, 1 << 16); }
+int stream_depth() { return env_int(dev::Tun::kAttnDepth, 2, 2, 3); }
 
 template <int DT, int D, int BS>
 bool launch_stream(AttnParams& p, hipStream_t s, bool no_alloc, std::string* err) {
@@ -1081,19 +1094,28 @@ bool launch_stream(AttnParams& p, hipStream_t s, bool no_alloc, std::string* err
     const size_t info_bytes = static_cast<size_t>(p.batch) * p.kv_heads * sizeof(int2);
     void* ws = nullptr;
     void* info = nullptr;
+    std::unique_lock<std::mutex> noalloc_lock;
+    NoAllocDevice* nd = nullptr;
+    bool capturing = false;
     if (no_alloc) {
         // nothing here needs to start zeroed: every partial and segment
         // record is written before it is read
-        uint8_t* base = nullptr;
-        if (!noalloc_scratch(&base, err)) return false;
         if (part_bytes + info_bytes > kNoAllocScratchBytes) {
             *err = "decode attention (no-alloc): this batch needs " +
                    std::to_string(part_bytes + info_bytes) + " bytes of scratch, the static "
                    "scratch holds " + std::to_string(kNoAllocScratchBytes);
             return false;
         }
-        ws = base;
-        info = base + part_bytes;
+        noalloc_lock = std::unique_lock<std::mutex>(g_noalloc_mu);
+        if (!noalloc_device(&nd, err)) return false;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        KCMM_HIP_CHECK(hipStreamIsCapturing(s, &cs), err);
+        // under graph capture the caller orders the graph's nodes
+        capturing = cs != hipStreamCaptureStatusNone;
+        if (!capturing && nd->used && nd->last != s)
+            KCMM_HIP_CHECK(hipStreamWaitEvent(s, nd->done, 0), err);
+        ws = nd->scratch;
+        info = nd->scratch + part_bytes;
     } else {
         if (!dev::stream_workspace(reinterpret_cast<uint64_t>(s), 0, part_bytes, &ws, false, err) ||
             !dev::stream_workspace(reinterpret_cast<uint64_t>(s), 2, info_bytes, &info, false, err))
@@ -1114,6 +1136,11 @@ bool launch_stream(AttnParams& p, hipStream_t s, bool no_alloc, std::string* err
     KCMM_HIP_CHECK(hipGetLastError(), err);
     launch_merge<DT == kDtFP8 ? kDtBF16 : DT, D>(p, s);
     KCMM_HIP_CHECK(hipGetLastError(), err);
+    if (no_alloc && !capturing) {
+        KCMM_HIP_CHECK(hipEventRecord(nd->done, s), err);
+        nd->last = s;
+        nd->used = true;
+    }
     return true;
 }
 
@@ -1157,7 +1184,8 @@ bool attn_decode(const AttnDecodeArgs& a, std::string* err) {
     // 8-token groups; 16-bit pages at head_dim 64 or 128, fp8 pages at 128.
     const bool grouped = p.num_q_heads % p.kv_heads == 0 && p.group <= 16;
     const bool stream_dim = a.head_dim == 64 || a.head_dim == 128;
-    const bool force_generic = std::getenv("KCMM_ATTN_GENERIC") != nullptr;
+    int generic_flag = 0;
+    const bool force_generic = dev::tunable(dev::Tun::kAttnGeneric, &generic_flag);
     if (grouped && a.block_size % 8 == 0 && !force_generic) {
         if (a.dtype == kDtFP8 && a.head_dim == 128)
             return launch_stream_bs<kDtFP8, 128>(p, s, a.no_alloc, err);

@@ -692,8 +692,9 @@ bool attn_prefill(const AttnPrefillArgs& a, std::string* err) {
     // (the MFMA kernel takes column maxima of the raw scores: scale > 0)
     const bool mfma_type = a.dtype == kDtF16 || a.dtype == kDtBF16 ||
                            (a.dtype == kDtFP8 && a.head_dim == 128);
+    int generic_flag = 0;
     if (mfma_type && mfma_group && mfma_dim && pow2_bs && a.scale > 0.0f &&
-        std::getenv("KCMM_ATTN_GENERIC") == nullptr) {
+        !dev::tunable(dev::Tun::kAttnGeneric, &generic_flag)) {
         if (a.dtype == kDtFP8) return launch_group<kDtFP8, 128>(a, p, s, err);
         if (a.dtype == kDtF16)
             return a.head_dim == 64 ? launch_group<kDtF16, 64>(a, p, s, err)

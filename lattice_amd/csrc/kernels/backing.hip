@@ -131,21 +131,85 @@ bool set_device(int device, std::string* err) {
 // never share one, and a buffer is only ever handed to the thread that
 // grows it, so a growth (which frees the old buffer once its stream has
 // drained) cannot free a buffer another thread is about to launch with.
-// `zero_fill` buffers start zeroed (their users restore zero).  Buffers of
-// threads that have exited stay allocated until the process ends.
+// `zero_fill` buffers start zeroed (their users restore zero).
+//
+// When a thread exits, its buffers become orphans (no HIP call is made at
+// thread exit: the runtime may be shutting down); the next workspace
+// allocation on any thread, or a pool destroy, synchronizes their device and
+// frees them, so a server whose worker threads come and go holds at most
+// the buffers of its live threads plus those of threads that exited since
+// the last allocation.
+namespace {
+
+struct Ws {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+using WsKey = std::tuple<int, uint64_t, int, std::thread::id>;
+
+// Never destroyed, so a thread's exit (including the main thread's, after
+// main returns) can always reach them.
+std::mutex& ws_mutex() {
+    static std::mutex* m = new std::mutex;
+    return *m;
+}
+std::map<WsKey, Ws>& ws_table() {
+    static auto* t = new std::map<WsKey, Ws>;
+    return *t;
+}
+std::vector<std::pair<int, void*>>& ws_orphans() {
+    static auto* v = new std::vector<std::pair<int, void*>>;
+    return *v;
+}
+
+struct ThreadWsOwner {
+    ~ThreadWsOwner() {
+        std::lock_guard<std::mutex> lk(ws_mutex());
+        const std::thread::id me = std::this_thread::get_id();
+        auto& t = ws_table();
+        for (auto it = t.begin(); it != t.end();) {
+            if (std::get<3>(it->first) == me) {
+                if (it->second.ptr) ws_orphans().emplace_back(std::get<0>(it->first), it->second.ptr);
+                it = t.erase(it);
+            } else {
+                ++it;
+            }
+        }
+    }
+};
+thread_local ThreadWsOwner t_ws_owner;
+
+// Frees the orphaned buffers; call with ws_mutex() held.
+bool free_orphans_locked(std::string* err) {
+    auto& o = ws_orphans();
+    if (o.empty()) return true;
+    int cur = 0;
+    KCMM_HIP_CHECK(hipGetDevice(&cur), err);
+    while (!o.empty()) {
+        const int dev = o.back().first;
+        KCMM_HIP_CHECK(hipSetDevice(dev), err);
+        KCMM_HIP_CHECK(hipDeviceSynchronize(), err);
+        for (size_t i = o.size(); i-- > 0;) {
+            if (o[i].first != dev) continue;
+            KCMM_HIP_CHECK(hipFree(o[i].second), err);
+            o.erase(o.begin() + static_cast<std::ptrdiff_t>(i));
+        }
+    }
+    KCMM_HIP_CHECK(hipSetDevice(cur), err);
+    return true;
+}
+
+}  // namespace
+
 bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool zero_fill,
                       std::string* err) {
-    struct Ws {
-        void* ptr = nullptr;
-        size_t bytes = 0;
-    };
-    static std::mutex mu;
-    static std::map<std::tuple<int, uint64_t, int, std::thread::id>, Ws> table;
+    (void)&t_ws_owner;   // registers this thread's owner (its destructor runs at thread exit)
     int dev = 0;
     KCMM_HIP_CHECK(hipGetDevice(&dev), err);
-    std::lock_guard<std::mutex> lk(mu);
-    Ws& w = table[std::make_tuple(dev, stream, slot, std::this_thread::get_id())];
+    std::lock_guard<std::mutex> lk(ws_mutex());
+    Ws& w = ws_table()[std::make_tuple(dev, stream, slot, std::this_thread::get_id())];
     if (w.bytes < bytes) {
+        if (!free_orphans_locked(err)) return false;
         if (w.ptr) {
             KCMM_HIP_CHECK(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)), err);
             KCMM_HIP_CHECK(hipFree(w.ptr), err);
@@ -166,6 +230,16 @@ bool stream_workspace(uint64_t stream, int slot, size_t bytes, void** out, bool 
     }
     *out = w.ptr;
     return true;
+}
+
+bool release_orphaned_workspaces(std::string* err) {
+    std::lock_guard<std::mutex> lk(ws_mutex());
+    return free_orphans_locked(err);
+}
+
+size_t orphaned_workspaces() {
+    std::lock_guard<std::mutex> lk(ws_mutex());
+    return ws_orphans().size();
 }
 
 bool synchronize_device(int device, std::string* err) {

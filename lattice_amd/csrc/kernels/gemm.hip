@@ -447,20 +447,15 @@ __global__ __launch_bounds__(256) void gemm_split_swiglu(const float* __restrict
     *reinterpret_cast<u32x2*>(act + i) = pack4_bf16(a);
 }
 
-int env_int(const char* name, int dflt) {
-    const char* e = std::getenv(name);
-    return e ? std::atoi(e) : dflt;
-}
-
 // K splits: the smallest divisor of K/kch giving at least `target` workgroups
 // (KCMM_GEMM_WGS, default 256: fewer, longer splits measured faster than
 // 512-1024 at the Llama-3-8B decode shapes) with each split at least two
 // chunks long; at most 16.
 int choose_splits(int N, int K, int kch, int mgroups) {
     const int chunks = K / kch;
-    const int forced = env_int("KCMM_GEMM_SPLITS", 0);
+    const int forced = dev::tunable_or(dev::Tun::kGemmSplits, 0);
     if (forced >= 1 && forced <= 16 && chunks % forced == 0) return forced;
-    const int target = env_int("KCMM_GEMM_WGS", 256);
+    const int target = dev::tunable_or(dev::Tun::kGemmWgs, 256);
     const int tiles = (N / 64) * mgroups;
     int best = 1;
     for (int s = 1; s <= std::min(chunks, 16); ++s) {
@@ -575,7 +570,7 @@ bool gemm_bf16(uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t n, uint3
     if (!shape_ok(m, n, k, err)) return false;
     // many tokens: the LDS-tiled MFMA kernel (KCMM_GEMM_TILED=0 keeps the
     // weight-stream kernel)
-    if (m > 128 && env_int("KCMM_GEMM_TILED", 1) != 0)
+    if (m > 128 && dev::tunable_or(dev::Tun::kGemmTiled, 1) != 0)
         return gemm_bf16_tiled(x, w, y, m, n, k, stream, residual, err);
     GemmParams p = base_params(x, w, m, n, k);
     p.Y = reinterpret_cast<uint16_t*>(y);
@@ -596,7 +591,7 @@ bool gemm_plan(uint32_t m, uint32_t n, uint32_t k, bool fp8_weights, GemmPlan* p
                std::string* err) {
     if (!shape_ok(m, n, k, err)) return false;
     *plan = GemmPlan{};
-    if (m > 128 && env_int("KCMM_GEMM_TILED", 1) != 0) {
+    if (m > 128 && dev::tunable_or(dev::Tun::kGemmTiled, 1) != 0) {
         plan->kernel = 1;
         gemm_tiled_plan(m, n, k, &plan->splits, &plan->tile);
     } else {
@@ -620,7 +615,7 @@ bool gemm_fp8w_bf16(uint64_t x, uint64_t w8, uint64_t wscale, uint64_t y, uint32
     }
     // many tokens: the LDS-tiled kernel (KCMM_GEMM_TILED=0 keeps the
     // weight-stream kernel)
-    if (m > 128 && env_int("KCMM_GEMM_TILED", 1) != 0)
+    if (m > 128 && dev::tunable_or(dev::Tun::kGemmTiled, 1) != 0)
         return gemm_tiled(x, w8, wscale, y, m, n, k, stream, residual, err);
     GemmParams p = base_params(x, w8, m, n, k);
     p.Y = reinterpret_cast<uint16_t*>(y);

@@ -273,11 +273,6 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_tiled_kernel(TiledParams p)
     }
 }
 
-int env_int(const char* name, int dflt) {
-    const char* e = std::getenv(name);
-    return e ? std::atoi(e) : dflt;
-}
-
 // Kernel configurations: tile (BN weight rows x BM tokens), wave grid and
 // LDS stages; every one keeps two waves on each SIMD (8-wave workgroups, or
 // 4-wave workgroups small enough for two per CU).
@@ -333,7 +328,7 @@ void by_config(int id, F&& f) {
 // (configuration index) and KCMM_GEMM_SPLITS override.
 TiledConfig choose(int M, int N, int K) {
     const int chunks = K / 64;
-    const int forced_tile = env_int("KCMM_GEMM_TILE", -1);
+    const int forced_tile = dev::tunable_or(dev::Tun::kGemmTile, -1);
     auto ok_split = [&](int s) { return chunks % s == 0 && chunks / s >= 8; };
     TiledConfig best{-1, 0, 0, 1};
     if (forced_tile >= 0 && forced_tile < kCfgs && N % kCfgBN[forced_tile] == 0) {
@@ -364,7 +359,7 @@ TiledConfig choose(int M, int N, int K) {
         }
         if (best.id < 0) best = TiledConfig{3, kCfgBN[3], kCfgBM[3], 1};   // N % 64 == 0 only
     }
-    const int forced = env_int("KCMM_GEMM_SPLITS", 0);
+    const int forced = dev::tunable_or(dev::Tun::kGemmSplits, 0);
     if (forced >= 1 && forced <= 16 && chunks % forced == 0) best.splits = forced;
     return best;
 }

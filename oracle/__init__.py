@@ -32,9 +32,17 @@ def lib() -> C.CDLL:
     return _lib
 
 
+REF_C_CALLER = Path("/root/reference/examples/kcmm_c_integration.c")
+
+
 def build() -> None:
+    """Compiles liboracle.so and, where the reference tree is present (this
+    container; the GPU box only has the built files), the reference's own C
+    caller of the ABI into _ref/ (see the Makefile)."""
     import subprocess
-    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    subprocess.run(["make", "-s", "-B", "-C", str(HERE), "liboracle.so"], check=True)
+    if REF_C_CALLER.exists():
+        subprocess.run(["make", "-s", "-B", "-C", str(HERE), "ref"], check=True)
 
 
 P = C.c_void_p

@@ -41,3 +41,22 @@ def gpu_lib():
     assert torch.cuda.is_available(), "GPU tests need a ROCm device"
     assert DEFAULT_LIB.exists(), f"{DEFAULT_LIB} not built (python -m lattice_amd.build)"
     return KcmmLibrary(DEFAULT_LIB)
+
+
+@pytest.fixture
+def tunables(gpu_lib, monkeypatch):
+    """Sets KCMM_* tuning variables for one test.  The library reads them once
+    per process, so every change, and the restore after the test, is
+    followed by kcmm_reload_tunables."""
+    class _Tunables:
+        def setenv(self, name, value):
+            monkeypatch.setenv(name, value)
+            gpu_lib.reload_tunables()
+
+        def delenv(self, name):
+            monkeypatch.delenv(name, raising=False)
+            gpu_lib.reload_tunables()
+
+    yield _Tunables()
+    monkeypatch.undo()
+    gpu_lib.reload_tunables()

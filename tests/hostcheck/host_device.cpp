@@ -143,6 +143,8 @@ bool synchronize_device(int, std::string*) { return true; }
 bool stream_workspace(uint64_t, int, size_t, void**, bool, std::string* err) {
     return no_device(err);
 }
+bool release_orphaned_workspaces(std::string*) { return true; }
+size_t orphaned_workspaces() { return 0; }
 bool attn_decode(const AttnDecodeArgs&, std::string* err) { return no_device(err); }
 bool attn_prefill(const AttnPrefillArgs&, std::string* err) { return no_device(err); }
 bool kv_write_rows(const KvRowsArgs&, std::string* err) { return no_device(err); }

@@ -99,10 +99,10 @@ def test_mfma_path_shapes(gpu_lib, hq, hkv, d, bs):
 
 @pytest.mark.parametrize("hw,hq,hkv", [("4", 24, 6), ("8", 24, 12), ("8", 10, 5)])
 @pytest.mark.parametrize("dtype", [KV_BF16, KV_FP8])
-def test_head_block_not_dividing(gpu_lib, monkeypatch, hw, hq, hkv, dtype):
+def test_head_block_not_dividing(gpu_lib, tunables, hw, hq, hkv, dtype):
     """Workgroups take the largest divisor of Hkv not above KCMM_ATTN_HW
     (6 kv heads at 4 -> 3, 12 at 8 -> 6, 5 at 8 -> 5)."""
-    monkeypatch.setenv("KCMM_ATTN_HW", hw)
+    tunables.setenv("KCMM_ATTN_HW", hw)
     rng = np.random.default_rng(hq + hkv)
     ctx = rng.integers(1, 900, size=7)
     case = build_decode_case(gpu_lib, batch=7, num_q_heads=hq, kv_heads=hkv, head_dim=128,
@@ -129,11 +129,11 @@ def test_generic_path_shapes(gpu_lib, hq, hkv, d, bs):
 
 @pytest.mark.parametrize("dtype", [KV_BF16, KV_F16, KV_FP8])
 @pytest.mark.parametrize("bs,ctx", [(16, [2500, 1, 1024, 1025, 0, 700]), (1, [1100, 3, 2049])])
-def test_generic_kernel_forced(gpu_lib, monkeypatch, dtype, bs, ctx):
+def test_generic_kernel_forced(gpu_lib, tunables, dtype, bs, ctx):
     """KCMM_ATTN_GENERIC forces the any-shape kernel at the Llama-3-8B head
     shape: contexts across its 1024-position staging chunks (and exactly at
     their edges), one-token pages, an empty sequence."""
-    monkeypatch.setenv("KCMM_ATTN_GENERIC", "1")
+    tunables.setenv("KCMM_ATTN_GENERIC", "1")
     case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
                              block_size=bs, ctx_lens=ctx, dtype=dtype, seed=21 + bs)
     try:
@@ -142,10 +142,10 @@ def test_generic_kernel_forced(gpu_lib, monkeypatch, dtype, bs, ctx):
         case.pool.destroy()
 
 
-def test_generic_kernel_many_pairs(gpu_lib, monkeypatch):
+def test_generic_kernel_many_pairs(gpu_lib, tunables):
     """1280 (sequence, head) pairs: the any-shape kernel's 256-lane
     workgroups."""
-    monkeypatch.setenv("KCMM_ATTN_GENERIC", "1")
+    tunables.setenv("KCMM_ATTN_GENERIC", "1")
     rng = np.random.default_rng(77)
     ctx = rng.integers(0, 700, size=40)
     case = build_decode_case(gpu_lib, batch=40, num_q_heads=32, kv_heads=8, head_dim=64,
@@ -224,23 +224,23 @@ def test_entry_point_variants_agree(gpu_lib):
 
 
 @pytest.fixture(params=["default", "depth3", "many_waves", "four_heads_per_wg", "all_heads_per_wg"])
-def stream_tuning(request, monkeypatch):
+def stream_tuning(request, tunables):
     """Streaming-kernel settings: the default, three tiles in flight, a tiny
     slice per workgroup (every (b, kv head) split over many slices, so the
     log-sum-exp merge runs everywhere), and workgroups of four waves (four
     kv heads) or of eight waves (all kv heads of a token row); the default
     is one wave per workgroup for 16-bit pages, eight for fp8."""
     if request.param == "depth3":
-        monkeypatch.setenv("KCMM_ATTN_DEPTH", "3")
+        tunables.setenv("KCMM_ATTN_DEPTH", "3")
     elif request.param == "many_waves":
-        monkeypatch.setenv("KCMM_ATTN_WAVES", "4096")
-        monkeypatch.setenv("KCMM_ATTN_MIN_TILES", "1")
+        tunables.setenv("KCMM_ATTN_WAVES", "4096")
+        tunables.setenv("KCMM_ATTN_MIN_TILES", "1")
     elif request.param == "four_heads_per_wg":
-        monkeypatch.setenv("KCMM_ATTN_HW", "4")
+        tunables.setenv("KCMM_ATTN_HW", "4")
     elif request.param == "all_heads_per_wg":
-        monkeypatch.setenv("KCMM_ATTN_HW", "8")
-        monkeypatch.setenv("KCMM_ATTN_WAVES", "2048")
-        monkeypatch.setenv("KCMM_ATTN_MIN_TILES", "2")
+        tunables.setenv("KCMM_ATTN_HW", "8")
+        tunables.setenv("KCMM_ATTN_WAVES", "2048")
+        tunables.setenv("KCMM_ATTN_MIN_TILES", "2")
     return request.param
 
 

@@ -33,9 +33,9 @@ def _randn_bf16(torch, shape, std, seed):
 
 @pytest.mark.parametrize("m,inter,k", [(5, 256, 512), (64, 1024, 4096), (64, 14336, 4096),
                                        (100, 512, 1024), (256, 768, 2048)])
-def test_swiglu_gemm_matches_unfused(gpu_lib, monkeypatch, m, inter, k):
+def test_swiglu_gemm_matches_unfused(gpu_lib, tunables, m, inter, k):
     import torch
-    monkeypatch.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
+    tunables.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
     x = _randn_bf16(torch, (m, k), 1.0, 1)
     w = _randn_bf16(torch, (2 * inter, k), 0.05, 2)
     gu = torch.empty((m, 2 * inter), dtype=torch.bfloat16, device="cuda")
@@ -59,13 +59,13 @@ def test_swiglu_gemm_matches_unfused(gpu_lib, monkeypatch, m, inter, k):
 @pytest.mark.parametrize("hq,hkv,d,h,nseq", [(32, 8, 128, 4096, 6), (8, 2, 64, 256, 6),
                                               (12, 4, 80, 512, 6), (32, 8, 128, 256, 6),
                                               (8, 2, 128, 1024, 160)])
-def test_qkv_rope_append_matches_unfused(gpu_lib, monkeypatch, hq, hkv, d, h, nseq):
+def test_qkv_rope_append_matches_unfused(gpu_lib, tunables, hq, hkv, d, h, nseq):
     """q_out and every byte of both regions identical between the fused QKV
     projection and projection -> RoPE/append; ragged lengths, a sequence
     with no token and one whose position lies past its table (both
     skipped: their q_out rows keep the NaN fill)."""
     import torch
-    monkeypatch.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
+    tunables.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
     lens = ([1, 16, 17, 300, 0, 48] * (nseq // 6 + 1))[:nseq]
     B = len(lens)
     n = (hq + 2 * hkv) * d
@@ -110,12 +110,12 @@ def test_qkv_rope_append_matches_unfused(gpu_lib, monkeypatch, hq, hkv, d, h, ns
 
 
 @pytest.mark.parametrize("splits", ["2", "4", "8", "16"])
-def test_split_k_in_kernel_reduction(gpu_lib, monkeypatch, splits):
+def test_split_k_in_kernel_reduction(gpu_lib, tunables, splits):
     """Forced split counts: every split count gives the oracle's product,
     and repeated calls give identical bits (partials are summed in split
     order)."""
     import torch
-    monkeypatch.setenv("KCMM_GEMM_SPLITS", splits)
+    tunables.setenv("KCMM_GEMM_SPLITS", splits)
     m, n, k = 64, 4096, 4096
     x = _randn_bf16(torch, (m, k), 1.0, 6)
     w = _randn_bf16(torch, (n, k), 0.02, 7)
@@ -137,9 +137,9 @@ def test_split_k_in_kernel_reduction(gpu_lib, monkeypatch, splits):
 
 
 @pytest.mark.parametrize("m,n,k", [(64, 4096, 4096), (7, 512, 256), (64, 512, 14336), (200, 1024, 1024)])
-def test_add_rmsnorm_matches_unfused(gpu_lib, monkeypatch, m, n, k):
+def test_add_rmsnorm_matches_unfused(gpu_lib, tunables, m, n, k):
     import torch
-    monkeypatch.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
+    tunables.setenv("KCMM_GEMM_TILED", "0")   # the unfused GEMM on the same kernel
     x = _randn_bf16(torch, (m, k), 1.0, 11)
     w = _randn_bf16(torch, (n, k), 0.02, 12)
     h0 = _randn_bf16(torch, (m, n), 1.0, 13)

@@ -14,11 +14,11 @@ def rel_err(got, ref):
 
 
 @pytest.fixture(params=["tiled", "stream"])
-def backend(request, monkeypatch):
+def backend(request, tunables):
     """kcmm_gemm_bf16 runs products with M > 128 on the LDS-tiled MFMA
     kernel; KCMM_GEMM_TILED=0 keeps them on the weight-stream kernel.  Both
     are checked."""
-    monkeypatch.setenv("KCMM_GEMM_TILED", "1" if request.param == "tiled" else "0")
+    tunables.setenv("KCMM_GEMM_TILED", "1" if request.param == "tiled" else "0")
     return request.param
 
 
@@ -72,12 +72,12 @@ def test_llama3_8b_projections(gpu_lib, backend, m, n, k):
 @pytest.mark.parametrize("target", ["1", "64", "256", "100000"])
 @pytest.mark.parametrize("m,n,k", [(1, 128, 256), (17, 384, 512), (33, 1280, 2304),
                                    (64, 256, 14336), (64, 6144, 4096), (48, 64, 1024)])
-def test_split_k_choices(gpu_lib, monkeypatch, target, m, n, k):
+def test_split_k_choices(gpu_lib, tunables, target, m, n, k):
     """The K split chosen for a target workgroup count (1 = never split,
     100000 = as many splits as chunks allow) gives the same product: split
     partials and their reduction are exact up to fp32 rounding."""
     import torch
-    monkeypatch.setenv("KCMM_GEMM_WGS", target)
+    tunables.setenv("KCMM_GEMM_WGS", target)
     g = torch.Generator(device="cuda")
     g.manual_seed(m * 31 + n + k + len(target))
     x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
@@ -92,15 +92,15 @@ def test_split_k_choices(gpu_lib, monkeypatch, target, m, n, k):
 @pytest.mark.parametrize("tile", [str(i) for i in range(11)])
 @pytest.mark.parametrize("splits", ["1", "2", "4"])
 @pytest.mark.parametrize("residual", [False, True])
-def test_tiled_tiles_splits_residual(gpu_lib, monkeypatch, tile, splits, residual):
+def test_tiled_tiles_splits_residual(gpu_lib, tunables, tile, splits, residual):
     """Every configuration of the tiled kernel (tiles 128x256, 128x128,
     128x64, 64x128, 64x64, 128x256 on 4 waves, 256x128, 128x256 with 2
     stages) with 1, 2 or 4 K splits, M not a multiple of the tile, with and
     without a residual (in place: R == Y), against the fp64 oracle; two
     calls in a row give the same bits."""
     import torch
-    monkeypatch.setenv("KCMM_GEMM_TILE", tile)
-    monkeypatch.setenv("KCMM_GEMM_SPLITS", splits)
+    tunables.setenv("KCMM_GEMM_TILE", tile)
+    tunables.setenv("KCMM_GEMM_SPLITS", splits)
     m, n, k = 300, 768, 1024
     rng = np.random.default_rng(int(tile) * 10 + int(splits) + residual)
     xb = O.encode(O.BF16, rng.standard_normal((m, k)))
@@ -183,15 +183,15 @@ def test_fp8_weights_llama3_8b_projections(gpu_lib, m, n, k):
 
 @pytest.mark.parametrize("tile", [str(i) for i in range(11)])
 @pytest.mark.parametrize("splits", ["1", "2", "4"])
-def test_fp8_weights_tiled(gpu_lib, monkeypatch, tile, splits):
+def test_fp8_weights_tiled(gpu_lib, tunables, tile, splits):
     """fp8 weights with more than 128 tokens take the LDS-tiled kernel (codes
     staged in 64-byte LDS rows, converted to bf16 as they are read): every
     tiling with 1, 2 or 4 K splits, M not a multiple of the tile, against the
     fp64 oracle; two calls give the same bits; the weight-stream kernel
     (KCMM_GEMM_TILED=0) agrees within the same tolerance."""
     import torch
-    monkeypatch.setenv("KCMM_GEMM_TILE", tile)
-    monkeypatch.setenv("KCMM_GEMM_SPLITS", splits)
+    tunables.setenv("KCMM_GEMM_TILE", tile)
+    tunables.setenv("KCMM_GEMM_SPLITS", splits)
     m, n, k = 300, 768, 1024
     rng = np.random.default_rng(int(tile) * 10 + int(splits) + 5)
     xb = O.encode(O.BF16, rng.standard_normal((m, k)))
@@ -211,7 +211,7 @@ def test_fp8_weights_tiled(gpu_lib, monkeypatch, tile, splits):
     err = rel_err(got, ref)
     print(f"fp8w tiled tile={tile} splits={splits} err={err:.3e}", flush=True)
     assert err <= 1e-2
-    monkeypatch.setenv("KCMM_GEMM_TILED", "0")
+    tunables.setenv("KCMM_GEMM_TILED", "0")
     y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
     gpu_lib.gemm_fp8w_bf16(x.data_ptr(), w8d.data_ptr(), sd.data_ptr(), y.data_ptr(), m, n, k,
                            torch.cuda.current_stream().cuda_stream)
@@ -221,9 +221,9 @@ def test_fp8_weights_tiled(gpu_lib, monkeypatch, tile, splits):
 
 
 @pytest.mark.parametrize("splits", ["1", "2", "4", "8"])
-def test_fp8_weights_split_k(gpu_lib, monkeypatch, splits):
+def test_fp8_weights_split_k(gpu_lib, tunables, splits):
     import torch
-    monkeypatch.setenv("KCMM_GEMM_SPLITS", splits)
+    tunables.setenv("KCMM_GEMM_SPLITS", splits)
     rng = np.random.default_rng(int(splits))
     m, n, k = 64, 512, 4096
     xb = O.encode(O.BF16, rng.standard_normal((m, k)))
@@ -281,7 +281,7 @@ def test_workspace_two_host_threads(gpu_lib):
     assert errors == []
 
 
-def test_gemm_plan(gpu_lib, monkeypatch):
+def test_gemm_plan(gpu_lib, tunables):
     """kcmm_gemm_plan reports what the product entry points run."""
     p = gpu_lib.gemm_plan(64, 6144, 4096)
     assert p["kernel"] == "stream" and p["tile"] == -1
@@ -289,9 +289,9 @@ def test_gemm_plan(gpu_lib, monkeypatch):
     assert gpu_lib.gemm_plan(256, 6144, 4096)["kernel"] == "tiled"
     assert gpu_lib.gemm_plan(256, 6144, 4096, fp8_weights=True)["kernel"] == "tiled"
     assert gpu_lib.gemm_plan(128, 6144, 4096, fp8_weights=True)["kernel"] == "stream"
-    monkeypatch.setenv("KCMM_GEMM_SPLITS", "2")
+    tunables.setenv("KCMM_GEMM_SPLITS", "2")
     assert gpu_lib.gemm_plan(64, 512, 4096)["splits"] == 2
-    monkeypatch.setenv("KCMM_GEMM_TILED", "0")
+    tunables.setenv("KCMM_GEMM_TILED", "0")
     assert gpu_lib.gemm_plan(256, 6144, 4096)["kernel"] == "stream"
     with pytest.raises(Exception):
         gpu_lib.gemm_plan(64, 100, 4096)          # n not a multiple of 64

@@ -108,14 +108,14 @@ def test_fp8_pages_on_mfma(gpu_lib, hq, hkv, bs):
         case.pool.destroy()
 
 
-def test_fp8_mfma_matches_generic(gpu_lib, monkeypatch):
+def test_fp8_mfma_matches_generic(gpu_lib, tunables):
     """The fp8 MFMA path and the generic kernel (KCMM_ATTN_GENERIC) agree
     within the fp8 tolerance on the same pages and queries."""
     case = build_decode_case(gpu_lib, batch=len(CTX), num_q_heads=32, kv_heads=8, head_dim=128,
                              block_size=16, ctx_lens=CTX, dtype=KV_FP8, seed=31)
     try:
         got, ref = run_prefill(case, LENS, 32, seed=32)
-        monkeypatch.setenv("KCMM_ATTN_GENERIC", "1")
+        tunables.setenv("KCMM_ATTN_GENERIC", "1")
         gen, _ = run_prefill(case, LENS, 32, seed=32)
         assert rel_err(got, gen) <= TOL[KV_FP8] and rel_err(gen, ref) <= TOL[KV_FP8]
     finally:

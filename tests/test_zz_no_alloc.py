@@ -51,6 +51,42 @@ def test_noalloc_matches_allocating_entry_point(gpu_lib):
             case.pool.destroy()
 
 
+def test_noalloc_calls_on_two_streams_take_turns(gpu_lib):
+    """Back-to-back calls on two streams with no host synchronization in
+    between share the one scratch array: each call on the other stream waits
+    for the previous call's kernels, so every output equals the allocating
+    entry point's (same kernels, same bits)."""
+    import torch
+    lib = gpu_lib.lib
+    rng = np.random.default_rng(8)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    cases = []
+    try:
+        for batch, lo, hi, seed in ((64, 512, 4096, 11), (48, 256, 3000, 12)):
+            ctx = rng.integers(lo, hi + 1, size=batch) + 1
+            cases.append(build_decode_case(gpu_lib, batch=batch, num_q_heads=32, kv_heads=8,
+                                           head_dim=128, block_size=16, ctx_lens=ctx,
+                                           dtype=KV_BF16, seed=seed, host_mirror=False))
+        refs = []
+        for case in cases:
+            ref = torch.full_like(case.dev["out"], float("nan"))
+            assert _call(case, lib.kcmm_paged_attn_decode_bf16_on_stream, ref, 0) == 0
+            refs.append(ref)
+        torch.cuda.synchronize()
+        outs = [[torch.full_like(c.dev["out"], float("nan")) for _ in range(3)] for c in cases]
+        for rep in range(3):
+            for case, out, st in zip(cases, outs, (s1, s2)):
+                assert _call(case, lib.kcmm_paged_attn_decode_bf16_noalloc_on_stream, out[rep],
+                             st.cuda_stream) == 0, case.pool.last_error()
+        torch.cuda.synchronize()
+        for ref, out in zip(refs, outs):
+            for rep, o in enumerate(out):
+                assert torch.equal(o.view(torch.int16), ref.view(torch.int16)), rep
+    finally:
+        for case in cases:
+            case.pool.destroy()
+
+
 def test_noalloc_refuses_batches_past_its_scratch(gpu_lib):
     """400 sequences of long tables need more than the static scratch: the
     call fails with an error naming the sizes; the inputs are real
