@@ -80,6 +80,10 @@ def parse():
     ap.add_argument("--gemm-only", action="store_true",
                     help="time the four M=64 projection GEMMs alone, as the layer's component "
                          "pass calls them (for HBM counter runs under rocprofv3)")
+    ap.add_argument("--m", type=int, default=64,
+                    help="--gemm-only: tokens per product (64: the decode batch, O and down add "
+                         "their residual; other values: plain products, e.g. 256 for the "
+                         "LDS-tiled kernel)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
     ap.add_argument("--no-sub-configs", action="store_true",
@@ -238,21 +242,23 @@ def gemm_bytes(lib, name, n, k, m):
 
 
 def bench_gemm(args):
-    """--gemm-only: the four Llama-3-8B projections at M = 64, each called as
-    in the layer's component pass (QKV and gate/up plain, O and down with the
-    residual added in place), two weight sets alternating so that the weights
-    come from HBM; HIP events per call."""
+    """--gemm-only: the four Llama-3-8B projections at M = --m tokens (64 by
+    default: each called as in the layer's component pass, QKV and gate/up
+    plain, O and down with the residual added in place; other M: plain
+    products), two weight sets alternating so that the weights come from
+    HBM; HIP events per call."""
     import torch
     from lattice_amd.bindings import KcmmLibrary
     lib = KcmmLibrary()
     dev = "cuda"
+    M = args.m
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed + 2)
     sets = [{name: (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16)
              for name, n, k in GEMMS} for _ in range(2)]
-    x = {k: torch.randn((B, k), generator=g, device=dev).to(torch.bfloat16) for k in (HIDDEN, INTER)}
-    y = torch.empty((B, 2 * INTER), dtype=torch.bfloat16, device=dev)
-    hidden = torch.randn((B, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
+    x = {k: torch.randn((M, k), generator=g, device=dev).to(torch.bfloat16) for k in (HIDDEN, INTER)}
+    y = torch.empty((M, 2 * INTER), dtype=torch.bfloat16, device=dev)
+    hidden = torch.randn((M, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
     sp = torch.cuda.current_stream().cuda_stream
     if args.calib_copy:
         src = torch.empty(128 << 20, dtype=torch.int16, device=dev)
@@ -265,10 +271,10 @@ def bench_gemm(args):
 
     def call(name, n, k, i):
         w = sets[i % 2][name].data_ptr()
-        if name in ("o", "down"):
-            lib.gemm_bf16_add(x[k].data_ptr(), w, hidden.data_ptr(), hidden.data_ptr(), B, n, k, sp)
+        if name in ("o", "down") and M == B:
+            lib.gemm_bf16_add(x[k].data_ptr(), w, hidden.data_ptr(), hidden.data_ptr(), M, n, k, sp)
         else:
-            lib.gemm_bf16(x[k].data_ptr(), w, y.data_ptr(), B, n, k, sp)
+            lib.gemm_bf16(x[k].data_ptr(), w, y.data_ptr(), M, n, k, sp)
 
     out = {}
     for name, n, k in GEMMS:
@@ -282,13 +288,16 @@ def bench_gemm(args):
         ev[-1].record()
         torch.cuda.synchronize()
         us = float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)])) * 1e3
-        alg, plan = gemm_bytes(lib, name, n, k, B)
+        alg, plan = gemm_bytes(lib, name, n, k, M)
+        if M != B and name in ("o", "down"):
+            alg -= 2.0 * M * n          # plain product: no residual read
         out[name] = {"us": round(us, 2), "algorithmic_bytes": int(alg), "plan": plan,
                      "gbs": round(alg / us / 1e3, 1),
-                     "frac_of_hbm_peak": round(alg / us / 1e3 / HBM_PEAK_GBS, 4)}
+                     "frac_of_hbm_peak": round(alg / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "tflops": round(2.0 * M * n * k / us / 1e6, 1)}
         log(f"{name}: {us:.2f} us, plan {plan}")
-    print(json.dumps({"metric": "M=64 projection GEMM time", "unit": "us", "steps": args.steps,
-                      "warmup": args.warmup, "m": B, "gemms": out}), flush=True)
+    print(json.dumps({"metric": f"M={M} projection GEMM time", "unit": "us", "steps": args.steps,
+                      "warmup": args.warmup, "m": M, "gemms": out}), flush=True)
 
 
 def bench_prefill(args):
