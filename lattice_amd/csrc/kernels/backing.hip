@@ -5,11 +5,13 @@
 //    GPU, so the configured capacity is committed up front and growth costs
 //    nothing.  Block ids and offsets are the reference's either way.
 //  * VmmBacking<HipVmmOps>: the reference's CUDA-VMM design (ref
-//    src/cache/cuda_vmm.rs:6-234, pool.rs:211-221,287-322) on HIP VMM.
-//    Switched off: a process that created and destroyed about a dozen VMM
-//    pools saw hipMemSetAccess fail with "invalid argument" and then a crash
-//    in pool teardown; the cause is not known, so KCMM_BACKING=vmm makes
-//    pool creation fail.
+//    src/cache/cuda_vmm.rs:6-234, pool.rs:211-221,287-322) on HIP VMM, one
+//    reservation per pool.  Switched off: a process that created and
+//    destroyed about a dozen VMM pools saw hipMemSetAccess fail with
+//    "invalid argument" and then a crash in pool teardown.  The call
+//    sequence breaks none of the API's documented preconditions (checked on
+//    the CPU against a mock that enforces them); the cause is not known, so
+//    KCMM_BACKING=vmm makes pool creation fail.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>

@@ -1,8 +1,12 @@
 // Grow-on-demand page backing over a virtual-memory API (the reference's
 // CUDA-VMM design, ref src/cache/cuda_vmm.rs:6-234 with the per-superblock
 // mapping of ref pool.rs:211-221,287-322): one virtual-address reservation
-// per region, and at growth one 2 MiB physical chunk created and mapped at
-// byte sb * 2 MiB of every region.
+// for the whole pool, carved into its regions (region r at base + r *
+// region_bytes; the reference reserves one range per region), requested
+// with alignment 0 as the reference does (ref cuda_vmm.rs:63-69); at growth
+// one 2 MiB physical chunk is created and mapped at byte sb * 2 MiB of every
+// region.  Region offsets, block ids and page offsets do not depend on where
+// the range lies.
 //
 // The bookkeeping is written once over an `Ops` type that issues the driver
 // calls, so that the HIP build (Ops = HIP VMM calls) and the host-check build
@@ -44,12 +48,20 @@ public:
             *err = "VMM granularity does not divide the 2 MiB superblock";
             return false;
         }
-        region_bytes_ = region_bytes;
-        for (size_t r = 0; r < num_regions; ++r) {
-            void* va = nullptr;
-            if (!ops_.reserve(region_bytes, kSuperblockBytes, &va, err)) return false;
-            bases_.push_back(va);
+        if (region_bytes % gran != 0 || num_regions == 0) {
+            *err = "VMM region size is not a multiple of the granularity";
+            return false;
         }
+        region_bytes_ = region_bytes;
+        va_bytes_ = num_regions * region_bytes;
+        void* va = nullptr;
+        if (!ops_.reserve(va_bytes_, 0, &va, err)) {
+            va_bytes_ = 0;
+            return false;
+        }
+        va_ = va;
+        for (size_t r = 0; r < num_regions; ++r)
+            bases_.push_back(static_cast<char*>(va) + r * region_bytes);
         return true;
     }
 
@@ -77,10 +89,12 @@ public:
         return true;
     }
 
-    // Unmap, then release the physical chunks, then free the reservations.
+    // Unmap, then release the physical chunks, then free the reservation.
     void release() override {
         rollback(0);
-        for (void* b : bases_) ops_.free_va(b, region_bytes_);
+        if (va_ != nullptr) ops_.free_va(va_, va_bytes_);
+        va_ = nullptr;
+        va_bytes_ = 0;
         bases_.clear();
     }
 
@@ -101,6 +115,8 @@ private:
 
     Ops ops_;
     size_t region_bytes_ = 0;
+    void* va_ = nullptr;        // the pool's one reservation
+    size_t va_bytes_ = 0;
     std::vector<void*> bases_;
     std::vector<std::pair<void*, Handle>> mapped_;
 };

@@ -49,18 +49,48 @@ private:
 };
 
 // Recording stand-in for the HIP VMM calls (KCMM_BACKING=vmm in this build
-// only): fake addresses, live-resource counts, misuse counted as violations,
-// and one injected failure (operation, n-th call) at a time.
+// only): fake addresses, live-resource counts, one injected failure
+// (operation, n-th call) at a time, and every call checked against the
+// preconditions the VMM API documents (CUDA's cuMem* and HIP's hipMem*
+// pages); a call that breaks one counts a violation:
+//  * sizes, addresses and alignments are multiples of the allocation
+//    granularity (the mock's minimum granularity is 64 KiB, below the 2 MiB
+//    superblock, and a reservation with alignment 0 comes back aligned to
+//    that granularity only, not to 2 MiB);
+//  * a mapping lies inside one live reservation, overlaps no other mapping,
+//    and maps a live handle that no other mapping uses;
+//  * access is set on a range inside one live mapping;
+//  * an unmap names exactly one mapping (its address and size);
+//  * a handle is released once, when it is no longer mapped;
+//  * a reservation is freed with exactly its base and size, with nothing
+//    mapped inside it.
 struct VmmMock {
+    static constexpr uint64_t kGran = 64 * 1024;
     std::mutex mu;
     int64_t reservations = 0, handles = 0, mappings = 0, violations = 0;
     int64_t calls[5] = {0, 0, 0, 0, 0};   // reserve, create, map, set_access, granularity
     int fail_op = -1;
     int64_t fail_at = -1;
-    uint64_t next_va = 0x200000000000ull, next_handle = 0;
-    std::map<uint64_t, uint64_t> mapped;          // address -> handle
-    std::map<uint64_t, size_t> reserved;          // base -> bytes
+    uint64_t next_va = 0x200000000000ull + kGran, next_handle = 0;
+    struct Mapping {
+        uint64_t bytes, handle;
+    };
+    std::map<uint64_t, Mapping> mapped;           // address -> mapping
+    std::map<uint64_t, uint64_t> reserved;        // base -> bytes
+    std::map<uint64_t, uint64_t> live_handles;    // handle -> bytes
     bool fail(int op) { return ++calls[op] == fail_at && op == fail_op; }
+    void check(bool ok) { if (!ok) ++violations; }
+    bool in_one_reservation(uint64_t a, uint64_t n) const {
+        auto it = reserved.upper_bound(a);
+        if (it == reserved.begin()) return false;
+        --it;
+        return a >= it->first && a + n <= it->first + it->second;
+    }
+    bool overlaps_mapping(uint64_t a, uint64_t n) const {
+        for (const auto& m : mapped)
+            if (a < m.first + m.second.bytes && m.first < a + n) return true;
+        return false;
+    }
 } g_vmm;
 
 struct MockVmmOps {
@@ -68,57 +98,86 @@ struct MockVmmOps {
     bool granularity(size_t* g, std::string* err) {
         std::lock_guard<std::mutex> lk(g_vmm.mu);
         if (g_vmm.fail(4)) { *err = "mock: granularity failed"; return false; }
-        *g = kSuperblockBytes;
+        *g = VmmMock::kGran;
         return true;
     }
-    bool reserve(size_t bytes, size_t, void** va, std::string* err) {
+    bool reserve(size_t bytes, size_t align, void** va, std::string* err) {
         std::lock_guard<std::mutex> lk(g_vmm.mu);
         if (g_vmm.fail(0)) { *err = "mock: reserve failed"; return false; }
-        *va = reinterpret_cast<void*>(g_vmm.next_va);
-        g_vmm.reserved[g_vmm.next_va] = bytes;
-        g_vmm.next_va += (bytes + kSuperblockBytes - 1) / kSuperblockBytes * kSuperblockBytes + kSuperblockBytes;
+        g_vmm.check(bytes > 0 && bytes % VmmMock::kGran == 0);
+        g_vmm.check(align == 0 || (align % VmmMock::kGran == 0 && (align & (align - 1)) == 0));
+        uint64_t base = g_vmm.next_va;
+        if (align != 0) base = (base + align - 1) / align * align;
+        *va = reinterpret_cast<void*>(base);
+        g_vmm.reserved[base] = bytes;
+        // the next reservation starts one granule past a 2 MiB boundary
+        g_vmm.next_va = (base + bytes + kSuperblockBytes) / kSuperblockBytes * kSuperblockBytes +
+                        VmmMock::kGran;
         ++g_vmm.reservations;
         return true;
     }
-    bool create(size_t, Handle* h, std::string* err) {
+    bool create(size_t bytes, Handle* h, std::string* err) {
         std::lock_guard<std::mutex> lk(g_vmm.mu);
         if (g_vmm.fail(1)) { *err = "mock: create failed"; return false; }
+        g_vmm.check(bytes > 0 && bytes % VmmMock::kGran == 0);
         *h = ++g_vmm.next_handle;
+        g_vmm.live_handles[*h] = bytes;
         ++g_vmm.handles;
         return true;
     }
-    bool map(void* at, size_t, Handle h, std::string* err) {
+    bool map(void* at, size_t bytes, Handle h, std::string* err) {
         std::lock_guard<std::mutex> lk(g_vmm.mu);
         if (g_vmm.fail(2)) { *err = "mock: map failed"; return false; }
         const uint64_t a = reinterpret_cast<uint64_t>(at);
-        if (g_vmm.mapped.count(a)) ++g_vmm.violations;   // mapped twice
-        g_vmm.mapped[a] = h;
+        g_vmm.check(a % VmmMock::kGran == 0 && bytes % VmmMock::kGran == 0);
+        g_vmm.check(g_vmm.in_one_reservation(a, bytes));
+        g_vmm.check(!g_vmm.overlaps_mapping(a, bytes));
+        auto hs = g_vmm.live_handles.find(h);
+        g_vmm.check(hs != g_vmm.live_handles.end() && hs->second == bytes);
+        for (const auto& m : g_vmm.mapped) g_vmm.check(m.second.handle != h);
+        g_vmm.mapped[a] = VmmMock::Mapping{bytes, h};
         ++g_vmm.mappings;
         return true;
     }
-    bool set_access(void* at, size_t, std::string* err) {
+    bool set_access(void* at, size_t bytes, std::string* err) {
         std::lock_guard<std::mutex> lk(g_vmm.mu);
         if (g_vmm.fail(3)) { *err = "mock: set_access failed"; return false; }
-        if (!g_vmm.mapped.count(reinterpret_cast<uint64_t>(at))) ++g_vmm.violations;
+        const uint64_t a = reinterpret_cast<uint64_t>(at);
+        bool inside = false;
+        for (const auto& m : g_vmm.mapped)
+            inside |= a >= m.first && a + bytes <= m.first + m.second.bytes;
+        g_vmm.check(inside && bytes > 0 && bytes % VmmMock::kGran == 0);
         return true;
     }
-    void unmap(void* at, size_t) {
+    void unmap(void* at, size_t bytes) {
         std::lock_guard<std::mutex> lk(g_vmm.mu);
-        if (g_vmm.mapped.erase(reinterpret_cast<uint64_t>(at)) == 0) ++g_vmm.violations;
+        auto it = g_vmm.mapped.find(reinterpret_cast<uint64_t>(at));
+        if (it == g_vmm.mapped.end() || it->second.bytes != bytes) {
+            ++g_vmm.violations;
+            return;
+        }
+        g_vmm.mapped.erase(it);
         --g_vmm.mappings;
     }
-    void release(Handle) {
+    void release(Handle h) {
         std::lock_guard<std::mutex> lk(g_vmm.mu);
+        for (const auto& m : g_vmm.mapped) g_vmm.check(m.second.handle != h);   // still mapped
+        if (g_vmm.live_handles.erase(h) == 0) {
+            ++g_vmm.violations;
+            return;
+        }
         --g_vmm.handles;
     }
     void free_va(void* va, size_t bytes) {
         std::lock_guard<std::mutex> lk(g_vmm.mu);
         const uint64_t a = reinterpret_cast<uint64_t>(va);
         auto it = g_vmm.reserved.find(a);
-        if (it == g_vmm.reserved.end() || it->second != bytes) ++g_vmm.violations;
-        else g_vmm.reserved.erase(it);
-        for (const auto& m : g_vmm.mapped)          // still mapped inside the range
-            if (m.first >= a && m.first < a + bytes) ++g_vmm.violations;
+        if (it == g_vmm.reserved.end() || it->second != bytes) {
+            ++g_vmm.violations;
+            return;
+        }
+        g_vmm.check(!g_vmm.overlaps_mapping(a, bytes));
+        g_vmm.reserved.erase(it);
         --g_vmm.reservations;
     }
 };

@@ -1,10 +1,17 @@
 """The grow-on-demand VMM page backing (ref src/cache/cuda_vmm.rs:6-234,
 pool.rs:287-322) on the CPU: the host-check build instantiates the same
 VmmBacking template the HIP build does, over a mock of the VMM driver calls
-that counts live reservations, physical handles and mappings and flags misuse
-(a range mapped twice, access set on or unmapping an unmapped range, a
-reservation freed with mappings inside).  One failure can be injected per
-run (reserve, create, map or set_access at its n-th call).
+that counts live reservations, physical handles and mappings and counts a
+violation for every call that breaks a documented precondition of the VMM
+API: sizes, addresses and alignments not multiples of the granularity (the
+mock's is 64 KiB and an alignment-0 reservation comes back aligned to that
+only), a mapping outside one live reservation, overlapping another, or of a
+handle that is not live or already mapped, access set outside one live
+mapping, an unmap that does not name exactly one mapping, a handle released
+while mapped or twice, a reservation freed with another size or with
+mappings inside.  One failure can be injected per run (reserve, create, map
+or set_access at its n-th call).  The pool makes one reservation (alignment
+0, as the reference) carved into its 2 L regions.
 
 Checked: repeated create / grow / destroy cycles release everything; a
 superblock that fails partway through its regions is rolled back (no region
@@ -100,7 +107,7 @@ def test_partial_superblock_rolls_back(vmm, op, region):
 
 def test_failed_reservation_fails_creation_cleanly(vmm):
     lib, state, arm = vmm
-    arm(RESERVE, 4)                                   # the 4th of 6 region reservations
+    arm(RESERVE, 1)                                   # the pool's one reservation
     with pytest.raises(Exception):
         lib.create_pool(make_config(**CFG), KV_BF16)
     assert state() == dict(reservations=0, handles=0, mappings=0, violations=0)
