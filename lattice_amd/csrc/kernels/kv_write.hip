@@ -96,17 +96,21 @@ __device__ void fp8_write_page_head(uint8_t* page, uint32_t kvh, const uint16_t*
                                     const int32_t* row_of, uint32_t bs, uint32_t kv_heads,
                                     uint32_t head_dim, uint32_t row_bytes, uint32_t data_bytes) {
     const int lane = threadIdx.x & 63;
+    float* sp = reinterpret_cast<float*>(page + data_bytes) + kvh;
+    const float old = *sp;
     float amax = 0.0f;
     for (uint32_t u = 0; u < bs; ++u) {
         const int32_t r = row_of[u];
         if (r < 0) continue;
         const uint16_t* src = src_base + (static_cast<uint64_t>(r) * kv_heads + kvh) * head_dim;
-        for (uint32_t d = lane; d < head_dim; d += 64) amax = fmaxf(amax, fabsf(bf16_bits_to_f32(src[d])));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {   // head_dim <= 256
+            const uint32_t d = lane + 64 * i;
+            if (d < head_dim) amax = fmaxf(amax, fabsf(bf16_bits_to_f32(src[d])));
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    float* sp = reinterpret_cast<float*>(page + data_bytes) + kvh;
-    const float old = *sp;
     const bool fresh = row_of[0] >= 0 || !(old > 0.0f && old <= 3.40282347e38f);
     float scale;
     if (fresh) {
@@ -115,12 +119,36 @@ __device__ void fp8_write_page_head(uint8_t* page, uint32_t kvh, const uint16_t*
         scale = old;
         if (amax > 448.0f * old) {
             scale = amax / 448.0f;
-            for (uint32_t u = 0; u < bs; ++u) {
-                if (row_of[u] >= 0) continue;
-                uint8_t* row = page + static_cast<uint64_t>(u) * row_bytes + kvh * head_dim;
-                for (uint32_t d = lane; d < head_dim; d += 64) {
-                    const float y = fp8e4m3_to_f32(row[d]) * old;
-                    row[d] = static_cast<uint8_t>(f32_to_fp8e4m3(y / scale));
+            if ((head_dim & 15) == 0 && (row_bytes & 15) == 0) {
+                // 16-byte pieces of all unwritten slots at once: one memory
+                // round trip for the page instead of one per slot
+                const uint32_t pieces = head_dim / 16;
+                for (uint32_t c = lane; c < bs * pieces; c += 64) {
+                    const uint32_t u = c / pieces;
+                    if (row_of[u] >= 0) continue;
+                    u32x4* q = reinterpret_cast<u32x4*>(page + static_cast<uint64_t>(u) * row_bytes +
+                                                        kvh * head_dim + (c - u * pieces) * 16);
+                    u32x4 v = *q;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        uint32_t o = 0;
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            const float y = fp8e4m3_to_f32((v[w] >> (8 * b)) & 0xffu) * old;
+                            o |= f32_to_fp8e4m3(y / scale) << (8 * b);
+                        }
+                        v[w] = o;
+                    }
+                    *q = v;
+                }
+            } else {
+                for (uint32_t u = 0; u < bs; ++u) {
+                    if (row_of[u] >= 0) continue;
+                    uint8_t* row = page + static_cast<uint64_t>(u) * row_bytes + kvh * head_dim;
+                    for (uint32_t d = lane; d < head_dim; d += 64) {
+                        const float y = fp8e4m3_to_f32(row[d]) * old;
+                        row[d] = static_cast<uint8_t>(f32_to_fp8e4m3(y / scale));
+                    }
                 }
             }
         }
@@ -130,8 +158,12 @@ __device__ void fp8_write_page_head(uint8_t* page, uint32_t kvh, const uint16_t*
         if (r < 0) continue;
         const uint16_t* src = src_base + (static_cast<uint64_t>(r) * kv_heads + kvh) * head_dim;
         uint8_t* row = page + static_cast<uint64_t>(u) * row_bytes + kvh * head_dim;
-        for (uint32_t d = lane; d < head_dim; d += 64)
-            row[d] = static_cast<uint8_t>(f32_to_fp8e4m3(bf16_bits_to_f32(src[d]) / scale));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d = lane + 64 * i;
+            if (d < head_dim)
+                row[d] = static_cast<uint8_t>(f32_to_fp8e4m3(bf16_bits_to_f32(src[d]) / scale));
+        }
     }
     if (lane == 0) *sp = scale;
 }
@@ -274,7 +306,11 @@ __global__ __launch_bounds__(64 * kFp8MaxWaves) void kv_slots_fp8_write(SlotArgs
     const int32_t rows = s_rows;
     if (rows == 0) return;
     const int lane = threadIdx.x & 63;
-    if (threadIdx.x < 64) {
+    if (rows == 1) {
+        // the page's only row is this one (the common decode append)
+        if (threadIdx.x == 0)
+            row_of[static_cast<uint32_t>(slot % a.block_size)] = static_cast<int32_t>(r);
+    } else if (threadIdx.x < 64) {
         // rows of this page, in call order, from this one on
         int32_t done = 0;
         for (uint32_t base = r; done < rows && base < batch; base += 64) {
