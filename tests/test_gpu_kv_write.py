@@ -199,9 +199,11 @@ def _prefill_rows(rng, tables, bs, tokens, order):
     return [flat[i] for i in rng.permutation(len(flat))]
 
 
+@pytest.mark.parametrize("geom", [(8, 128, 16), (2, 64, 8), (4, 256, 32), (1, 72, 16)],
+                         ids=["hk8-d128-bs16", "hk2-d64-bs8", "hk4-d256-bs32", "hk1-d72-bs16"])
 @pytest.mark.parametrize("order", ["seq", "interleaved", "shuffled"])
 @pytest.mark.parametrize("path", ["device", "host"])
-def test_fp8_multi_token_pages_vs_oracle(gpu_lib, order, path):
+def test_fp8_multi_token_pages_vs_oracle(gpu_lib, order, path, geom):
     """fp8 pages written by calls that put many tokens of a sequence (two and
     a half pages' worth) into the same pages, in several row orders: the rows
     a call writes into a page act as one set (the last row for a repeated
@@ -209,11 +211,12 @@ def test_fp8_multi_token_pages_vs_oracle(gpu_lib, order, path):
     (torch's e4m3 cast times the footer scale) within one e4m3 step of its
     bf16 input."""
     import torch
-    rng = np.random.default_rng(77 + len(order) + (path == "host"))
-    B, hk, d, bs, L = 5, 8, 128, 16, 1
+    rng = np.random.default_rng(77 + len(order) + (path == "host") + geom[1])
+    B, L = 5, 1
+    hk, d, bs = geom
     tokens = 2 * bs + bs // 2
     pool = gpu_lib.create_pool(make_config(num_layers=L, kv_heads=hk, head_dim=d, max_batch=B,
-                                           max_seq_len=64), KV_FP8)
+                                           max_seq_len=4 * bs, block_size=bs), KV_FP8)
     try:
         n_pages = 3
         ids = pool.alloc_blocks(B * n_pages)
