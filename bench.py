@@ -620,6 +620,7 @@ def main():
         # weight-stream kernel (KCMM_GEMM_TILED=0) and torch.matmul (ROCm's
         # GEMM libraries, not part of the library) are timed beside it
         m256, m256_stream, m256_torch = {}, {}, {}
+        m64_cold, m64_torch = {}, {}      # M = 64 under the same protocol
         x256 = {k: torch.randn((256, k), generator=g, device=dev).to(torch.bfloat16)
                 for k in (HIDDEN, INTER)}
         y256 = torch.empty((256, 2 * INTER), dtype=torch.bfloat16, device=dev)
@@ -628,16 +629,18 @@ def main():
         # outside the events
         flush = torch.zeros(1 << 29, dtype=torch.uint8, device=dev)
         tiled_env = os.environ.get("KCMM_GEMM_TILED")
-        for backend, out in (("1", m256), ("0", m256_stream), ("torch", m256_torch)):
+        for mm, backend, out in ((256, "1", m256), (256, "0", m256_stream), (256, "torch", m256_torch),
+                                 (B, "1", m64_cold), (B, "torch", m64_torch)):
             os.environ["KCMM_GEMM_TILED"] = "0" if backend == "0" else "1"
             lib.reload_tunables()       # the library reads KCMM_* once
             for name, n, k in GEMMS:
+                xm = x256[k][:mm]      # the first mm rows (contiguous)
                 if backend == "torch":
-                    fn = lambda l, n=n, k=k, name=name: torch.matmul(
-                        x256[k], weights[l % len(weights)][name].t())
+                    fn = lambda l, n=n, k=k, name=name, xm=xm: torch.matmul(
+                        xm, weights[l % len(weights)][name].t())
                 else:
-                    fn = lambda l, n=n, k=k, name=name: lib.gemm_bf16(
-                        x256[k].data_ptr(), W(l, name), y256.data_ptr(), 256, n, k, sp)
+                    fn = lambda l, n=n, k=k, name=name, xm=xm, mm=mm: lib.gemm_bf16(
+                        xm.data_ptr(), W(l, name), y256.data_ptr(), mm, n, k, sp)
                 evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                        for _ in range(args.steps)]
                 for i in range(min(args.warmup, args.steps)):
@@ -853,6 +856,14 @@ def main():
             os.environ["KCMM_GEMM_TILED"] = prev
         lib.reload_tunables()
         result["gemm_m256_torch_reference"] = gemm_report(m256_torch, 256, False, plan=False)
+        # plain products at M = 64 with the Infinity Cache flushed before each
+        # call: this library's weight-stream kernel against torch.matmul
+        result["gemm_m64_cold"] = {
+            "kcmm": gemm_report(m64_cold, B, False),
+            "torch_reference": gemm_report(m64_torch, B, False, plan=False),
+            "note": "plain products (no residual), each timed call after a 512 MiB write that "
+                    "flushes the Infinity Cache; torch.matmul is ROCm's GEMM library, timed "
+                    "for comparison only"}
         result["tiering"] = tiering_report(lib, args)
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))
