@@ -86,6 +86,8 @@ def parse():
                          "LDS-tiled kernel)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration under rocprofv3)")
+    ap.add_argument("--decode-graph", action="store_true",
+                    help="also time the decode step replayed from a HIP graph")
     ap.add_argument("--no-sub-configs", action="store_true",
                     help="cfg2: skip the cfg3 prefill and cfg5 fp8 runs that the default run "
                          "adds as sub-objects of its JSON line")
@@ -239,6 +241,49 @@ def gemm_bytes(lib, name, n, k, m):
     res = 2 if name in ("o", "down") else 1
     plan = lib.gemm_plan(m, n, k)
     return 2.0 * (n * k + m * k + m * n * res), plan
+
+
+def time_decode_graph(decode_step, logits, sp, steps, warmup):
+    """The decode step captured once in a HIP graph (torch.cuda.CUDAGraph) on a
+    stream of its own and replayed: ms per replay.  The stream's workspaces
+    grow in two eager steps before the capture; the eager step's logits are
+    the reference, and three replays -- each followed by an eager step on the
+    bench's stream -- must reproduce them bit for bit before any timing."""
+    import torch
+    gs = torch.cuda.Stream()
+    gsp = gs.cuda_stream
+    torch.cuda.synchronize()
+    decode_step(0, gsp)
+    decode_step(0, gsp)
+    torch.cuda.synchronize()
+    ref = logits.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=gs):
+        decode_step(0, gsp)
+    torch.cuda.synchronize()
+    for r in range(3):
+        logits.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(logits, ref):
+            raise RuntimeError(f"decode-step graph replay {r} differs from the eager step")
+        decode_step(0)
+        torch.cuda.synchronize()
+        if not torch.equal(logits, ref):
+            raise RuntimeError(f"eager step after graph replay {r} differs")
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        graph.replay()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        evs[i].record(stream)
+        graph.replay()
+    evs[-1].record(stream)
+    torch.cuda.synchronize()
+    ms = float(np.mean([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]))
+    del graph
+    return ms
 
 
 def bench_gemm(args):
@@ -474,20 +519,22 @@ def main():
                                     hidden_size=HIDDEN, num_q_heads=HQ, intermediate_size=INTER,
                                     max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
 
-    def decode_step(_):
+    def decode_step(_, s=None):
         """One decode step: token embedding, all 32 layers in one call (weight
-        sets alternate), then the final norm and lm_head to bf16 logits."""
+        sets alternate), then the final norm and lm_head to bf16 logits (on
+        stream s, default the bench's stream)."""
+        s = sp if s is None else s
         lib.embed_tokens_bf16(embed.data_ptr(), token_ids.data_ptr(), hidden.data_ptr(), B, HIDDEN,
-                              VOCAB, sp)
+                              VOCAB, s)
         case.pool.decode_layers(first_layer=0, weights=[layer_w[i % nw] for i in range(MODEL_LAYERS)],
                                 hidden_ptr=hidden.data_ptr(), block_tables_ptr=dv["bt"].data_ptr(),
                                 seq_lens_ptr=dv["sl"].data_ptr(),
                                 block_offsets_f16_ptr=dv["offs"].data_ptr(),
                                 inv_freq_ptr=inv_freq.data_ptr(), batch=B, hidden_size=HIDDEN,
                                 num_q_heads=HQ, intermediate_size=INTER,
-                                max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=sp)
+                                max_blocks_per_seq=case.mbps, rms_eps=RMS_EPS, stream_ptr=s)
         lib.decode_logits_bf16(hidden.data_ptr(), final_norm.data_ptr(), lm_head.data_ptr(),
-                               logits.data_ptr(), B, HIDDEN, VOCAB, RMS_EPS, sp)
+                               logits.data_ptr(), B, HIDDEN, VOCAB, RMS_EPS, s)
 
     # the same two weight sets with fp8-e4m3 projections (per-row amax/448
     # scales, quantized on the device), for the fp8-weight decode step
@@ -613,6 +660,9 @@ def main():
             evs[-1].record(stream)
             torch.cuda.synchronize()
             extra[label] = float(np.mean([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]))
+        if args.decode_graph:
+            extra["decode_step_graph"] = time_decode_graph(decode_step, logits, sp, full_steps,
+                                                           args.warmup)
         log(f"layer step (one call) ms={extra['layer_step']:.4f}, append ms={extra['append']:.4f}, "
             f"32-layer decode step ms={extra['decode_step']:.4f}")
         # the projections at M = 256 tokens (configs[3]'s second size), same weights:
@@ -807,6 +857,12 @@ def main():
         result["t_decode_step_us"] = round(t_step_s * 1e6, 1)
         result["t_layer_us"] = round((t_step_s - extra["logits"] / 1e3) / MODEL_LAYERS * 1e6, 2)
         result["t_logits_us"] = round(extra["logits"] * 1e3, 2)
+        if "decode_step_graph" in extra:
+            tg = extra["decode_step_graph"] / 1e3
+            result["decode_graph"] = {
+                "decode_tokens_per_s": round(B / tg, 1), "t_decode_step_us": round(tg * 1e6, 1),
+                "note": "the same decode step captured once in a HIP graph and replayed; every "
+                        "replay checked bit-exact against the eager step before timing"}
         result["t_layer_single_call_us"] = round(extra["layer_step"] * 1e3, 2)
         result["t_layer_components_us"] = {n: round(per[n] * 1e3, 2) for n in names}
         if "decode_step_fp8w" in extra:
