@@ -112,11 +112,13 @@ struct Shape {
     static constexpr int CH = D / 8;          // 16-byte chunks per key row
     static constexpr int KC = D / 32;         // k-steps of S^T = K Q^T
     static constexpr int DB = D / 16;         // 16-row blocks of O^T
-    // Padded LDS rows: K is read 16 keys x 16 B at a time (ds_read_b128), V
-    // 8 keys x 32 B (transposing reads); a 16-byte (K) / 32-byte (V) pad puts
-    // those keys in distinct banks, and keeps every fragment offset linear in
-    // (key block, chunk) so it is an instruction immediate.
-    static constexpr int KROW = 2 * D + 16;
+    // Padded LDS rows, 32 bytes past the row's data for both K and V: the
+    // K fragment reads (ds_read_b128, 16 keys x 16 B) and the transposing V
+    // reads are then free of bank conflicts on gfx950 (measured: a 16-byte
+    // pad on K rows costs every K read 8 LDS cycles instead of 4), and every
+    // fragment offset stays linear in (key block, chunk), an instruction
+    // immediate.
+    static constexpr int KROW = 2 * D + 32;
     static constexpr int VROW = 2 * D + 32;
     static constexpr int KTILE = KT * KROW;
     static constexpr int BUF = KTILE + KT * VROW;   // one K + V tile of KT keys
