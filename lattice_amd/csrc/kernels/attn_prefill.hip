@@ -17,15 +17,15 @@
 //    fastest, with its Q rows held in registers for the whole key loop;
 //  * the workgroup walks 32-key tiles up to its last query's position: the
 //    512 threads gather a tile's K and V rows (16 B each, coalesced per row)
-//    into registers one tile ahead, store them to a double-buffered,
-//    XOR-swizzled LDS tile, and every wave computes from LDS, so each key
+//    into registers one tile ahead, store them to a double-buffered LDS
+//    tile of padded rows, and every wave computes from LDS, so each key
 //    row leaves L2 once per workgroup instead of once per wave;
 //  * page bases come two tiles ahead (block table one tile before offsets),
 //    so no load waits on a dependent load inside the loop;
 //  * S^T = K Q^T on v_mfma_f32_16x16x32 (K rows by ds_read_b128); V^T comes
 //    straight from the row-major V tile by the gfx950 transposing LDS read
-//    ds_read_b64_tr_b16, then O^T += V^T P^T; one V^T fragment serves the
-//    4 column blocks;
+//    ds_read_b64_tr_b16, then O^T += V^T P^T; one V^T fragment serves both
+//    of the wave's column blocks;
 //  * causal masking only on tiles that cross a column's position; online
 //    softmax in the log2 domain, rescaling only when a column's maximum grows
 //    by more than 8 (until then P <= 2^8, harmless in fp32 / 16-bit).
