@@ -54,19 +54,26 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // Sum of the `splits` fp32 partials at pp, pp + MN, ... in split order; up
-// to 8 splits' loads are in flight together.
-__device__ __forceinline__ f32x4 sum_partials(const float* pp, size_t MN, int splits) {
+// to W splits' loads are in flight together (indices past the last split
+// re-read it and are not added: no branch around a load).
+template <int W>
+__device__ __forceinline__ f32x4 sum_partials_w(const float* pp, size_t MN, int splits) {
     f32x4 s = f32x4{0, 0, 0, 0};
-    for (int k0 = 0; k0 < splits; k0 += 8) {
-        f32x4 v[8];
+    for (int k0 = 0; k0 < splits; k0 += W) {
+        f32x4 v[W];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < W; ++k)
             v[k] = *reinterpret_cast<const f32x4*>(pp + static_cast<size_t>(min(k0 + k, splits - 1)) * MN);
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < W; ++k)
             if (k0 + k < splits) s += v[k];
     }
     return s;
+}
+// Four-wide when every split fits in one round (the GEMM plans at most 4 at
+// the decode shapes), so no load is spent re-reading the last split.
+__device__ __forceinline__ f32x4 sum_partials(const float* pp, size_t MN, int splits) {
+    return splits <= 4 ? sum_partials_w<4>(pp, MN, splits) : sum_partials_w<8>(pp, MN, splits);
 }
 
 // One row per workgroup; H % 8 == 0.  FROM_PARTIALS: the row is first
@@ -81,6 +88,40 @@ __global__ __launch_bounds__(NT) void rmsnorm_rows(uint16_t* __restrict__ x,
     __shared__ float red[NT / 64];
     uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * H;
     uint16_t* yr = y + static_cast<size_t>(blockIdx.x) * H;
+    if (H <= NT * 8) {
+        // one 8-element piece per thread (the launcher's choice up to H =
+        // 8192): the weights are loaded with the row, and the finished row
+        // stays in registers across the reduction, so the kernel makes one
+        // memory round trip instead of two
+        const int i = threadIdx.x * 8;
+        const bool mine = i < H;
+        const int ic = mine ? i : 0;   // idle threads read piece 0 and store nothing
+        float f[8], g[8];
+        unpack8(*reinterpret_cast<const u32x4*>(xr + ic), f);
+        unpack8(*reinterpret_cast<const u32x4*>(w + ic), g);
+        if constexpr (FROM_PARTIALS) {
+            const size_t MN = static_cast<size_t>(gridDim.x) * H;
+            const float* pp = part + static_cast<size_t>(blockIdx.x) * H + ic;
+            const f32x4 s0 = sum_partials(pp, MN, splits);
+            const f32x4 s1 = sum_partials(pp + 4, MN, splits);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f[j] = bf16_round_f32(bf16_round_f32(s0[j]) + f[j]);
+                f[4 + j] = bf16_round_f32(bf16_round_f32(s1[j]) + f[4 + j]);
+            }
+            if (mine) *reinterpret_cast<u32x4*>(xr + i) = pack8(f);
+        }
+        float ss = 0.0f;
+        if (mine) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+        }
+        const float r = 1.0f / sqrtf(block_sum<NT>(ss, red) / static_cast<float>(H) + eps);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = g[j] * bf16_round_f32(f[j] * r);
+        if (mine) *reinterpret_cast<u32x4*>(yr + i) = pack8(f);
+        return;
+    }
     float ss = 0.0f;
     for (int i = threadIdx.x * 8; i < H; i += NT * 8) {
         float f[8];
@@ -141,26 +182,23 @@ struct RopeAppendParams {
 template <bool FROM_PARTIALS>
 __global__ __launch_bounds__(256) void rope_append_rows(RopeAppendParams p) {
     const int b = blockIdx.x;
-    const int L = p.seq_lens[b];
     const int D = p.head_dim;
-    const int pos = L - 1;
-    const bool has_row = pos >= 0 && pos < p.mbps * p.block_size;   // no token / past the table
-    if (p.slots != nullptr && blockIdx.y == 0 && threadIdx.x == 0)
-        p.slots[b] = has_row ? static_cast<int64_t>(p.block_tables[static_cast<size_t>(b) * p.mbps +
-                                                                   pos / p.block_size]) *
-                                       p.block_size +
-                                   pos % p.block_size
-                             : -1;
-    if (!has_row) return;
     const int quads = D / 8;
     const int hs = 256 / quads;
     const int iq = threadIdx.x % quads;
     const int hl = threadIdx.x / quads;
-    const int h = blockIdx.y * hs + hl;
     const int heads = p.num_q_heads + 2 * p.kv_heads;
-    if (hl >= hs || h >= heads) return;                    // (threads past whole heads idle)
+    // threads past whole heads load head 0's elements and store nothing
+    const bool live = hl < hs && blockIdx.y * hs + hl < heads;
+    const int h = live ? blockIdx.y * hs + hl : 0;
     const int stride = heads * D;
     const int e1 = h * D + 4 * iq, e2 = e1 + D / 2;
+    // The row's elements and the rotation frequencies do not depend on the
+    // sequence length: they are loaded before it, so only the K / V page
+    // lookup (block table, then page offset) waits for seq_lens.
+    float fr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fr[j] = p.inv_freq[4 * iq + j];
     // elements e..e+3 of the row (as bf16 values)
     float x1[4], x2[4];
     if constexpr (FROM_PARTIALS) {
@@ -185,12 +223,22 @@ __global__ __launch_bounds__(256) void rope_append_rows(RopeAppendParams p) {
             x2[2 * j + 1] = __uint_as_float(c[j] & 0xffff0000u);
         }
     }
+    const int L = p.seq_lens[b];
+    const int pos = L - 1;
+    const bool has_row = pos >= 0 && pos < p.mbps * p.block_size;   // no token / past the table
+    if (p.slots != nullptr && blockIdx.y == 0 && threadIdx.x == 0)
+        p.slots[b] = has_row ? static_cast<int64_t>(p.block_tables[static_cast<size_t>(b) * p.mbps +
+                                                                   pos / p.block_size]) *
+                                       p.block_size +
+                                   pos % p.block_size
+                             : -1;
+    if (!has_row || !live) return;
     float y1[4], y2[4];
     if (h < p.num_q_heads + p.kv_heads) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float cs, sn;
-            rope_cos_sin(pos, p.inv_freq[4 * iq + j], &cs, &sn);
+            rope_cos_sin(pos, fr[j], &cs, &sn);
             y1[j] = rope_first(x1[j], x2[j], cs, sn);
             y2[j] = rope_second(x1[j], x2[j], cs, sn);
         }
