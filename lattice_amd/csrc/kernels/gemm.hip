@@ -216,8 +216,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
     }
 }
 
-// Weight-streaming GEMM.  Workgroup = 4 waves = 64 weight rows (16 per wave)
-// x up to 16*MB tokens x one K split of `klen`, walked in chunks of KCH:
+// Weight-streaming GEMM.  Workgroup = NW waves = 16*NW weight rows (16 per
+// wave; NW = 4, or 8 for unsplit plain products) x up to 16*MB tokens x one
+// K split of `klen`, walked in chunks of KCH:
 //  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
 //    whole-line streaming loads (8 rows x 128 B per instruction) and is put
 //    into MFMA A layout by fix_lines, one line at a time; chunk c+1 is in
@@ -241,10 +242,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
 // then stream each weight line: 20-40% slower); summing the split partials inside this kernel
 // by the last workgroup of each tile, whose coherent stores and arrival count
 // put several memory round trips on every tile's tail.)
-template <int MB, int KCH, int EPI, bool WF8 = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+template <int MB, int KCH, int EPI, bool WF8 = false, int NW = 4>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_bf16_stream(GemmParams p) {
-    constexpr int NT = 256;
+    constexpr int NT = NW * 64;
     // 128-byte lines per weight row per chunk (fp8 weights: half as many)
     constexpr int LINES = WF8 ? KCH / 128 : KCH / 64;
     constexpr int KC = KCH / 32;             // MFMA k-steps per chunk
@@ -269,7 +270,7 @@ void gemm_bf16_stream(GemmParams p) {
     const uint32_t rowb = static_cast<uint32_t>(K) * (WF8 ? 1 : 2);   // weight row bytes
 
     // weight rows of this wave: rowA + 0..7 (MFMA rows 0..7), rowB + 0..7 (8..15)
-    const int gw = blockIdx.x * 4 + wave;
+    const int gw = blockIdx.x * NW + wave;
     int rowA, rowB;
     if constexpr (EPI == kEpiRope) {
         const int wph = p.D / 16;            // waves per head: 8 rotation pairs each
@@ -513,8 +514,18 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
             *err = "fp8 weights need 128-element chunks";
             return false;
         } else {
-            const dim3 grid(p.N / 64, splits, (p.M + 16 * MB - 1) / (16 * MB));
-            hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8>), grid, dim3(256), 0, s, p);
+            const unsigned mg = static_cast<unsigned>((p.M + 16 * MB - 1) / (16 * MB));
+            // unsplit plain products (the lm_head at decode): 8-wave
+            // workgroups, so that one staged activation chunk serves 128
+            // weight rows (KCMM_GEMM_WAVES=4 keeps 4-wave workgroups)
+            if (EPI == kEpiPlain && p.part == nullptr && p.N % 128 == 0 &&
+                dev::tunable_or(dev::Tun::kGemmWaves, 8) == 8) {
+                const dim3 grid(p.N / 128, 1, mg);
+                hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8>), grid, dim3(512), 0, s, p);
+            } else {
+                const dim3 grid(p.N / 64, splits, mg);
+                hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8>), grid, dim3(256), 0, s, p);
+            }
             KCMM_HIP_CHECK(hipGetLastError(), err);
             return true;
         }

@@ -89,6 +89,69 @@ def test_split_k_choices(gpu_lib, tunables, target, m, n, k):
     assert err <= 1e-2
 
 
+@pytest.mark.parametrize("m,n,k", [(64, 16384, 1024), (1, 16384, 512), (100, 16384, 768),
+                                   (64, 128256, 4096)])
+@pytest.mark.parametrize("residual", [False, True])
+def test_eight_wave_workgroups(gpu_lib, tunables, m, n, k, residual):
+    """Unsplit plain products in 8-wave workgroups (KCMM_GEMM_WAVES=8: 128
+    weight rows share one staged activation chunk; the last shape is the
+    Llama-3-8B lm_head at the decode batch) give the same bits as 4-wave
+    workgroups, each output being summed by one wave in the same k order;
+    both against a torch fp32 product."""
+    import torch
+    assert gpu_lib.gemm_plan(m, n, k)["splits"] == 1
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m + n + k + residual)
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    r = torch.randn((m, n), generator=g, device="cuda").to(torch.bfloat16)
+    s = torch.cuda.current_stream().cuda_stream
+    outs = {}
+    for waves in ("4", "8"):
+        tunables.setenv("KCMM_GEMM_WAVES", waves)
+        if residual:
+            y = r.clone()
+            gpu_lib.gemm_bf16_add(x.data_ptr(), w.data_ptr(), y.data_ptr(), y.data_ptr(), m, n, k, s)
+        else:
+            y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+            gpu_lib.gemm_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, s)
+        torch.cuda.synchronize()
+        outs[waves] = y
+    assert torch.equal(outs["4"], outs["8"])
+    prod = x.float() @ w.float().t()
+    ref = prod.to(torch.bfloat16).float() + r.float() if residual else prod
+    err = float((outs["8"].float() - ref).abs().max() / ref.abs().max())
+    print(f"8-wave gemm {m}x{n}x{k} residual={residual} err={err:.3e}", flush=True)
+    assert err <= 1e-2
+
+
+def test_eight_wave_workgroups_fp8_weights(gpu_lib, tunables):
+    """The same for fp8-e4m3 weights (row scales applied in the store)."""
+    import torch
+    m, n, k = 64, 16384, 2048
+    assert gpu_lib.gemm_plan(m, n, k, fp8_weights=True)["splits"] == 1
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    wf = torch.randn((n, k), generator=g, device="cuda") * 0.02
+    sc = (wf.abs().amax(dim=1) / 448.0).clamp_min(1e-12)
+    w8 = (wf / sc[:, None]).to(torch.float8_e4m3fn)
+    s = torch.cuda.current_stream().cuda_stream
+    outs = {}
+    for waves in ("4", "8"):
+        tunables.setenv("KCMM_GEMM_WAVES", waves)
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        gpu_lib.gemm_fp8w_bf16(x.data_ptr(), w8.view(torch.uint8).data_ptr(), sc.data_ptr(),
+                               y.data_ptr(), m, n, k, s)
+        torch.cuda.synchronize()
+        outs[waves] = y
+    assert torch.equal(outs["4"], outs["8"])
+    ref = x.float() @ (w8.float() * sc[:, None]).t()
+    err = float((outs["8"].float() - ref).abs().max() / ref.abs().max())
+    print(f"8-wave fp8w gemm {m}x{n}x{k} err={err:.3e}", flush=True)
+    assert err <= 1e-2
+
+
 @pytest.mark.parametrize("tile", [str(i) for i in range(11)])
 @pytest.mark.parametrize("splits", ["1", "2", "4"])
 @pytest.mark.parametrize("residual", [False, True])
