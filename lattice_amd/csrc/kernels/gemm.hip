@@ -518,10 +518,16 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
             // unsplit plain products (the lm_head at decode): 8-wave
             // workgroups, so that one staged activation chunk serves 128
             // weight rows (KCMM_GEMM_WAVES=4 keeps 4-wave workgroups)
-            if (EPI == kEpiPlain && p.part == nullptr && p.N % 128 == 0 &&
-                dev::tunable_or(dev::Tun::kGemmWaves, 8) == 8) {
-                const dim3 grid(p.N / 128, 1, mg);
-                hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8>), grid, dim3(512), 0, s, p);
+            bool wide = false;
+            if constexpr (EPI == kEpiPlain)
+                wide = p.part == nullptr && p.N % 128 == 0 &&
+                       dev::tunable_or(dev::Tun::kGemmWaves, 8) == 8;
+            if (wide) {
+                if constexpr (EPI == kEpiPlain) {
+                    const dim3 grid(p.N / 128, 1, mg);
+                    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8>), grid, dim3(512), 0,
+                                       s, p);
+                }
             } else {
                 const dim3 grid(p.N / 64, splits, mg);
                 hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8>), grid, dim3(256), 0, s, p);
