@@ -30,7 +30,7 @@ enum class Tun {
     kGemmWgs,       // KCMM_GEMM_WGS
     kGemmTiled,     // KCMM_GEMM_TILED
     kGemmTile,      // KCMM_GEMM_TILE
-    kGemmWaves,     // KCMM_GEMM_WAVES (waves per workgroup of unsplit plain decode products)
+    kGemmWaves,     // KCMM_GEMM_WAVES (waves per workgroup of unsplit plain / SwiGLU products)
     kCount
 };
 // true and *value = atoi(variable) when the variable is set.

@@ -217,8 +217,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
 }
 
 // Weight-streaming GEMM.  Workgroup = NW waves = 16*NW weight rows (16 per
-// wave; NW = 4, or 8 for unsplit plain products) x up to 16*MB tokens x one
-// K split of `klen`, walked in chunks of KCH:
+// wave; NW = 4, or 8 for unsplit plain and SwiGLU products) x up to 16*MB
+// tokens x one K split of `klen`, walked in chunks of KCH:
 //  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
 //    whole-line streaming loads (8 rows x 128 B per instruction) and is put
 //    into MFMA A layout by fix_lines, one line at a time; chunk c+1 is in
@@ -515,15 +515,16 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
             return false;
         } else {
             const unsigned mg = static_cast<unsigned>((p.M + 16 * MB - 1) / (16 * MB));
-            // unsplit plain products (the lm_head at decode): 8-wave
-            // workgroups, so that one staged activation chunk serves 128
-            // weight rows (KCMM_GEMM_WAVES=4 keeps 4-wave workgroups)
+            // unsplit plain and SwiGLU products (the lm_head and gate/up at
+            // decode): 8-wave workgroups, so that one staged activation
+            // chunk serves 128 weight rows (KCMM_GEMM_WAVES=4 keeps 4-wave
+            // workgroups)
             bool wide = false;
-            if constexpr (EPI == kEpiPlain)
+            if constexpr (EPI == kEpiPlain || EPI == kEpiSwiglu)
                 wide = p.part == nullptr && p.N % 128 == 0 &&
                        dev::tunable_or(dev::Tun::kGemmWaves, 8) == 8;
             if (wide) {
-                if constexpr (EPI == kEpiPlain) {
+                if constexpr (EPI == kEpiPlain || EPI == kEpiSwiglu) {
                     const dim3 grid(p.N / 128, 1, mg);
                     hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8>), grid, dim3(512), 0,
                                        s, p);

@@ -125,6 +125,35 @@ def test_eight_wave_workgroups(gpu_lib, tunables, m, n, k, residual):
     assert err <= 1e-2
 
 
+def test_eight_wave_swiglu(gpu_lib, tunables):
+    """The fused gate/up + SwiGLU product at the Llama-3-8B decode shape
+    (unsplit, 224 workgroups of 8 waves) gives the same bits as 4-wave
+    workgroups; against silu(g)*u of a torch fp32 product.  (fp8 weights
+    reach this kernel through the layer driver: tests/test_gpu_glue.py.)"""
+    import torch
+    m, inter, k = 64, 14336, 4096
+    assert gpu_lib.gemm_plan(m, 2 * inter, k)["splits"] == 1
+    g = torch.Generator(device="cuda")
+    g.manual_seed(17)
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((2 * inter, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    s = torch.cuda.current_stream().cuda_stream
+    outs = {}
+    for waves in ("4", "8"):
+        tunables.setenv("KCMM_GEMM_WAVES", waves)
+        act = torch.full((m, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
+        gpu_lib.gemm_bf16_swiglu(x.data_ptr(), w.data_ptr(), act.data_ptr(), m, inter, k, s)
+        torch.cuda.synchronize()
+        outs[waves] = act
+    assert torch.equal(outs["4"], outs["8"])
+    gu = (x.float() @ w.float().t()).to(torch.bfloat16).float()
+    gate, up = gu[:, :inter], gu[:, inter:]
+    ref = (gate * torch.sigmoid(gate)).to(torch.bfloat16).float() * up
+    err = float((outs["8"].float() - ref).abs().max() / ref.abs().max())
+    print(f"8-wave swiglu err={err:.3e}", flush=True)
+    assert err <= 1e-2
+
+
 def test_eight_wave_workgroups_fp8_weights(gpu_lib, tunables):
     """The same for fp8-e4m3 weights (row scales applied in the store)."""
     import torch

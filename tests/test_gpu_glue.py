@@ -530,6 +530,64 @@ def test_fp8_weight_layers_match_bf16_layers_on_exact_weights(gpu_lib, hq, hkv, 
     assert np.isfinite(outs[0]).all() and err <= 1e-2 and same >= 0.5
 
 
+@pytest.mark.parametrize("fp8w", [False, True])
+def test_decode_layers_same_bits_at_4_and_8_waves(gpu_lib, tunables, fp8w):
+    """At the Llama-3-8B intermediate size the gate/up + SwiGLU projection is
+    unsplit and runs in 8-wave workgroups (KCMM_GEMM_WAVES=4: 4-wave).  Two
+    layers from the same hidden state and pages give the same bits either
+    way, with bf16 and with fp8-e4m3 projection weights."""
+    import torch
+    hq, hkv, d, h, inter = 32, 8, 128, 4096, 14336
+    lens = [1, 16, 17, 130, 700, 64, 3, 2049]
+    B = len(lens)
+    case = build_decode_case(gpu_lib, batch=B, num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=16, ctx_lens=lens, dtype=KV_BF16, seed=41, num_layers=2)
+    try:
+        assert gpu_lib.gemm_plan(B, 2 * inter, h, fp8_weights=fp8w)["splits"] == 1
+        g = torch.Generator(device="cuda")
+        g.manual_seed(43 + fp8w)
+        shapes = {"qkv": ((hq + 2 * hkv) * d, h), "o": (h, hq * d), "gate_up": (2 * inter, h),
+                  "down": (h, inter)}
+        keep = []
+        lws = []
+        for _ in range(2):
+            t = {"attn_norm": (1.0 + 0.1 * torch.randn(h, generator=g, device="cuda")).to(torch.bfloat16),
+                 "mlp_norm": (1.0 + 0.1 * torch.randn(h, generator=g, device="cuda")).to(torch.bfloat16)}
+            for name, shp in shapes.items():
+                wf = torch.randn(shp, generator=g, device="cuda") * 0.05
+                if fp8w:
+                    sc = (wf.abs().amax(dim=1) / 448.0).clamp_min(1e-12)
+                    t[name] = (wf / sc[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+                    t[name + "_scale"] = sc.contiguous()
+                else:
+                    t[name] = wf.to(torch.bfloat16)
+            keep.append(t)
+            cls = KcmmLayerWeightsFp8 if fp8w else KcmmLayerWeights
+            lws.append(cls(**{k: v.data_ptr() for k, v in t.items()}))
+        hid0 = torch.randn((B, h), generator=g, device="cuda").to(torch.bfloat16)
+        invd = torch.from_numpy(O.default_inv_freq(500000.0, d).astype(np.float32)).cuda()
+        dv = case.dev
+        outs = {}
+        for waves in ("4", "8"):
+            tunables.setenv("KCMM_GEMM_WAVES", waves)
+            hd = hid0.clone()
+            kw = dict(first_layer=0, weights=lws, hidden_ptr=hd.data_ptr(),
+                      block_tables_ptr=dv["bt"].data_ptr(), seq_lens_ptr=dv["sl"].data_ptr(),
+                      block_offsets_f16_ptr=dv["offs"].data_ptr(), inv_freq_ptr=invd.data_ptr(),
+                      batch=B, hidden_size=h, num_q_heads=hq, intermediate_size=inter,
+                      max_blocks_per_seq=case.mbps, rms_eps=1e-5)
+            if fp8w:
+                case.pool.decode_layers_fp8w(**kw)
+            else:
+                case.pool.decode_layers(**kw)
+            torch.cuda.synchronize()
+            outs[waves] = hd
+        assert bool(torch.isfinite(outs["8"].float()).all())
+        assert torch.equal(outs["4"], outs["8"])
+    finally:
+        case.pool.destroy()
+
+
 @pytest.mark.parametrize("b,h,vocab", [(5, 512, 1024), (64, 4096, 2048), (8, 256, 128256)])
 def test_decode_logits(gpu_lib, b, h, vocab):
     """Final RMSNorm + lm_head vs the oracle's bf16 norm and fp64 product
