@@ -1,0 +1,175 @@
+"""Seeded random sweeps of the decode and prefill attention entry points and
+the projection GEMMs against the oracle (fp64), over combinations the
+hand-picked cases do not list together.  Attention: page type, GQA group,
+head_dim, block size, batch, ragged lengths (empty, one token, tile and page
+edges), softmax scale, and the decode kernel's work split (total waves, waves
+per workgroup, minimum slice, tiles in flight).  GEMM: shapes around the
+kernel dispatch boundaries, bf16 or fp8 weights, the residual form, forced K
+splits and workgroup widths.  Every case prints its parameters before it
+runs.  Tolerances as the other tests: bf16 / f16 1e-2, fp8 pages 3e-2, GEMM
+1e-2."""
+import math
+
+import numpy as np
+import pytest
+
+from lattice_amd.bindings import KV_BF16, KV_F16, KV_FP8
+from lattice_amd.workload import build_decode_case
+from tests.test_gpu_attention import check as check_decode
+from tests.test_gpu_prefill import TOL, rel_err, run_prefill
+
+pytestmark = pytest.mark.gpu
+
+GROUPS = [(8, 8), (16, 8), (32, 8), (32, 4), (16, 2), (32, 2), (16, 1), (12, 4), (10, 5)]
+
+
+def ragged_lengths(rng, batch, block_size, max_len):
+    """Lengths drawn from a mix of edge cases and uniform values."""
+    edges = [0, 1, 2, block_size - 1, block_size, block_size + 1, 31, 32, 33, 63, 64, 65]
+    out = []
+    for _ in range(batch):
+        r = rng.random()
+        if r < 0.35:
+            out.append(int(rng.choice(edges)))
+        elif r < 0.5:
+            k = int(rng.integers(1, max(2, max_len // 32)))
+            out.append(int(32 * k + rng.integers(-1, 2)))
+        else:
+            out.append(int(rng.integers(1, max_len + 1)))
+    if max(out) <= 0:
+        out[0] = 1
+    return [max(0, min(x, max_len)) for x in out]
+
+
+def decode_params(seed):
+    rng = np.random.default_rng(1000 + seed)
+    dtype = [KV_BF16, KV_F16, KV_FP8][seed % 3]
+    hq, hkv = GROUPS[int(rng.integers(len(GROUPS)))]
+    d = 128 if dtype == KV_FP8 or rng.random() < 0.6 else 64
+    bs = int(rng.choice([8, 16, 32]))
+    batch = int(rng.integers(1, 25))
+    ctx = ragged_lengths(rng, batch, bs, int(rng.choice([200, 700, 1500])))
+    scale = float(rng.choice([1.0 / math.sqrt(d), 0.05, 0.2]))
+    tun = {}
+    if rng.random() < 0.6:
+        tun["KCMM_ATTN_WAVES"] = str(int(rng.choice([64, 256, 1024, 3000])))
+    if rng.random() < 0.4:
+        tun["KCMM_ATTN_HW"] = str(int(rng.choice([1, 2, 4, 8])))
+    if rng.random() < 0.4:
+        tun["KCMM_ATTN_MIN_TILES"] = str(int(rng.choice([1, 2, 8, 40])))
+    if rng.random() < 0.3:
+        tun["KCMM_ATTN_DEPTH"] = "3"
+    return dtype, hq, hkv, d, bs, ctx, scale, tun
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_decode_attention_random(gpu_lib, tunables, seed):
+    dtype, hq, hkv, d, bs, ctx, scale, tun = decode_params(seed)
+    print(f"decode seed={seed} dtype={dtype} Hq={hq} Hkv={hkv} D={d} bs={bs} B={len(ctx)} "
+          f"ctx={ctx} scale={scale:.4f} tunables={tun}", flush=True)
+    for k, v in tun.items():
+        tunables.setenv(k, v)
+    case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=bs, ctx_lens=ctx, dtype=dtype, seed=seed)
+    try:
+        check_decode(case, scale=scale)
+    finally:
+        case.pool.destroy()
+
+
+def prefill_params(seed):
+    rng = np.random.default_rng(2000 + seed)
+    dtype = [KV_BF16, KV_F16, KV_FP8][seed % 3]
+    hq, hkv = GROUPS[int(rng.integers(len(GROUPS)))]
+    d = 128 if dtype == KV_FP8 or rng.random() < 0.6 else 64
+    bs = int(rng.choice([8, 16, 32]))
+    batch = int(rng.integers(1, 9))
+    ctx = [max(1, x) for x in ragged_lengths(rng, batch, bs, int(rng.choice([120, 400])))]
+    lens = [int(rng.integers(1, L + 1)) if rng.random() < 0.8 else L for L in ctx]
+    scale = float(rng.choice([1.0 / math.sqrt(d), 0.05]))
+    return dtype, hq, hkv, d, bs, ctx, lens, scale
+
+
+@pytest.mark.parametrize("seed", range(18))
+def test_prefill_attention_random(gpu_lib, seed):
+    dtype, hq, hkv, d, bs, ctx, lens, scale = prefill_params(seed)
+    print(f"prefill seed={seed} dtype={dtype} Hq={hq} Hkv={hkv} D={d} bs={bs} ctx={ctx} "
+          f"lens={lens} scale={scale:.4f}", flush=True)
+    case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=bs, ctx_lens=ctx, dtype=dtype, seed=seed + 50)
+    try:
+        got, ref = run_prefill(case, lens, hq, seed=seed + 60, scale=scale)
+        err = rel_err(got, ref)
+        print(f"  err={err:.3e}", flush=True)
+        assert np.isfinite(got).all() and err <= TOL[dtype], err
+    finally:
+        case.pool.destroy()
+
+
+def gemm_params(seed):
+    rng = np.random.default_rng(3000 + seed)
+    edges = [1, 2, 16, 17, 32, 33, 64, 65, 127, 128, 129, 200, 255, 256, 257, 300]
+    m = int(rng.choice(edges)) if rng.random() < 0.7 else int(rng.integers(1, 301))
+    n = 64 * int(rng.integers(1, 41))
+    k = 256 * int(rng.integers(1, 13))
+    fp8 = seed % 3 == 2
+    residual = not fp8 and rng.random() < 0.4
+    tun = {}
+    if rng.random() < 0.4:
+        tun["KCMM_GEMM_SPLITS"] = str(int(rng.choice([1, 2, 4, 8])))
+    if rng.random() < 0.3:
+        tun["KCMM_GEMM_TILED"] = "0"
+    if rng.random() < 0.3:
+        tun["KCMM_GEMM_WAVES"] = "4"
+    return m, n, k, fp8, residual, tun
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_gemm_random(gpu_lib, tunables, seed):
+    """kcmm_gemm_bf16 / kcmm_gemm_bf16_add / kcmm_gemm_fp8w_bf16 on random
+    shapes around the dispatch boundaries (M = 128 / 129 between the
+    weight-stream and tiled kernels, N not a multiple of 128, forced K
+    splits) against the fp64 oracle (1e-2); a repeated call gives the same
+    bits."""
+    import torch
+    import oracle as O
+    m, n, k, fp8, residual, tun = gemm_params(seed)
+    print(f"gemm seed={seed} m={m} n={n} k={k} fp8={fp8} residual={residual} tunables={tun}",
+          flush=True)
+    for name, v in tun.items():
+        tunables.setenv(name, v)
+    rng = np.random.default_rng(seed + 70)
+    xb = O.encode(O.BF16, rng.standard_normal((m, k)))
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    rb = O.encode(O.BF16, rng.standard_normal((m, n)))
+    s = torch.cuda.current_stream().cuda_stream
+    if fp8:
+        w8, sc = O.quantize_fp8_rows(rng.standard_normal((n, k)).astype(np.float32) * 0.02)
+        w8d, scd = torch.from_numpy(w8).cuda(), torch.from_numpy(sc).cuda()
+        ref = O.gemm_fp8w_f64(xb, w8, sc)
+    else:
+        wb = O.encode(O.BF16, rng.standard_normal((n, k)) * 0.02)
+        w = torch.from_numpy(wb.view(np.int16)).view(torch.bfloat16).cuda()
+        ref = O.gemm_bf16_f64(xb, wb)
+        if residual:
+            ref = O.decode(O.BF16, O.encode(O.BF16, ref)).astype(np.float64) + \
+                O.decode(O.BF16, rb).astype(np.float64)
+    outs = []
+    for _ in range(2):
+        if residual:
+            y = torch.from_numpy(rb.view(np.int16)).view(torch.bfloat16).cuda()
+            gpu_lib.gemm_bf16_add(x.data_ptr(), w.data_ptr(), y.data_ptr(), y.data_ptr(), m, n, k, s)
+        else:
+            y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+            if fp8:
+                gpu_lib.gemm_fp8w_bf16(x.data_ptr(), w8d.data_ptr(), scd.data_ptr(), y.data_ptr(),
+                                       m, n, k, s)
+            else:
+                gpu_lib.gemm_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, s)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(outs[0], outs[1])
+    got = O.decode(O.BF16, outs[0]).astype(np.float64)
+    err = float(np.abs(got - ref).max() / np.abs(ref).max())
+    print(f"  err={err:.3e}", flush=True)
+    assert np.isfinite(got).all() and err <= 1e-2, err
