@@ -25,10 +25,14 @@ consecutive calls on the cycled KV sets); decode tokens/s = 64 / t_step with
 t_step the embedding, the 32-layer call, the final norm and lm_head (sampling
 is outside this path and excluded).
 
-`roofline` prices the attention call (streaming kernel + log-sum-exp merge,
-timed by HIP events on the launch stream) against MI355X's 8 TB/s; its
-`traffic` (HBM bytes per call) is read from the rocprofv3 FETCH_SIZE /
-WRITE_SIZE summary committed in profiles/, which records the commands and the
+`roofline` prices the dominant kernel, the attention's streaming kernel
+(attn_decode_stream), against MI355X's 8 TB/s: algorithmic K+V bytes / its
+average launch duration, from HIP events that the library records around
+each launch on the launch stream (kcmm_attn_stream_timing_*) over the same
+back-to-back calls; `roofline.call` repeats the figures for the whole call
+(the kernel, the log-sum-exp merge and the gap between them).  `traffic`
+(HBM bytes per launch) is read from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+summary committed in profiles/, which records the commands and the
 copy-kernel calibration it was scaled with.
 """
 from __future__ import annotations
@@ -116,13 +120,14 @@ TRAFFIC_FILES = {"cfg2": ROOT / "profiles" / "attn_decode_cfg2_hbm_traffic.txt",
                  "cfg5": ROOT / "profiles" / "attn_decode_fp8_cfg5_hbm_traffic.txt"}
 
 
-def measured_traffic(config="cfg2"):
-    """HBM bytes per attention call from the committed rocprofv3 counter
-    summary of that config (None if the file is absent)."""
+def measured_traffic(config="cfg2", key="traffic_bytes_per_call"):
+    """HBM bytes per attention call (or, with key="traffic_bytes_stream_kernel",
+    per launch of the streaming kernel alone) from the committed rocprofv3
+    counter summary of that config (None if the file or the line is absent)."""
     try:
         for line in TRAFFIC_FILES[config].read_text().splitlines():
-            if line.startswith("traffic_bytes_per_call:"):
-                return int(line.split(":")[1])
+            if line.startswith(key + ":"):
+                return int(line.split(":")[1].split()[0])
     except OSError:
         pass
     return None
@@ -733,6 +738,19 @@ def main():
     attn_b2b_ms = ea.elapsed_time(eb) / args.steps
     log(f"attention back to back: {attn_b2b_ms:.4f} ms per call (in the component pass "
         f"{per['attn']:.4f})")
+    # the dominant kernel alone: the same back-to-back calls again, with HIP
+    # events recorded by the library around each streaming-kernel launch (on
+    # the stream it is launched on); the merge after it is outside the pair
+    lib.attn_stream_timing_start(args.steps)
+    try:
+        for i in range(args.steps):
+            calls["attn"](i % args.layers)
+        torch.cuda.synchronize()
+    finally:
+        stream_us, n_timed = lib.attn_stream_timing_stop()
+    assert n_timed == args.steps, (n_timed, args.steps)
+    log(f"attention streaming kernel: {stream_us:.2f} us per launch (HIP events, {n_timed} launches)")
+    stream_gbs = kv_bytes / (stream_us * 1e-6) / 1e9
     attn_s = attn_b2b_ms / 1e3
     kv_gbs = kv_bytes / attn_s / 1e9
     result = {
@@ -763,12 +781,20 @@ def main():
         "attn_us_per_call": round(attn_b2b_ms * 1e3, 2),
         "attn_us_in_component_pass": round(per["attn"] * 1e3, 2),
         "kv_bytes_per_layer_step": kv_bytes,
-        "roofline": {"bound": "hbm", "achieved": round(kv_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(kv_gbs / HBM_PEAK_GBS, 4),
-                     # counter-measured HBM bytes exist for the Cfg2 call only
-                     "traffic": measured_traffic(args.config),
-                     "kernel": "paged decode attention call (attn_decode_stream + attn_decode_merge)",
-                     "algorithmic_bytes": kv_bytes},
+        "attn_stream_kernel_us": round(stream_us, 2),
+        # the dominant kernel (attn_decode_stream): algorithmic K+V bytes per
+        # launch / its average launch duration by HIP events; `value` above
+        # prices the whole call (the kernel, the log-sum-exp merge and the gap)
+        "roofline": {"bound": "hbm", "achieved": round(stream_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(stream_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(args.config, "traffic_bytes_stream_kernel"),
+                     "kernel": "attn_decode_stream (HIP events around each launch, back to back "
+                               "over the cycled KV sets)",
+                     "kernel_us": round(stream_us, 2),
+                     "algorithmic_bytes": kv_bytes,
+                     "call": {"us": round(attn_b2b_ms * 1e3, 2), "gbs": round(kv_gbs, 1),
+                              "frac": round(kv_gbs / HBM_PEAK_GBS, 4),
+                              "traffic": measured_traffic(args.config)}},
         "append_us": round((per["append"] if args.attn_only else extra["append"]) * 1e3, 2),
         "wall_s_timed": round(wall, 3),
     }

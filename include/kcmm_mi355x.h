@@ -118,6 +118,22 @@ int kcmm_paged_attn_decode_bf16_noalloc_on_stream(
     uint32_t kv_heads, uint32_t head_dim, uint32_t block_size,
     uint32_t max_blocks_per_seq, float scale, uint64_t stream_ptr);
 
+/** Measurement: HIP-event timing of the decode-attention streaming kernel
+ *  alone (the kernel that reads the KV pages; the attention call also runs
+ *  a log-sum-exp merge after it).  start creates max_calls (1..65536) event
+ *  pairs on the current device; each streaming-kernel launch on that device
+ *  after it, by any decode-attention entry point and not under graph
+ *  capture, is bracketed by the next free pair.  stop waits for the
+ *  recorded pairs, writes their average duration in microseconds and their
+ *  number, and frees the events.  Call stop after the timed calls have
+ *  returned; not for concurrent use from several threads.  Off by default
+ *  (a launch then only reads one atomic flag).  No counterpart in the
+ *  reference (it has no per-kernel timing); for bench.py's roofline of the
+ *  dominant kernel.  0 on success, -1 on error (stop without start, bad
+ *  arguments, an event query that failed). */
+int kcmm_attn_stream_timing_start(uint32_t max_calls);
+int kcmm_attn_stream_timing_stop(double *avg_us, uint32_t *count);
+
 /** Reads the KCMM_* tuning variables (KCMM_ATTN_*, KCMM_GEMM_*) again.  The
  *  library reads them once, on first use, so that launch paths make no
  *  getenv call; tests and tuning runs that change them call this after the

@@ -178,6 +178,8 @@ SIGNATURES = {
     "kcmm_gemm_bf16_on_stream": ([_U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_gemm_fp8w_bf16_on_stream": ([_U64, _U64, _U64, _U64, _U32, _U32, _U32, _U64], C.c_int),
     "kcmm_gemm_plan": ([_U32, _U32, _U32, _U32, C.POINTER(C.c_int64)], C.c_int),
+    "kcmm_attn_stream_timing_start": ([_U32], C.c_int),
+    "kcmm_attn_stream_timing_stop": ([C.POINTER(C.c_double), C.POINTER(C.c_uint32)], C.c_int),
     "kcmm_prefix_hash_blocks": ([_P, _U32, _U32, _U64, _P, _U32, C.POINTER(_U32)], C.c_int),
     "kcmm_prefix_register": ([_P, _U32, _P, _U32, C.POINTER(_U32)], C.c_int),
     "kcmm_prefix_match": ([_P, _P, _U32, _P, C.POINTER(_U32)], C.c_int),
@@ -264,6 +266,18 @@ class KcmmLibrary:
                                             seed, out.ctypes.data, out.size, C.byref(cnt)) != 0:
             raise KcmmError("kcmm_prefix_hash_blocks failed")
         return out[: cnt.value]
+
+    def attn_stream_timing_start(self, max_calls: int) -> None:
+        """Start HIP-event timing of the decode-attention streaming kernel."""
+        if self.lib.kcmm_attn_stream_timing_start(max_calls) != 0:
+            raise KcmmError("kcmm_attn_stream_timing_start failed")
+
+    def attn_stream_timing_stop(self) -> tuple[float, int]:
+        """(average streaming-kernel duration in us, launches timed)."""
+        avg, n = C.c_double(), C.c_uint32()
+        if self.lib.kcmm_attn_stream_timing_stop(C.byref(avg), C.byref(n)) != 0:
+            raise KcmmError("kcmm_attn_stream_timing_stop failed")
+        return float(avg.value), int(n.value)
 
     def gemm_plan(self, m, n, k, fp8_weights=False) -> dict:
         """How a plain product of this shape runs: kernel ('stream' / 'tiled'),

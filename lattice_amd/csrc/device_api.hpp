@@ -73,6 +73,14 @@ struct AttnDecodeArgs {
 };
 bool attn_decode(const AttnDecodeArgs& a, std::string* err);
 
+// Event timing of the decode-attention streaming kernel, for measurement:
+// start creates `max_calls` event pairs on the current device, and each
+// streaming-kernel launch after it (not under graph capture) is bracketed by
+// the next pair; stop waits for the recorded pairs and returns their average
+// duration in microseconds and how many there were, then frees the events.
+bool attn_stream_timing_start(uint32_t max_calls, std::string* err);
+bool attn_stream_timing_stop(double* avg_us, uint32_t* count, std::string* err);
+
 // Causal chunked-prefill attention over one layer's K/V regions: sequence b's
 // last qsl[b+1]-qsl[b] cached tokens are the queries (rows qsl[b]..).
 struct AttnPrefillArgs {

@@ -572,6 +572,25 @@ int kcmm_paged_attn_decode_bf16_noalloc_on_stream(KCMM_ATTN_ARGS, uint64_t strea
                      KCMM_ATTN_PASS, stream, false, true, true);
 }
 
+int kcmm_attn_stream_timing_start(uint32_t max_calls) {
+    std::string err;
+    if (!kcmm::dev::attn_stream_timing_start(max_calls, &err)) {
+        std::fprintf(stderr, "kcmm_attn_stream_timing_start: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+int kcmm_attn_stream_timing_stop(double* avg_us, uint32_t* count) {
+    if (avg_us == nullptr || count == nullptr) return -1;
+    std::string err;
+    if (!kcmm::dev::attn_stream_timing_stop(avg_us, count, &err)) {
+        std::fprintf(stderr, "kcmm_attn_stream_timing_stop: %s\n", err.c_str());
+        return -1;
+    }
+    return 0;
+}
+
 int kcmm_paged_attn_decode_f32(KCMM_ATTN_ARGS) {
     return attn_impl(pool, kcmm::kF32, "kcmm_paged_attn_decode_f32", KCMM_ATTN_PASS, 0, true,
                      true);

@@ -33,12 +33,15 @@
 //    (unnormalised output, max, denominator) that attn_decode_merge combines
 //    by log-sum-exp.
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <mutex>
 #include <string>
+#include <vector>
 #include <cmath>
 #include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 #include "../device_api.hpp"
 #include "common.hpp"
@@ -71,6 +74,35 @@ struct NoAllocDevice {
 };
 std::mutex g_noalloc_mu;
 NoAllocDevice g_noalloc[kMaxDevices];
+
+// Event timing of the streaming kernel (dev::attn_stream_timing_start /
+// stop): event pairs created at start on the then-current device and taken
+// in order by the streaming-kernel launches that follow on that device.  Off
+// by default; a launch under graph capture takes no pair.
+struct StreamTiming {
+    std::atomic<bool> on{false};
+    std::mutex mu;
+    int device = -1;
+    uint32_t next = 0;
+    std::vector<hipEvent_t> ev;   // pair i: ev[2i] before the launch, ev[2i+1] after it
+};
+StreamTiming g_timing;
+
+// The event pair for a streaming-kernel launch on s: {nullptr, nullptr}
+// when timing is off, every pair is taken, s is capturing or belongs to
+// another device.
+std::pair<hipEvent_t, hipEvent_t> timing_pair(hipStream_t s) {
+    if (!g_timing.on.load(std::memory_order_acquire)) return {nullptr, nullptr};
+    std::lock_guard<std::mutex> lk(g_timing.mu);
+    int dev = -1;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (!g_timing.on.load(std::memory_order_relaxed) || 2 * (g_timing.next + 1) > g_timing.ev.size() ||
+        hipGetDevice(&dev) != hipSuccess || dev != g_timing.device ||
+        hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return {nullptr, nullptr};
+    const uint32_t i = g_timing.next++;
+    return {g_timing.ev[2 * i], g_timing.ev[2 * i + 1]};
+}
 
 // The current device's state, set up on its first call; g_noalloc_mu held.
 bool noalloc_device(NoAllocDevice** out, std::string* err) {
@@ -1125,6 +1157,8 @@ bool launch_stream(AttnParams& p, hipStream_t s, bool no_alloc, std::string* err
     p.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + idle_bytes);
     p.part_acc = p.part_ml + units * 2;
     p.seg_info = static_cast<int2*>(info);
+    const auto tp = timing_pair(s);
+    if (tp.first != nullptr) KCMM_HIP_CHECK(hipEventRecord(tp.first, s), err);
     if (depth == 3)
         hipLaunchKernelGGL((attn_decode_stream<DT, D, BS, 3>), dim3(p.total_waves), dim3(64 * hw),
                            0, s, p, p.block_tables, p.seq_lens, p.offsets_f16, p.k_base, p.v_base,
@@ -1134,6 +1168,7 @@ bool launch_stream(AttnParams& p, hipStream_t s, bool no_alloc, std::string* err
                            0, s, p, p.block_tables, p.seq_lens, p.offsets_f16, p.k_base, p.v_base,
                            idle);
     KCMM_HIP_CHECK(hipGetLastError(), err);
+    if (tp.second != nullptr) KCMM_HIP_CHECK(hipEventRecord(tp.second, s), err);
     launch_merge<DT == kDtFP8 ? kDtBF16 : DT, D>(p, s);
     KCMM_HIP_CHECK(hipGetLastError(), err);
     if (no_alloc && !capturing) {
@@ -1201,6 +1236,60 @@ bool attn_decode(const AttnDecodeArgs& a, std::string* err) {
         default: launch_generic<kDtFP8>(p, hd, a.scale, s); break;
     }
     KCMM_HIP_CHECK(hipGetLastError(), err);
+    return true;
+}
+
+bool attn_stream_timing_start(uint32_t max_calls, std::string* err) {
+    if (max_calls == 0 || max_calls > (1u << 16)) {
+        *err = "attention timing: max_calls must be 1..65536";
+        return false;
+    }
+    std::lock_guard<std::mutex> lk(g_timing.mu);
+    if (g_timing.on.load()) {
+        *err = "attention timing already started";
+        return false;
+    }
+    KCMM_HIP_CHECK(hipGetDevice(&g_timing.device), err);
+    g_timing.ev.assign(2 * static_cast<size_t>(max_calls), nullptr);
+    for (auto& e : g_timing.ev) {
+        if (hipEventCreate(&e) != hipSuccess) {
+            for (auto& f : g_timing.ev)
+                if (f != nullptr) (void)hipEventDestroy(f);
+            g_timing.ev.clear();
+            *err = "attention timing: hipEventCreate failed";
+            return false;
+        }
+    }
+    g_timing.next = 0;
+    g_timing.on.store(true, std::memory_order_release);
+    return true;
+}
+
+bool attn_stream_timing_stop(double* avg_us, uint32_t* count, std::string* err) {
+    std::lock_guard<std::mutex> lk(g_timing.mu);
+    if (!g_timing.on.load()) {
+        *err = "attention timing not started";
+        return false;
+    }
+    g_timing.on.store(false);
+    double total_ms = 0.0;
+    bool ok = true;
+    for (uint32_t i = 0; i < g_timing.next && ok; ++i) {
+        float ms = 0.0f;
+        ok = hipEventSynchronize(g_timing.ev[2 * i + 1]) == hipSuccess &&
+             hipEventElapsedTime(&ms, g_timing.ev[2 * i], g_timing.ev[2 * i + 1]) == hipSuccess;
+        total_ms += ms;
+    }
+    const uint32_t n = g_timing.next;
+    for (auto& e : g_timing.ev) (void)hipEventDestroy(e);
+    g_timing.ev.clear();
+    g_timing.next = 0;
+    if (!ok) {
+        *err = "attention timing: event query failed";
+        return false;
+    }
+    *count = n;
+    *avg_us = n > 0 ? total_ms * 1e3 / n : 0.0;
     return true;
 }
 

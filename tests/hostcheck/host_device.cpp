@@ -205,6 +205,8 @@ bool stream_workspace(uint64_t, int, size_t, void**, bool, std::string* err) {
 bool release_orphaned_workspaces(std::string*) { return true; }
 size_t orphaned_workspaces() { return 0; }
 bool attn_decode(const AttnDecodeArgs&, std::string* err) { return no_device(err); }
+bool attn_stream_timing_start(uint32_t, std::string* err) { return no_device(err); }
+bool attn_stream_timing_stop(double*, uint32_t*, std::string* err) { return no_device(err); }
 bool attn_prefill(const AttnPrefillArgs&, std::string* err) { return no_device(err); }
 bool kv_write_rows(const KvRowsArgs&, std::string* err) { return no_device(err); }
 bool kv_write_device_slots(const KvDeviceSlotsArgs&, std::string* err) { return no_device(err); }

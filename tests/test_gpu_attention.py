@@ -350,3 +350,43 @@ def test_fp8_device_filled_long_contexts(gpu_lib):
         assert err <= TOL[KV_FP8]
     finally:
         case.pool.destroy()
+
+
+def test_stream_kernel_timing(gpu_lib):
+    """kcmm_attn_stream_timing_start / stop: one event pair per streaming-kernel
+    launch, an average below the whole call's (which adds the merge), the
+    output unchanged by the timing, and errors for a stop without a start and
+    a second start."""
+    import torch
+    from lattice_amd.bindings import KcmmError
+    ctx = [900, 1, 33, 2500, 64, 700, 17, 1500]
+    case = build_decode_case(gpu_lib, batch=len(ctx), num_q_heads=32, kv_heads=8, head_dim=128,
+                             block_size=16, ctx_lens=ctx, dtype=KV_BF16, seed=77)
+    try:
+        sp = torch.cuda.current_stream().cuda_stream
+        case.run_attention(stream_ptr=sp)
+        torch.cuda.synchronize()
+        ref = case.out_bits().copy()
+        with pytest.raises(KcmmError):
+            gpu_lib.attn_stream_timing_stop()
+        gpu_lib.attn_stream_timing_start(8)
+        with pytest.raises(KcmmError):
+            gpu_lib.attn_stream_timing_start(8)
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record()
+        for _ in range(3):
+            case.run_attention(stream_ptr=sp)
+        eb.record()
+        torch.cuda.synchronize()
+        avg_us, n = gpu_lib.attn_stream_timing_stop()
+        call_us = ea.elapsed_time(eb) * 1e3 / 3
+        print(f"stream kernel {avg_us:.2f} us, call {call_us:.2f} us, {n} launches", flush=True)
+        assert n == 3 and 0 < avg_us < call_us
+        assert np.array_equal(case.out_bits(), ref)
+        # off again: launches take no event pair
+        case.run_attention(stream_ptr=sp)
+        gpu_lib.attn_stream_timing_start(2)
+        _, n0 = gpu_lib.attn_stream_timing_stop()
+        assert n0 == 0
+    finally:
+        case.pool.destroy()
