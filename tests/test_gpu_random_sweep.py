@@ -173,3 +173,79 @@ def test_gemm_random(gpu_lib, tunables, seed):
     err = float(np.abs(got - ref).max() / np.abs(ref).max())
     print(f"  err={err:.3e}", flush=True)
     assert np.isfinite(got).all() and err <= 1e-2, err
+
+
+LAYER_HEADS = [(8, 2, 64), (16, 4, 64), (16, 8, 128), (8, 8, 128), (32, 4, 128), (32, 8, 128)]
+
+
+def layer_params(seed):
+    rng = np.random.default_rng(4000 + seed)
+    hq, hkv, d = LAYER_HEADS[int(rng.integers(len(LAYER_HEADS)))]
+    h = int(rng.choice([512, 1024, 2048]))
+    inter = int(rng.choice([512, 768, 1024, 1536]))
+    dtype = KV_FP8 if seed % 3 == 2 and d == 128 else KV_BF16
+    batch = int(rng.integers(1, 41))
+    lens = [max(1, x) for x in ragged_lengths(rng, batch, 16, int(rng.choice([100, 300])))]
+    return hq, hkv, d, h, inter, dtype, lens
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_decode_layer_random(gpu_lib, seed):
+    """kcmm_decode_layer_step_on_stream on random layer shapes, pool types,
+    batches and ragged lengths: every stage against the oracle's stage
+    (tests/layer_stages.py), the fused step against its components bit for
+    bit, and the whole layer against the oracle's layer (as
+    test_gpu_glue.test_decode_layer_step)."""
+    import torch
+    import oracle as O
+    from lattice_amd.bindings import memcpy_htod
+    from tests import layer_stages as LS
+    from tests.test_gpu_glue import _layer_weights, _region, bf16_dev, bits_of
+    from tests.test_gpu_glue import rel_err as rel_err_glue
+    hq, hkv, d, h, inter, dtype, lens = layer_params(seed)
+    print(f"layer seed={seed} Hq={hq} Hkv={hkv} D={d} h={h} inter={inter} dtype={dtype} "
+          f"lens={lens}", flush=True)
+    fp8 = dtype == KV_FP8
+    case = build_decode_case(gpu_lib, batch=len(lens), num_q_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=16, ctx_lens=lens, dtype=dtype, seed=seed + 80)
+    try:
+        g = case.geometry
+        rng = np.random.default_rng(seed + 90)
+        w, wdev, lw = _layer_weights(torch, rng, h, inter, hq, hkv, d)
+        hid = O.encode(O.BF16, rng.standard_normal((len(lens), h)))
+        inv = O.default_inv_freq(500000.0, d)
+        invd = torch.from_numpy(inv.astype(np.float32)).cuda()
+        dv = case.dev
+        stream = torch.cuda.current_stream().cuda_stream
+        st = LS.run_stages(gpu_lib, case, wdev, hid, invd, hq, h, inter, 1e-5, stream)
+        errs = LS.check_stages(st, case, w, inv, hq, inter, 1e-5, dtype)
+        print("  stages " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
+        kreg, vreg = st["kv0"]
+        memcpy_htod(case.pool.va_k(0), kreg)
+        memcpy_htod(case.pool.va_v(0), vreg)
+        hd = bf16_dev(torch, hid)
+        case.pool.decode_layer_step(layer_idx=0, weights=lw, hidden_ptr=hd.data_ptr(),
+                                    block_tables_ptr=dv["bt"].data_ptr(),
+                                    seq_lens_ptr=dv["sl"].data_ptr(),
+                                    block_offsets_f16_ptr=dv["offs"].data_ptr(),
+                                    inv_freq_ptr=invd.data_ptr(), batch=len(lens),
+                                    hidden_size=h, num_q_heads=hq, intermediate_size=inter,
+                                    max_blocks_per_seq=case.mbps, rms_eps=1e-5,
+                                    stream_ptr=stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits_of(hd), st["out"]), "layer step != its components"
+        assert np.array_equal(_region(case, "k"), st["kv1"][0])
+        assert np.array_equal(_region(case, "v"), st["kv1"][1])
+        got = O.decode(O.BF16, bits_of(hd)).astype(np.float64)
+        ref = O.decode_layer_step_f64(hid, w, kreg.copy(), vreg.copy(), case.block_tables,
+                                      case.seq_lens, case.offsets_f16, inv, hq, hkv, d, inter, 16,
+                                      g["row_bytes"], 1e-5, dtype=dtype,
+                                      data_bytes=g["data_bytes"])
+        x = O.decode(O.BF16, hid).astype(np.float64)
+        err = rel_err_glue(got, ref)
+        upd = rel_err_glue(got - x, ref - x)
+        print(f"  layer err {err:.2e}, update err {upd:.2e}", flush=True)
+        assert np.isfinite(got).all() and err <= (3e-2 if fp8 else 1e-2)
+        assert upd <= (1.75e-2 if fp8 else 1.25e-2)
+    finally:
+        case.pool.destroy()
