@@ -5,9 +5,12 @@ head_dim, block size, batch, ragged lengths (empty, one token, tile and page
 edges), softmax scale, and the decode kernel's work split (total waves, waves
 per workgroup, minimum slice, tiles in flight).  GEMM: shapes around the
 kernel dispatch boundaries, bf16 or fp8 weights, the residual form, forced K
-splits and workgroup widths.  Every case prints its parameters before it
-runs.  Tolerances as the other tests: bf16 / f16 1e-2, fp8 pages 3e-2, GEMM
-1e-2."""
+splits and workgroup widths.  Decoder layer: head shapes, hidden and
+intermediate sizes, bf16 or fp8 pools, ragged batches, checked stage by stage
+and end to end.  Every case prints its parameters before it runs.
+Tolerances as the other tests: bf16 / f16 1e-2, fp8 pages 3e-2, GEMM 1e-2;
+the layer's stages 1e-2 (3e-2 on fp8 pools) and its end-to-end bounds as
+test_gpu_glue.test_decode_layer_step."""
 import math
 
 import numpy as np
