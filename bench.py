@@ -377,21 +377,31 @@ def bench_prefill(args):
         for i in range(args.warmup):
             case.run(layer=i % args.layers, stream_ptr=sp)
         torch.cuda.synchronize()
+        # back-to-back calls between two events (as the decode attention's
+        # value), then the same calls with an event after each one
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record(stream)
+        for i in range(args.steps):
+            case.run(layer=i % args.layers, stream_ptr=sp)
+        eb.record(stream)
+        torch.cuda.synchronize()
+        ms = ea.elapsed_time(eb) / args.steps
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
         ev[0].record(stream)
         for i in range(args.steps):
             case.run(layer=i % args.layers, stream_ptr=sp)
             ev[i + 1].record(stream)
         torch.cuda.synchronize()
-        ms = float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]))
+        ms_evented = float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]))
         flops = case.flops()
         case.pool.destroy()
-        return ms, flops
+        return ms, flops, ms_evented
 
-    ms, flops = timed(KV_BF16_CODE)
+    ms, flops, ms_ev = timed(KV_BF16_CODE)
     tflops = flops / (ms * 1e-3) / 1e12
-    log(f"prefill per-call ms: {ms:.4f}, {flops / 1e9:.1f} GFLOP")
-    ms8, _ = timed(KV_FP8_CODE)
+    log(f"prefill per-call ms: {ms:.4f} back to back ({ms_ev:.4f} with an event after each "
+        f"call), {flops / 1e9:.1f} GFLOP")
+    ms8, _, _ = timed(KV_FP8_CODE)
     log(f"prefill per-call ms with fp8-e4m3 pages: {ms8:.4f}")
     result = {
         "metric": "chunked prefill attention TFLOP/s (% bf16 MFMA peak), 1 GPU",
@@ -406,6 +416,7 @@ def bench_prefill(args):
                      "traffic": measured_traffic("cfg3"),
                      "kernel": "attn_prefill_mfma (bf16 pages)"},
         "gflop_per_call": round(flops / 1e9, 2),
+        "ms_per_call_evented": round(ms_ev, 4),
         # the same chunk over fp8-e4m3 pages (dequantized to bf16 in LDS by
         # the same MFMA kernel): half the K/V bytes, the same flops
         "fp8_pages": {"ms": round(ms8, 4), "tflops": round(flops / (ms8 * 1e-3) / 1e12, 1)},
