@@ -752,7 +752,7 @@ def main():
     # the dominant kernel alone: the same back-to-back calls again, with HIP
     # events recorded by the library around each streaming-kernel launch (on
     # the stream it is launched on); the merge after it is outside the pair
-    lib.attn_stream_timing_start(args.steps)
+    lib.attn_stream_timing_start(max(1, args.steps))
     try:
         for i in range(args.steps):
             calls["attn"](i % args.layers)
