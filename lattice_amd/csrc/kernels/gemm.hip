@@ -241,7 +241,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
 // 4- or 8-wave workgroups (halves the activation reads per MFMA, but two waves
 // then stream each weight line: 20-40% slower); summing the split partials inside this kernel
 // by the last workgroup of each tile, whose coherent stores and arrival count
-// put several memory round trips on every tile's tail.)
+// put several memory round trips on every tile's tail; for the split products,
+// 8-wave workgroups whose two wave groups take alternate k halves (summed in
+// LDS), a 3-deep weight ring, and 6-wave workgroups of 96 rows for QKV (the
+// product itself 15% faster, but the attention kernel launched two kernels
+// later then loses more than that: its one-wave workgroups land unevenly on
+// the SIMDs after a kernel whose workgroups are not a multiple of four waves).)
 template <int MB, int KCH, int EPI, bool WF8 = false, int NW = 4>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_bf16_stream(GemmParams p) {
