@@ -216,8 +216,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
     }
 }
 
-// Weight-streaming GEMM.  Workgroup = NW waves = 16*NW weight rows (16 per
-// wave; NW = 4, or 8 for unsplit plain and SwiGLU products) x up to 16*MB
+// Weight-streaming GEMM.  Workgroup = NW waves, of which the first CW stream
+// 16 weight rows each (NW = CW = 4; NW = CW = 8 for unsplit plain and SwiGLU
+// products; NW = 8, CW = 6 for the split QKV / RoPE product) x up to 16*MB
 // tokens x one K split of `klen`, walked in chunks of KCH:
 //  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
 //    whole-line streaming loads (8 rows x 128 B per instruction) and is put
@@ -246,8 +247,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
 // LDS), a 3-deep weight ring, and 6-wave workgroups of 96 rows for QKV (the
 // product itself 15% faster, but the attention kernel launched two kernels
 // later then loses more than that: its one-wave workgroups land unevenly on
-// the SIMDs after a kernel whose workgroups are not a multiple of four waves).)
-template <int MB, int KCH, int EPI, bool WF8 = false, int NW = 4>
+// the SIMDs after a kernel whose workgroups are not a multiple of four waves;
+// two helper waves that only stage activations make the same grid 8-wave
+// and keep the gain).)
+template <int MB, int KCH, int EPI, bool WF8 = false, int NW = 4, int CW = NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_bf16_stream(GemmParams p) {
     constexpr int NT = NW * 64;
@@ -274,8 +277,12 @@ void gemm_bf16_stream(GemmParams p) {
     const int nchunks = p.klen / KCH;
     const uint32_t rowb = static_cast<uint32_t>(K) * (WF8 ? 1 : 2);   // weight row bytes
 
+    // the first CW waves stream weight rows; the rest (CW < NW) only help
+    // stage the activation chunks and take part in the barriers
+    static_assert(CW >= 1 && CW <= NW, "compute waves must be 1..NW");
+    const bool streams = CW == NW || wave < CW;
     // weight rows of this wave: rowA + 0..7 (MFMA rows 0..7), rowB + 0..7 (8..15)
-    const int gw = blockIdx.x * NW + wave;
+    const int gw = blockIdx.x * CW + wave;
     int rowA, rowB;
     if constexpr (EPI == kEpiRope) {
         const int wph = p.D / 16;            // waves per head: 8 rotation pairs each
@@ -382,7 +389,7 @@ void gemm_bf16_stream(GemmParams p) {
 
     u32x4 wa0[2 * LINES], wa1[2 * LINES];
     load_x(0);
-    load_w(wa0, 0);
+    if (streams) load_w(wa0, 0);
     __builtin_amdgcn_sched_barrier(0);
     store_x(0);
     __syncthreads();
@@ -391,11 +398,11 @@ void gemm_bf16_stream(GemmParams p) {
         constexpr bool MORE = decltype(more_tag)::value;
         if constexpr (MORE) {
             load_x(c + 1);
-            load_w(later, c + 1);
+            if (streams) load_w(later, c + 1);
         }
         // keep the compiler from sinking these loads below the chunk's math
         __builtin_amdgcn_sched_barrier(0);
-        compute(now, buf);
+        if (streams) compute(now, buf);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (MORE) {
             store_x(buf ^ 1);
@@ -416,6 +423,7 @@ void gemm_bf16_stream(GemmParams p) {
         step(wa0, wa1, 0, c, Last{});
     }
 
+    if (!streams) return;
     gemm_epilogue<MB, EPI>(p, acc, rowA, rowB, m_base, ln, lg);
 }
 
@@ -528,13 +536,33 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
             if constexpr (EPI == kEpiPlain || EPI == kEpiSwiglu)
                 wide = p.part == nullptr && p.N % 128 == 0 &&
                        dev::tunable_or(dev::Tun::kGemmWaves, 8) == 8;
+            // QKV with the RoPE epilogue: 384 four-wave workgroups per 4
+            // splits would put two on half the CUs and one on the rest; when
+            // the 16-row waves of all splits come to 256 x 6, the grid is
+            // one 8-wave workgroup per CU, 6 waves streaming weights and 2
+            // only helping to stage the activations. (Grids of 6-wave
+            // workgroups leave the one-wave workgroups of the attention
+            // kernel two launches later unevenly placed on the SIMDs; for
+            // gate/up, 256 workgroups of 7 streaming waves and one helper
+            // were slower than 224 of 8 streaming waves.)
+            bool pad = false;
+            if constexpr (EPI == kEpiRope) {
+                const int waves16 = p.N / 16;   // per split
+                pad = mg == 1 && waves16 % 6 == 0 && waves16 / 6 * splits == 256 &&
+                      dev::tunable_or(dev::Tun::kGemmPad, 1) != 0;
+                if (pad) {
+                    const dim3 grid(waves16 / 6, splits, 1);
+                    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8, 6>), grid, dim3(512),
+                                       0, s, p);
+                }
+            }
             if (wide) {
                 if constexpr (EPI == kEpiPlain || EPI == kEpiSwiglu) {
                     const dim3 grid(p.N / 128, 1, mg);
                     hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8>), grid, dim3(512), 0,
                                        s, p);
                 }
-            } else {
+            } else if (!pad) {
                 const dim3 grid(p.N / 64, splits, mg);
                 hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8>), grid, dim3(256), 0, s, p);
             }

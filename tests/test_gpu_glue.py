@@ -530,20 +530,28 @@ def test_fp8_weight_layers_match_bf16_layers_on_exact_weights(gpu_lib, hq, hkv, 
     assert np.isfinite(outs[0]).all() and err <= 1e-2 and same >= 0.5
 
 
+@pytest.mark.parametrize("knob", [("KCMM_GEMM_WAVES", "4", "8"), ("KCMM_GEMM_PAD", "0", "1")])
 @pytest.mark.parametrize("fp8w", [False, True])
-def test_decode_layers_same_bits_at_4_and_8_waves(gpu_lib, tunables, fp8w):
-    """At the Llama-3-8B intermediate size the gate/up + SwiGLU projection is
-    unsplit and runs in 8-wave workgroups (KCMM_GEMM_WAVES=4: 4-wave).  Two
-    layers from the same hidden state and pages give the same bits either
-    way, with bf16 and with fp8-e4m3 projection weights."""
+def test_decode_layers_same_bits_across_workgroup_shapes(gpu_lib, tunables, fp8w, knob):
+    """Workgroup shapes that change no output's summation order give the same
+    bits.  At the Llama-3-8B sizes the gate/up + SwiGLU projection is unsplit
+    and runs in 8-wave workgroups (KCMM_GEMM_WAVES=4: 4-wave), and the QKV
+    projection with the RoPE epilogue (4 splits, 6144 rows: 256 x 6 waves of
+    16 rows) runs one 8-wave workgroup per CU with 6 streaming waves
+    (KCMM_GEMM_PAD=0: 4-wave workgroups).  Two layers from the same hidden
+    state and pages give the same bits either way, with bf16 and with
+    fp8-e4m3 projection weights."""
     import torch
     hq, hkv, d, h, inter = 32, 8, 128, 4096, 14336
     lens = [1, 16, 17, 130, 700, 64, 3, 2049]
     B = len(lens)
+    name, off, on = knob
     case = build_decode_case(gpu_lib, batch=B, num_q_heads=hq, kv_heads=hkv, head_dim=d,
                              block_size=16, ctx_lens=lens, dtype=KV_BF16, seed=41, num_layers=2)
     try:
         assert gpu_lib.gemm_plan(B, 2 * inter, h, fp8_weights=fp8w)["splits"] == 1
+        n_qkv = (hq + 2 * hkv) * d
+        assert gpu_lib.gemm_plan(B, n_qkv, h, fp8_weights=fp8w)["splits"] * n_qkv // 16 == 256 * 6
         g = torch.Generator(device="cuda")
         g.manual_seed(43 + fp8w)
         shapes = {"qkv": ((hq + 2 * hkv) * d, h), "o": (h, hq * d), "gate_up": (2 * inter, h),
@@ -568,8 +576,8 @@ def test_decode_layers_same_bits_at_4_and_8_waves(gpu_lib, tunables, fp8w):
         invd = torch.from_numpy(O.default_inv_freq(500000.0, d).astype(np.float32)).cuda()
         dv = case.dev
         outs = {}
-        for waves in ("4", "8"):
-            tunables.setenv("KCMM_GEMM_WAVES", waves)
+        for value in (off, on):
+            tunables.setenv(name, value)
             hd = hid0.clone()
             kw = dict(first_layer=0, weights=lws, hidden_ptr=hd.data_ptr(),
                       block_tables_ptr=dv["bt"].data_ptr(), seq_lens_ptr=dv["sl"].data_ptr(),
@@ -581,9 +589,9 @@ def test_decode_layers_same_bits_at_4_and_8_waves(gpu_lib, tunables, fp8w):
             else:
                 case.pool.decode_layers(**kw)
             torch.cuda.synchronize()
-            outs[waves] = hd
-        assert bool(torch.isfinite(outs["8"].float()).all())
-        assert torch.equal(outs["4"], outs["8"])
+            outs[value] = hd
+        assert bool(torch.isfinite(outs[on].float()).all())
+        assert torch.equal(outs[off], outs[on])
     finally:
         case.pool.destroy()
 
