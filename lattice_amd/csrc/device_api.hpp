@@ -31,7 +31,7 @@ enum class Tun {
     kGemmTiled,     // KCMM_GEMM_TILED
     kGemmTile,      // KCMM_GEMM_TILE
     kGemmWaves,     // KCMM_GEMM_WAVES (waves per workgroup of unsplit plain / SwiGLU products)
-    kGemmPad,       // KCMM_GEMM_PAD (0: QKV/RoPE product without the padded 8-wave grid)
+    kGemmHelpers,   // KCMM_GEMM_HELPERS (0: split products without activation-staging helper waves)
     kCount
 };
 // true and *value = atoi(variable) when the variable is set.

@@ -217,9 +217,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
 }
 
 // Weight-streaming GEMM.  Workgroup = NW waves, of which the first CW stream
-// 16 weight rows each (NW = CW = 4; NW = CW = 8 for unsplit plain and SwiGLU
-// products; NW = 8, CW = 6 for the split QKV / RoPE product) x up to 16*MB
-// tokens x one K split of `klen`, walked in chunks of KCH:
+// 16 weight rows each (NW = CW = 4, or 8 for unsplit plain and SwiGLU
+// products; NW = 8 with CW = 4, or 6 for the QKV / RoPE product, for split
+// products, whose NW - CW helper waves do all of the activation staging) x up
+// to 16*MB tokens x one K split of `klen`, walked in chunks of KCH:
 //  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
 //    whole-line streaming loads (8 rows x 128 B per instruction) and is put
 //    into MFMA A layout by fix_lines, one line at a time; chunk c+1 is in
@@ -248,8 +249,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
 // product itself 15% faster, but the attention kernel launched two kernels
 // later then loses more than that: its one-wave workgroups land unevenly on
 // the SIMDs after a kernel whose workgroups are not a multiple of four waves;
-// two helper waves that only stage activations make the same grid 8-wave
-// and keep the gain).)
+// two helper waves make the same grid 8-wave and keep the gain, and they gain
+// more when they take over the activation staging); 7 streaming waves and a
+// helper for gate/up (256 workgroups: slower than 224 of 8 streaming waves).)
 template <int MB, int KCH, int EPI, bool WF8 = false, int NW = 4, int CW = NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_bf16_stream(GemmParams p) {
@@ -259,9 +261,15 @@ void gemm_bf16_stream(GemmParams p) {
     constexpr int KC = KCH / 32;             // MFMA k-steps per chunk
     constexpr int PIECES = KCH / 8;          // 16-byte pieces per activation row
     constexpr int MROWS = 16 * MB;
-    constexpr int XLOADS = MROWS * PIECES / NT;
-    constexpr int XROWSTEP = NT / PIECES;    // activation rows per load round
-    static_assert(XLOADS * NT == MROWS * PIECES, "activation chunk must split over the threads");
+    // threads that stage the activation chunks: all of them, or (CW < NW)
+    // only the NW - CW helper waves, while the CW streaming waves never
+    // touch the activation path
+    static_assert(CW >= 1 && CW <= NW, "streaming waves must be 1..NW");
+    constexpr bool SPEC = CW < NW;
+    constexpr int XN = SPEC ? (NW - CW) * 64 : NT;
+    constexpr int XLOADS = MROWS * PIECES / XN;
+    constexpr int XROWSTEP = XN / PIECES;    // activation rows per load round
+    static_assert(XLOADS * XN == MROWS * PIECES, "activation chunk must split over the threads");
     constexpr int ROWB = PIECES * 16;         // LDS row; 16-byte pieces XOR-swizzled by row
     constexpr int XBUF = MROWS * ROWB;
     __shared__ __attribute__((aligned(16))) uint8_t xs[2 * XBUF];
@@ -277,10 +285,9 @@ void gemm_bf16_stream(GemmParams p) {
     const int nchunks = p.klen / KCH;
     const uint32_t rowb = static_cast<uint32_t>(K) * (WF8 ? 1 : 2);   // weight row bytes
 
-    // the first CW waves stream weight rows; the rest (CW < NW) only help
-    // stage the activation chunks and take part in the barriers
-    static_assert(CW >= 1 && CW <= NW, "compute waves must be 1..NW");
-    const bool streams = CW == NW || wave < CW;
+    // the first CW waves stream weight rows; the rest (CW < NW) only stage
+    // the activation chunks
+    const bool streams = !SPEC || wave < CW;
     // weight rows of this wave: rowA + 0..7 (MFMA rows 0..7), rowB + 0..7 (8..15)
     const int gw = blockIdx.x * CW + wave;
     int rowA, rowB;
@@ -310,19 +317,20 @@ void gemm_bf16_stream(GemmParams p) {
             dst[2 * c2 + 1] = load_stream(wp1 + o);
         }
     };
+    const int xt = SPEC ? tid - CW * 64 : tid;   // index among the staging threads
     u32x4 xr[XLOADS];
     auto load_x = [&](int c) {
 #pragma unroll
         for (int i = 0; i < XLOADS; ++i) {
-            const int m = min(m_base + tid / PIECES + i * XROWSTEP, p.M - 1);
+            const int m = min(m_base + xt / PIECES + i * XROWSTEP, p.M - 1);
             xr[i] = *reinterpret_cast<const u32x4*>(p.X + static_cast<size_t>(m) * K + kbeg + c * KCH +
-                                                    (tid % PIECES) * 8);
+                                                    (xt % PIECES) * 8);
         }
     };
     auto store_x = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < XLOADS; ++i) {
-            const int r = tid / PIECES + i * XROWSTEP, pc = tid % PIECES;
+            const int r = xt / PIECES + i * XROWSTEP, pc = xt % PIECES;
             *reinterpret_cast<u32x4*>(xs + buf * XBUF + r * ROWB + ((pc ^ (r & (PIECES - 1))) * 16)) = xr[i];
         }
     };
@@ -387,9 +395,54 @@ void gemm_bf16_stream(GemmParams p) {
         (void)KC;
     };
 
+    if constexpr (SPEC) {
+        // Chunk c lives in buffer c & 1. Barrier 0 follows chunk 0's
+        // staging; barrier c + 1 follows both the streaming waves' reads of
+        // chunk c and the helpers' stores of chunk c + 1 into the other
+        // buffer (whose previous chunk, c - 1, was read before barrier c).
+        // Both sides pass nchunks barriers.
+        if (!streams) {
+            load_x(0);
+            store_x(0);
+            if (nchunks > 1) load_x(1);
+            __syncthreads();
+            for (int c = 0; c + 1 < nchunks; ++c) {
+                store_x((c + 1) & 1);             // registers loaded one chunk ago
+                if (c + 2 < nchunks) load_x(c + 2);
+                __syncthreads();
+            }
+            return;
+        }
+        u32x4 wa0[2 * LINES], wa1[2 * LINES];
+        load_w(wa0, 0);
+        __syncthreads();
+        auto sstep = [&](u32x4* now, u32x4* later, int c, auto more_tag) {
+            constexpr bool MORE = decltype(more_tag)::value;
+            if constexpr (MORE) load_w(later, c + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(now, c & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (MORE) __syncthreads();
+        };
+        using More = std::integral_constant<bool, true>;
+        using Last = std::integral_constant<bool, false>;
+        int c = 0;
+        for (; c + 2 < nchunks; c += 2) {
+            sstep(wa0, wa1, c, More{});
+            sstep(wa1, wa0, c + 1, More{});
+        }
+        if (c + 1 < nchunks) {
+            sstep(wa0, wa1, c, More{});
+            sstep(wa1, wa0, c + 1, Last{});
+        } else {
+            sstep(wa0, wa1, c, Last{});
+        }
+        gemm_epilogue<MB, EPI>(p, acc, rowA, rowB, m_base, ln, lg);
+        return;
+    }
     u32x4 wa0[2 * LINES], wa1[2 * LINES];
     load_x(0);
-    if (streams) load_w(wa0, 0);
+    load_w(wa0, 0);
     __builtin_amdgcn_sched_barrier(0);
     store_x(0);
     __syncthreads();
@@ -398,11 +451,11 @@ void gemm_bf16_stream(GemmParams p) {
         constexpr bool MORE = decltype(more_tag)::value;
         if constexpr (MORE) {
             load_x(c + 1);
-            if (streams) load_w(later, c + 1);
+            load_w(later, c + 1);
         }
         // keep the compiler from sinking these loads below the chunk's math
         __builtin_amdgcn_sched_barrier(0);
-        if (streams) compute(now, buf);
+        compute(now, buf);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (MORE) {
             store_x(buf ^ 1);
@@ -423,7 +476,6 @@ void gemm_bf16_stream(GemmParams p) {
         step(wa0, wa1, 0, c, Last{});
     }
 
-    if (!streams) return;
     gemm_epilogue<MB, EPI>(p, acc, rowA, rowB, m_base, ln, lg);
 }
 
@@ -536,25 +588,25 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
             if constexpr (EPI == kEpiPlain || EPI == kEpiSwiglu)
                 wide = p.part == nullptr && p.N % 128 == 0 &&
                        dev::tunable_or(dev::Tun::kGemmWaves, 8) == 8;
-            // QKV with the RoPE epilogue: 384 four-wave workgroups per 4
-            // splits would put two on half the CUs and one on the rest; when
-            // the 16-row waves of all splits come to 256 x 6, the grid is
-            // one 8-wave workgroup per CU, 6 waves streaming weights and 2
-            // only helping to stage the activations. (Grids of 6-wave
-            // workgroups leave the one-wave workgroups of the attention
-            // kernel two launches later unevenly placed on the SIMDs; for
-            // gate/up, 256 workgroups of 7 streaming waves and one helper
-            // were slower than 224 of 8 streaming waves.)
-            bool pad = false;
-            if constexpr (EPI == kEpiRope) {
+            // split products at one token group (QKV, O and down at decode):
+            // 8-wave workgroups in which helper waves stage the activation
+            // chunks and the streaming waves only stream weights and run the
+            // MFMAs, so that the two paths overlap (KCMM_GEMM_HELPERS=0 keeps
+            // 4-wave workgroups). QKV with the RoPE epilogue (384 four-wave
+            // workgroups at 4 splits, two on half the CUs) takes 6 streaming
+            // waves of 16 rows when that makes one workgroup per CU; other
+            // split products 4.
+            bool helpers = false;
+            if constexpr (EPI == kEpiRope || EPI == kEpiPlain) {
+                helpers = mg == 1 && p.part != nullptr &&
+                          dev::tunable_or(dev::Tun::kGemmHelpers, 1) != 0;
                 const int waves16 = p.N / 16;   // per split
-                pad = mg == 1 && waves16 % 6 == 0 && waves16 / 6 * splits == 256 &&
-                      dev::tunable_or(dev::Tun::kGemmPad, 1) != 0;
-                if (pad) {
-                    const dim3 grid(waves16 / 6, splits, 1);
-                    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8, 6>), grid, dim3(512),
-                                       0, s, p);
-                }
+                if (helpers && EPI == kEpiRope && waves16 % 6 == 0 && waves16 / 6 * splits == 256)
+                    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8, 6>),
+                                       dim3(waves16 / 6, splits, 1), dim3(512), 0, s, p);
+                else if (helpers)
+                    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8, 4>),
+                                       dim3(p.N / 64, splits, 1), dim3(512), 0, s, p);
             }
             if (wide) {
                 if constexpr (EPI == kEpiPlain || EPI == kEpiSwiglu) {
@@ -562,7 +614,7 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
                     hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8>), grid, dim3(512), 0,
                                        s, p);
                 }
-            } else if (!pad) {
+            } else if (!helpers) {
                 const dim3 grid(p.N / 64, splits, mg);
                 hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8>), grid, dim3(256), 0, s, p);
             }

@@ -15,7 +15,7 @@ namespace {
 const char* const kNames[static_cast<int>(Tun::kCount)] = {
     "KCMM_ATTN_WAVES", "KCMM_ATTN_HW",   "KCMM_ATTN_MIN_TILES", "KCMM_ATTN_DEPTH",
     "KCMM_ATTN_GENERIC", "KCMM_GEMM_SPLITS", "KCMM_GEMM_WGS", "KCMM_GEMM_TILED",
-    "KCMM_GEMM_TILE", "KCMM_GEMM_WAVES", "KCMM_GEMM_PAD"};
+    "KCMM_GEMM_TILE", "KCMM_GEMM_WAVES", "KCMM_GEMM_HELPERS"};
 
 std::atomic<int> g_set[static_cast<int>(Tun::kCount)];
 std::atomic<int> g_val[static_cast<int>(Tun::kCount)];

@@ -530,17 +530,18 @@ def test_fp8_weight_layers_match_bf16_layers_on_exact_weights(gpu_lib, hq, hkv, 
     assert np.isfinite(outs[0]).all() and err <= 1e-2 and same >= 0.5
 
 
-@pytest.mark.parametrize("knob", [("KCMM_GEMM_WAVES", "4", "8"), ("KCMM_GEMM_PAD", "0", "1")])
+@pytest.mark.parametrize("knob", [("KCMM_GEMM_WAVES", "4", "8"), ("KCMM_GEMM_HELPERS", "0", "1")])
 @pytest.mark.parametrize("fp8w", [False, True])
 def test_decode_layers_same_bits_across_workgroup_shapes(gpu_lib, tunables, fp8w, knob):
     """Workgroup shapes that change no output's summation order give the same
     bits.  At the Llama-3-8B sizes the gate/up + SwiGLU projection is unsplit
-    and runs in 8-wave workgroups (KCMM_GEMM_WAVES=4: 4-wave), and the QKV
-    projection with the RoPE epilogue (4 splits, 6144 rows: 256 x 6 waves of
-    16 rows) runs one 8-wave workgroup per CU with 6 streaming waves
-    (KCMM_GEMM_PAD=0: 4-wave workgroups).  Two layers from the same hidden
-    state and pages give the same bits either way, with bf16 and with
-    fp8-e4m3 projection weights."""
+    and runs in 8-wave workgroups (KCMM_GEMM_WAVES=4: 4-wave).  The split
+    products run 8-wave workgroups whose helper waves stage the activations
+    (KCMM_GEMM_HELPERS=0: 4-wave workgroups that stage them themselves): O
+    and down with 4 streaming waves, and the QKV projection with the RoPE
+    epilogue (4 splits, 6144 rows: 256 x 6 waves of 16 rows) one workgroup
+    per CU with 6.  Two layers from the same hidden state and pages give the
+    same bits either way, with bf16 and with fp8-e4m3 projection weights."""
     import torch
     hq, hkv, d, h, inter = 32, 8, 128, 4096, 14336
     lens = [1, 16, 17, 130, 700, 64, 3, 2049]

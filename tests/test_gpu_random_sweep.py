@@ -124,6 +124,8 @@ def gemm_params(seed):
         tun["KCMM_GEMM_TILED"] = "0"
     if rng.random() < 0.3:
         tun["KCMM_GEMM_WAVES"] = "4"
+    if rng.random() < 0.3:
+        tun["KCMM_GEMM_HELPERS"] = "0"
     return m, n, k, fp8, residual, tun
 
 
