@@ -217,10 +217,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
 }
 
 // Weight-streaming GEMM.  Workgroup = NW waves, of which the first CW stream
-// 16 weight rows each (NW = CW = 4, or 8 for unsplit plain and SwiGLU
-// products; NW = 8 with CW = 4, or 6 for the QKV / RoPE product, for split
-// products, whose NW - CW helper waves do all of the activation staging) x up
-// to 16*MB tokens x one K split of `klen`, walked in chunks of KCH:
+// 16 weight rows each (NW = CW = 4 without helper waves; split products NW =
+// 8 with CW = 4, or 6 for the QKV / RoPE product; unsplit plain and SwiGLU
+// products NW = 12 with CW = 8, or NW = CW = 8 without helpers; the NW - CW
+// helper waves do all of the activation staging) x up to 16*MB tokens x one
+// K split of `klen`, walked in chunks of KCH:
 //  * each wave's weight chunk (16 rows x KCH) goes HBM -> registers with
 //    whole-line streaming loads (8 rows x 128 B per instruction) and is put
 //    into MFMA A layout by fix_lines, one line at a time; chunk c+1 is in
@@ -253,7 +254,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, f32x4 (&acc)[
 // more when they take over the activation staging); 7 streaming waves and a
 // helper for gate/up (256 workgroups: slower than 224 of 8 streaming waves).)
 template <int MB, int KCH, int EPI, bool WF8 = false, int NW = 4, int CW = NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW > 8 ? 3 : 2)))
 void gemm_bf16_stream(GemmParams p) {
     constexpr int NT = NW * 64;
     // 128-byte lines per weight row per chunk (fp8 weights: half as many)
@@ -607,6 +608,18 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
                 else if (helpers)
                     hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8, 4>),
                                        dim3(p.N / 64, splits, 1), dim3(512), 0, s, p);
+            }
+            // unsplit plain and SwiGLU products: 12-wave workgroups, 8 waves
+            // streaming 128 weight rows and 4 helpers staging activations
+            // (three waves per SIMD; fp8 gate/up and the lm_head gain, bf16
+            // gate/up is unchanged)
+            if constexpr (EPI == kEpiPlain || EPI == kEpiSwiglu) {
+                if (wide && mg == 1 && dev::tunable_or(dev::Tun::kGemmHelpers, 1) != 0) {
+                    hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 12, 8>),
+                                       dim3(p.N / 128, 1, 1), dim3(768), 0, s, p);
+                    wide = false;
+                    helpers = true;
+                }
             }
             if (wide) {
                 if constexpr (EPI == kEpiPlain || EPI == kEpiSwiglu) {

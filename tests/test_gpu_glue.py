@@ -535,12 +535,13 @@ def test_fp8_weight_layers_match_bf16_layers_on_exact_weights(gpu_lib, hq, hkv, 
 def test_decode_layers_same_bits_across_workgroup_shapes(gpu_lib, tunables, fp8w, knob):
     """Workgroup shapes that change no output's summation order give the same
     bits.  At the Llama-3-8B sizes the gate/up + SwiGLU projection is unsplit
-    and runs in 8-wave workgroups (KCMM_GEMM_WAVES=4: 4-wave).  The split
-    products run 8-wave workgroups whose helper waves stage the activations
-    (KCMM_GEMM_HELPERS=0: 4-wave workgroups that stage them themselves): O
-    and down with 4 streaming waves, and the QKV projection with the RoPE
-    epilogue (4 splits, 6144 rows: 256 x 6 waves of 16 rows) one workgroup
-    per CU with 6.  Two layers from the same hidden state and pages give the
+    and runs in 12-wave workgroups, 8 waves streaming 128 weight rows and 4
+    helpers staging the activations (KCMM_GEMM_WAVES=4: 4-wave workgroups).
+    The split products run 8-wave workgroups whose helper waves stage the
+    activations: O and down with 4 streaming waves, and the QKV projection
+    with the RoPE epilogue (4 splits, 6144 rows: 256 x 6 waves of 16 rows)
+    one workgroup per CU with 6 (KCMM_GEMM_HELPERS=0: no helpers anywhere;
+    4-wave split products, 8-wave gate/up).  Two layers from the same hidden state and pages give the
     same bits either way, with bf16 and with fp8-e4m3 projection weights."""
     import torch
     hq, hkv, d, h, inter = 32, 8, 128, 4096, 14336
