@@ -593,16 +593,16 @@ bool launch_stream(GemmParams p, int splits, bool want_partials, float** part, u
             // 8-wave workgroups in which helper waves stage the activation
             // chunks and the streaming waves only stream weights and run the
             // MFMAs, so that the two paths overlap (KCMM_GEMM_HELPERS=0 keeps
-            // 4-wave workgroups). QKV with the RoPE epilogue (384 four-wave
-            // workgroups at 4 splits, two on half the CUs) takes 6 streaming
-            // waves of 16 rows when that makes one workgroup per CU; other
-            // split products 4.
+            // 4-wave workgroups). A product whose 16-row waves over all
+            // splits number 256 x 6 (QKV at 4 splits: 384 four-wave
+            // workgroups, two on half the CUs) takes 6 streaming waves, one
+            // workgroup per CU; other split products 4.
             bool helpers = false;
             if constexpr (EPI == kEpiRope || EPI == kEpiPlain) {
                 helpers = mg == 1 && p.part != nullptr &&
                           dev::tunable_or(dev::Tun::kGemmHelpers, 1) != 0;
                 const int waves16 = p.N / 16;   // per split
-                if (helpers && EPI == kEpiRope && waves16 % 6 == 0 && waves16 / 6 * splits == 256)
+                if (helpers && waves16 % 6 == 0 && waves16 / 6 * splits == 256)
                     hipLaunchKernelGGL((gemm_bf16_stream<MB, KCH, EPI, WF8, 8, 6>),
                                        dim3(waves16 / 6, splits, 1), dim3(512), 0, s, p);
                 else if (helpers)
